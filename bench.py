@@ -1,0 +1,242 @@
+"""Benchmark of the EXL3 quantized matmul path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+
+Workload (the configuration its metric "EXL3 GEMV
+HBM GB/s at bs=1" is quoted on): a decode pass at batch 1 over the linears of
+a 36-layer Qwen3-8B-shaped decoder (per layer q/o 4096->4096, k/v
+4096->1024, gate/up 4096->12288, down 12288->4096), EXL3 K=4 mul1 weights,
+uniform-random trellis words, suh +-1, svh f16(+-U[0.5,1.5]*0.02), f16
+N(0,1) activations.  One step = one matmul (prepare + decode GEMV + finish)
+per linear, 252 linears, 3.47 GB of distinct packed weights (beyond the 256 MB
+Infinity Cache, so every step reads HBM).  The step is captured once into a
+HIP graph and replayed.
+
+`value` = packed-weight bytes per step * steps / timed seconds (GB/s).
+`roofline` = the dominant kernel (the K=4 batch-1 decode GEMV) measured with
+HIP event pairs around each launch, over every linear of the model:
+algorithmic bytes (in*out*K/8 per launch) / average launch duration, against
+the 8 TB/s HBM peak.  `cpu_baseline` = the CPU oracle's projection
+(prepare + decode + f32 dot + finish, the reference's CPU path restated in
+C, oracle/exl3_oracle.c) on the host cores over a bounded sample of the same
+linears.  `extra` carries the prefill GEMM (M=2048, K=4) TFLOP/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "EXL3 GEMV HBM GB/s (% of peak) at bs=1; prefill GEMM TFLOPS; decode tok/s"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+LAYERS = 36
+SHAPES = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
+          ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096)]
+K_BITS = 4
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(torch, X, layers: int, seed: int):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    lins = []
+    n = 16 * K_BITS
+    for _ in range(layers):
+        for name, i, o in SHAPES:
+            t = torch.randint(-32768, 32768, (i // 16, o // 16, n), dtype=torch.int32, device="cuda",
+                              generator=g).to(torch.int16)
+            suh = (torch.randint(0, 2, (i,), device="cuda", generator=g) * 2 - 1).to(torch.float16)
+            sgn = torch.randint(0, 2, (o,), device="cuda", generator=g) * 2 - 1
+            mag = torch.rand(o, device="cuda", generator=g) + 0.5
+            svh = (sgn * mag * 0.02).to(torch.float16)
+            lins.append((name, i, o, X.Linear(t, suh, svh)))
+    return lins
+
+
+def packed_bytes(i: int, o: int) -> int:
+    return i * o * K_BITS // 8
+
+
+def cpu_baseline(seconds: float):
+    from oracle import oracle as O
+    rng = np.random.default_rng(7)
+    n = 16 * K_BITS
+    todo = []
+    for name, i, o in SHAPES:
+        t = rng.integers(0, 65536, (i // 16, o // 16, n), dtype=np.uint16)
+        suh = np.where(rng.random(i) < 0.5, -1.0, 1.0).astype(np.float16).view(np.uint16)
+        svh = (np.where(rng.random(o) < 0.5, -1.0, 1.0) * rng.uniform(0.5, 1.5, o) * 0.02
+               ).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal((1, i)).astype(np.float32)
+        todo.append((i, o, t, suh, svh, x))
+    done_bytes = 0
+    linears = 0
+    t0 = time.perf_counter()
+    while True:
+        for i, o, t, suh, svh, x in todo:
+            O.project(x, t, suh, svh, i, o, n)
+            done_bytes += packed_bytes(i, o)
+            linears += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": O.threads(),
+            "kind": "port",
+            "sample": f"{linears} batch-1 K=4 projections cycling one Qwen3-8B layer's 7 linears "
+                      f"(q,k,v,o,gate,up,down; {sum(packed_bytes(i, o) for _, i, o in SHAPES) / 1e6:.1f} MB "
+                      f"packed), {el:.1f} s, oracle/exl3_oracle.c exl3o_project"}
+
+
+def gemm_tflops(torch, X, iters: int = 10):
+    """Prefill GEMM M=2048 at K=4 on the gate/up shape (4096 -> 12288)."""
+    rows, i, o = 2048, 4096, 12288
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    lins = []
+    for _ in range(3):  # rotate 3 weights (75 MB) with a 50 MB activation block
+        t = torch.randint(-32768, 32768, (i // 16, o // 16, 64), dtype=torch.int32, device="cuda",
+                          generator=g).to(torch.int16)
+        suh = torch.ones(i, dtype=torch.float16, device="cuda")
+        svh = torch.full((o,), 0.02, dtype=torch.float16, device="cuda")
+        lins.append(X.Linear(t, suh, svh))
+    x = torch.randn(rows, i, device="cuda", generator=g).to(torch.float16)
+    y = torch.empty(rows, o, dtype=torch.float16, device="cuda")
+    for lin in lins:
+        lin(x, out=y)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for it in range(iters):
+        lins[it % 3](x, out=y)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / iters
+    tf = 2.0 * rows * i * o / (ms * 1e-3) / 1e12
+    return {"prefill_gemm_m2048_gate_up_k4": {"tflops": round(tf, 2), "ms": round(ms, 4),
+                                              "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
+                                              "includes": "prepare + LDS-decode MFMA GEMM + finish"}}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the EXL3 path has no multi-GPU leg); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from plugins_amd import exl3 as X
+    torch.cuda.set_device(0)
+    log("building model:", args.layers, "layers")
+    lins = build_model(torch, X, args.layers, seed=1234)
+    step_bytes = sum(packed_bytes(i, o) for _, i, o, _ in lins)
+    xs = {i: torch.randn(1, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
+    ys = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+
+    def step():
+        for (name, i, o, lin), y in zip(lins, ys):
+            lin(xs[i], out=y)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    run = step
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+            step()
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        run = graph.replay
+    log("timing", args.steps, "steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_per_step = el * 1e3 / args.steps
+    value = step_bytes * args.steps / el / 1e9
+
+    # roofline leg: event pairs around each decode-GEMV launch (inner product
+    # only: prepared rows in, z out), every linear once per pass, 3 passes
+    log("roofline leg")
+    xps = {i: X.prepare(lins[[l[1] for l in lins].index(i)][3].weight, xs[i]) for i in (4096, 12288)}
+    zs = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+    pairs = []
+    for _ in range(3):
+        for (name, i, o, lin), z in zip(lins, zs):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            X.check(X.lib().exl3_inner(X.ctypes.byref(lin.weight), X.array(xps[i]), X.array(z),
+                                       X.stream_handle()), "inner")
+            b.record()
+            pairs.append((packed_bytes(i, o), a, b))
+    torch.cuda.synchronize()
+    kbytes = sum(p[0] for p in pairs)
+    kms = sum(a.elapsed_time(b) for _, a, b in pairs)
+    achieved = kbytes / (kms * 1e-3) / 1e9
+    per_shape = {}
+    for (name, i, o, _), (nb, a, b) in zip(lins * 3, pairs):
+        d = per_shape.setdefault(name, [0, 0.0])
+        d[0] += nb
+        d[1] += a.elapsed_time(b)
+    shapes = {k: round(v[0] / (v[1] * 1e-3) / 1e9, 1) for k, v in per_shape.items()}
+
+    extra = {}
+    try:
+        extra.update(gemm_tflops(torch, X))
+    except Exception as ex:  # reported, not hidden
+        extra["prefill_gemm_error"] = repr(ex)
+    extra["gemv_gbs_per_shape"] = shapes
+    extra["graph"] = graph is not None
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"decode GEMV pass, batch 1, EXL3 K={K_BITS} mul1, "
+                               f"{args.layers}-layer Qwen3-8B-shaped linears (q,k,v,o,gate,up,down)",
+                   "layers": args.layers, "batch": 1, "K": K_BITS, "packed_bytes_per_step": step_bytes,
+                   "linears_per_step": len(lins)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "exl3::gemv_kernel<4,1,0>", "launches": len(pairs),
+                     "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,310 @@
+/*
+ * exl3_mi355x.h -- C ABI of the MI355X (gfx950) EXL3 quantized-matmul library.
+ *
+ * This is the drop-in boundary for the turboexl3 plugins' quant path.  The
+ * reference exposes it as mlx-serve's quant plugin table, `QuantTable`, an
+ * extern struct of C-callconv function pointers
+ * (turboexl3_qwen38/overlay/mlx_serve/abi/quant.zig:24-108), which
+ * turboexl3_ds41 fills in turboexl3_ds41/plugin.zig:28-43.  The kit that
+ * defines `Str`, `Verdict`, `Claim`, `Array`, `Stream`, `Weight`, `LoadCtx`,
+ * `Source`, `PackDir` and `Swiglu` is an external dependency absent from the
+ * reference tree, so those types are re-declared here from their use sites
+ * (cited per type).  MLX handles become plain descriptors: a device pointer
+ * with dtype and shape, and a hipStream_t.
+ *
+ * Paths in citations are relative to /root/reference/plugins/.
+ *
+ * Threading: every entry is thread-compatible.  Work is recorded on the stream
+ * passed in; calls that share a weight must be ordered on one stream.
+ * `claims`, `validate` and `bill` never touch the GPU
+ * (turboexl3_qwen38/overlay/mlx_serve/abi/quant.zig:22-23).
+ * Errors are named refusals, never a silent fallback: every entry that can
+ * fail returns an `exl3_verdict` whose `why` is a static string.
+ */
+#ifndef EXL3_MI355X_H
+#define EXL3_MI355X_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Version of this table; `exl3_quant_table.version` carries it
+ * (quant.zig:16 `version: u32 = 1`). */
+#define EXL3_ABI_VERSION 1u
+
+/* kit `Str`: a byte slice, not NUL-terminated (used as `Str.of(..)` /
+ * `.slice()` throughout turboexl3_ds41/config.zig:43-61). */
+typedef struct exl3_str {
+  const char *ptr;
+  size_t len;
+} exl3_str;
+
+/* kit `Verdict{code, why}` with codes ok, unsupported, failed, too_large
+ * (refusals: turboexl3_ds41/plugin.zig:50,93,187; quant.zig:98). */
+enum {
+  EXL3_OK = 0,
+  EXL3_UNSUPPORTED = 1,
+  EXL3_FAILED = 2,
+  EXL3_TOO_LARGE = 3,
+};
+typedef struct exl3_verdict {
+  int32_t code;
+  const char *why; /* static string; "" when ok */
+} exl3_verdict;
+
+/* kit `Claim`: `.no` and `.by_marker` are the values the reference returns
+ * (turboexl3_ds41/config.zig:43-47, turboexl3_qwen38/config.zig:18-28). */
+enum {
+  EXL3_CLAIM_NO = 0,
+  EXL3_CLAIM_BY_MODE = 1,
+  EXL3_CLAIM_BY_MARKER = 2,
+};
+typedef int32_t exl3_claim;
+
+/* Element types, numbered as mlx-c's `mlx_dtype` (the ABI passes dtypes as
+ * that enum: quant.zig:113 "mlx-c's `mlx_dtype`"). */
+enum {
+  EXL3_DT_BOOL = 0,
+  EXL3_DT_U8 = 1,
+  EXL3_DT_U16 = 2,
+  EXL3_DT_U32 = 3,
+  EXL3_DT_U64 = 4,
+  EXL3_DT_I8 = 5,
+  EXL3_DT_I16 = 6,
+  EXL3_DT_I32 = 7,
+  EXL3_DT_I64 = 8,
+  EXL3_DT_F16 = 9,
+  EXL3_DT_F32 = 10,
+  EXL3_DT_F64 = 11,
+  EXL3_DT_BF16 = 12,
+};
+
+/* kit `Array` (an MLX array handle) as a descriptor of a dense row-major
+ * device buffer.  An array with data == NULL is "empty" (the reference's
+ * `.{}` / `ctx == null`, e.g. `inds` of a dense SwiGLU,
+ * turboexl3_ds41/plugin.zig:271).  `owned` is set on arrays this library
+ * allocated; free them with exl3_array_free. */
+#define EXL3_MAX_DIMS 4
+typedef struct exl3_array {
+  void *data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[EXL3_MAX_DIMS];
+  uint32_t owned;
+  uint32_t _pad;
+} exl3_array;
+
+/* kit `Stream`: here a hipStream_t (NULL = the device's null stream). */
+typedef void *exl3_stream;
+
+/* kit `Weight{w, scales, biases, side, flags}` (turboexl3_ds41/plugin.zig:89,
+ * 183, 231-237): for EXL3, w = trellis u16 [in/16, out/16, n] (a bank:
+ * [E, in/16, out/16, n]), scales = suh f16 [in] ([E, in]), biases = svh f16
+ * [out] ([E, out]).  `priv` holds the weight's decode parameters (codebook,
+ * window, rate) so no process-global decode state exists
+ * (contrast sushi_ds41/src/sushi/exl3/root.zig:117-120). */
+typedef struct exl3_weight {
+  exl3_array w;
+  exl3_array scales;
+  exl3_array biases;
+  exl3_array side;
+  uint32_t flags;
+  uint32_t _pad;
+  void *priv;
+} exl3_weight;
+
+/* A host-side view of one stored tensor, as a weight source hands it out. */
+typedef struct exl3_host_tensor {
+  const void *data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[EXL3_MAX_DIMS];
+} exl3_host_tensor;
+
+/* kit `Source`: where a format reads a pack's tensors (quant.zig:17-18;
+ * `ctx.source.tensor(name)` in turboexl3_ds41/plugin.zig:147,194).
+ * `tensor` fills *out with a borrowed host view and returns 1, or returns 0
+ * when the pack has no such tensor. */
+typedef struct exl3_source {
+  void *self;
+  int (*tensor)(void *self, exl3_str name, exl3_host_tensor *out);
+} exl3_source;
+
+/* kit `PackDir` (`d.fileBytes(name)`, turboexl3_ds41/plugin.zig:62). */
+typedef struct exl3_pack_dir {
+  void *self;
+  uint64_t (*file_bytes)(void *self, exl3_str name);
+} exl3_pack_dir;
+
+/* kit `LoadCtx` (fields used: host, block_json, dir, source, stream;
+ * turboexl3_ds41/plugin.zig:52-80,86-91).  `device` selects the GPU;
+ * `state` is written by `open` and read by the loads. */
+typedef struct exl3_load_ctx {
+  uint32_t size;
+  int32_t device;
+  exl3_str block_json;
+  exl3_str config_json;
+  const exl3_source *source;
+  const exl3_pack_dir *dir;
+  exl3_stream stream;
+  void *state;
+} exl3_load_ctx;
+
+/* kit `Swiglu` options (`.limit`, `.verify_rows`:
+ * turboexl3_qwen38/src/direct/moe.zig:65, turboexl3_ds41/plugin.zig:272-280).
+ * limit > 0 clamps gate to min(g, limit) and up to [-limit, limit]. */
+typedef struct exl3_swiglu_opts {
+  uint32_t size;
+  int32_t limit;
+  bool verify_rows;
+} exl3_swiglu_opts;
+
+/* ---------------------------------------------------------------- entries
+ * One flat symbol per QuantTable entry, each also reachable through the table
+ * below.  Each replaces the reference entry cited beside it.
+ */
+
+/* QuantTable.claims (quant.zig:29; turboexl3_ds41/config.zig:43-47):
+ * claims an EXL3 quantization block (`quant_method: "exl3"` or
+ * `format: "exl3"`) by marker, anything else `no`. */
+exl3_claim exl3_claims(exl3_str block_json, exl3_str config_json);
+
+/* QuantTable.validate (quant.zig:31; turboexl3_ds41/config.zig:49-54, and
+ * turboexl3's block rules as turboexl3_qwen38/config.zig:86-105 restates
+ * them): refuses by name NotExl3, Exl3CodebookUnsupported (anything but mul1
+ * or mcg, e.g. 3inst), Exl3WindowUnsupported (window outside 8..16),
+ * Exl3RateUnsupported (k with 16k not an even integer in 16..128),
+ * Exl3TopKExceedsReduceBank (num_experts_per_tok > 32). */
+exl3_verdict exl3_validate(exl3_str block_json, exl3_str config_json,
+                           const exl3_pack_dir *dir);
+
+/* QuantTable.bill (quant.zig:33; turboexl3_ds41/config.zig:56-61): resident
+ * bytes once loaded = the stored bytes (the HBM layout is the pack layout). */
+uint64_t exl3_bill(exl3_str block_json, exl3_str model_dir, uint64_t stored);
+
+/* QuantTable.open / close (quant.zig:34-35; turboexl3_ds41/plugin.zig:52-82):
+ * parses the block (codebook, window) into ctx->state and initialises the
+ * device; close frees ctx->state (loaded weights outlive it). */
+exl3_verdict exl3_open(exl3_load_ctx *ctx);
+void exl3_close(exl3_load_ctx *ctx);
+
+/* QuantTable.load_tensor (quant.zig:37; turboexl3_ds41/plugin.zig:86-103):
+ * `<name>.trellis` (i16/u16 [in/16, out/16, n]), `<name>.suh` (f16 [in]),
+ * `<name>.svh` (f16 [out]) from ctx->source, copied to device memory on
+ * ctx->stream.  in_dim != 0 must equal in.  Refusals: MissingWeight,
+ * NotShaped (the reference's `not_shaped` text). */
+exl3_verdict exl3_load_tensor(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                              exl3_weight *out);
+
+/* QuantTable.load_bank (quant.zig:39; turboexl3_ds41/plugin.zig:127-185):
+ * the routed experts `<prefix>.<e><suffix>` for e = 0.. (name =
+ * `<prefix>.<proj>`, split at its last '.') stacked on a new first axis. */
+exl3_verdict exl3_load_bank(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                            exl3_weight *out);
+
+/* QuantTable.release (quant.zig:40; turboexl3_ds41/plugin.zig:231-237):
+ * frees every array the weight owns and zeroes it. */
+void exl3_release(exl3_weight *w);
+
+/* QuantTable.matmul (quant.zig:41-42; turboexl3_ds41/plugin.zig:243-248 ->
+ * turboexl3 `linear`): out = x @ W^T, x [..., in] in f16/bf16/f32, out
+ * [..., out] in x's dtype.  Rounding points (quant.zig:52-55):
+ * xp = f16(H(f16(x)*suh)/sqrt(128)); z = f16(sum_k xp*W) (f32 accumulate);
+ * y = f16(H(z)/sqrt(128)*svh) then x's dtype.  If out->data is NULL the
+ * library allocates the result (owned = 1); otherwise it writes into the
+ * caller's buffer, which must have x's dtype and the result's shape. */
+exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3_array *out);
+
+/* QuantTable.moe (quant.zig:43-45): turboexl3_ds41 refuses it ("routed
+ * experts run through swiglu", turboexl3_ds41/plugin.zig:263-265); so does
+ * this library, with the same reason. */
+exl3_verdict exl3_moe(const exl3_weight *bank, exl3_array x, exl3_array lhs, exl3_array rhs,
+                      bool sorted, exl3_stream s, exl3_array *out);
+
+/* QuantTable.swiglu (quant.zig:48-50; turboexl3_ds41/plugin.zig:267-283 ->
+ * turboexl3 `moe` / `moeClamped`): x [B, S, D] through the banks' experts
+ * inds [B, S, K] (i32/u32) weighted by scores [B, S, K] (f32/f16/bf16):
+ * y = sum_k score_k * down_e(silu(gate_e(x)) * up_e(x)), in x's dtype.
+ * Empty inds: the dense SwiGLU MLP of the (single-bank) weights.  Output
+ * ownership as exl3_matmul. */
+exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const exl3_weight *down,
+                         exl3_array x, exl3_array inds, exl3_array scores,
+                         const exl3_swiglu_opts *opts, exl3_stream s, exl3_array *out);
+
+/* ----------------------------------------------------- the plugin table */
+
+/* kit `QuantTable` (quant.zig:24-50), the entries turboexl3_ds41 fills
+ * (turboexl3_ds41/plugin.zig:28-43).  Optional entries the reference leaves
+ * null for this plugin (the GDN-tail, attention and resident entries of
+ * quant.zig:51-107) are not part of this table. */
+typedef struct exl3_quant_table {
+  uint32_t size;
+  uint32_t version;
+  exl3_str name;
+  exl3_claim (*claims)(exl3_str block_json, exl3_str config_json);
+  exl3_verdict (*validate)(exl3_str block_json, exl3_str config_json, const exl3_pack_dir *dir);
+  uint64_t (*bill)(exl3_str block_json, exl3_str model_dir, uint64_t stored);
+  exl3_verdict (*open)(exl3_load_ctx *ctx);
+  void (*close)(exl3_load_ctx *ctx);
+  exl3_verdict (*load_tensor)(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                              exl3_weight *out);
+  exl3_verdict (*load_bank)(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                            exl3_weight *out);
+  void (*release)(exl3_weight *w);
+  exl3_verdict (*matmul)(const exl3_weight *w, exl3_array x, exl3_stream s, exl3_array *out);
+  exl3_verdict (*moe)(const exl3_weight *bank, exl3_array x, exl3_array lhs, exl3_array rhs,
+                      bool sorted, exl3_stream s, exl3_array *out);
+  exl3_verdict (*register_kernels)(const void *host);
+  exl3_verdict (*swiglu)(const exl3_weight *gate, const exl3_weight *up, const exl3_weight *down,
+                         exl3_array x, exl3_array inds, exl3_array scores,
+                         const exl3_swiglu_opts *opts, exl3_stream s, exl3_array *out);
+} exl3_quant_table;
+
+/* The exported table (the reference exports it as `exportName(name,
+ * version)`, quant.zig:22; plugin name turboexl3_ds41/plugin.zig:22). */
+const exl3_quant_table *exl3_quant_table_get(void);
+
+/* ------------------------------------------------------- support entries */
+
+/* Frees an array this library allocated (owned != 0); no-op otherwise. */
+void exl3_array_free(exl3_array *a);
+
+/* A weight over device arrays the caller already holds (borrowed, not freed
+ * by release): the reference's `share` of source arrays
+ * (turboexl3_ds41/plugin.zig:213-218) for callers whose weights are already
+ * resident.  block_json supplies codebook and window (NULL/empty: mul1, 16). */
+exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh,
+                              exl3_str block_json, int32_t device, exl3_weight *out);
+
+/* The decoded tile matrix W_inner f16 [in, out] of a single-bank weight (a
+ * bank: expert `expert`), bit-exact to the reference decode
+ * (sushi_ds41/src/sushi/exl3/expert_exl3.zig:416-438; the Metal
+ * `q3_exl3_dig_decmat_*` kernels, turboexl3_ds41/src/exl3/kernels/exl3/
+ * q3_exl3_dig_decmat_5120x2304_mul1hk3.metal:1-52).  out: f16 [in, out]. */
+exl3_verdict exl3_decode_matrix(const exl3_weight *w, int32_t expert, exl3_array out,
+                                exl3_stream s);
+
+/* The prepare and finish halves of matmul as their own launches
+ * (quant.zig:52-55, turboexl3's `linear_prepared` / `linear_finish` split):
+ * prepare: x [rows, in] -> xp f16 [rows, in]; finish: z f16 [rows, out] ->
+ * y [rows, out] in y's dtype. */
+exl3_verdict exl3_prepare(const exl3_weight *w, exl3_array x, exl3_array xp, exl3_stream s);
+exl3_verdict exl3_finish(const exl3_weight *w, exl3_array z, exl3_array y, exl3_stream s);
+
+/* The inner product alone: xp f16 [rows, in] -> z f16 [rows, out]
+ * (sushi_ds41/src/sushi/exl3/expert_exl3.zig:503-532). */
+exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_stream s);
+
+/* Library version string and the kernel variant a matmul of `rows` rows
+ * takes ("gemv", "gemm"): diagnostics for tests and benchmarks. */
+const char *exl3_version(void);
+const char *exl3_matmul_path(const exl3_weight *w, int64_t rows);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,183 @@
+// exl3_device.h -- device-side pieces shared by the EXL3 kernels (gfx950, wave64).
+//
+// The EXL3 trellis format (paths relative to /root/reference/plugins/):
+//  * a linear is stored as 16x16 tiles, trellis [in/16][out/16][n] u16 with
+//    n = 16K halfwords per tile (sushi_ds41/src/sushi/exl3/expert_exl3.zig:176-245);
+//  * u32 word m of a tile is hw[2m] | hw[2m+1] << 16, i.e. the little-endian
+//    dword at byte 4m (expert_exl3.zig:313-315), and stream bit b is bit
+//    31 - b%32 of word b/32 (expert_exl3.zig:1065-1066);
+//  * codeword t is the 16 stream bits ending at floor((t+1) n / 16), circular
+//    over the tile's 16n bits (expert_exl3.zig:202-205, 317-336);
+//  * codeword p = 8t+j sits at row rows[j%4], column t/4 + (j<4 ? 0 : 8) of the
+//    tile, rows = {2q, 2q+1, 2q+8, 2q+9}, q = t%4 (expert_exl3.zig:379-398).
+//
+// The 32 codewords 32a..32a+31 of a tile ("chunk a") are exactly columns a and
+// a+8 over all 16 rows, and for an integer rate K they occupy the K dwords
+// K*a..K*a+K-1, plus 16-K history bits from the previous chunk's last dword.
+// One lane therefore decodes one chunk with compile-time bit windows and no
+// exchange inside the tile beyond that one history dword.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+// 1/sqrt(128) as the reference's kernels write it (expert_exl3_kernels.zig:930).
+constexpr float HAD_SCALE = 0.08838834764831845f;
+// mul1: x = cw * 0x83DCD12D; w = f16((1024 + bytesum(x)) * f16(0x1EEE) + f16(0xC931))
+// (expert_exl3.zig:275-284; turboexl3_ds41/src/exl3/kernels.zig:966-975).
+constexpr uint32_t MUL1_MULT = 0x83DCD12Du;
+constexpr uint16_t MUL1_INV = 0x1EEEu;
+constexpr uint16_t MUL1_BIAS = 0xC931u;
+// mcg: p = 0x3B603B60 ^ ((cw * 0xCBAC1FED) & 0x8FFF8FFF); w = f16(half(p.lo) + half(p.hi))
+// (expert_exl3.zig:267-273).
+constexpr uint32_t MCG_MULT = 0xCBAC1FEDu;
+
+enum Codebook { CB_MUL1 = 0, CB_MCG = 1 };
+enum OutType { OUT_F16 = 0, OUT_BF16 = 1, OUT_F32 = 2 };
+
+template <typename T, typename F>
+__device__ __forceinline__ T bits(F f) {
+  return __builtin_bit_cast(T, f);
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)bits<_Float16>(h); }
+// f32 -> f16, round to nearest even (v_cvt_f16_f32 under the default mode).
+__device__ __forceinline__ uint16_t f2h(float f) { return bits<uint16_t>((_Float16)f); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return bits<float>((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = bits<uint32_t>(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Reads element i of an activation array of type `dt` as f32.
+__device__ __forceinline__ float load_act(const void *p, size_t i, int dt) {
+  if (dt == OUT_F16) return h2f(((const uint16_t *)p)[i]);
+  if (dt == OUT_BF16) return bf2f(((const uint16_t *)p)[i]);
+  return ((const float *)p)[i];
+}
+
+// Stores a finished f16 value in the output dtype ("then the output dtype",
+// turboexl3_qwen38/overlay/mlx_serve/abi/quant.zig:52-55).
+__device__ __forceinline__ void store_out(void *p, size_t i, uint16_t y16, int dt) {
+  if (dt == OUT_F16)
+    ((uint16_t *)p)[i] = y16;
+  else if (dt == OUT_BF16)
+    ((uint16_t *)p)[i] = f2bf(h2f(y16));
+  else
+    ((float *)p)[i] = h2f(y16);
+}
+
+// ------------------------------------------------------------ codebooks
+
+// Two codewords (low 16 bits of v0, v1 after the window mask) to a packed f16
+// pair [w1 | w0].  mul1: v_sad_u8 sums x's bytes onto 0x6400 (f16 1024.0) and
+// v_sad_hi_u8 puts the second sum in the high half, so h = f16 pair (1024+s1,
+// 1024+s0) exactly; one packed f16 FMA then rounds once, as the reference's
+// single RNE does (kernels.zig:966-975).
+template <int CB>
+__device__ __forceinline__ uint32_t decode_pair(uint32_t v0, uint32_t v1, uint32_t mask) {
+  if constexpr (CB == CB_MUL1) {
+    const uint32_t x0 = (v0 & mask) * MUL1_MULT;
+    const uint32_t x1 = (v1 & mask) * MUL1_MULT;
+    uint32_t h = __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u);
+    h = __builtin_amdgcn_sad_hi_u8(x1, 0u, h);
+    const h2_t inv = {bits<_Float16>(MUL1_INV), bits<_Float16>(MUL1_INV)};
+    const h2_t bias = {bits<_Float16>(MUL1_BIAS), bits<_Float16>(MUL1_BIAS)};
+    return bits<uint32_t>(__builtin_elementwise_fma(bits<h2_t>(h), inv, bias));
+  } else {
+    const uint32_t p0 = 0x3B603B60u ^ (((v0 & mask) * MCG_MULT) & 0x8FFF8FFFu);
+    const uint32_t p1 = 0x3B603B60u ^ (((v1 & mask) * MCG_MULT) & 0x8FFF8FFFu);
+    const uint32_t lo = __builtin_amdgcn_perm(p1, p0, 0x05040100u);  // [p1.lo | p0.lo]
+    const uint32_t hi = __builtin_amdgcn_perm(p1, p0, 0x07060302u);  // [p1.hi | p0.hi]
+    return bits<uint32_t>(bits<h2_t>(lo) + bits<h2_t>(hi));
+  }
+}
+
+// One codeword's f16 bits (scalar form of decode_pair).
+template <int CB>
+__device__ __forceinline__ uint16_t decode_one(uint32_t v, uint32_t mask) {
+  return (uint16_t)(decode_pair<CB>(v, v, mask) & 0xFFFFu);
+}
+
+// ---------------------------------------------------- integer-rate chunks
+
+// Codeword i (0..31) of a chunk held as w[0] = history dword (the previous
+// chunk's last dword, circularly), w[1..K] = the chunk's K dwords.  In this
+// (K+1)-dword buffer codeword i ends at bit E = 32 + (i+1)K; its LSB is bit
+// 31 - (E-1)%32 of dword (E-1)/32, and a 16-bit window spans at most two
+// dwords, so one v_alignbit_b32 extracts it (bits above 16 are left over).
+template <int K, int I>
+__device__ __forceinline__ uint32_t chunk_window(const uint32_t (&w)[K + 1]) {
+  constexpr int E = 32 + (I + 1) * K;
+  constexpr int J1 = (E - 1) >> 5;
+  constexpr int SH = 31 - ((E - 1) & 31);
+  static_assert(J1 >= 1 && J1 <= K, "window outside the chunk buffer");
+  return __builtin_amdgcn_alignbit(w[J1 - 1], w[J1], SH);
+}
+
+// Row and column-half of codeword i of a chunk (expert_exl3.zig:379-398):
+// i = 8q + j -> row {2q, 2q+1, 2q+8, 2q+9}[j%4], column a (j<4) or a+8.
+__host__ __device__ constexpr int chunk_row(int i) {
+  return ((i & 3) == 0)   ? 2 * (i >> 3)
+         : ((i & 3) == 1) ? 2 * (i >> 3) + 1
+         : ((i & 3) == 2) ? 2 * (i >> 3) + 8
+                          : 2 * (i >> 3) + 9;
+}
+__host__ __device__ constexpr int chunk_colhalf(int i) { return (i & 7) >= 4 ? 1 : 0; }
+
+// Decodes pair p (codewords 2p, 2p+1: rows r, r+1 of one column) of a chunk.
+template <int K, int CB, int P>
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1], uint32_t mask) {
+  return decode_pair<CB>(chunk_window<K, 2 * P>(w), chunk_window<K, 2 * P + 1>(w), mask);
+}
+
+// ------------------------------------------------------------ generic rate
+
+// Codeword t (0..255) of a tile of n halfwords whose n/2 dwords are in `tw`
+// (any even n in 16..128, fractional rates included): ends at bit
+// floor((t+1) n / 16), window circular over the tile's 16n bits.
+__device__ __forceinline__ uint32_t tile_window(const uint32_t *tw, uint32_t n, uint32_t t) {
+  const uint32_t nw = n >> 1;
+  const uint32_t e = ((t + 1u) * n) >> 4;  // 1 .. 16n
+  const uint32_t j1 = (e - 1u) >> 5;
+  const uint32_t j0 = j1 == 0u ? nw - 1u : j1 - 1u;
+  const uint32_t sh = 31u - ((e - 1u) & 31u);
+  return __builtin_amdgcn_alignbit(tw[j0], tw[j1], sh);
+}
+
+// ----------------------------------------------------------- Hadamard-128
+
+// Butterfly stage of the 128-point Walsh-Hadamard transform in the order of
+// the reference's prepare/finish kernels (expert_exl3_kernels.zig:902-970):
+// stages on index bits 0..6 in turn, each (lo + hi, lo - hi) with lo the
+// element whose bit is clear.  Every element sees the same f32 operations in
+// the same order, so results are bit-identical to that order.
+// In-LDS form over `rows` blocks of 128 floats, executed by `nthreads` threads.
+__device__ __forceinline__ void had128_lds(float *v, int rows, int tid, int nthreads) {
+  for (int bit = 0; bit < 7; ++bit) {
+    const int m = 1 << bit;
+    for (int p = tid; p < rows * 64; p += nthreads) {
+      const int r = p >> 6, q = p & 63;
+      const int lo = ((q >> bit) << (bit + 1)) | (q & (m - 1));
+      float *b = v + r * 128;
+      const float a = b[lo], c = b[lo + m];
+      b[lo] = a + c;
+      b[lo + m] = a - c;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace exl3

@@ -1,0 +1,756 @@
+// exl3_host.cpp -- the C ABI of include/exl3_mi355x.h: the quant plugin
+// table's entries (claims, validate, bill, open, close, load_tensor,
+// load_bank, release, matmul, moe, swiglu) over the HIP kernels.
+//
+// Reference entries (paths relative to /root/reference/plugins/):
+//   turboexl3_ds41/config.zig:43-61   claims / validate / bill
+//   turboexl3_ds41/plugin.zig:52-287  open .. swiglu
+//   turboexl3_qwen38/config.zig:86-105 turboexl3's block rules (named refusals)
+// Errors are returned as named refusals; nothing falls back to another path.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/exl3_mi355x.h"
+#include "exl3_json.h"
+#include "exl3_kernels.h"
+
+using exl3::Format;
+using exl3::Json;
+
+namespace {
+
+const char *const kName = "turboexl3_mi355x";
+
+exl3_verdict ok() { return exl3_verdict{EXL3_OK, ""}; }
+exl3_verdict refuse(int32_t code, const char *why) { return exl3_verdict{code, why}; }
+
+// --------------------------------------------------------------- blocks
+
+// A parsed EXL3 quantization block: the codebook and window the pack's
+// search used (a bank's rate comes from each tensor's packed dim).
+struct Block {
+  bool exl3 = false;
+  int codebook = 0;  // 0 mul1, 1 mcg, -1 other
+  int window = 16;   // -1: not an integer in 8..16
+  bool has_k = false;
+  double k = 0.0;
+};
+
+Block parse_block(const Json &b) {
+  Block out;
+  if (!b.is_object()) return out;
+  const Json *qm = b.get("quant_method");
+  const Json *fm = b.get("format");
+  out.exl3 = (qm && qm->is_string("exl3")) || (fm && fm->is_string("exl3"));
+  if (const Json *cb = b.get("codebook")) {
+    if (cb->is_string("mul1"))
+      out.codebook = 0;
+    else if (cb->is_string("mcg"))
+      out.codebook = 1;
+    else
+      out.codebook = -1;
+  }
+  if (const Json *w = b.get("window")) {
+    if (w->kind == Json::NUMBER && w->integral && w->num >= 8 && w->num <= 16)
+      out.window = (int)w->num;
+    else
+      out.window = -1;
+  }
+  if (const Json *k = b.get("k")) {
+    out.has_k = true;
+    out.k = k->kind == Json::NUMBER ? k->num : -1.0;
+  }
+  return out;
+}
+
+Json parse(exl3_str s) { return Json::parse(s.ptr, s.len); }
+
+// 16k halfwords per tile must be an even integer in 16..128
+// (turboexl3_qwen38/config.zig:95-103).
+bool rate_ok(double k) {
+  const double scaled = k * 16.0;
+  const double n = std::round(scaled);
+  return std::fabs(scaled - n) <= 1e-6 && n >= 16 && n <= 128 && std::fmod(n, 2.0) == 0.0;
+}
+
+bool n_ok(int64_t n) { return n >= 16 && n <= 128 && n % 2 == 0; }
+
+// ------------------------------------------------------------- weights
+
+struct WeightPriv {
+  Format f;
+  int64_t in = 0, out = 0, experts = 0;  // experts = 0: a single linear
+  int device = 0;
+  bool borrowed = false;
+};
+
+WeightPriv *priv_of(const exl3_weight *w) {
+  return w ? static_cast<WeightPriv *>(w->priv) : nullptr;
+}
+
+int64_t numel(const exl3_array &a) {
+  int64_t n = 1;
+  for (int i = 0; i < a.ndim; ++i) n *= a.shape[i];
+  return n;
+}
+
+size_t dt_size(int dt) {
+  switch (dt) {
+    case EXL3_DT_BOOL:
+    case EXL3_DT_U8:
+    case EXL3_DT_I8: return 1;
+    case EXL3_DT_U16:
+    case EXL3_DT_I16:
+    case EXL3_DT_F16:
+    case EXL3_DT_BF16: return 2;
+    case EXL3_DT_U32:
+    case EXL3_DT_I32:
+    case EXL3_DT_F32: return 4;
+    default: return 8;
+  }
+}
+
+// mlx dtype -> kernel activation type (-1: not an activation dtype)
+int act_of(int dt) {
+  if (dt == EXL3_DT_F16) return exl3::ACT_F16;
+  if (dt == EXL3_DT_BF16) return exl3::ACT_BF16;
+  if (dt == EXL3_DT_F32) return exl3::ACT_F32;
+  return -1;
+}
+
+exl3_array make_array(void *data, int dt, std::initializer_list<int64_t> shape, bool owned) {
+  exl3_array a{};
+  a.data = data;
+  a.dtype = dt;
+  a.ndim = (int32_t)shape.size();
+  int i = 0;
+  for (int64_t s : shape) a.shape[i++] = s;
+  a.owned = owned ? 1u : 0u;
+  return a;
+}
+
+// -------------------------------------------------------------- scratch
+
+// Device scratch per (device, stream): prepared rows, split-K partials and
+// tickets, MoE staging.  Grown on demand (after draining the stream); the
+// tickets are zeroed once and each use leaves them zero.
+struct StreamScratch {
+  void *xp = nullptr;
+  size_t xp_bytes = 0;
+  void *partial = nullptr;
+  size_t partial_bytes = 0;
+  void *ticket = nullptr;
+  size_t ticket_bytes = 0;
+  void *moe = nullptr;
+  size_t moe_bytes = 0;
+  void *moe_ticket = nullptr;
+  size_t moe_ticket_bytes = 0;
+};
+
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, StreamScratch> g_scratch;
+
+hipError_t grow(void **p, size_t *have, size_t need, hipStream_t s, bool zero) {
+  if (*have >= need && *p != nullptr) return hipSuccess;
+  if (*p != nullptr) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return e;
+    (void)hipFree(*p);
+    *p = nullptr;
+    *have = 0;
+  }
+  size_t bytes = std::max<size_t>(need, 256);
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return e;
+  if (zero) {
+    e = hipMemsetAsync(*p, 0, bytes, s);
+    if (e != hipSuccess) return e;
+  }
+  *have = bytes;
+  return hipSuccess;
+}
+
+StreamScratch *scratch_for(int device, hipStream_t s) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  return &g_scratch[{device, s}];
+}
+
+exl3_verdict hip_failed(hipError_t e) {
+  (void)e;
+  return refuse(EXL3_FAILED, "turboexl3_mi355x: a HIP call failed");
+}
+
+// Reads <base>.<part> from the source.
+bool source_tensor(const exl3_load_ctx *ctx, const std::string &name, exl3_host_tensor *t) {
+  if (!ctx->source || !ctx->source->tensor) return false;
+  exl3_str s{name.data(), name.size()};
+  std::memset(t, 0, sizeof(*t));
+  return ctx->source->tensor(ctx->source->self, s, t) != 0 && t->data != nullptr;
+}
+
+struct Parts {
+  exl3_host_tensor t, u, v;
+};
+
+// trellis [in/16, out/16, n] (i16 or u16), suh f16 [in], svh f16 [out]
+// (turboexl3_ds41/plugin.zig:96-103); in_dim 0 = any.
+bool shaped(const Parts &p, uint32_t in_dim) {
+  if (p.t.ndim != 3 || p.u.ndim != 1 || p.v.ndim != 1) return false;
+  if (p.t.dtype != EXL3_DT_I16 && p.t.dtype != EXL3_DT_U16) return false;
+  if (p.u.shape[0] != p.t.shape[0] * 16 || p.v.shape[0] != p.t.shape[1] * 16) return false;
+  if (in_dim != 0 && p.u.shape[0] != (int64_t)in_dim) return false;
+  return p.u.dtype == EXL3_DT_F16 && p.v.dtype == EXL3_DT_F16;
+}
+
+int parts_of(const exl3_load_ctx *ctx, const std::string &base, Parts *p) {
+  if (!source_tensor(ctx, base + ".trellis", &p->t)) return 0;
+  if (!source_tensor(ctx, base + ".suh", &p->u)) return 0;
+  if (!source_tensor(ctx, base + ".svh", &p->v)) return 0;
+  return 1;
+}
+
+const exl3_verdict kNotShaped = {
+    EXL3_UNSUPPORTED,
+    "turboexl3_mi355x: not an EXL3 linear of the expected input width (trellis [in/16, out/16, "
+    "n], suh f16 [in], svh f16 [out])"};
+const exl3_verdict kMissing = {EXL3_FAILED, "MissingWeight"};
+const exl3_verdict kRate = {EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3RateUnsupported"};
+const exl3_verdict kShape = {EXL3_UNSUPPORTED, "turboexl3_mi355x: BadExl3Shape"};
+const exl3_verdict kDtype = {EXL3_UNSUPPORTED, "turboexl3_mi355x: BadExl3Dtype"};
+
+struct OpenState {
+  int codebook = 0;
+  int window = 16;
+};
+
+}  // namespace
+
+// ================================================================ entries
+
+extern "C" {
+
+exl3_claim exl3_claims(exl3_str block_json, exl3_str config_json) {
+  (void)config_json;
+  const Json b = parse(block_json);
+  if (!b.is_object()) return EXL3_CLAIM_NO;
+  return parse_block(b).exl3 ? EXL3_CLAIM_BY_MARKER : EXL3_CLAIM_NO;
+}
+
+exl3_verdict exl3_validate(exl3_str block_json, exl3_str config_json, const exl3_pack_dir *dir) {
+  (void)dir;
+  const Json b = parse(block_json);
+  const Block blk = parse_block(b);
+  if (!blk.exl3) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: NotExl3");
+  if (blk.codebook < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookUnsupported");
+  if (blk.window < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3WindowUnsupported");
+  if (blk.has_k && !rate_ok(blk.k)) return kRate;
+  const Json c = parse(config_json);
+  if (c.is_object()) {
+    const Json *text = c.get("text_config");
+    const Json *root = (text && text->is_object()) ? text : &c;
+    const Json *k = root->get("num_experts_per_tok");
+    if (k && k->kind == Json::NUMBER && k->integral && k->num > 32)
+      return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3TopKExceedsReduceBank");
+  }
+  return ok();
+}
+
+uint64_t exl3_bill(exl3_str block_json, exl3_str model_dir, uint64_t stored) {
+  (void)block_json;
+  (void)model_dir;
+  return stored;
+}
+
+exl3_verdict exl3_open(exl3_load_ctx *ctx) {
+  if (!ctx) return refuse(EXL3_FAILED, "turboexl3_mi355x: no load context");
+  const Block blk = parse_block(parse(ctx->block_json));
+  if (!blk.exl3 || blk.codebook < 0 || blk.window < 0)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: not an exllamav3 mul1 or mcg block");
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: no HIP device");
+  if (ctx->device < 0 || ctx->device >= count)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: no such device");
+  if (hipSetDevice(ctx->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  OpenState *st = new OpenState{blk.codebook, blk.window};
+  ctx->state = st;
+  return ok();
+}
+
+void exl3_close(exl3_load_ctx *ctx) {
+  if (ctx && ctx->state) {
+    delete static_cast<OpenState *>(ctx->state);
+    ctx->state = nullptr;
+  }
+}
+
+static exl3_verdict upload(const exl3_load_ctx *ctx, const std::vector<const exl3_host_tensor *> &parts,
+                           size_t each_bytes, void **dst) {
+  hipStream_t s = (hipStream_t)ctx->stream;
+  hipError_t e = hipMalloc(dst, std::max<size_t>(each_bytes * parts.size(), 256));
+  if (e != hipSuccess) return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
+  for (size_t i = 0; i < parts.size(); ++i) {
+    e = hipMemcpyAsync((char *)*dst + i * each_bytes, parts[i]->data, each_bytes,
+                       hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_failed(e);
+  }
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_failed(e);
+  return ok();
+}
+
+static void free_weight_arrays(exl3_weight *w) {
+  for (exl3_array *a : {&w->w, &w->scales, &w->biases, &w->side})
+    if (a->owned && a->data) {
+      (void)hipFree(a->data);
+      a->data = nullptr;
+    }
+}
+
+// Builds a weight from a stack of E linears (E = 0: one linear, rank 3).
+static exl3_verdict load_parts(const exl3_load_ctx *ctx, const std::vector<Parts> &ps, bool bank,
+                               exl3_weight *out) {
+  const OpenState *st = static_cast<const OpenState *>(ctx->state);
+  if (!st) return refuse(EXL3_FAILED, "turboexl3_mi355x: load before open");
+  const Parts &p0 = ps[0];
+  const int64_t it = p0.t.shape[0], ot = p0.t.shape[1], n = p0.t.shape[2];
+  if (!n_ok(n)) return kRate;
+  const int64_t in = it * 16, outf = ot * 16;
+  if (in % 128 != 0 || outf % 128 != 0) return kNotShaped;
+  for (const Parts &p : ps)
+    if (p.t.shape[0] != it || p.t.shape[1] != ot || p.t.shape[2] != n) return kNotShaped;
+  if (hipSetDevice(ctx->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  std::vector<const exl3_host_tensor *> tv, uv, vv;
+  for (const Parts &p : ps) {
+    tv.push_back(&p.t);
+    uv.push_back(&p.u);
+    vv.push_back(&p.v);
+  }
+  exl3_weight w{};
+  void *dt = nullptr, *du = nullptr, *dv = nullptr;
+  exl3_verdict v = upload(ctx, tv, (size_t)(it * ot * n) * 2, &dt);
+  if (v.code == EXL3_OK) v = upload(ctx, uv, (size_t)in * 2, &du);
+  if (v.code == EXL3_OK) v = upload(ctx, vv, (size_t)outf * 2, &dv);
+  if (v.code != EXL3_OK) {
+    for (void *d : {dt, du, dv})
+      if (d) (void)hipFree(d);
+    return v;
+  }
+  const int64_t E = (int64_t)ps.size();
+  if (bank) {
+    w.w = make_array(dt, EXL3_DT_U16, {E, it, ot, n}, true);
+    w.scales = make_array(du, EXL3_DT_F16, {E, in}, true);
+    w.biases = make_array(dv, EXL3_DT_F16, {E, outf}, true);
+  } else {
+    w.w = make_array(dt, EXL3_DT_U16, {it, ot, n}, true);
+    w.scales = make_array(du, EXL3_DT_F16, {in}, true);
+    w.biases = make_array(dv, EXL3_DT_F16, {outf}, true);
+  }
+  WeightPriv *pv = new WeightPriv;
+  pv->f.n = (int)n;
+  pv->f.codebook = st->codebook;
+  pv->f.window = st->window;
+  pv->in = in;
+  pv->out = outf;
+  pv->experts = bank ? E : 0;
+  pv->device = ctx->device;
+  w.priv = pv;
+  *out = w;
+  return ok();
+}
+
+exl3_verdict exl3_load_tensor(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                              exl3_weight *out) {
+  if (!ctx || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  const std::string base(name.ptr ? name.ptr : "", name.len);
+  std::vector<Parts> ps(1);
+  if (!parts_of(ctx, base, &ps[0])) {
+    Parts g;
+    if (parts_of(ctx, base + ".slice.0", &g))
+      return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: grouped linears are not served");
+    return kMissing;
+  }
+  if (!shaped(ps[0], in_dim)) return kNotShaped;
+  return load_parts(ctx, ps, false, out);
+}
+
+exl3_verdict exl3_load_bank(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
+                            exl3_weight *out) {
+  if (!ctx || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  const std::string full(name.ptr ? name.ptr : "", name.len);
+  const size_t dot = full.rfind('.');
+  if (dot == std::string::npos) return kMissing;
+  const std::string prefix = full.substr(0, dot), suffix = full.substr(dot);
+  std::vector<Parts> ps;
+  for (int e = 0;; ++e) {
+    Parts p;
+    if (!parts_of(ctx, prefix + "." + std::to_string(e) + suffix, &p)) break;
+    if (!shaped(p, in_dim)) return kNotShaped;
+    ps.push_back(p);
+  }
+  if (ps.empty()) return kMissing;
+  // Every expert the layer's router scores (<layer>.gate.weight [experts,
+  // hidden]) must be in the bank (turboexl3_ds41/plugin.zig:132-151).
+  const std::string tail = ".experts";
+  if (prefix.size() > tail.size() && prefix.compare(prefix.size() - tail.size(), tail.size(), tail) == 0) {
+    exl3_host_tensor g;
+    const std::string router = prefix.substr(0, prefix.size() - tail.size()) + ".gate.weight";
+    if (!source_tensor(ctx, router, &g) || g.ndim != 2 || g.shape[0] != (int64_t)ps.size())
+      return refuse(EXL3_UNSUPPORTED,
+                    "turboexl3_mi355x: the bank holds another count of experts than its router scores");
+  }
+  return load_parts(ctx, ps, true, out);
+}
+
+void exl3_release(exl3_weight *w) {
+  if (!w) return;
+  WeightPriv *pv = priv_of(w);
+  if (pv && !pv->borrowed) free_weight_arrays(w);
+  delete pv;
+  std::memset(w, 0, sizeof(*w));
+}
+
+void exl3_array_free(exl3_array *a) {
+  if (a && a->owned && a->data) {
+    (void)hipFree(a->data);
+    a->data = nullptr;
+    a->owned = 0;
+  }
+}
+
+exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh,
+                              exl3_str block_json, int32_t device, exl3_weight *out) {
+  if (!out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  Block blk;
+  if (block_json.ptr && block_json.len) {
+    blk = parse_block(parse(block_json));
+    if (blk.codebook < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookUnsupported");
+    if (blk.window < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3WindowUnsupported");
+  }
+  const bool bank = trellis.ndim == 4;
+  if (!(trellis.ndim == 3 || bank) || !trellis.data || !suh.data || !svh.data) return kShape;
+  if (trellis.dtype != EXL3_DT_U16 && trellis.dtype != EXL3_DT_I16) return kDtype;
+  if (suh.dtype != EXL3_DT_F16 || svh.dtype != EXL3_DT_F16) return kDtype;
+  const int o = bank ? 1 : 0;
+  const int64_t it = trellis.shape[o], ot = trellis.shape[o + 1], n = trellis.shape[o + 2];
+  if (!n_ok(n)) return kRate;
+  const int64_t E = bank ? trellis.shape[0] : 0;
+  if (bank) {
+    if (suh.ndim != 2 || svh.ndim != 2 || suh.shape[0] != E || svh.shape[0] != E) return kShape;
+    if (suh.shape[1] != it * 16 || svh.shape[1] != ot * 16) return kShape;
+  } else {
+    if (suh.ndim != 1 || svh.ndim != 1 || suh.shape[0] != it * 16 || svh.shape[0] != ot * 16)
+      return kShape;
+  }
+  if ((it * 16) % 128 != 0 || (ot * 16) % 128 != 0) return kShape;
+  exl3_weight w{};
+  w.w = trellis;
+  w.w.owned = 0;
+  w.scales = suh;
+  w.scales.owned = 0;
+  w.biases = svh;
+  w.biases.owned = 0;
+  WeightPriv *pv = new WeightPriv;
+  pv->f.n = (int)n;
+  pv->f.codebook = blk.codebook;
+  pv->f.window = blk.window;
+  pv->in = it * 16;
+  pv->out = ot * 16;
+  pv->experts = E;
+  pv->device = device;
+  pv->borrowed = true;
+  w.priv = pv;
+  *out = w;
+  return ok();
+}
+
+// Allocates the output array when the caller passed none; checks it otherwise.
+static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t last,
+                               int64_t rows) {
+  if (out->data == nullptr) {
+    void *p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>((size_t)(rows * last) * dt_size(x.dtype), 256)) != hipSuccess)
+      return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
+    exl3_array a = x;
+    a.data = p;
+    a.shape[a.ndim - 1] = last;
+    a.owned = 1;
+    *out = a;
+    return ok();
+  }
+  if (out->dtype != x.dtype || out->ndim < 1 || out->shape[out->ndim - 1] != last ||
+      numel(*out) != rows * last)
+    return kShape;
+  return ok();
+}
+
+// The inner product z (f16) or the finished y of rows prepared activations:
+// the GEMV for up to 8 rows, the GEMM above (rate with integer K; other rates
+// take the GEMV 8 rows at a time).
+static hipError_t inner_rows(const WeightPriv *pv, const uint16_t *trellis, const uint16_t *xp,
+                             const uint16_t *svh, void *y, int ydt, uint16_t *zout, int64_t rows,
+                             StreamScratch *ss, hipStream_t s) {
+  const int in = (int)pv->in, outf = (int)pv->out;
+  if (rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate())
+    return exl3::launch_gemm(trellis, pv->f, xp, svh, y, ydt, zout, (int)rows, in, outf, s);
+  const size_t ysz = ydt == exl3::ACT_F32 ? 4 : 2;
+  for (int64_t r0 = 0; r0 < rows; r0 += exl3::GEMV_ROWS_MAX) {
+    const int r = (int)std::min<int64_t>(exl3::GEMV_ROWS_MAX, rows - r0);
+    size_t pf = 0, tk = 0;
+    exl3::gemv_scratch_need(r, in, outf, &pf, &tk);
+    hipError_t e = grow(&ss->partial, &ss->partial_bytes, pf * sizeof(float), s, false);
+    if (e != hipSuccess) return e;
+    e = grow(&ss->ticket, &ss->ticket_bytes, tk * sizeof(uint32_t), s, true);
+    if (e != hipSuccess) return e;
+    exl3::Scratch sc;
+    sc.partial = (float *)ss->partial;
+    sc.partial_floats = ss->partial_bytes / sizeof(float);
+    sc.ticket = (uint32_t *)ss->ticket;
+    sc.tickets = ss->ticket_bytes / sizeof(uint32_t);
+    e = exl3::launch_gemv(trellis, pv->f, xp + (size_t)r0 * in, svh,
+                          y ? (char *)y + (size_t)r0 * outf * ysz : nullptr, ydt,
+                          zout ? zout + (size_t)r0 * outf : nullptr, r, in, outf, sc, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
+                         exl3_array *out) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  if (x.ndim < 1 || x.ndim > EXL3_MAX_DIMS || !x.data || x.shape[x.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(x) / pv->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = output_for(out, x, pv->out, rows);
+  if (v.code != EXL3_OK) return v;
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * pv->in * 2, s, false);
+  if (e != hipSuccess) return hip_failed(e);
+  uint16_t *xp = (uint16_t *)ss->xp;
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+    const int r = (int)std::min<int64_t>(65535, rows - r0);
+    e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * pv->in * dt_size(x.dtype), xdt,
+                             (const uint16_t *)w->scales.data, xp + (size_t)r0 * pv->in, r,
+                             (int)pv->in, s);
+  }
+  if (e == hipSuccess)
+    e = inner_rows(pv, (const uint16_t *)w->w.data, xp, (const uint16_t *)w->biases.data, out->data,
+                   xdt, nullptr, rows, ss, s);
+  if (e != hipSuccess) return hip_failed(e);
+  return ok();
+}
+
+exl3_verdict exl3_moe(const exl3_weight *bank, exl3_array x, exl3_array lhs, exl3_array rhs,
+                      bool sorted, exl3_stream s, exl3_array *out) {
+  (void)bank;
+  (void)x;
+  (void)lhs;
+  (void)rhs;
+  (void)sorted;
+  (void)s;
+  (void)out;
+  return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: routed experts run through swiglu");
+}
+
+exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const exl3_weight *down,
+                         exl3_array x, exl3_array inds, exl3_array scores,
+                         const exl3_swiglu_opts *opts, exl3_stream stream, exl3_array *out) {
+  const WeightPriv *pg = priv_of(gate), *pu = priv_of(up), *pd = priv_of(down);
+  if (!pg || !pu || !pd || !out || !opts) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  if (x.ndim < 1 || !x.data) return kShape;
+  const int64_t hidden = x.shape[x.ndim - 1];
+  const int64_t rows = numel(x) / std::max<int64_t>(hidden, 1);
+  if (opts->limit < 0 || opts->limit > 128)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: InvalidExl3Clamp");
+  if (pg->in != hidden || pu->in != hidden || pd->out != hidden || pg->out != pu->out ||
+      pd->in != pg->out)
+    return kShape;
+  if (pg->experts != pu->experts || pg->experts != pd->experts) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pg->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3::MoeArgs a{};
+  a.x = x.data;
+  a.xdt = xdt;
+  a.rows = (int)rows;
+  a.hidden = (int)hidden;
+  a.inter = (int)pg->out;
+  a.limit = (float)opts->limit;
+  a.experts = (int)std::max<int64_t>(pg->experts, 1);
+  if (inds.data == nullptr) {
+    // No routes: the dense SwiGLU MLP of single-linear weights
+    // (turboexl3_ds41/plugin.zig:270-276): one expert, score 1.
+    if (pg->experts != 0) return kShape;
+    a.inds = nullptr;
+    a.scores = nullptr;
+    a.topk = 1;
+  } else {
+    if (pg->experts == 0) return kShape;
+    if (inds.dtype != EXL3_DT_I32 && inds.dtype != EXL3_DT_U32) return kDtype;
+    const int sdt = act_of(scores.dtype);
+    if (sdt < 0 || !scores.data) return kDtype;
+    if (inds.ndim < 1 || scores.ndim != inds.ndim) return kShape;
+    for (int i = 0; i < inds.ndim; ++i)
+      if (inds.shape[i] != scores.shape[i]) return kShape;
+    const int64_t topk = inds.shape[inds.ndim - 1];
+    if (topk <= 0 || topk > 32 || numel(inds) != rows * topk) return kShape;
+    a.inds = (const uint32_t *)inds.data;
+    a.scores = scores.data;
+    a.sdt = sdt;
+    a.topk = (int)topk;
+  }
+  if (pg->f.n != pu->f.n) return kRate;
+  exl3_verdict v = output_for(out, x, hidden, rows);
+  if (v.code != EXL3_OK) return v;
+  a.y = out->data;
+  a.ydt = xdt;
+  exl3::MoeBank bg{(const uint16_t *)gate->w.data, (const uint16_t *)gate->scales.data,
+                   (const uint16_t *)gate->biases.data, pg->f, (int)pg->in, (int)pg->out};
+  exl3::MoeBank bu{(const uint16_t *)up->w.data, (const uint16_t *)up->scales.data,
+                   (const uint16_t *)up->biases.data, pu->f, (int)pu->in, (int)pu->out};
+  exl3::MoeBank bd{(const uint16_t *)down->w.data, (const uint16_t *)down->scales.data,
+                   (const uint16_t *)down->biases.data, pd->f, (int)pd->in, (int)pd->out};
+  StreamScratch *ss = scratch_for(pg->device, s);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  size_t ntick = 0;
+  const size_t need = exl3::moe_scratch_bytes(a, &ntick);
+  hipError_t e = grow(&ss->moe, &ss->moe_bytes, need, s, false);
+  if (e != hipSuccess) return hip_failed(e);
+  e = grow(&ss->moe_ticket, &ss->moe_ticket_bytes, ntick * 4, s, true);
+  if (e != hipSuccess) return hip_failed(e);
+  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, (uint32_t *)ss->moe_ticket,
+                       ss->moe_ticket_bytes / 4, s);
+  if (e != hipSuccess) {
+    if (e == hipErrorInvalidValue) return kShape;
+    return hip_failed(e);
+  }
+  return ok();
+}
+
+exl3_verdict exl3_decode_matrix(const exl3_weight *w, int32_t expert, exl3_array out,
+                                exl3_stream stream) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (out.dtype != EXL3_DT_F16 || !out.data || numel(out) != pv->in * pv->out) return kShape;
+  const int64_t E = std::max<int64_t>(pv->experts, 1);
+  if (expert < 0 || expert >= E) return kShape;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  const size_t per = (size_t)(pv->in / 16) * (pv->out / 16) * pv->f.n;
+  hipError_t e = exl3::launch_decode_matrix((const uint16_t *)w->w.data + per * expert, pv->f,
+                                            (int)pv->in, (int)pv->out, (uint16_t *)out.data,
+                                            (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
+exl3_verdict exl3_prepare(const exl3_weight *w, exl3_array x, exl3_array xp, exl3_stream stream) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->experts != 0) return kShape;
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0 || xp.dtype != EXL3_DT_F16) return kDtype;
+  if (!x.data || !xp.data || x.ndim < 1 || x.shape[x.ndim - 1] != pv->in || numel(xp) != numel(x))
+    return kShape;
+  const int64_t rows = numel(x) / pv->in;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  hipError_t e = hipSuccess;
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+    const int r = (int)std::min<int64_t>(65535, rows - r0);
+    e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * pv->in * dt_size(x.dtype), xdt,
+                             (const uint16_t *)w->scales.data,
+                             (uint16_t *)xp.data + (size_t)r0 * pv->in, r, (int)pv->in,
+                             (hipStream_t)stream);
+  }
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
+exl3_verdict exl3_finish(const exl3_weight *w, exl3_array z, exl3_array y, exl3_stream stream) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->experts != 0) return kShape;
+  const int ydt = act_of(y.dtype);
+  if (ydt < 0 || z.dtype != EXL3_DT_F16) return kDtype;
+  if (!z.data || !y.data || z.ndim < 1 || z.shape[z.ndim - 1] != pv->out || numel(y) != numel(z))
+    return kShape;
+  const int64_t rows = numel(z) / pv->out;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  const size_t ysz = dt_size(y.dtype);
+  hipError_t e = hipSuccess;
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+    const int r = (int)std::min<int64_t>(65535, rows - r0);
+    e = exl3::launch_finish((const uint16_t *)z.data + (size_t)r0 * pv->out,
+                            (const uint16_t *)w->biases.data,
+                            (char *)y.data + (size_t)r0 * pv->out * ysz, ydt, r, (int)pv->out,
+                            (hipStream_t)stream);
+  }
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
+exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_stream stream) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->experts != 0) return kShape;
+  if (xp.dtype != EXL3_DT_F16 || z.dtype != EXL3_DT_F16) return kDtype;
+  if (!xp.data || !z.data || xp.ndim < 1 || xp.shape[xp.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(xp) / pv->in;
+  if (numel(z) != rows * pv->out) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  hipError_t e = inner_rows(pv, (const uint16_t *)w->w.data, (const uint16_t *)xp.data, nullptr,
+                            nullptr, 0, (uint16_t *)z.data, rows, ss, s);
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
+const char *exl3_version(void) { return "exl3_mi355x 0.1.0 (gfx950)"; }
+
+const char *exl3_matmul_path(const exl3_weight *w, int64_t rows) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return "none";
+  if (rows <= exl3::GEMV_ROWS_MAX) return "gemv";
+  return pv->f.integer_rate() ? "gemm" : "gemv";
+}
+
+static exl3_verdict register_kernels(const void *host) {
+  (void)host;
+  return ok();
+}
+
+static const exl3_quant_table kTable = {
+    (uint32_t)sizeof(exl3_quant_table),
+    EXL3_ABI_VERSION,
+    {kName, 16},
+    &exl3_claims,
+    &exl3_validate,
+    &exl3_bill,
+    &exl3_open,
+    &exl3_close,
+    &exl3_load_tensor,
+    &exl3_load_bank,
+    &exl3_release,
+    &exl3_matmul,
+    &exl3_moe,
+    &register_kernels,
+    &exl3_swiglu,
+};
+
+const exl3_quant_table *exl3_quant_table_get(void) { return &kTable; }
+
+}  // extern "C"

@@ -1,0 +1,99 @@
+// exl3_kernels.h -- host-callable launchers of the EXL3 HIP kernels (internal
+// to libexl3_mi355x.so; the public boundary is include/exl3_mi355x.h).
+//
+// Every launcher checks on the host the shape facts its kernel's indexing and
+// grid assume and returns a nonzero hipError_t-style code (or -1 for a shape
+// refusal) instead of launching when they do not hold.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+// Decode parameters of one EXL3 weight: n halfwords per 16x16 tile (even,
+// 16..128), codebook (0 mul1, 1 mcg) and window bits (8..16).
+struct Format {
+  int n = 0;
+  int codebook = 0;
+  int window = 16;
+  uint32_t mask() const { return (window >= 16) ? 0xFFFFu : ((1u << window) - 1u); }
+  bool integer_rate() const { return n % 16 == 0 && n >= 16 && n <= 128; }
+};
+
+// Device scratch a matmul uses: split-K partial sums and per-column-group
+// tickets (zero between calls: the last workgroup of a group resets its own).
+struct Scratch {
+  float *partial = nullptr;
+  size_t partial_floats = 0;
+  uint32_t *ticket = nullptr;
+  size_t tickets = 0;
+  void *bytes = nullptr;  // generic staging (MoE routing, prepared rows)
+  size_t nbytes = 0;
+};
+
+// Output / activation element types understood by the kernels.
+enum ActType { ACT_F16 = 0, ACT_BF16 = 1, ACT_F32 = 2 };
+
+// prepare: x [rows, in] (ACT_*) -> xp f16 [rows, in]; suh f16 [in].
+hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t *xp, int rows,
+                          int in, hipStream_t s);
+// finish: z f16 [rows, out] -> y [rows, out] (ACT_*); svh f16 [out].
+hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int ydt, int rows,
+                         int out, hipStream_t s);
+// decode: trellis [in/16][out/16][n] -> W_inner f16 [in, out].
+hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in, int out,
+                                uint16_t *w, hipStream_t s);
+
+// The GEMV split: how many k-splits a (rows, in, out) GEMV takes.
+int gemv_ksplit(int in, int out, int groups);
+// Largest row count the GEMV path serves; wider calls take the GEMM.
+constexpr int GEMV_ROWS_MAX = 8;
+
+// GEMV (rows <= GEMV_ROWS_MAX): y = finish(xp @ W) with z rounded to f16 after
+// the split-K sum; or, with y == nullptr, z f16 [rows, out] written to zout.
+hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
+                       int out, Scratch &sc, hipStream_t s);
+// GEMM (any rows): the same contract through LDS-staged decode and MFMA.
+hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
+                       int out, hipStream_t s);
+// Scratch the GEMV needs for (rows, in, out): partial floats and tickets.
+void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t *tickets);
+
+// ------------------------------------------------------------------- MoE
+
+struct MoeBank {
+  const uint16_t *trellis;  // [E][in/16][out/16][n]
+  const uint16_t *suh;      // [E][in]
+  const uint16_t *svh;      // [E][out]
+  Format f;
+  int in, out;
+};
+
+// Routed SwiGLU over `rows` rows of x [rows, hidden] (ACT_*), experts
+// inds [rows, topk] (i32 or u32: both read as u32, out-of-range slots
+// contribute nothing), scores [rows, topk] (ACT_*); inds == nullptr: the
+// dense SwiGLU of expert 0 (topk 1, score 1).  limit > 0 clamps gate and up.
+// y [rows, hidden] in ydt.
+struct MoeArgs {
+  const void *x;
+  int xdt;
+  const uint32_t *inds;
+  const void *scores;
+  int sdt;
+  int rows, topk, experts, hidden, inter;
+  float limit;
+  void *y;
+  int ydt;
+};
+// Scratch bytes for a call, and (in *tickets) the count of u32 tickets it
+// needs in a separate buffer that starts zeroed and is left zeroed.
+size_t moe_scratch_bytes(const MoeArgs &a, size_t *tickets);
+hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
+                      const MoeBank &down, void *scratch, size_t scratch_bytes, uint32_t *tickets,
+                      size_t ntickets, hipStream_t s);
+
+}  // namespace exl3

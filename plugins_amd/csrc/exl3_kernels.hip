@@ -1,0 +1,1105 @@
+// exl3_kernels.hip -- HIP kernels for the EXL3 trellis-quantized linear on
+// MI355X (gfx950, wave64) and their host launchers.
+//
+// Kernels (reference roles, paths relative to /root/reference/plugins/):
+//  * prepare / finish: the Hadamard-128 rotations around the inner product
+//    (sushi_ds41/src/sushi/exl3/expert_exl3_kernels.zig:902-970; contract
+//    turboexl3_qwen38/overlay/mlx_serve/abi/quant.zig:52-55);
+//  * decode_matrix: whole-matrix decode to f16 (the `q3_exl3_dig_decmat_*`
+//    role, turboexl3_ds41/src/exl3/kernels/exl3/q3_exl3_dig_decmat_5120x2304_mul1hk3.metal);
+//  * gemv: rows <= 8, weights decoded in registers, split-K over workgroups
+//    with the finish fused into the last workgroup of each 128-column group
+//    (the decode GEMV role: expert_exl3_kernels.zig:1653-1849,
+//    turboexl3_ds41/src/exl3/kernels/exl3/dsv41_exl3_mul1h_k3_2304.metal);
+//  * gemm: any rows, weight tiles decoded into LDS as f16 in MFMA operand
+//    layout, v_mfma_f32_32x32x16_f16 with f32 accumulation, finish fused
+//    (the prefill GEMM role: expert_exl3_kernels.zig:676-750,
+//    dsv41_prefill_dig_gemm_5120x2304_gu_xmul1hk3_m128.metal).
+//
+// Compiled with -ffp-contract=off: every f32 multiply and add rounds on its
+// own where the reference's order of operations is reproduced; fused
+// multiply-adds are written out where they are meant.
+#include <algorithm>
+#include <utility>
+
+#include "exl3_device.h"
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+template <int... Is, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F &&f) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+// Agent-scope (all XCDs) loads and stores for the split-K hand-off.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// =================================================================== prepare
+
+// One wave per 128-block of one row: element i of the block lives in lane
+// i%64, register i/64.  Stages on index bits 0..5 exchange across lanes,
+// bit 6 is in-register; each stage is (lo + hi, lo - hi).
+__global__ __launch_bounds__(64) void prepare_kernel(const void *__restrict__ x, int xdt,
+                                                     const uint16_t *__restrict__ suh,
+                                                     uint16_t *__restrict__ xp, int in) {
+  const int lane = threadIdx.x;
+  const size_t row = blockIdx.y;
+  const int i0 = blockIdx.x * 128 + lane;
+  const size_t base = row * (size_t)in;
+  // f16(x) * suh in f32 (expert_exl3.zig:490-493; the kernel's
+  // float(x) * float(suh), expert_exl3_kernels.zig:908-912).
+  float v0 = h2f(f2h(load_act(x, base + i0, xdt))) * h2f(suh[i0]);
+  float v1 = h2f(f2h(load_act(x, base + i0 + 64, xdt))) * h2f(suh[i0 + 64]);
+#pragma unroll
+  for (int bit = 1; bit <= 32; bit <<= 1) {
+    const float p0 = __shfl_xor(v0, bit, 64);
+    const float p1 = __shfl_xor(v1, bit, 64);
+    const bool lower = (lane & bit) == 0;
+    v0 = lower ? v0 + p0 : p0 - v0;
+    v1 = lower ? v1 + p1 : p1 - v1;
+  }
+  const float a = v0 + v1, b = v0 - v1;
+  xp[base + i0] = f2h(a * HAD_SCALE);
+  xp[base + i0 + 64] = f2h(b * HAD_SCALE);
+}
+
+// The same rotation on an f16 [rows, 128-block] of inner products, then
+// * svh, rounded to f16, stored in the output dtype
+// (expert_exl3_kernels.zig:938-970; expert_exl3.zig:534-544).
+__device__ __forceinline__ void finish_row_wave(const uint16_t *z, const uint16_t *svh, void *y,
+                                                int ydt, size_t yoff, int lane) {
+  float v0 = h2f(z[lane]);
+  float v1 = h2f(z[lane + 64]);
+#pragma unroll
+  for (int bit = 1; bit <= 32; bit <<= 1) {
+    const float p0 = __shfl_xor(v0, bit, 64);
+    const float p1 = __shfl_xor(v1, bit, 64);
+    const bool lower = (lane & bit) == 0;
+    v0 = lower ? v0 + p0 : p0 - v0;
+    v1 = lower ? v1 + p1 : p1 - v1;
+  }
+  const float a = v0 + v1, b = v0 - v1;
+  const float s0 = a * HAD_SCALE, s1 = b * HAD_SCALE;
+  store_out(y, yoff + lane, f2h(s0 * h2f(svh[lane])), ydt);
+  store_out(y, yoff + lane + 64, f2h(s1 * h2f(svh[lane + 64])), ydt);
+}
+
+__global__ __launch_bounds__(64) void finish_kernel(const uint16_t *__restrict__ z,
+                                                    const uint16_t *__restrict__ svh,
+                                                    void *__restrict__ y, int ydt, int out) {
+  const size_t off = (size_t)blockIdx.y * out + blockIdx.x * 128;
+  finish_row_wave(z + off, svh + blockIdx.x * 128, y, ydt, off, threadIdx.x);
+}
+
+hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t *xp, int rows,
+                          int in, hipStream_t s) {
+  if (rows <= 0 || in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
+  if (rows > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(prepare_kernel, dim3(in / 128, rows), dim3(64), 0, s, x, xdt, suh, xp, in);
+  return hipGetLastError();
+}
+
+hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int ydt, int rows,
+                         int out, hipStream_t s) {
+  if (rows <= 0 || out <= 0 || out % 128 != 0 || rows > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(finish_kernel, dim3(out / 128, rows), dim3(64), 0, s, z, svh, y, ydt, out);
+  return hipGetLastError();
+}
+
+// ============================================================ decode matrix
+
+// One wave per (k-tile row tk, 8 consecutive output tiles): lane = 8*tile +
+// chunk.  Decoded values are staged in LDS as the 16 x 128 row block and
+// written out as contiguous rows of W_inner [in, out].
+template <int K, int CB>
+__global__ __launch_bounds__(64) void decode_matrix_kernel(const uint32_t *__restrict__ tw,
+                                                           uint16_t *__restrict__ w, int out_tiles,
+                                                           uint32_t mask) {
+  __shared__ uint32_t blk[16 * 64];  // 16 rows x 128 f16, as dwords
+  const int lane = threadIdx.x;
+  const int tk = blockIdx.y, cg = blockIdx.x;
+  const int tl = lane >> 3, c = lane & 7;
+  const size_t tile = (size_t)tk * out_tiles + cg * 8 + tl;
+  const uint32_t *tp = tw + tile * (8 * K);
+  uint32_t wd[K + 1];
+#pragma unroll
+  for (int i = 0; i < K; ++i) wd[i + 1] = tp[c * K + i];
+  wd[0] = tp[((c + 7) & 7) * K + (K - 1)];
+  uint16_t *row16 = reinterpret_cast<uint16_t *>(blk);
+  static_for<16>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    const uint32_t v = chunk_pair<K, CB, p>(wd, mask);
+    constexpr int r = chunk_row(2 * p);
+    const int col = tl * 16 + c + 8 * chunk_colhalf(2 * p);
+    row16[r * 128 + col] = (uint16_t)(v & 0xFFFFu);
+    row16[(r + 1) * 128 + col] = (uint16_t)(v >> 16);
+  });
+  __syncthreads();
+  const size_t out = (size_t)out_tiles * 16;
+  // 16 rows x 64 dwords: lane writes dword `lane` of every row.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(w + ((size_t)tk * 16 + r) * out + cg * 128);
+    dst[lane] = blk[r * 64 + lane];
+  }
+}
+
+// Any even n: the 8 tiles' dwords are staged in LDS and each lane extracts its
+// 32 codewords with run-time windows.
+template <int CB>
+__global__ __launch_bounds__(64) void decode_matrix_generic_kernel(const uint32_t *__restrict__ tw,
+                                                                   uint16_t *__restrict__ w,
+                                                                   int out_tiles, int n,
+                                                                   uint32_t mask) {
+  __shared__ uint32_t words[8 * 64];
+  __shared__ uint32_t blk[16 * 64];
+  const int lane = threadIdx.x;
+  const int tk = blockIdx.y, cg = blockIdx.x;
+  const int nw = n >> 1;
+  const uint32_t *src = tw + ((size_t)tk * out_tiles + cg * 8) * nw;
+  for (int i = lane; i < 8 * nw; i += 64) words[i] = src[i];
+  __syncthreads();
+  const int tl = lane >> 3, c = lane & 7;
+  const uint32_t *mine = words + tl * nw;
+  uint16_t *row16 = reinterpret_cast<uint16_t *>(blk);
+  for (int p = 0; p < 16; ++p) {
+    const uint32_t t = 32u * c + 2u * p;
+    const uint32_t v = decode_pair<CB>(tile_window(mine, n, t), tile_window(mine, n, t + 1u), mask);
+    const int r = chunk_row(2 * p);
+    const int col = tl * 16 + c + 8 * chunk_colhalf(2 * p);
+    row16[r * 128 + col] = (uint16_t)(v & 0xFFFFu);
+    row16[(r + 1) * 128 + col] = (uint16_t)(v >> 16);
+  }
+  __syncthreads();
+  const size_t out = (size_t)out_tiles * 16;
+  for (int r = 0; r < 16; ++r) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(w + ((size_t)tk * 16 + r) * out + cg * 128);
+    dst[lane] = blk[r * 64 + lane];
+  }
+}
+
+template <int CB>
+static hipError_t decode_matrix_cb(const uint32_t *tw, const Format &f, int in, int out,
+                                   uint16_t *w, hipStream_t s) {
+  const dim3 grid(out / 128, in / 16);
+  const int ot = out / 16;
+  const uint32_t m = f.mask();
+  switch (f.integer_rate() ? f.n / 16 : 0) {
+#define EXL3_DM(KK)                                                                             \
+  case KK:                                                                                      \
+    hipLaunchKernelGGL((decode_matrix_kernel<KK, CB>), grid, dim3(64), 0, s, tw, w, ot, m); \
+    break;
+    EXL3_DM(1) EXL3_DM(2) EXL3_DM(3) EXL3_DM(4) EXL3_DM(5) EXL3_DM(6) EXL3_DM(7) EXL3_DM(8)
+#undef EXL3_DM
+    default:
+      hipLaunchKernelGGL((decode_matrix_generic_kernel<CB>), grid, dim3(64), 0, s, tw, w, ot, f.n,
+                         m);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in, int out,
+                                uint16_t *w, hipStream_t s) {
+  if (in <= 0 || out <= 0 || in % 16 != 0 || out % 128 != 0) return hipErrorInvalidValue;
+  if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
+  if (in / 16 > 65535) return hipErrorInvalidValue;
+  const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
+  return f.codebook == CB_MCG ? decode_matrix_cb<CB_MCG>(tw, f, in, out, w, s)
+                              : decode_matrix_cb<CB_MUL1>(tw, f, in, out, w, s);
+}
+
+// ===================================================================== GEMV
+//
+// Workgroup = 4 waves on one 128-column group (8 output tiles) and one k-split
+// [ks*tps, (ks+1)*tps) of the k-tile rows; wave w takes rows ks*tps + w, +4,
+// ...  Lane = 8*tile + chunk: it loads its chunk's K dwords (one 16-byte load
+// at K=4; a wave's 64 loads are one contiguous 16K*64-bit span), receives the
+// history dword from the previous chunk's lane (ds_bpermute), decodes 32
+// weights in registers and accumulates columns a and a+8 of its tile with
+// v_dot2_f32_f16 against the rows' prepared activations.  Per-row f32
+// partial sums go to scratch; the last workgroup of a column group (a ticket
+// counter) sums the k-splits in order, rounds z to f16, and runs the finish
+// for its 128 columns, which are exactly one Hadamard block.
+
+constexpr int GEMV_THREADS = 256;
+
+template <int K, int B, int CB>
+__device__ __forceinline__ void gemv_accum(const uint32_t *__restrict__ wchunk, size_t row_words,
+                                           const uint32_t *__restrict__ xp, const int (&xoff)[B],
+                                           int tk, int tk_end, uint32_t mask, int src_lane,
+                                           float (&acc)[B][2]) {
+  uint32_t nxt[K];
+  if (tk < tk_end) {
+    const uint32_t *p = wchunk + (size_t)tk * row_words;
+#pragma unroll
+    for (int i = 0; i < K; ++i) nxt[i] = p[i];
+  }
+  while (tk < tk_end) {
+    uint32_t wd[K + 1];
+#pragma unroll
+    for (int i = 0; i < K; ++i) wd[i + 1] = nxt[i];
+    const int tk_next = tk + 4;
+    if (tk_next < tk_end) {
+      const uint32_t *p = wchunk + (size_t)tk_next * row_words;
+#pragma unroll
+      for (int i = 0; i < K; ++i) nxt[i] = p[i];
+    }
+    wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane, (int)wd[K]);
+    uint32_t xv[B][8];
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) xv[b][d] = xp[xoff[b] + tk * 8 + d];
+    static_for<16>([&](auto P) {
+      constexpr int p = decltype(P)::value;
+      const uint32_t wp = chunk_pair<K, CB, p>(wd, mask);
+      constexpr int xd = (p >> 2) + ((p & 1) ? 4 : 0);
+      constexpr int ch = (p & 2) ? 1 : 0;
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+        acc[b][ch] = __builtin_amdgcn_fdot2(bits<h2_t>(wp), bits<h2_t>(xv[b][xd]), acc[b][ch], false);
+    });
+    tk = tk_next;
+  }
+}
+
+// Any even n: each wave stages its 8 tiles' dwords for one k-tile row in its
+// own LDS slice, then every lane extracts its chunk's codewords.
+template <int B, int CB>
+__device__ __forceinline__ void gemv_accum_generic(const uint32_t *__restrict__ tw8,
+                                                   size_t row_words, int n,
+                                                   const uint32_t *__restrict__ xp,
+                                                   const int (&xoff)[B], int tk, int tk_end,
+                                                   uint32_t mask, int lane, uint32_t *stage,
+                                                   float (&acc)[B][2]) {
+  const int nw = n >> 1;
+  const int tl = lane >> 3, c = lane & 7;
+  for (; tk < tk_end; tk += 4) {
+    const uint32_t *src = tw8 + (size_t)tk * row_words;
+    for (int i = lane; i < 8 * nw; i += 64) stage[i] = src[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t *mine = stage + tl * nw;
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t t = 32u * c + 2u * p;
+      const uint32_t wp =
+          decode_pair<CB>(tile_window(mine, n, t), tile_window(mine, n, t + 1u), mask);
+      const int xd = (p >> 2) + ((p & 1) ? 4 : 0);
+      const int ch = (p & 2) ? 1 : 0;
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const uint32_t xv = xp[xoff[b] + tk * 8 + xd];
+        acc[b][ch] = __builtin_amdgcn_fdot2(bits<h2_t>(wp), bits<h2_t>(xv), acc[b][ch], false);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Sums the 4 waves' per-lane accumulators into red[b][128] (LDS, wave 0's
+// region reused) in wave order.
+template <int B>
+__device__ __forceinline__ void gemv_wave_reduce(float (&acc)[B][2], float *red, int wave,
+                                                 int lane) {
+  const int col = (lane >> 3) * 16 + (lane & 7);
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    red[(wave * B + b) * 128 + col] = acc[b][0];
+    red[(wave * B + b) * 128 + col + 8] = acc[b][1];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+    const float s = ((red[e] + red[B * 128 + e]) + red[2 * B * 128 + e]) + red[3 * B * 128 + e];
+    red[4 * B * 128 + e] = s;
+  }
+  __syncthreads();
+}
+
+// Split-K hand-off: writes this workgroup's sums (row b of the call goes to
+// partial row prow[b] of ptotal), takes a ticket, and returns true in the
+// last workgroup of the column group, with z = f16(sum over splits, in split
+// order) in zf[b*128 + col] as f32.
+template <int B>
+__device__ __forceinline__ bool gemv_splitk_last(const float *sums, float *zf, float *partial,
+                                                 uint32_t *ticket, int ksplit, int ks, int nrows,
+                                                 const int (&prow)[B], size_t ptotal, size_t out,
+                                                 int col0) {
+  __shared__ int s_last;
+  if (ksplit == 1) {
+    for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) zf[e] = h2f(f2h(sums[e]));
+    __syncthreads();
+    return true;
+  }
+  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+    const int b = e >> 7, col = e & 127;
+    if (b < nrows) st_agent(partial + ((size_t)ks * ptotal + prow[b]) * out + col0 + col, sums[e]);
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = atomicAdd(ticket, 1u);
+    s_last = (prev == (uint32_t)ksplit - 1u) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return false;
+  __threadfence();
+  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+    const int b = e >> 7, col = e & 127;
+    float s = 0.0f;
+    if (b < nrows)
+      for (int k = 0; k < ksplit; ++k)
+        s = s + ld_agent(partial + ((size_t)k * ptotal + prow[b]) * out + col0 + col);
+    zf[e] = h2f(f2h(s));
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  return true;
+}
+
+// The finish over zf[B][128] (f32 holding f16 values): rotation, * 1/sqrt(128),
+// * svh, f16, output dtype at element offset yoff[b] + col; or z itself as
+// f16 into zout when y is null.
+template <int B>
+__device__ __forceinline__ void gemv_finish(float *zf, const uint16_t *__restrict__ svh, void *y,
+                                            int ydt, uint16_t *zout, int nrows,
+                                            const size_t (&yoff)[B], int col0) {
+  if (y == nullptr) {
+    for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+      const int b = e >> 7, col = e & 127;
+      if (b < nrows) zout[yoff[b] + col0 + col] = f2h(zf[e]);
+    }
+    return;
+  }
+  had128_lds(zf, B, threadIdx.x, GEMV_THREADS);
+  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+    const int b = e >> 7, col = e & 127;
+    if (b < nrows) {
+      const float sc = zf[e] * HAD_SCALE;
+      store_out(y, yoff[b] + col0 + col, f2h(sc * h2f(svh[col0 + col])), ydt);
+    }
+  }
+}
+
+// The whole GEMV for one (column group, k-split) workgroup over nrows <= B
+// rows: activations at dword offsets xoff[b] of xp, partial rows prow[b] of
+// ptotal, outputs at element offsets yoff[b].
+template <int K, int B, int CB>
+__device__ __forceinline__ void gemv_body(const uint32_t *__restrict__ tw,
+                                          const uint32_t *__restrict__ xp,
+                                          const uint16_t *__restrict__ svh, void *y, int ydt,
+                                          uint16_t *zout, float *partial, uint32_t *ticket,
+                                          int nrows, const int (&xoff)[B], const int (&prow)[B],
+                                          size_t ptotal, const size_t (&yoff)[B], int in_tiles,
+                                          int out_tiles, int n, int ksplit, int tps, uint32_t mask,
+                                          int cg, int ks, float *red, uint32_t *stage) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tn = cg * 8 + (lane >> 3), c = lane & 7;
+  float acc[B][2];
+#pragma unroll
+  for (int b = 0; b < B; ++b) acc[b][0] = acc[b][1] = 0.0f;
+  const int tk0 = ks * tps + wave;
+  const int tk_end = min(in_tiles, (ks + 1) * tps);
+  const int nw = n >> 1;
+  const size_t row_words = (size_t)out_tiles * nw;  // dwords per k-tile row
+  if constexpr (K > 0) {
+    const int src = (((lane & ~7) | ((lane + 7) & 7)) << 2);
+    gemv_accum<K, B, CB>(tw + (size_t)tn * (8 * K) + c * K, row_words, xp, xoff, tk0, tk_end, mask,
+                         src, acc);
+  } else {
+    gemv_accum_generic<B, CB>(tw + (size_t)cg * 8 * nw, row_words, n, xp, xoff, tk0, tk_end, mask,
+                              lane, stage + wave * 512, acc);
+  }
+  gemv_wave_reduce<B>(acc, red, wave, lane);
+  float *sums = red + 4 * B * 128;
+  float *zf = red;
+  const size_t out = (size_t)out_tiles * 16;
+  if (!gemv_splitk_last<B>(sums, zf, partial, ticket, ksplit, ks, nrows, prow, ptotal, out, cg * 128))
+    return;
+  gemv_finish<B>(zf, svh, y, ydt, zout, nrows, yoff, cg * 128);
+}
+
+template <int K, int B, int CB>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
+    const uint32_t *__restrict__ tw, const uint32_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
+    float *__restrict__ partial, uint32_t *__restrict__ ticket, int rows, int in_tiles,
+    int out_tiles, int n, int ksplit, int tps, uint32_t mask) {
+  __shared__ float red[5 * B * 128];
+  __shared__ uint32_t stage[K == 0 ? 4 * 512 : 1];
+  const int in2 = in_tiles * 8;
+  const size_t out = (size_t)out_tiles * 16;
+  int xoff[B], prow[B];
+  size_t yoff[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const int r = b < rows ? b : 0;
+    xoff[b] = r * in2;
+    prow[b] = r;
+    yoff[b] = (size_t)r * out;
+  }
+  gemv_body<K, B, CB>(tw, xp, svh, y, ydt, zout, partial, ticket + blockIdx.x, rows, xoff, prow,
+                      (size_t)rows, yoff, in_tiles, out_tiles, n, ksplit, tps, mask, blockIdx.x,
+                      blockIdx.y, red, stage);
+}
+
+int gemv_ksplit(int in, int out, int groups) {
+  const int in_tiles = in / 16;
+  const int cgs = std::max(1, out / 128) * std::max(1, groups);
+  // Aim for ~4 workgroups (16 waves) per CU on 256 CUs, with at least 8
+  // k-tile rows (2 per wave) per split.
+  int ks = std::max(1, 1024 / cgs);
+  ks = std::min(ks, std::max(1, in_tiles / 8));
+  const int tps = (in_tiles + ks - 1) / ks;
+  return (in_tiles + tps - 1) / tps;
+}
+
+void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t *tickets) {
+  const int ks = gemv_ksplit(in, out, 1);
+  *partial_floats = (size_t)ks * rows * out;
+  *tickets = (size_t)out / 128;
+}
+
+template <int K, int B, int CB>
+static void gemv_go(dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
+                    const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
+                    uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
+                    int tps, uint32_t mask) {
+  hipLaunchKernelGGL((gemv_kernel<K, B, CB>), grid, dim3(GEMV_THREADS), 0, s, tw, xp, svh, y, ydt,
+                     zout, partial, ticket, rows, in_tiles, out_tiles, n, ksplit, tps, mask);
+}
+
+template <int B, int CB>
+static void gemv_rate(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
+                      const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
+                      uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
+                      int tps, uint32_t mask) {
+  switch (kk) {
+#define EXL3_GV(KK)                                                                               \
+  case KK:                                                                                        \
+    gemv_go<KK, B, CB>(grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles,      \
+                       out_tiles, n, ksplit, tps, mask);                                          \
+    break;
+    EXL3_GV(1) EXL3_GV(2) EXL3_GV(3) EXL3_GV(4) EXL3_GV(5) EXL3_GV(6) EXL3_GV(7) EXL3_GV(8)
+#undef EXL3_GV
+    default:
+      gemv_go<0, B, CB>(grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles,
+                        out_tiles, n, ksplit, tps, mask);
+  }
+}
+
+template <int CB>
+static void gemv_rows(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
+                      const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
+                      uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
+                      int tps, uint32_t mask) {
+#define EXL3_GR(BB)                                                                        \
+  gemv_rate<BB, CB>(kk, grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles, \
+                    out_tiles, n, ksplit, tps, mask)
+  switch (rows) {
+    case 1: EXL3_GR(1); break;
+    case 2: EXL3_GR(2); break;
+    case 3: EXL3_GR(3); break;
+    case 4: EXL3_GR(4); break;
+    case 5: EXL3_GR(5); break;
+    case 6: EXL3_GR(6); break;
+    case 7: EXL3_GR(7); break;
+    default: EXL3_GR(8); break;
+  }
+#undef EXL3_GR
+}
+
+hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
+                       int out, Scratch &sc, hipStream_t s) {
+  if (rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
+  if (in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
+  if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
+  if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
+  const int in_tiles = in / 16, out_tiles = out / 16;
+  const int ksplit = gemv_ksplit(in, out, 1);
+  const int tps = (in_tiles + ksplit - 1) / ksplit;
+  if (ksplit > 65535 || out / 128 > 2147483647) return hipErrorInvalidValue;
+  if (ksplit > 1) {
+    if (sc.partial == nullptr || sc.partial_floats < (size_t)ksplit * rows * out)
+      return hipErrorInvalidValue;
+    if (sc.ticket == nullptr || sc.tickets < (size_t)out / 128) return hipErrorInvalidValue;
+  }
+  const dim3 grid(out / 128, ksplit);
+  const int kk = f.integer_rate() ? f.n / 16 : 0;
+  const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
+  const uint32_t *xw = reinterpret_cast<const uint32_t *>(xp);
+  if (f.codebook == CB_MCG)
+    gemv_rows<CB_MCG>(kk, grid, s, tw, xw, svh, y, ydt, zout, sc.partial, sc.ticket, rows, in_tiles,
+                      out_tiles, f.n, ksplit, tps, f.mask());
+  else
+    gemv_rows<CB_MUL1>(kk, grid, s, tw, xw, svh, y, ydt, zout, sc.partial, sc.ticket, rows,
+                       in_tiles, out_tiles, f.n, ksplit, tps, f.mask());
+  return hipGetLastError();
+}
+
+// ===================================================================== GEMM
+//
+// Workgroup tile 128 rows x 128 columns (one Hadamard block of the output),
+// 4 waves in a 2x2 grid of 64x64 sub-tiles, each 2x2 v_mfma_f32_32x32x16_f16
+// tiles with f32 accumulators.  The k loop runs in stages of 32 (two k-tile
+// rows of 8 output tiles = 16 tiles = 128 chunks); every thread decodes half
+// a chunk (16 codewords) of the next stage into the other LDS buffer while the
+// MFMAs consume the current one.  The B^T tile sits in LDS as [n][k] with k
+// contiguous (a chunk's column is 16 consecutive k), so an MFMA B operand (8
+// consecutive k of one column) is one ds_read_b128; A operands (prepared
+// activations, row-major f16) load straight from global memory in operand
+// layout.  The epilogue rounds z to f16 in LDS and runs the finish per row.
+
+constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_THREADS = 256;
+constexpr int GM_LDK = GM_BK + 8;  // k stride (halfs) of a B^T column in LDS
+constexpr int GM_ZLD = GM_BN + 8;  // column stride (halfs) of the z tile
+constexpr int GM_LDS_HALFS =
+    (2 * GM_BN * GM_LDK > GM_BM * GM_ZLD) ? 2 * GM_BN * GM_LDK : GM_BM * GM_ZLD;
+
+// Decodes this thread's half chunk (codewords 16h..16h+15: pairs 8h..8h+7)
+// into bt (LDS).  h is uniform per wave, so only one arm runs.
+template <int K, int CB, int H>
+__device__ __forceinline__ void gemm_decode_half(const uint32_t (&wd)[K + 1], uint32_t *btw,
+                                                 int tkl, int tnl, int c, uint32_t mask) {
+  static_for<8>([&](auto Q) {
+    constexpr int p = decltype(Q)::value + 8 * H;
+    const uint32_t v = chunk_pair<K, CB, p>(wd, mask);
+    constexpr int r = chunk_row(2 * p);
+    constexpr int ch = chunk_colhalf(2 * p);
+    const int nl = tnl * 16 + c + 8 * ch;
+    const int kl = tkl * 16 + r;
+    btw[(nl * GM_LDK + kl) >> 1] = v;
+  });
+}
+
+template <int K, int CB>
+__device__ __forceinline__ void gemm_decode_stage(const uint32_t (&wd)[K + 1], uint16_t *bt,
+                                                  int tkl, int tnl, int c, int h, uint32_t mask) {
+  uint32_t *btw = reinterpret_cast<uint32_t *>(bt);
+  if (h)
+    gemm_decode_half<K, CB, 1>(wd, btw, tkl, tnl, c, mask);
+  else
+    gemm_decode_half<K, CB, 0>(wd, btw, tkl, tnl, c, mask);
+}
+
+template <int K>
+__device__ __forceinline__ void gemm_load_words(const uint32_t *__restrict__ tw, size_t tbase,
+                                                int c, int h, uint32_t (&wd)[K + 1]) {
+  const uint32_t *tp = tw + tbase;
+#pragma unroll
+  for (int i = 0; i < K; ++i) wd[i + 1] = tp[c * K + i];
+  // codewords 16..31 of a chunk never reach the history dword
+  wd[0] = h ? 0u : tp[((c + 7) & 7) * K + (K - 1)];
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
+    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
+    int M, int in_tiles, int out_tiles, uint32_t mask) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_HALFS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int cg = blockIdx.x;
+  const int m0 = blockIdx.y * GM_BM;
+  const int in = in_tiles * 16;
+  const size_t out = (size_t)out_tiles * 16;
+  const int nw = 8 * K;
+  // decoder role: 16 tiles (2 k-tile rows x 8 output tiles) x 8 chunks = 128
+  // chunks; waves 2q and 2q+1 take chunks 64q..64q+63, halves 0 and 1.
+  const int h = __builtin_amdgcn_readfirstlane(wave & 1);
+  const int chunk_id = (wave >> 1) * 64 + lane;
+  const int tl = chunk_id >> 3, tkl = tl >> 3, tnl = tl & 7, c = chunk_id & 7;
+  const size_t tcol = (size_t)cg * 8 + tnl;
+
+  f16v_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // A operand rows of this lane (rows past M read as zero)
+  const int arow0 = m0 + wr * 64 + (lane & 31);
+  const int akoff = 8 * (lane >> 5);
+  const bool aok0 = arow0 < M, aok1 = arow0 + 32 < M;
+  const uint16_t *ap0 = xp + (size_t)(aok0 ? arow0 : 0) * in + akoff;
+  const uint16_t *ap1 = xp + (size_t)(aok1 ? arow0 + 32 : 0) * in + akoff;
+
+  const int stages = in_tiles / 2;
+  uint32_t wd[K + 1];
+  gemm_load_words<K>(tw, ((size_t)tkl * out_tiles + tcol) * nw, c, h, wd);
+  gemm_decode_stage<K, CB>(wd, lds, tkl, tnl, c, h, mask);
+  __syncthreads();
+
+  for (int st = 0; st < stages; ++st) {
+    uint16_t *cur = lds + (st & 1) * (GM_BN * GM_LDK);
+    uint16_t *nxt = lds + ((st + 1) & 1) * (GM_BN * GM_LDK);
+    const bool more = st + 1 < stages;
+    if (more) gemm_load_words<K>(tw, ((size_t)(2 * (st + 1) + tkl) * out_tiles + tcol) * nw, c, h, wd);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int k0 = st * GM_BK + kk * 16;
+      h8_t a0 = {}, a1 = {};
+      if (aok0) a0 = *reinterpret_cast<const h8_t *>(ap0 + k0);
+      if (aok1) a1 = *reinterpret_cast<const h8_t *>(ap1 + k0);
+      h8_t b[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int nl = wc * 64 + j * 32 + (lane & 31);
+        b[j] = *reinterpret_cast<const h8_t *>(cur + nl * GM_LDK + kk * 16 + akoff);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b[j], acc[0][j], 0, 0, 0);
+        acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j], acc[1][j], 0, 0, 0);
+      }
+    }
+    if (more) gemm_decode_stage<K, CB>(wd, nxt, tkl, tnl, c, h, mask);
+    __syncthreads();
+  }
+
+  // z = f16(acc) into the z tile: D[i][j] of a 32x32 MFMA sits in lane
+  // l = j + 32 * ((i / 4) % 2), register 4 * (i / 8) + i % 4.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int col = wc * 64 + j * 32 + (lane & 31);
+        lds[row * GM_ZLD + col] = f2h(acc[i][j][r]);
+      }
+  __syncthreads();
+  for (int row = wave; row < GM_BM; row += 4) {
+    const int m = m0 + row;
+    if (m >= M) break;
+    const uint16_t *zr = lds + row * GM_ZLD;
+    if (y == nullptr) {
+      zout[(size_t)m * out + cg * 128 + lane] = zr[lane];
+      zout[(size_t)m * out + cg * 128 + lane + 64] = zr[lane + 64];
+    } else {
+      finish_row_wave(zr, svh + cg * 128, y, ydt, (size_t)m * out + cg * 128, lane);
+    }
+  }
+}
+
+template <int CB>
+static void gemm_cb(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
+                    const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
+                    int out_tiles, uint32_t mask) {
+  switch (kk) {
+#define EXL3_GM(KK)                                                                          \
+  case KK:                                                                                   \
+    hipLaunchKernelGGL((gemm_kernel<KK, CB>), grid, dim3(GM_THREADS), 0, s, tw, xp, svh, y, \
+                       ydt, zout, M, in_tiles, out_tiles, mask);                             \
+    break;
+    EXL3_GM(1) EXL3_GM(2) EXL3_GM(3) EXL3_GM(4) EXL3_GM(5) EXL3_GM(6) EXL3_GM(7) EXL3_GM(8)
+#undef EXL3_GM
+    default:
+      break;
+  }
+}
+
+hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
+                       int out, hipStream_t s) {
+  if (rows < 1 || in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
+  if (!f.integer_rate()) return hipErrorInvalidValue;
+  if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
+  const int mblocks = (rows + GM_BM - 1) / GM_BM;
+  if (mblocks > 65535) return hipErrorInvalidValue;
+  const dim3 grid(out / 128, mblocks);
+  const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
+  if (f.codebook == CB_MCG)
+    gemm_cb<CB_MCG>(f.n / 16, grid, s, tw, xp, svh, y, ydt, zout, rows, in / 16, out / 16, f.mask());
+  else
+    gemm_cb<CB_MUL1>(f.n / 16, grid, s, tw, xp, svh, y, ydt, zout, rows, in / 16, out / 16, f.mask());
+  return hipGetLastError();
+}
+
+// ====================================================================== MoE
+//
+// Routed SwiGLU experts (sushi_ds41/src/sushi/exl3/expert_exl3_kernels.zig:
+// 3151-3206 for the arithmetic; decode chain :2765-3113):
+//   1. route: one workgroup counts the (row, k) slots per expert, orders the
+//      slots by expert (within an expert in any order: every slot's
+//      arithmetic is independent of its position) and emits work items of
+//      up to 8 slots of one expert;
+//   2. prepare: per slot, x[row] * suh_gate[e] and x[row] * suh_up[e] rotated;
+//   3. grouped GEMV (gate and up in one launch): each work item is a GEMV over
+//      its expert's packed weights for its slots, split-K with the fused
+//      finish, giving g and u (f16) per slot;
+//   4. mid: h = silu(g) * u in f32 (limit > 0: g <= limit, |u| <= limit,
+//      turboexl3_ds41/src/exl3/kernels/exl3/q3_exl3_prep_gu_epi.metal:47-56),
+//      then the down projection's prepare with suh_down[e];
+//   5. grouped GEMV down, finished per slot (f16);
+//   6. combine: y[row] = sum_k score[row, k] * d[slot(row, k)] in f32, in k
+//      order, then the output dtype.
+
+struct MoeItem {
+  uint32_t expert, start, count, pad;
+};
+
+constexpr int MOE_ROUTE_THREADS = 1024;
+constexpr int MOE_ITEM_ROWS = 8;
+
+// Exclusive prefix sum over the 1024 threads of a block; *total gets the sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp,
+                                                         uint32_t *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t t = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += t;
+  }
+  if (lane == 63) tmp[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < MOE_ROUTE_THREADS / 64; ++w) {
+      const uint32_t t = tmp[w];
+      tmp[w] = run;
+      run += t;
+    }
+    *total = run;
+  }
+  __syncthreads();
+  const uint32_t r = tmp[wave] + inc - v;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(
+    const uint32_t *__restrict__ inds, int slots, int experts, uint32_t *__restrict__ sorted,
+    MoeItem *__restrict__ items, uint32_t *__restrict__ n_items) {
+  __shared__ uint32_t cnt[MOE_ROUTE_THREADS], cur[MOE_ROUTE_THREADS], tmp[MOE_ROUTE_THREADS / 64];
+  __shared__ uint32_t total;
+  const int t = threadIdx.x;
+  cnt[t] = 0;
+  __syncthreads();
+  for (int s = t; s < slots; s += MOE_ROUTE_THREADS) {
+    const uint32_t e = inds ? inds[s] : 0u;
+    if (e < (uint32_t)experts) atomicAdd(&cnt[e], 1u);
+  }
+  __syncthreads();
+  const uint32_t c = t < experts ? cnt[t] : 0u;
+  const uint32_t off = block_exclusive_scan(c, tmp, &total);
+  const uint32_t nit = (c + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
+  const uint32_t ioff = block_exclusive_scan(nit, tmp, &total);
+  cur[t] = off;
+  __syncthreads();
+  for (int s = t; s < slots; s += MOE_ROUTE_THREADS) {
+    const uint32_t e = inds ? inds[s] : 0u;
+    if (e < (uint32_t)experts) sorted[atomicAdd(&cur[e], 1u)] = (uint32_t)s;
+  }
+  for (uint32_t r = 0; r < nit; ++r) {
+    MoeItem it;
+    it.expert = (uint32_t)t;
+    it.start = off + r * MOE_ITEM_ROWS;
+    it.count = min((uint32_t)MOE_ITEM_ROWS, c - r * MOE_ITEM_ROWS);
+    it.pad = 0;
+    items[ioff + r] = it;
+  }
+  if (t == 0) *n_items = total;
+}
+
+// Per slot s (row s / topk, expert inds[s]): the gate and up prepares.
+__global__ __launch_bounds__(64) void moe_prepare2_kernel(
+    const void *__restrict__ x, int xdt, const uint32_t *__restrict__ inds, int topk, int experts,
+    const uint16_t *__restrict__ suh_g, const uint16_t *__restrict__ suh_u,
+    uint16_t *__restrict__ xg, uint16_t *__restrict__ xu, int hidden) {
+  const int lane = threadIdx.x;
+  const size_t slot = blockIdx.y;
+  const uint32_t e = inds ? inds[slot] : 0u;
+  if (e >= (uint32_t)experts) return;
+  const size_t row = slot / topk;
+  const int i0 = blockIdx.x * 128 + lane;
+  const float x0 = h2f(f2h(load_act(x, row * hidden + i0, xdt)));
+  const float x1 = h2f(f2h(load_act(x, row * hidden + i0 + 64, xdt)));
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const uint16_t *su = (which ? suh_u : suh_g) + (size_t)e * hidden;
+    float v0 = x0 * h2f(su[i0]);
+    float v1 = x1 * h2f(su[i0 + 64]);
+#pragma unroll
+    for (int bit = 1; bit <= 32; bit <<= 1) {
+      const float p0 = __shfl_xor(v0, bit, 64);
+      const float p1 = __shfl_xor(v1, bit, 64);
+      const bool lower = (lane & bit) == 0;
+      v0 = lower ? v0 + p0 : p0 - v0;
+      v1 = lower ? v1 + p1 : p1 - v1;
+    }
+    const float a = v0 + v1, b = v0 - v1;
+    uint16_t *dst = (which ? xu : xg) + slot * hidden;
+    dst[i0] = f2h(a * HAD_SCALE);
+    dst[i0 + 64] = f2h(b * HAD_SCALE);
+  }
+}
+
+// h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e].
+__global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict__ g,
+                                                     const uint16_t *__restrict__ u,
+                                                     const uint32_t *__restrict__ inds, int experts,
+                                                     const uint16_t *__restrict__ suh_d,
+                                                     uint16_t *__restrict__ xd, int inter,
+                                                     float limit) {
+  const int lane = threadIdx.x;
+  const size_t slot = blockIdx.y;
+  const uint32_t e = inds ? inds[slot] : 0u;
+  if (e >= (uint32_t)experts) return;
+  const int i0 = blockIdx.x * 128 + lane;
+  float v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = i0 + 64 * j;
+    float gv = h2f(g[slot * inter + i]), uv = h2f(u[slot * inter + i]);
+    if (limit > 0.0f) {
+      gv = gv < limit ? gv : limit;
+      uv = uv > -limit ? uv : -limit;
+      uv = uv < limit ? uv : limit;
+    }
+    const float h = (gv / (1.0f + expf(-gv))) * uv;
+    v[j] = h2f(f2h(h)) * h2f(suh_d[(size_t)e * inter + i]);
+  }
+#pragma unroll
+  for (int bit = 1; bit <= 32; bit <<= 1) {
+    const float p0 = __shfl_xor(v[0], bit, 64);
+    const float p1 = __shfl_xor(v[1], bit, 64);
+    const bool lower = (lane & bit) == 0;
+    v[0] = lower ? v[0] + p0 : p0 - v[0];
+    v[1] = lower ? v[1] + p1 : p1 - v[1];
+  }
+  const float a = v[0] + v[1], b = v[0] - v[1];
+  xd[slot * inter + i0] = f2h(a * HAD_SCALE);
+  xd[slot * inter + i0 + 64] = f2h(b * HAD_SCALE);
+}
+
+// Grouped GEMV: blockIdx.z = item * nsel + which; each item is up to 8 slots
+// of one expert (slot ids sorted[start .. start+count)).
+struct MoeGemvSide {
+  const uint32_t *tw;   // bank trellis, dwords
+  const uint16_t *svh;  // [E][out]
+  const uint32_t *xp;   // [slots][in] prepared, as dwords
+  uint16_t *y;          // [slots][out] f16
+  float *partial;       // [ksplit][slots][out]
+  uint32_t *ticket;     // [max_items][out/128]
+};
+
+template <int K, int B, int CB>
+__device__ __forceinline__ void moe_gemv_item(const MoeGemvSide &sd, const uint32_t *sorted,
+                                              const MoeItem &it, int slots, int in_tiles,
+                                              int out_tiles, int n, int ksplit, int tps,
+                                              uint32_t mask, int item, float *red,
+                                              uint32_t *stage) {
+  const int in2 = in_tiles * 8;
+  const size_t out = (size_t)out_tiles * 16;
+  int xoff[B], prow[B];
+  size_t yoff[B];
+  const int nrows = (int)it.count;
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const int slot = (int)sorted[it.start + (b < nrows ? b : 0)];
+    xoff[b] = slot * in2;
+    prow[b] = slot;
+    yoff[b] = (size_t)slot * out;
+  }
+  const size_t per_expert = (size_t)in_tiles * out_tiles * (n >> 1);
+  gemv_body<K, B, CB>(sd.tw + per_expert * it.expert, sd.xp, sd.svh + out * it.expert, sd.y,
+                      OUT_F16, nullptr, sd.partial, sd.ticket + (size_t)item * (out_tiles / 8) + blockIdx.x,
+                      nrows, xoff, prow, (size_t)slots, yoff, in_tiles, out_tiles, n, ksplit, tps,
+                      mask, blockIdx.x, blockIdx.y, red, stage);
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
+    MoeGemvSide s0, MoeGemvSide s1, int nsel, const uint32_t *__restrict__ sorted,
+    const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, int slots,
+    int in_tiles, int out_tiles, int n, int ksplit, int tps, uint32_t mask) {
+  __shared__ float red[5 * MOE_ITEM_ROWS * 128];
+  __shared__ uint32_t stage[K == 0 ? 4 * 512 : 1];
+  const int item = blockIdx.z / nsel, which = blockIdx.z % nsel;
+  if ((uint32_t)item >= *n_items) return;
+  const MoeItem it = items[item];
+  const MoeGemvSide &sd = which ? s1 : s0;
+  if (it.count <= 1)
+    moe_gemv_item<K, 1, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
+  else if (it.count <= 2)
+    moe_gemv_item<K, 2, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
+  else if (it.count <= 4)
+    moe_gemv_item<K, 4, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
+  else
+    moe_gemv_item<K, 8, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
+}
+
+// y[row] = sum_k score * d[slot] (f32, k order), in the output dtype.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ d,
+                                                          const uint32_t *__restrict__ inds,
+                                                          const void *__restrict__ scores, int sdt,
+                                                          int topk, int experts, int hidden,
+                                                          void *__restrict__ y, int ydt) {
+  const size_t row = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= hidden) return;
+  float acc = 0.0f;
+  for (int k = 0; k < topk; ++k) {
+    const size_t slot = row * topk + k;
+    const uint32_t e = inds ? inds[slot] : 0u;
+    if (e >= (uint32_t)experts) continue;
+    const float w = scores ? load_act(scores, slot, sdt) : 1.0f;
+    acc = acc + w * h2f(d[slot * hidden + i]);
+  }
+  if (ydt == OUT_F16)
+    ((uint16_t *)y)[row * hidden + i] = f2h(acc);
+  else if (ydt == OUT_BF16)
+    ((uint16_t *)y)[row * hidden + i] = f2bf(acc);
+  else
+    ((float *)y)[row * hidden + i] = acc;
+}
+
+namespace {
+
+struct MoeLayout {
+  size_t sorted, items, n_items, xg, xu, g, u, xd, d, pgu, pd, total;
+  size_t tickets;  // in the separate ticket buffer: gate, up, down
+  int slots, max_items, ks_gu, ks_d, tps_gu, tps_d;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+MoeLayout moe_layout(const MoeArgs &a) {
+  MoeLayout L{};
+  const int slots = a.rows * a.topk;
+  L.slots = slots;
+  L.max_items = std::min(a.experts, slots) + (slots + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
+  const int groups = std::max(1, std::min(a.experts, slots));
+  L.ks_gu = gemv_ksplit(a.hidden, a.inter, 2 * groups);
+  L.ks_d = gemv_ksplit(a.inter, a.hidden, groups);
+  L.tps_gu = (a.hidden / 16 + L.ks_gu - 1) / L.ks_gu;
+  L.tps_d = (a.inter / 16 + L.ks_d - 1) / L.ks_d;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align256(bytes);
+    return at;
+  };
+  L.sorted = take((size_t)slots * 4);
+  L.items = take((size_t)L.max_items * sizeof(MoeItem));
+  L.n_items = take(4);
+  L.xg = take((size_t)slots * a.hidden * 2);
+  L.xu = take((size_t)slots * a.hidden * 2);
+  L.g = take((size_t)slots * a.inter * 2);
+  L.u = take((size_t)slots * a.inter * 2);
+  L.xd = take((size_t)slots * a.inter * 2);
+  L.d = take((size_t)slots * a.hidden * 2);
+  L.pgu = take((size_t)2 * L.ks_gu * slots * a.inter * 4);
+  L.pd = take((size_t)L.ks_d * slots * a.hidden * 4);
+  L.total = o;
+  L.tickets = (size_t)L.max_items * (2 * (a.inter / 128) + a.hidden / 128);
+  return L;
+}
+
+template <int CB>
+void moe_gemv_launch(int kk, dim3 grid, hipStream_t s, const MoeGemvSide &s0, const MoeGemvSide &s1,
+                     int nsel, const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
+                     int slots, int in_tiles, int out_tiles, int n, int ksplit, int tps,
+                     uint32_t mask) {
+  switch (kk) {
+#define EXL3_MG(KK)                                                                            \
+  case KK:                                                                                     \
+    hipLaunchKernelGGL((moe_gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), 0, s, s0, s1, nsel, \
+                       sorted, items, n_items, slots, in_tiles, out_tiles, n, ksplit, tps, mask); \
+    break;
+    EXL3_MG(1) EXL3_MG(2) EXL3_MG(3) EXL3_MG(4) EXL3_MG(5) EXL3_MG(6) EXL3_MG(7) EXL3_MG(8)
+#undef EXL3_MG
+    default:
+      hipLaunchKernelGGL((moe_gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), 0, s, s0, s1, nsel,
+                         sorted, items, n_items, slots, in_tiles, out_tiles, n, ksplit, tps, mask);
+  }
+}
+
+void moe_gemv(const Format &f, dim3 grid, hipStream_t s, const MoeGemvSide &s0,
+              const MoeGemvSide &s1, int nsel, const uint32_t *sorted, const MoeItem *items,
+              const uint32_t *n_items, int slots, int in, int out, int ksplit, int tps) {
+  const int kk = f.integer_rate() ? f.n / 16 : 0;
+  if (f.codebook == CB_MCG)
+    moe_gemv_launch<CB_MCG>(kk, grid, s, s0, s1, nsel, sorted, items, n_items, slots, in / 16,
+                            out / 16, f.n, ksplit, tps, f.mask());
+  else
+    moe_gemv_launch<CB_MUL1>(kk, grid, s, s0, s1, nsel, sorted, items, n_items, slots, in / 16,
+                             out / 16, f.n, ksplit, tps, f.mask());
+}
+
+}  // namespace
+
+size_t moe_scratch_bytes(const MoeArgs &a, size_t *tickets) {
+  if (a.rows <= 0 || a.topk <= 0) {
+    *tickets = 1;
+    return 256;
+  }
+  const MoeLayout L = moe_layout(a);
+  *tickets = L.tickets;
+  return L.total;
+}
+
+hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
+                      const MoeBank &down, void *scratch, size_t scratch_bytes, uint32_t *tickets,
+                      size_t ntickets, hipStream_t s) {
+  if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
+    return hipErrorInvalidValue;
+  if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
+  if (gate.f.n != up.f.n || gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden ||
+      gate.out != a.inter || up.out != a.inter || down.in != a.inter)
+    return hipErrorInvalidValue;
+  const MoeLayout L = moe_layout(a);
+  if (scratch_bytes < L.total || ntickets < L.tickets || L.slots > 65535 ||
+      L.max_items * 2 > 65535)
+    return hipErrorInvalidValue;
+  char *base = (char *)scratch;
+  uint32_t *sorted = (uint32_t *)(base + L.sorted);
+  MoeItem *items = (MoeItem *)(base + L.items);
+  uint32_t *n_items = (uint32_t *)(base + L.n_items);
+  uint16_t *xg = (uint16_t *)(base + L.xg), *xu = (uint16_t *)(base + L.xu);
+  uint16_t *g = (uint16_t *)(base + L.g), *u = (uint16_t *)(base + L.u);
+  uint16_t *xd = (uint16_t *)(base + L.xd), *d = (uint16_t *)(base + L.d);
+  float *pgu = (float *)(base + L.pgu), *pd = (float *)(base + L.pd);
+  uint32_t *tgu = tickets, *td = tickets + (size_t)2 * L.max_items * (a.inter / 128);
+
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
+                     a.experts, sorted, items, n_items);
+  hipLaunchKernelGGL(moe_prepare2_kernel, dim3(a.hidden / 128, L.slots), dim3(64), 0, s, a.x, a.xdt,
+                     a.inds, a.topk, a.experts, gate.suh, up.suh, xg, xu, a.hidden);
+  const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
+  MoeGemvSide sg{(const uint32_t *)gate.trellis, gate.svh, (const uint32_t *)xg, g, pgu, tgu};
+  MoeGemvSide su{(const uint32_t *)up.trellis, up.svh, (const uint32_t *)xu, u, pgu + gu_part,
+                 tgu + (size_t)L.max_items * (a.inter / 128)};
+  moe_gemv(gate.f, dim3(a.inter / 128, L.ks_gu, L.max_items * 2), s, sg, su, 2, sorted, items,
+           n_items, L.slots, a.hidden, a.inter, L.ks_gu, L.tps_gu);
+  hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
+                     a.experts, down.suh, xd, a.inter, a.limit);
+  MoeGemvSide sd{(const uint32_t *)down.trellis, down.svh, (const uint32_t *)xd, d, pd, td};
+  moe_gemv(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items), s, sd, sd, 1, sorted, items, n_items,
+           L.slots, a.inter, a.hidden, L.ks_d, L.tps_d);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
+                     a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
+  return hipGetLastError();
+}
+
+}  // namespace exl3

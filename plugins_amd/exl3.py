@@ -1,0 +1,391 @@
+"""Python host mirror of the EXL3 quant-plugin boundary (include/exl3_mi355x.h).
+
+The reference's host code is Zig calling the quant plugin table through its
+C ABI (turboexl3_qwen38/overlay/mlx_serve/abi/quant.zig:24-108, filled by
+turboexl3_ds41/plugin.zig:28-43; paths relative to /root/reference/plugins/).
+This module binds the same entries of libexl3_mi355x.so with ctypes, under
+the reference's names (claims, validate, bill, open, close, load_tensor,
+load_bank, release, matmul, moe, swiglu) and with the same meaning: each
+returns a Verdict (code, why) and refuses by name instead of falling back.
+
+PyTorch supplies device memory and the HIP stream handle only; every
+computation runs in the library's HIP kernels.  If the library is not built,
+loading fails loudly (no CPU path exists here).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+from ctypes import (CFUNCTYPE, POINTER, Structure, c_bool, c_char_p, c_int, c_int32, c_int64,
+                    c_size_t, c_uint32, c_uint64, c_void_p)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libexl3_mi355x.so")
+
+# Verdict codes (kit Verdict: ok, unsupported, failed, too_large)
+OK, UNSUPPORTED, FAILED, TOO_LARGE = 0, 1, 2, 3
+# Claim values
+CLAIM_NO, CLAIM_BY_MODE, CLAIM_BY_MARKER = 0, 1, 2
+# mlx-c dtype numbering
+DT_BOOL, DT_U8, DT_U16, DT_U32, DT_U64, DT_I8, DT_I16, DT_I32, DT_I64 = range(9)
+DT_F16, DT_F32, DT_F64, DT_BF16 = 9, 10, 11, 12
+MAX_DIMS = 4
+
+
+class Str(Structure):
+    _fields_ = [("ptr", c_char_p), ("len", c_size_t)]
+
+    @classmethod
+    def of(cls, s) -> "Str":
+        b = s.encode() if isinstance(s, str) else (s or b"")
+        return cls(b, len(b))
+
+
+class Verdict(Structure):
+    _fields_ = [("code", c_int32), ("why", c_char_p)]
+
+    def is_ok(self) -> bool:
+        return self.code == OK
+
+    @property
+    def reason(self) -> str:
+        return (self.why or b"").decode()
+
+    def __repr__(self) -> str:
+        return f"Verdict(code={self.code}, why={self.reason!r})"
+
+
+class Array(Structure):
+    _fields_ = [("data", c_void_p), ("dtype", c_int32), ("ndim", c_int32),
+                ("shape", c_int64 * MAX_DIMS), ("owned", c_uint32), ("_pad", c_uint32)]
+
+    def dims(self) -> tuple:
+        return tuple(self.shape[i] for i in range(self.ndim))
+
+
+class Weight(Structure):
+    _fields_ = [("w", Array), ("scales", Array), ("biases", Array), ("side", Array),
+                ("flags", c_uint32), ("_pad", c_uint32), ("priv", c_void_p)]
+
+
+class HostTensor(Structure):
+    _fields_ = [("data", c_void_p), ("dtype", c_int32), ("ndim", c_int32),
+                ("shape", c_int64 * MAX_DIMS)]
+
+
+TENSOR_FN = CFUNCTYPE(c_int, c_void_p, Str, POINTER(HostTensor))
+FILE_BYTES_FN = CFUNCTYPE(c_uint64, c_void_p, Str)
+
+
+class Source(Structure):
+    _fields_ = [("self", c_void_p), ("tensor", TENSOR_FN)]
+
+
+class PackDir(Structure):
+    _fields_ = [("self", c_void_p), ("file_bytes", FILE_BYTES_FN)]
+
+
+class LoadCtx(Structure):
+    _fields_ = [("size", c_uint32), ("device", c_int32), ("block_json", Str),
+                ("config_json", Str), ("source", POINTER(Source)), ("dir", POINTER(PackDir)),
+                ("stream", c_void_p), ("state", c_void_p)]
+
+
+class SwigluOpts(Structure):
+    _fields_ = [("size", c_uint32), ("limit", c_int32), ("verify_rows", c_bool)]
+
+
+class QuantTable(Structure):
+    _fields_ = [("size", c_uint32), ("version", c_uint32), ("name", Str),
+                ("claims", c_void_p), ("validate", c_void_p), ("bill", c_void_p),
+                ("open", c_void_p), ("close", c_void_p), ("load_tensor", c_void_p),
+                ("load_bank", c_void_p), ("release", c_void_p), ("matmul", c_void_p),
+                ("moe", c_void_p), ("register_kernels", c_void_p), ("swiglu", c_void_p)]
+
+
+# Every symbol include/exl3_mi355x.h declares, with its ctypes signature.
+SIGNATURES = {
+    "exl3_claims": (c_int32, [Str, Str]),
+    "exl3_validate": (Verdict, [Str, Str, POINTER(PackDir)]),
+    "exl3_bill": (c_uint64, [Str, Str, c_uint64]),
+    "exl3_open": (Verdict, [POINTER(LoadCtx)]),
+    "exl3_close": (None, [POINTER(LoadCtx)]),
+    "exl3_load_tensor": (Verdict, [POINTER(LoadCtx), Str, c_uint32, POINTER(Weight)]),
+    "exl3_load_bank": (Verdict, [POINTER(LoadCtx), Str, c_uint32, POINTER(Weight)]),
+    "exl3_release": (None, [POINTER(Weight)]),
+    "exl3_matmul": (Verdict, [POINTER(Weight), Array, c_void_p, POINTER(Array)]),
+    "exl3_moe": (Verdict, [POINTER(Weight), Array, Array, Array, c_bool, c_void_p, POINTER(Array)]),
+    "exl3_swiglu": (Verdict, [POINTER(Weight), POINTER(Weight), POINTER(Weight), Array, Array, Array,
+                              POINTER(SwigluOpts), c_void_p, POINTER(Array)]),
+    "exl3_quant_table_get": (POINTER(QuantTable), []),
+    "exl3_array_free": (None, [POINTER(Array)]),
+    "exl3_weight_wrap": (Verdict, [Array, Array, Array, Str, c_int32, POINTER(Weight)]),
+    "exl3_decode_matrix": (Verdict, [POINTER(Weight), c_int32, Array, c_void_p]),
+    "exl3_prepare": (Verdict, [POINTER(Weight), Array, Array, c_void_p]),
+    "exl3_finish": (Verdict, [POINTER(Weight), Array, Array, c_void_p]),
+    "exl3_inner": (Verdict, [POINTER(Weight), Array, Array, c_void_p]),
+    "exl3_version": (c_char_p, []),
+    "exl3_matmul_path": (c_char_p, [POINTER(Weight), c_int64]),
+}
+
+_lib = None
+
+
+class Exl3Error(RuntimeError):
+    def __init__(self, verdict: Verdict, what: str = ""):
+        self.code = verdict.code
+        self.why = verdict.reason
+        super().__init__(f"{what}: {self.why} (code {self.code})" if what else self.why)
+
+
+def lib():
+    """The loaded libexl3_mi355x.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m plugins_amd.build` "
+                               "(the EXL3 path has no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(v: Verdict, what: str = "") -> None:
+    if v.code != OK:
+        raise Exl3Error(v, what)
+
+
+# ------------------------------------------------------------ torch glue
+
+def _torch():
+    import torch
+    return torch
+
+
+def dtype_of(t) -> int:
+    torch = _torch()
+    table = {torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.float32: DT_F32,
+             torch.int16: DT_I16, torch.int32: DT_I32, torch.uint8: DT_U8, torch.int64: DT_I64,
+             torch.float64: DT_F64, torch.bool: DT_BOOL}
+    for name, code in (("uint16", DT_U16), ("uint32", DT_U32)):
+        if hasattr(torch, name):
+            table[getattr(torch, name)] = code
+    if t.dtype not in table:
+        raise TypeError(f"no ABI dtype for {t.dtype}")
+    return table[t.dtype]
+
+
+def array(t, dtype: int | None = None) -> Array:
+    """An Array descriptor over a contiguous device tensor (None: empty)."""
+    a = Array()
+    if t is None:
+        return a
+    if not t.is_contiguous():
+        raise ValueError("the ABI takes dense row-major arrays")
+    if t.dim() > MAX_DIMS:
+        raise ValueError("too many dims")
+    a.data = t.data_ptr()
+    a.dtype = dtype_of(t) if dtype is None else dtype
+    a.ndim = t.dim()
+    for i, s in enumerate(t.shape):
+        a.shape[i] = s
+    return a
+
+
+def stream_handle(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+# --------------------------------------------------------- table entries
+
+def claims(block_json: str, config_json: str = "{}") -> int:
+    return int(lib().exl3_claims(Str.of(block_json), Str.of(config_json)))
+
+
+def validate(block_json: str, config_json: str = "{}", dir: PackDir | None = None) -> Verdict:
+    return lib().exl3_validate(Str.of(block_json), Str.of(config_json),
+                               ctypes.byref(dir) if dir is not None else None)
+
+
+def bill(block_json: str, model_dir: str, stored: int) -> int:
+    return int(lib().exl3_bill(Str.of(block_json), Str.of(model_dir), stored))
+
+
+def quant_table() -> QuantTable:
+    return lib().exl3_quant_table_get().contents
+
+
+def version() -> str:
+    return lib().exl3_version().decode()
+
+
+class DictSource:
+    """A weight source over host arrays (numpy) keyed by tensor name: the
+    reference's `Source` (`ctx.source.tensor(name)`) for tests and tools."""
+
+    _DT = {"float16": DT_F16, "int16": DT_I16, "uint16": DT_U16, "float32": DT_F32,
+           "bfloat16": DT_BF16, "int32": DT_I32, "uint32": DT_U32}
+
+    def __init__(self, tensors: dict):
+        import numpy as np
+        self.tensors = {k: np.ascontiguousarray(v) for k, v in tensors.items()}
+        self._fn = TENSOR_FN(self._lookup)
+        self.struct = Source(None, self._fn)
+
+    def _lookup(self, _self, name: Str, out) -> int:
+        key = ctypes.string_at(name.ptr, name.len).decode()
+        a = self.tensors.get(key)
+        if a is None:
+            return 0
+        t = out.contents
+        t.data = a.ctypes.data
+        t.dtype = self._DT[str(a.dtype)]
+        t.ndim = a.ndim
+        for i, s in enumerate(a.shape):
+            t.shape[i] = s
+        return 1
+
+
+class Loader:
+    """open / load_tensor / load_bank / close over a weight source
+    (turboexl3_ds41/plugin.zig:52-185)."""
+
+    def __init__(self, block_json: str, source: DictSource, config_json: str = "{}", device: int = 0,
+                 stream=None):
+        self.source = source
+        self._keep = (Str.of(block_json), Str.of(config_json))
+        self.ctx = LoadCtx()
+        self.ctx.size = ctypes.sizeof(LoadCtx)
+        self.ctx.device = device
+        self.ctx.block_json = self._keep[0]
+        self.ctx.config_json = self._keep[1]
+        self.ctx.source = ctypes.pointer(source.struct)
+        self.ctx.stream = stream_handle(stream) if stream is not None else None
+        self.opened = lib().exl3_open(ctypes.byref(self.ctx))
+
+    def load_tensor(self, name: str, in_dim: int = 0) -> tuple[Verdict, Weight]:
+        w = Weight()
+        v = lib().exl3_load_tensor(ctypes.byref(self.ctx), Str.of(name), in_dim, ctypes.byref(w))
+        return v, w
+
+    def load_bank(self, name: str, in_dim: int = 0) -> tuple[Verdict, Weight]:
+        w = Weight()
+        v = lib().exl3_load_bank(ctypes.byref(self.ctx), Str.of(name), in_dim, ctypes.byref(w))
+        return v, w
+
+    def close(self) -> None:
+        lib().exl3_close(ctypes.byref(self.ctx))
+
+
+def release(w: Weight) -> None:
+    lib().exl3_release(ctypes.byref(w))
+
+
+def wrap(trellis, suh, svh, codebook: str = "mul1", window: int = 16, device: int = 0) -> Weight:
+    """A Weight over device tensors the caller keeps alive (borrowed)."""
+    w = Weight()
+    block = json.dumps({"format": "exl3", "codebook": codebook, "window": window})
+    tdt = DT_U16 if str(trellis.dtype) in ("torch.int16", "torch.uint16") else dtype_of(trellis)
+    check(lib().exl3_weight_wrap(array(trellis, tdt), array(suh), array(svh), Str.of(block), device,
+                                 ctypes.byref(w)), "weight_wrap")
+    return w
+
+
+def _out_tensor(like, last: int, dtype=None):
+    torch = _torch()
+    return torch.empty(*like.shape[:-1], last, dtype=dtype or like.dtype, device=like.device)
+
+
+def matmul(w: Weight, x, out=None, stream=None):
+    """x @ W^T through the library (QuantTable.matmul).  `out` is written if
+    given, else allocated with torch (the library never owns it here)."""
+    out_f = w.biases.shape[w.biases.ndim - 1]
+    y = out if out is not None else _out_tensor(x, out_f)
+    a = array(y)
+    check(lib().exl3_matmul(ctypes.byref(w), array(x), stream_handle(stream), ctypes.byref(a)),
+          "matmul")
+    return y
+
+
+def moe(bank: Weight, x, lhs=None, rhs=None, sorted_: bool = False, stream=None) -> Verdict:
+    a = Array()
+    return lib().exl3_moe(ctypes.byref(bank), array(x), array(lhs), array(rhs), sorted_,
+                          stream_handle(stream), ctypes.byref(a))
+
+
+def swiglu(gate: Weight, up: Weight, down: Weight, x, inds=None, scores=None, limit: int = 0,
+           verify_rows: bool = False, out=None, stream=None):
+    """Routed (or, with inds None, dense) SwiGLU experts (QuantTable.swiglu)."""
+    y = out if out is not None else _torch().empty_like(x)
+    opts = SwigluOpts(ctypes.sizeof(SwigluOpts), int(limit), bool(verify_rows))
+    a = array(y)
+    check(lib().exl3_swiglu(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), array(x),
+                            array(inds), array(scores), ctypes.byref(opts), stream_handle(stream),
+                            ctypes.byref(a)), "swiglu")
+    return y
+
+
+def decode_matrix(w: Weight, expert: int = 0, stream=None):
+    torch = _torch()
+    in_f = w.scales.shape[w.scales.ndim - 1]
+    out_f = w.biases.shape[w.biases.ndim - 1]
+    dev = torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(in_f, out_f, dtype=torch.float16, device=dev)
+    check(lib().exl3_decode_matrix(ctypes.byref(w), expert, array(out), stream_handle(stream)),
+          "decode_matrix")
+    return out
+
+
+def prepare(w: Weight, x, stream=None):
+    torch = _torch()
+    xp = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    check(lib().exl3_prepare(ctypes.byref(w), array(x), array(xp), stream_handle(stream)), "prepare")
+    return xp
+
+
+def finish(w: Weight, z, dtype=None, stream=None):
+    torch = _torch()
+    y = torch.empty(z.shape, dtype=dtype or torch.float16, device=z.device)
+    check(lib().exl3_finish(ctypes.byref(w), array(z), array(y), stream_handle(stream)), "finish")
+    return y
+
+
+def inner(w: Weight, xp, stream=None):
+    torch = _torch()
+    out_f = w.biases.shape[w.biases.ndim - 1]
+    z = torch.empty(*xp.shape[:-1], out_f, dtype=torch.float16, device=xp.device)
+    check(lib().exl3_inner(ctypes.byref(w), array(xp), array(z), stream_handle(stream)), "inner")
+    return z
+
+
+def matmul_path(w: Weight, rows: int) -> str:
+    return lib().exl3_matmul_path(ctypes.byref(w), rows).decode()
+
+
+class Linear:
+    """One EXL3 linear on device tensors: trellis [in/16, out/16, n] (int16 or
+    uint16 bits), suh f16 [in], svh f16 [out].  Keeps the tensors alive for the
+    borrowed Weight."""
+
+    def __init__(self, trellis, suh, svh, codebook: str = "mul1", window: int = 16):
+        self.tensors = (trellis, suh, svh)
+        self.weight = wrap(trellis, suh, svh, codebook, window, trellis.device.index or 0)
+        self.in_features = suh.shape[-1]
+        self.out_features = svh.shape[-1]
+
+    def __call__(self, x, out=None, stream=None):
+        return matmul(self.weight, x, out=out, stream=stream)
+
+    def __del__(self):
+        try:
+            if self.weight.priv:
+                release(self.weight)
+        except Exception:
+            pass

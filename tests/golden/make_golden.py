@@ -12,7 +12,12 @@ What it copies, as data only (no reference code is imported or run):
     f16 row-major decode), read by turboexl3_ds41/src/frac_test.zig:23-44;
   * the known-answer values written in the reference's tests:
     decodeMul1 (sushi_ds41/src/sushi/exl3/expert_exl3.zig:699-704) and the
-    bitEnd tables (expert_exl3.zig:661-697).
+    bitEnd tables (expert_exl3.zig:661-697);
+  * into reference_configs.json, the quantization blocks of the reference's
+    pack-config fixtures that its claims/validate tests read
+    (turboexl3_ds41/tests/fixtures/config.json via config.zig:67-82;
+    turboexl3_qwen38/tests/fixtures/k{2,3,4,5}.json via config.zig:108-190):
+    model_type, the EXL3 blocks and the top-k, nothing else.
 """
 from __future__ import annotations
 
@@ -60,6 +65,29 @@ def main() -> None:
     with open(os.path.join(HERE, "reference_golden.json"), "w") as f:
         json.dump(out, f, separators=(",", ":"))
     print("wrote", os.path.join(HERE, "reference_golden.json"), len(tiles), "frac tiles")
+
+    ds = json.load(open(os.path.join(REF, "turboexl3_ds41/tests/fixtures/config.json")))
+    configs = {
+        "what": "quantization blocks of the reference's pack-config fixtures (tests/golden/make_golden.py)",
+        "ds41": {
+            "source": "turboexl3_ds41/tests/fixtures/config.json",
+            "model_type": ds["model_type"],
+            "quantization_config": ds["quantization_config"],
+            "num_experts_per_tok": ds.get("text_config", {}).get("num_experts_per_tok"),
+        },
+    }
+    for k in ("k2", "k3", "k4", "k5"):
+        d = json.load(open(os.path.join(REF, f"turboexl3_qwen38/tests/fixtures/{k}.json")))
+        configs[k] = {
+            "source": f"turboexl3_qwen38/tests/fixtures/{k}.json",
+            "model_type": d["model_type"],
+            "trunk_quant": d["trunk_quant"],
+            "expert_quant": d["expert_quant"],
+            "num_experts_per_tok": d.get("text_config", {}).get("num_experts_per_tok"),
+        }
+    with open(os.path.join(HERE, "reference_configs.json"), "w") as f:
+        json.dump(configs, f, indent=1)
+    print("wrote", os.path.join(HERE, "reference_configs.json"))
 
 
 if __name__ == "__main__":

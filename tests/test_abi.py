@@ -1,0 +1,132 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol
+include/exl3_mi355x.h declares, and its host-side entries (claims, validate,
+bill, the table) behave as the reference's do on the reference's own
+fixtures (turboexl3_ds41/config.zig:69-82, turboexl3_qwen38/config.zig:
+135-190; paths relative to /root/reference/plugins/)."""
+import ctypes
+import json
+import os
+import re
+
+import pytest
+
+from plugins_amd import exl3 as X
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CONFIGS = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_configs.json")))
+
+
+def test_header_symbols_are_exported_and_bound():
+    text = open(os.path.join(ROOT, "include", "exl3_mi355x.h")).read()
+    declared = set(re.findall(r"\b(exl3_[a-z_0-9]+)\s*\(", text))
+    declared -= {"exl3_str", "exl3_verdict", "exl3_claim"}
+    L = X.lib()
+    for name in sorted(declared):
+        assert hasattr(L, name), name
+    assert declared == set(X.SIGNATURES), declared ^ set(X.SIGNATURES)
+
+
+def test_quant_table_fields():
+    t = X.quant_table()
+    assert t.size == ctypes.sizeof(X.QuantTable)
+    assert t.version == 1
+    assert ctypes.string_at(t.name.ptr, t.name.len) == b"turboexl3_mi355x"
+    for f in ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank", "release",
+              "matmul", "moe", "swiglu"):
+        assert getattr(t, f), f
+    # the table's pointers are the flat symbols
+    assert t.matmul == ctypes.cast(X.lib().exl3_matmul, ctypes.c_void_p).value
+
+
+def _ds41_block():
+    return json.dumps(CONFIGS["ds41"]["quantization_config"])
+
+
+def _ds41_config():
+    c = CONFIGS["ds41"]
+    return json.dumps({"model_type": c["model_type"], "quantization_config": c["quantization_config"],
+                       "text_config": {"num_experts_per_tok": c["num_experts_per_tok"]}})
+
+
+def test_claims_exl3_blocks_by_marker():
+    # ds41's fixture block (quant_method exl3) and the qwen38 packs' blocks (format exl3)
+    assert X.claims(_ds41_block(), _ds41_config()) == X.CLAIM_BY_MARKER
+    for k in ("k2", "k3", "k4", "k5"):
+        assert X.claims(json.dumps(CONFIGS[k]["trunk_quant"])) == X.CLAIM_BY_MARKER
+        assert X.claims(json.dumps(CONFIGS[k]["expert_quant"])) == X.CLAIM_BY_MARKER
+
+
+def test_claims_nothing_else():
+    # turboexl3_ds41/config.zig:72-74 and turboexl3_qwen38/config.zig:141-147
+    for block in ('{"quant_method":"fp8"}', "{", "[]", "7", "", '{"format":"gptq"}', "null"):
+        assert X.claims(block, _ds41_config()) == X.CLAIM_NO, block
+
+
+def test_validate_admits_the_fixture_packs():
+    assert X.validate(_ds41_block(), _ds41_config()).is_ok()
+    for k in ("k2", "k3", "k4", "k5"):
+        cfg = json.dumps({"text_config": {"num_experts_per_tok": CONFIGS[k]["num_experts_per_tok"]}})
+        assert X.validate(json.dumps(CONFIGS[k]["trunk_quant"]), cfg).is_ok(), k
+        assert X.validate(json.dumps(CONFIGS[k]["expert_quant"]), cfg).is_ok(), k
+
+
+@pytest.mark.parametrize("edit,why", [
+    ({"codebook": "3inst"}, "Exl3CodebookUnsupported"),   # turboexl3_qwen38/config.zig:171
+    ({"codebook": 7}, "Exl3CodebookUnsupported"),
+    ({"window": 20}, "Exl3WindowUnsupported"),            # :172
+    ({"window": 7}, "Exl3WindowUnsupported"),
+    ({"window": 12.5}, "Exl3WindowUnsupported"),
+    ({"format": "gptq"}, "NotExl3"),                      # :173
+    ({"k": 9.25}, "Exl3RateUnsupported"),                 # :174
+    ({"k": 0.5}, "Exl3RateUnsupported"),
+    ({"k": 1.0625}, "Exl3RateUnsupported"),               # 17 halfwords: odd
+    ({"k": "4"}, "Exl3RateUnsupported"),
+])
+def test_validate_refuses_by_name(edit, why):
+    block = dict(CONFIGS["k4"]["expert_quant"])
+    block.update(edit)
+    v = X.validate(json.dumps(block))
+    assert v.code == X.UNSUPPORTED
+    assert v.reason == "turboexl3_mi355x: " + why
+
+
+def test_validate_rates_every_even_halfword_count():
+    for n in range(16, 129):
+        v = X.validate(json.dumps({"format": "exl3", "codebook": "mcg", "k": n / 16}))
+        assert v.is_ok() == (n % 2 == 0), n
+
+
+def test_validate_refuses_topk_beyond_the_reduce_bank():
+    # turboexl3_qwen38/config.zig:81-83 (max_topk = 32)
+    block = json.dumps(CONFIGS["k4"]["expert_quant"])
+    assert X.validate(block, json.dumps({"text_config": {"num_experts_per_tok": 32}})).is_ok()
+    v = X.validate(block, json.dumps({"text_config": {"num_experts_per_tok": 33}}))
+    assert v.reason == "turboexl3_mi355x: Exl3TopKExceedsReduceBank"
+    v = X.validate(block, json.dumps({"num_experts_per_tok": 40}))
+    assert v.reason == "turboexl3_mi355x: Exl3TopKExceedsReduceBank"
+
+
+def test_bill_is_the_stored_bytes():
+    # turboexl3_ds41/config.zig:56-61: resident as the pack stores it
+    for stored in (0, 1, 8 << 20, 3 << 40):
+        assert X.bill(_ds41_block(), "/packs/x", stored) == stored
+
+
+def test_moe_entry_refuses_like_the_reference():
+    # turboexl3_ds41/plugin.zig:263-265
+    v = X.lib().exl3_moe(None, X.Array(), X.Array(), X.Array(), False, None, None)
+    assert v.code == X.UNSUPPORTED and b"swiglu" in v.why
+
+
+def test_matmul_refuses_without_a_weight():
+    v = X.lib().exl3_matmul(None, X.Array(), None, None)
+    assert v.code == X.FAILED
+
+
+def test_json_reader_edge_cases():
+    # escapes, nesting and trailing garbage go through the C++ reader
+    assert X.claims('{"quant_method":"ex\\u006c3"}') == X.CLAIM_BY_MARKER
+    assert X.claims('{"a":[1,2,{"b":null}],"format":"exl3"}') == X.CLAIM_BY_MARKER
+    assert X.claims('{"format":"exl3"} x') == X.CLAIM_NO
+    assert X.claims('{"format":"exl3",}') == X.CLAIM_NO
+    assert X.claims('[' * 300 + ']' * 300) == X.CLAIM_NO

@@ -1,0 +1,313 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Bars: decoded f16 tiles bit-exact; the prepare and
+finish rotations bit-exact (same f32 operation order); matmul outputs within
+1e-3 relative Frobenius error of an fp32-or-better CPU reference, plus the
+reference's per-element bar on the inner product
+(sushi_ds41/src/sushi/exl3/expert_exl3_kernels.zig:3402-3461: |err| <=
+(2^-11 + depth 2^-24) sum|w x|, relative to the exact dot of the same decoded
+weights; paths relative to /root/reference/plugins/).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from plugins_amd import exl3 as X  # noqa: E402
+from tests import _synth as S  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_golden.json")))
+DEV = "cuda:0"
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(DEV)
+
+
+def dev_f16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16) if a.dtype == np.uint16
+                            else np.ascontiguousarray(a, np.float16)).to(DEV)
+
+
+def host_u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def make(rng, in_f, out_f, n, codebook="mul1", window=16):
+    trellis, suh, svh = S.linear(rng, in_f, out_f, n)
+    lin = X.Linear(dev_u16(trellis), dev_f16(suh), dev_f16(svh), codebook, window)
+    return lin, trellis, suh, svh
+
+
+CB = {"mul1": O.CB_MUL1, "mcg": O.CB_MCG}
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("codebook", ["mul1", "mcg"])
+@pytest.mark.parametrize("n", [16, 32, 48, 64, 80, 96, 112, 128, 24, 40, 18, 50, 126])
+def test_decode_matrix_bit_exact(n, codebook):
+    rng = np.random.default_rng(1000 + n)
+    lin, trellis, _, _ = make(rng, 256, 384, n, codebook)
+    got = host_u16(X.decode_matrix(lin.weight))
+    want = O.reconstruct_inner(trellis, 256, 384, n, CB[codebook])
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("window", [8, 11, 15])
+@pytest.mark.parametrize("n", [32, 40, 64])
+def test_decode_matrix_windows(n, window):
+    rng = np.random.default_rng(77 + window)
+    for cb in ("mul1", "mcg"):
+        lin, trellis, _, _ = make(rng, 128, 128, n, cb, window)
+        got = host_u16(X.decode_matrix(lin.weight))
+        np.testing.assert_array_equal(got, O.reconstruct_inner(trellis, 128, 128, n, CB[cb], window))
+
+
+@pytest.mark.parametrize("name", ["gate_up", "down", "gate_up_k2", "down_k2"])
+def test_decode_matrix_reproduces_reference_golden_planes(name):
+    # turboexl3_ds41/src/exl3/kernels/exl3/manifest.json golden.planes
+    p = GOLD["planes"][name]
+    n = 16 * p["K"]
+    code = O.synth_plane(p["seed"], (p["in"] // 16) * (p["out"] // 16) * n)
+    t = dev_u16(code.reshape(p["in"] // 16, p["out"] // 16, n))
+    ones_in = torch.ones(p["in"], dtype=torch.float16, device=DEV)
+    ones_out = torch.ones(p["out"], dtype=torch.float16, device=DEV)
+    lin = X.Linear(t, ones_in, ones_out)
+    w = host_u16(X.decode_matrix(lin.weight))
+    assert hashlib.sha256(w.astype("<u2").tobytes()).hexdigest() == p["w_hat_sha256"]
+
+
+@pytest.mark.parametrize("n", [24, 32, 40, 48])
+def test_decode_matrix_reference_frac_tiles(n):
+    # turboexl3_ds41/src/frac_tiles.json: real pack tiles, row-major f16
+    tiles = [t for t in GOLD["frac_tiles"] if t["n"] == n][:8]
+    assert len(tiles) == 8
+    trellis = np.stack([np.array(t["words"], np.uint16) for t in tiles]).reshape(1, 8, n)
+    ones = torch.ones(128, dtype=torch.float16, device=DEV)
+    # a weight's input width is a multiple of 128: stack the tile row 8 times
+    stacked = np.concatenate([trellis] * 8, axis=0)  # [8, 8, n]: in = 128, out = 128
+    lin = X.Linear(dev_u16(stacked), ones, ones)
+    w = host_u16(X.decode_matrix(lin.weight))
+    for j, t in enumerate(tiles):
+        got = w[0:16, 16 * j:16 * j + 16].reshape(-1)
+        np.testing.assert_array_equal(got, np.array(t["expect"], np.uint16), err_msg=t["src"])
+
+
+# ------------------------------------------------------- prepare / finish
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_prepare_bit_exact(dtype):
+    rng = np.random.default_rng(3)
+    lin, _, suh, _ = make(rng, 512, 128, 64)
+    x32 = (rng.standard_normal((5, 512)) * 3).astype(np.float32)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    x = torch.from_numpy(x32).to(tdt)
+    xp = host_u16(X.prepare(lin.weight, x.to(DEV)))
+    want = O.prepare(x.float().numpy(), suh)
+    np.testing.assert_array_equal(xp, want)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_finish_bit_exact(dtype):
+    rng = np.random.default_rng(4)
+    lin, _, _, svh = make(rng, 128, 384, 64)
+    z = rng.standard_normal((3, 384)).astype(np.float16).view(np.uint16)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    y = X.finish(lin.weight, dev_f16(z), dtype=tdt).cpu()
+    want16 = torch.from_numpy(O.finish(z, svh).view(np.float16))
+    assert torch.equal(y, want16.to(tdt)), (y - want16.to(tdt)).abs().max()
+
+
+# ---------------------------------------------------------- inner product
+
+def _inner_bar(xp_bits, w_bits, z_bits):
+    """The reference's parity bar: per element against the exact f64 dot of
+    the same decoded weights, |err| <= (2^-11 + depth 2^-24) sum|w x|."""
+    xp = S.h2f(xp_bits).astype(np.float64)
+    W = S.h2f(w_bits).astype(np.float64)
+    exact = xp @ W
+    mag = np.abs(xp) @ np.abs(W)
+    depth = W.shape[0]
+    err = np.abs(S.h2f(z_bits).astype(np.float64) - exact)
+    return err <= (2.0 ** -11 + depth * 2.0 ** -24) * mag + 1e-30
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8, 9, 31, 130])
+@pytest.mark.parametrize("n", [32, 64, 96])
+def test_inner_against_oracle(rows, n):
+    rng = np.random.default_rng(rows * 131 + n)
+    in_f, out_f = 512, 384
+    lin, trellis, suh, _ = make(rng, in_f, out_f, n)
+    x = S.activations(rng, rows, in_f)
+    xp = O.prepare(x.astype(np.float32), suh)
+    z = host_u16(X.inner(lin.weight, dev_f16(xp)))
+    w = O.reconstruct_inner(trellis, in_f, out_f, n)
+    assert _inner_bar(xp, w, z).all()
+    zo = O.inner(trellis, xp, in_f, out_f, n)
+    assert S.rel_fro(S.h2f(z), S.h2f(zo)) < 1e-3
+
+
+@pytest.mark.parametrize("n", [16, 48, 80, 112, 128, 24, 40])
+@pytest.mark.parametrize("rows", [1, 6, 20])
+def test_inner_every_rate(n, rows):
+    rng = np.random.default_rng(9 * n + rows)
+    in_f, out_f = 384, 256
+    lin, trellis, suh, _ = make(rng, in_f, out_f, n)
+    xp = O.prepare(S.activations(rng, rows, in_f).astype(np.float32), suh)
+    z = host_u16(X.inner(lin.weight, dev_f16(xp)))
+    assert _inner_bar(xp, O.reconstruct_inner(trellis, in_f, out_f, n), z).all()
+
+
+def test_inner_mcg_window():
+    rng = np.random.default_rng(12)
+    lin, trellis, suh, _ = make(rng, 256, 256, 48, "mcg", 12)
+    for rows in (1, 4, 40):
+        xp = O.prepare(S.activations(rng, rows, 256).astype(np.float32), suh)
+        z = host_u16(X.inner(lin.weight, dev_f16(xp)))
+        assert _inner_bar(xp, O.reconstruct_inner(trellis, 256, 256, 48, O.CB_MCG, 12), z).all()
+
+
+# ----------------------------------------------------------------- matmul
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16, 200])
+@pytest.mark.parametrize("k", [2, 3, 4, 5, 6, 8])
+def test_matmul_against_fp64_reference(rows, k):
+    rng = np.random.default_rng(100 * k + rows)
+    in_f, out_f = 512, 256
+    lin, trellis, suh, svh = make(rng, in_f, out_f, 16 * k)
+    x = S.activations(rng, rows, in_f)
+    y = lin(dev_f16(x)).float().cpu().numpy()
+    Wt = S.public_weight(O.reconstruct_inner(trellis, in_f, out_f, 16 * k), suh, svh)
+    want = x.astype(np.float64) @ Wt
+    assert S.rel_fro(y, want) < 1e-3
+    yo = S.h2f(O.project(x.astype(np.float32), trellis, suh, svh, in_f, out_f, 16 * k))
+    assert S.rel_fro(y, yo) < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_matmul_dtypes_and_leading_dims(dtype):
+    rng = np.random.default_rng(5)
+    lin, trellis, suh, svh = make(rng, 256, 256, 64)
+    x = torch.from_numpy(rng.standard_normal((2, 3, 256)).astype(np.float32)).to(dtype)
+    y = lin(x.to(DEV))
+    assert y.shape == (2, 3, 256) and y.dtype == dtype
+    yo = O.project(x.float().numpy().reshape(6, 256), trellis, suh, svh, 256, 256, 64)
+    assert S.rel_fro(y.float().cpu().numpy().reshape(6, 256), S.h2f(yo)) < 1e-3
+
+
+def test_matmul_is_row_invariant():
+    # a row's output bytes do not depend on how many rows share the call
+    # within one kernel path (sushi_ds41/src/sushi/exl3/linear.zig:450-491)
+    rng = np.random.default_rng(6)
+    lin, *_ = make(rng, 512, 256, 64)
+    x = dev_f16(S.activations(rng, 8, 512))
+    full = lin(x)
+    for r in (1, 3, 5, 8):
+        assert torch.equal(lin(x[:r].contiguous()), full[:r])
+    xg = dev_f16(S.activations(rng, 300, 512))
+    big = lin(xg)
+    assert torch.equal(lin(xg[:129].contiguous()), big[:129])
+
+
+def test_matmul_qwen3_8b_shapes_k4():
+    # BASELINE configs 0-1 at full size (K=4, q/o, k/v, gate/up, down), one
+    # row per shape against the oracle's projection
+    rng = np.random.default_rng(2048)
+    for in_f, out_f in ((4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096)):
+        lin, trellis, suh, svh = make(rng, in_f, out_f, 64)
+        x = S.activations(rng, 2, in_f)
+        y = lin(dev_f16(x)).float().cpu().numpy()
+        yo = S.h2f(O.project(x.astype(np.float32), trellis, suh, svh, in_f, out_f, 64))
+        assert S.rel_fro(y, yo) < 1e-3, (in_f, out_f)
+
+
+def test_gemm_full_size_sampled_rows():
+    # prefill config: M=2048 rows through the GEMM; rows are independent, so
+    # a sample of them is checked against the oracle
+    rng = np.random.default_rng(4096)
+    in_f, out_f = 4096, 4096
+    lin, trellis, suh, svh = make(rng, in_f, out_f, 64)
+    x = S.activations(rng, 2048, in_f)
+    assert X.matmul_path(lin.weight, 2048) == "gemm"
+    y = lin(dev_f16(x)).float().cpu().numpy()
+    pick = np.array([0, 1, 127, 128, 1000, 2047])
+    yo = S.h2f(O.project(x[pick].astype(np.float32), trellis, suh, svh, in_f, out_f, 64))
+    assert S.rel_fro(y[pick], yo) < 1e-3
+
+
+# --------------------------------------------------------------- loading
+
+def test_load_tensor_from_a_source_and_refusals():
+    rng = np.random.default_rng(8)
+    trellis, suh, svh = S.linear(rng, 256, 128, 48)
+    src = X.DictSource({"m.q.trellis": trellis.view(np.int16), "m.q.suh": suh.view(np.float16),
+                        "m.q.svh": svh.view(np.float16),
+                        "m.bad.trellis": trellis.view(np.int16), "m.bad.suh": suh.view(np.float16),
+                        "m.bad.svh": svh[:64].view(np.float16)})
+    L = X.Loader('{"format":"exl3","codebook":"mul1"}', src)
+    assert L.opened.is_ok(), L.opened
+    v, w = L.load_tensor("m.q", 256)
+    assert v.is_ok(), v
+    assert w.w.dims() == (16, 8, 48) and w.scales.dims() == (256,) and w.biases.dims() == (128,)
+    x = S.activations(rng, 3, 256)
+    y = X.matmul(w, dev_f16(x)).float().cpu().numpy()
+    yo = S.h2f(O.project(x.astype(np.float32), trellis, suh, svh, 256, 128, 48))
+    assert S.rel_fro(y, yo) < 1e-3
+    v2, _ = L.load_tensor("m.q", 512)
+    assert v2.code == X.UNSUPPORTED and "expected input width" in v2.reason
+    v3, _ = L.load_tensor("m.bad")
+    assert v3.code == X.UNSUPPORTED
+    v4, _ = L.load_tensor("m.missing")
+    assert v4.code == X.FAILED and v4.reason == "MissingWeight"
+    X.release(w)
+    assert w.priv is None and w.w.data is None
+    L.close()
+
+
+# -------------------------------------------------------------------- MoE
+
+def _bank(rng, E, in_f, out_f, n):
+    t, u, v = S.linear(rng, in_f, out_f, n, experts=E)
+    return (t, u, v), X.wrap(dev_u16(t), dev_f16(u), dev_f16(v)), (dev_u16(t), dev_f16(u), dev_f16(v))
+
+
+@pytest.mark.parametrize("rows,limit", [(1, 0), (3, 0), (16, 0), (5, 10), (64, 0)])
+def test_swiglu_routed_against_oracle(rows, limit):
+    rng = np.random.default_rng(rows + 50 * limit)
+    E, hidden, inter, topk, n = 8, 256, 128, 3, 48
+    g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
+    u_np, u, u_keep = _bank(rng, E, hidden, inter, n)
+    d_np, d, d_keep = _bank(rng, E, inter, hidden, n)
+    x = (rng.standard_normal((rows, hidden)) * (20.0 if limit else 1.0)).astype(np.float16)
+    inds, scores = O.route_topk(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    y = X.swiglu(g, u, d, dev_f16(x).reshape(rows, 1, hidden),
+                 torch.from_numpy(inds).to(DEV).reshape(rows, 1, topk),
+                 torch.from_numpy(scores).to(DEV).reshape(rows, 1, topk), limit=limit)
+    want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n,
+                        limit=float(limit))
+    assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
+
+
+def test_swiglu_dense_shared_expert():
+    rng = np.random.default_rng(31)
+    hidden, inter, n = 256, 256, 64
+    tg, sg, vg = S.linear(rng, hidden, inter, n)
+    tu, su, vu = S.linear(rng, hidden, inter, n)
+    td, sd, vd = S.linear(rng, inter, hidden, n)
+    G = X.Linear(dev_u16(tg), dev_f16(sg), dev_f16(vg))
+    U = X.Linear(dev_u16(tu), dev_f16(su), dev_f16(vu))
+    D = X.Linear(dev_u16(td), dev_f16(sd), dev_f16(vd))
+    x = S.activations(rng, 4, hidden)
+    y = X.swiglu(G.weight, U.weight, D.weight, dev_f16(x)).float().cpu().numpy()
+    want = O.moe_swiglu(x.astype(np.float32), (tg[None], sg[None], vg[None]), (tu[None], su[None], vu[None]),
+                        (td[None], sd[None], vd[None]), np.zeros((4, 1), np.int32),
+                        np.ones((4, 1), np.float32), hidden, inter, n)
+    assert S.rel_fro(y, want) < 1e-3
