@@ -157,14 +157,19 @@ def main() -> int:
         for (name, i, o, lin), y in zip(lins, ys):
             lin(xs[i], out=y)
 
-    for _ in range(args.warmup):
-        step()
+    # Warm up on the stream the graph is captured on: the library keeps its
+    # scratch per stream and sizes it at the first call, outside the capture.
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        for _ in range(args.warmup):
+            step()
     torch.cuda.synchronize()
     run = step
     graph = None
     if not args.no_graph:
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+        with torch.cuda.graph(graph, stream=cap, capture_error_mode="thread_local"):
             step()
         for _ in range(2):
             graph.replay()

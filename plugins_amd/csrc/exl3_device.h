@@ -51,8 +51,18 @@ __device__ __forceinline__ T bits(F f) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)bits<_Float16>(h); }
-// f32 -> f16, round to nearest even (v_cvt_f16_f32 under the default mode).
-__device__ __forceinline__ uint16_t f2h(float f) { return bits<uint16_t>((_Float16)f); }
+// Materialises an f32 value in a VGPR so the operation that produced it is
+// not merged into a following conversion.  The backend otherwise turns
+// f16(a * b) into one v_fma_mixlo_f16, which rounds the exact product once;
+// the reference rounds the f32 product first and then converts, and the two
+// differ whenever the f32 product is an exact f16 tie.
+__device__ __forceinline__ float f32_value(float f) {
+  asm volatile("" : "+v"(f));
+  return f;
+}
+// f32 -> f16, round to nearest even (v_cvt_f16_f32 under the default mode),
+// of the f32 value as rounded (see f32_value).
+__device__ __forceinline__ uint16_t f2h(float f) { return bits<uint16_t>((_Float16)f32_value(f)); }
 __device__ __forceinline__ float bf2f(uint16_t b) { return bits<float>((uint32_t)b << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {
   uint32_t u = bits<uint32_t>(f);
