@@ -43,6 +43,9 @@ __device__ __forceinline__ void st_agent(float *p, float v) {
 __device__ __forceinline__ float ld_agent(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// s_waitcnt vmcnt(0): this wave's outstanding vector-memory operations,
+// stores included on gfx9-family parts, have completed.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // =================================================================== prepare
 
@@ -343,19 +346,24 @@ __device__ __forceinline__ bool gemv_splitk_last(const float *sums, float *zf, f
     __syncthreads();
     return true;
   }
+  // The partial sums and the ticket are agent-scope atomics (coherent across
+  // the XCDs' L2s on their own), so no fence is needed, only order: each
+  // wave waits for its stores to be acknowledged before the barrier, and the
+  // last workgroup's loads are issued after its ticket returned.  (A device
+  // fence here would write back and invalidate the L2 in every workgroup.)
   for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
     if (b < nrows) st_agent(partial + ((size_t)ks * ptotal + prow[b]) * out + col0 + col, sums[e]);
   }
-  __threadfence();
+  wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(ticket, 1u);
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == (uint32_t)ksplit - 1u) ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return false;
-  __threadfence();
   for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
     float s = 0.0f;
