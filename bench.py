@@ -7,14 +7,15 @@ HBM GB/s at bs=1" is quoted on): a decode pass at batch 1 over the linears of
 a 36-layer Qwen3-8B-shaped decoder (per layer q/o 4096->4096, k/v
 4096->1024, gate/up 4096->12288, down 12288->4096), EXL3 K=4 mul1 weights,
 uniform-random trellis words, suh +-1, svh f16(+-U[0.5,1.5]*0.02), f16
-N(0,1) activations.  One step = one matmul (prepare + decode GEMV + finish)
+N(0,1) activations.  One step = one matmul (one kernel: prepare + decode GEMV + finish)
 per linear, 252 linears, 3.47 GB of distinct packed weights (beyond the 256 MB
 Infinity Cache, so every step reads HBM).  The step is captured once into a
 HIP graph and replayed.
 
 `value` = packed-weight bytes per step * steps / timed seconds (GB/s).
-`roofline` = the dominant kernel (the K=4 batch-1 decode GEMV) measured with
-HIP event pairs around each launch, over every linear of the model:
+`roofline` = the dominant kernel (the K=4 decode GEMV, which is the whole
+matmul: prepare, GEMV and finish in one launch) measured with HIP event pairs
+around each launch, over every linear of the model:
 algorithmic bytes (in*out*K/8 per launch) / average launch duration, against
 the 8 TB/s HBM peak.  `cpu_baseline` = the CPU oracle's projection
 (prepare + decode + f32 dot + finish, the reference's CPU path restated in
@@ -185,30 +186,34 @@ def main() -> int:
     ms_per_step = el * 1e3 / args.steps
     value = step_bytes * args.steps / el / 1e9
 
-    # roofline leg: event pairs around each decode-GEMV launch (inner product
-    # only: prepared rows in, z out), every linear once per pass, 3 passes
+    # roofline leg: the matmul of each linear is one kernel launch (prepare,
+    # decode GEMV and finish fused); HIP event pairs around each launch, every
+    # linear of the model once per pass, 3 passes.  A sleep kernel first lets
+    # the host queue every launch ahead of the GPU, so the pairs time the
+    # kernels and not the host's submission.
     log("roofline leg")
-    xps = {i: X.prepare(lins[[l[1] for l in lins].index(i)][3].weight, xs[i]) for i in (4096, 12288)}
-    zs = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+    torch.cuda.synchronize()
     pairs = []
+    torch.cuda._sleep(int(2.4e9 * 0.05))
     for _ in range(3):
-        for (name, i, o, lin), z in zip(lins, zs):
+        for (name, i, o, lin), y in zip(lins, ys):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            X.check(X.lib().exl3_inner(X.ctypes.byref(lin.weight), X.array(xps[i]), X.array(z),
-                                       X.stream_handle()), "inner")
+            lin(xs[i], out=y)
             b.record()
-            pairs.append((packed_bytes(i, o), a, b))
+            pairs.append((name, packed_bytes(i, o), a, b))
     torch.cuda.synchronize()
-    kbytes = sum(p[0] for p in pairs)
-    kms = sum(a.elapsed_time(b) for _, a, b in pairs)
+    kbytes = sum(p[1] for p in pairs)
+    kms = sum(a.elapsed_time(b) for _, _, a, b in pairs)
     achieved = kbytes / (kms * 1e-3) / 1e9
     per_shape = {}
-    for (name, i, o, _), (nb, a, b) in zip(lins * 3, pairs):
-        d = per_shape.setdefault(name, [0, 0.0])
+    for name, nb, a, b in pairs:
+        d = per_shape.setdefault(name, [0, 0.0, 0])
         d[0] += nb
         d[1] += a.elapsed_time(b)
-    shapes = {k: round(v[0] / (v[1] * 1e-3) / 1e9, 1) for k, v in per_shape.items()}
+        d[2] += 1
+    shapes = {k: {"gbs": round(v[0] / (v[1] * 1e-3) / 1e9, 1), "us": round(v[1] * 1e3 / v[2], 2)}
+              for k, v in per_shape.items()}
 
     extra = {}
     try:
@@ -234,7 +239,7 @@ def main() -> int:
                    "linears_per_step": len(lins)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "exl3::gemv_kernel<4,1,0>", "launches": len(pairs),
+                     "kernel": "exl3::gemv_kernel<4,0> (mul1, K=4)", "launches": len(pairs),
                      "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -493,16 +493,35 @@ static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t las
   return ok();
 }
 
-// The inner product z (f16) or the finished y of rows prepared activations:
-// the GEMV for up to 8 rows, the GEMM above (rate with integer K; other rates
-// take the GEMV 8 rows at a time).
-static hipError_t inner_rows(const WeightPriv *pv, const uint16_t *trellis, const uint16_t *xp,
-                             const uint16_t *svh, void *y, int ydt, uint16_t *zout, int64_t rows,
+// One linear over `rows` rows: x raw (xdt, prepared in the kernels) or
+// already prepared (f16), to the finished y (ydt) or, with y null, the inner
+// product z (f16).  Up to 16 rows take the GEMV, one launch per 16 rows; wider
+// calls of an integer rate take the GEMM after a prepare launch (other rates
+// take the GEMV 16 rows at a time).
+static hipError_t run_linear(const exl3_weight *w, const WeightPriv *pv, const void *x, int xdt,
+                             bool prepared, void *y, int ydt, uint16_t *zout, int64_t rows,
                              StreamScratch *ss, hipStream_t s) {
   const int in = (int)pv->in, outf = (int)pv->out;
-  if (rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate())
-    return exl3::launch_gemm(trellis, pv->f, xp, svh, y, ydt, zout, (int)rows, in, outf, s);
+  const uint16_t *trellis = (const uint16_t *)w->w.data;
+  const uint16_t *suh = (const uint16_t *)w->scales.data;
+  const uint16_t *svh = (const uint16_t *)w->biases.data;
+  const size_t xsz = prepared ? 2 : (xdt == exl3::ACT_F32 ? 4 : 2);
   const size_t ysz = ydt == exl3::ACT_F32 ? 4 : 2;
+  if (rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate()) {
+    const uint16_t *xp = (const uint16_t *)x;
+    if (!prepared) {
+      hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, false);
+      if (e != hipSuccess) return e;
+      for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const int r = (int)std::min<int64_t>(65535, rows - r0);
+        e = exl3::launch_prepare((const char *)x + (size_t)r0 * in * xsz, xdt, suh,
+                                 (uint16_t *)ss->xp + (size_t)r0 * in, r, in, s);
+        if (e != hipSuccess) return e;
+      }
+      xp = (const uint16_t *)ss->xp;
+    }
+    return exl3::launch_gemm(trellis, pv->f, xp, svh, y, ydt, zout, (int)rows, in, outf, s);
+  }
   for (int64_t r0 = 0; r0 < rows; r0 += exl3::GEMV_ROWS_MAX) {
     const int r = (int)std::min<int64_t>(exl3::GEMV_ROWS_MAX, rows - r0);
     size_t pf = 0, tk = 0;
@@ -516,8 +535,8 @@ static hipError_t inner_rows(const WeightPriv *pv, const uint16_t *trellis, cons
     sc.partial_floats = ss->partial_bytes / sizeof(float);
     sc.ticket = (uint32_t *)ss->ticket;
     sc.tickets = ss->ticket_bytes / sizeof(uint32_t);
-    e = exl3::launch_gemv(trellis, pv->f, xp + (size_t)r0 * in, svh,
-                          y ? (char *)y + (size_t)r0 * outf * ysz : nullptr, ydt,
+    e = exl3::launch_gemv(trellis, pv->f, (const char *)x + (size_t)r0 * in * xsz, xdt, prepared,
+                          suh, svh, y ? (char *)y + (size_t)r0 * outf * ysz : nullptr, ydt,
                           zout ? zout + (size_t)r0 * outf : nullptr, r, in, outf, sc, s);
     if (e != hipSuccess) return e;
   }
@@ -540,18 +559,7 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(g_scratch_mu);
-  hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * pv->in * 2, s, false);
-  if (e != hipSuccess) return hip_failed(e);
-  uint16_t *xp = (uint16_t *)ss->xp;
-  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
-    const int r = (int)std::min<int64_t>(65535, rows - r0);
-    e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * pv->in * dt_size(x.dtype), xdt,
-                             (const uint16_t *)w->scales.data, xp + (size_t)r0 * pv->in, r,
-                             (int)pv->in, s);
-  }
-  if (e == hipSuccess)
-    e = inner_rows(pv, (const uint16_t *)w->w.data, xp, (const uint16_t *)w->biases.data, out->data,
-                   xdt, nullptr, rows, ss, s);
+  hipError_t e = run_linear(w, pv, x.data, xdt, false, out->data, xdt, nullptr, rows, ss, s);
   if (e != hipSuccess) return hip_failed(e);
   return ok();
 }
@@ -714,8 +722,8 @@ exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(g_scratch_mu);
-  hipError_t e = inner_rows(pv, (const uint16_t *)w->w.data, (const uint16_t *)xp.data, nullptr,
-                            nullptr, 0, (uint16_t *)z.data, rows, ss, s);
+  hipError_t e = run_linear(w, pv, xp.data, exl3::ACT_F16, true, nullptr, 0, (uint16_t *)z.data,
+                            rows, ss, s);
   return e == hipSuccess ? ok() : hip_failed(e);
 }
 

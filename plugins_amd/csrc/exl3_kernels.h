@@ -46,16 +46,19 @@ hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int yd
 hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in, int out,
                                 uint16_t *w, hipStream_t s);
 
-// The GEMV split: how many k-splits a (rows, in, out) GEMV takes.
+// The GEMV split: whole 128-input blocks per split (ksplit splits of tps
+// k-tile rows) for a GEMV over `groups` weights of (in, out).
+void gemv_plan(int in, int out, int groups, int *ksplit, int *tps);
 int gemv_ksplit(int in, int out, int groups);
-// Largest row count the GEMV path serves; wider calls take the GEMM.
-constexpr int GEMV_ROWS_MAX = 8;
+// Largest row count the GEMV path serves (the MFMA M); wider calls take the GEMM.
+constexpr int GEMV_ROWS_MAX = 16;
 
-// GEMV (rows <= GEMV_ROWS_MAX): y = finish(xp @ W) with z rounded to f16 after
-// the split-K sum; or, with y == nullptr, z f16 [rows, out] written to zout.
-hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const uint16_t *xp,
-                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
-                       int out, Scratch &sc, hipStream_t s);
+// GEMV (rows <= GEMV_ROWS_MAX), one launch: prepare (or, with prepared, xp
+// f16 rows as given), decode GEMV, split-K sum, z rounded to f16, finish into
+// y; or, with y == nullptr, z f16 [rows, out] written to zout.
+hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,
+                       bool prepared, const uint16_t *suh, const uint16_t *svh, void *y, int ydt,
+                       uint16_t *zout, int rows, int in, int out, Scratch &sc, hipStream_t s);
 // GEMM (any rows): the same contract through LDS-staged decode and MFMA.
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,

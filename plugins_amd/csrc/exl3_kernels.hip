@@ -223,153 +223,153 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 
 // ===================================================================== GEMV
 //
-// Workgroup = 4 waves on one 128-column group (8 output tiles) and one k-split
-// [ks*tps, (ks+1)*tps) of the k-tile rows; wave w takes rows ks*tps + w, +4,
-// ...  Lane = 8*tile + chunk: it loads its chunk's K dwords (one 16-byte load
-// at K=4; a wave's 64 loads are one contiguous 16K*64-bit span), receives the
-// history dword from the previous chunk's lane (ds_bpermute), decodes 32
-// weights in registers and accumulates columns a and a+8 of its tile with
-// v_dot2_f32_f16 against the rows' prepared activations.  Per-row f32
-// partial sums go to scratch; the last workgroup of a column group (a ticket
-// counter) sums the k-splits in order, rounds z to f16, and runs the finish
-// for its 128 columns, which are exactly one Hadamard block.
+// One launch per matmul of up to 16 rows.  A workgroup (4 waves) owns one
+// 128-column group (8 output tiles: one Hadamard block of the output) and one
+// k-split of tps k-tile rows (a multiple of 8, so the split is whole input
+// Hadamard blocks):
+//  1. it prepares its rows' input slice in LDS (x * suh, Hadamard-128, f16:
+//     the reference's prepare, run per split instead of as its own launch);
+//  2. wave w owns tiles 2w, 2w+1 of the group; lane l = 16g + 8t + c takes
+//     chunk c of tile 2w+t in k-tile row 4i+g of the split at step i, loads
+//     its K dwords (+ the history dword from lane l-1 of its tile through
+//     ds_bpermute), decodes its 32 codewords in registers into four 8 x f16
+//     MFMA B operands (column a / a+8, rows 0-7 / 8-15 of the tile), and
+//     v_mfma_f32_16x16x32_f16 sums them against the rows' activations (MFMA
+//     A operands from LDS) over the 4 k-tile rows of the step.  MFMA rows are
+//     the call's rows, so 1..16 rows cost the same decode;
+//  3. the per-row f32 sums go to scratch; the last workgroup of the column
+//     group (a ticket counter) adds the splits in split order, rounds z to
+//     f16 and runs the finish (Hadamard-128, * svh) on its 128 columns.
+// Codewords 32a..32a+31 of a tile are columns a and a+8 over all 16 rows, so
+// a lane's decoded weights are already whole B-operand columns.
 
 constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_ROWS = 16;
+constexpr int GEMV_TPS_MAX = 64;
 
-template <int K, int B, int CB>
-__device__ __forceinline__ void gemv_accum(const uint32_t *__restrict__ wchunk, size_t row_words,
-                                           const uint32_t *__restrict__ xp, const int (&xoff)[B],
-                                           int tk, int tk_end, uint32_t mask, int src_lane,
-                                           float (&acc)[B][2]) {
-  uint32_t nxt[K];
-  if (tk < tk_end) {
-    const uint32_t *p = wchunk + (size_t)tk * row_words;
-#pragma unroll
-    for (int i = 0; i < K; ++i) nxt[i] = p[i];
-  }
-  while (tk < tk_end) {
-    uint32_t wd[K + 1];
-#pragma unroll
-    for (int i = 0; i < K; ++i) wd[i + 1] = nxt[i];
-    const int tk_next = tk + 4;
-    if (tk_next < tk_end) {
-      const uint32_t *p = wchunk + (size_t)tk_next * row_words;
-#pragma unroll
-      for (int i = 0; i < K; ++i) nxt[i] = p[i];
+struct GemvRow {
+  int in_off;   // element offset of the row's activations
+  int out_off;  // element offset of the row's output
+  int prow;     // row of the split-K partial buffer
+  int pad;
+};
+
+struct GemvArgs {
+  const uint32_t *tw;   // trellis dwords (a bank's expert 0)
+  size_t expert_words;  // dwords per expert
+  const void *x;        // activations (ACT_*), or prepared rows (f16) when prepared
+  int xdt;
+  int prepared;
+  const uint16_t *suh;  // [E][in]; unused when prepared
+  const uint16_t *svh;  // [E][out]
+  void *y;              // finished output, or nullptr:
+  int ydt;
+  uint16_t *zout;       // the inner product z (f16) instead
+  float *partial;       // [ksplit][ptotal][out]
+  size_t ptotal;
+  int in_tiles, out_tiles, n, ksplit, tps;
+  uint32_t mask;
+};
+
+// Dynamic LDS of a GEMV workgroup: row table, prepared rows, z tile, and
+// (generic rate) a word stage per wave.
+__host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, bool generic) {
+  return 256 + (size_t)rows_alloc * (tps * 16 + 8) * 2 + (size_t)rows_alloc * 128 * 4 +
+         (generic ? 4 * 512 * 4 : 0);
+}
+
+// The rows' input slice [tk0*16, tk0*16 + ntk*16) prepared into xs (row
+// stride kr halfs): one wave per (row, 128-block).
+__device__ __forceinline__ void gemv_prepare(const GemvArgs &a, int expert, int nrows,
+                                             const GemvRow *rows, uint16_t *xs, int kr, int tk0,
+                                             int ntk, int wave, int lane) {
+  const int nb = ntk >> 3;
+  const int in = a.in_tiles * 16;
+  for (int it = wave; it < nrows * nb; it += 4) {
+    const int r = it / nb, blk = it - r * nb;
+    const int k = tk0 * 16 + blk * 128 + lane;
+    uint16_t *dst = xs + r * kr + blk * 128 + lane;
+    if (a.prepared) {
+      const uint16_t *src = (const uint16_t *)a.x + rows[r].in_off + k;
+      dst[0] = src[0];
+      dst[64] = src[64];
+      continue;
     }
-    wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane, (int)wd[K]);
-    uint32_t xv[B][8];
+    const uint16_t *su = a.suh + (size_t)expert * in + k;
+    float v0 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k, a.xdt))) * h2f(su[0]);
+    float v1 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k + 64, a.xdt))) * h2f(su[64]);
 #pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int d = 0; d < 8; ++d) xv[b][d] = xp[xoff[b] + tk * 8 + d];
-    static_for<16>([&](auto P) {
-      constexpr int p = decltype(P)::value;
-      const uint32_t wp = chunk_pair<K, CB, p>(wd, mask);
-      constexpr int xd = (p >> 2) + ((p & 1) ? 4 : 0);
-      constexpr int ch = (p & 2) ? 1 : 0;
-#pragma unroll
-      for (int b = 0; b < B; ++b)
-        acc[b][ch] = __builtin_amdgcn_fdot2(bits<h2_t>(wp), bits<h2_t>(xv[b][xd]), acc[b][ch], false);
-    });
-    tk = tk_next;
-  }
-}
-
-// Any even n: each wave stages its 8 tiles' dwords for one k-tile row in its
-// own LDS slice, then every lane extracts its chunk's codewords.
-template <int B, int CB>
-__device__ __forceinline__ void gemv_accum_generic(const uint32_t *__restrict__ tw8,
-                                                   size_t row_words, int n,
-                                                   const uint32_t *__restrict__ xp,
-                                                   const int (&xoff)[B], int tk, int tk_end,
-                                                   uint32_t mask, int lane, uint32_t *stage,
-                                                   float (&acc)[B][2]) {
-  const int nw = n >> 1;
-  const int tl = lane >> 3, c = lane & 7;
-  for (; tk < tk_end; tk += 4) {
-    const uint32_t *src = tw8 + (size_t)tk * row_words;
-    for (int i = lane; i < 8 * nw; i += 64) stage[i] = src[i];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t *mine = stage + tl * nw;
-    for (int p = 0; p < 16; ++p) {
-      const uint32_t t = 32u * c + 2u * p;
-      const uint32_t wp =
-          decode_pair<CB>(tile_window(mine, n, t), tile_window(mine, n, t + 1u), mask);
-      const int xd = (p >> 2) + ((p & 1) ? 4 : 0);
-      const int ch = (p & 2) ? 1 : 0;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const uint32_t xv = xp[xoff[b] + tk * 8 + xd];
-        acc[b][ch] = __builtin_amdgcn_fdot2(bits<h2_t>(wp), bits<h2_t>(xv), acc[b][ch], false);
-      }
+    for (int bit = 1; bit <= 32; bit <<= 1) {
+      const float p0 = __shfl_xor(v0, bit, 64);
+      const float p1 = __shfl_xor(v1, bit, 64);
+      const bool lower = (lane & bit) == 0;
+      v0 = lower ? v0 + p0 : p0 - v0;
+      v1 = lower ? v1 + p1 : p1 - v1;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float s0 = v0 + v1, s1 = v0 - v1;
+    dst[0] = f2h(s0 * HAD_SCALE);
+    dst[64] = f2h(s1 * HAD_SCALE);
   }
 }
 
-// Sums the 4 waves' per-lane accumulators into red[b][128] (LDS, wave 0's
-// region reused) in wave order.
-template <int B>
-__device__ __forceinline__ void gemv_wave_reduce(float (&acc)[B][2], float *red, int wave,
-                                                 int lane) {
-  const int col = (lane >> 3) * 16 + (lane & 7);
-#pragma unroll
-  for (int b = 0; b < B; ++b) {
-    red[(wave * B + b) * 128 + col] = acc[b][0];
-    red[(wave * B + b) * 128 + col + 8] = acc[b][1];
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
-    const float s = ((red[e] + red[B * 128 + e]) + red[2 * B * 128 + e]) + red[3 * B * 128 + e];
-    red[4 * B * 128 + e] = s;
-  }
-  __syncthreads();
+__device__ __forceinline__ h8_t frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u4_t v = {a, b, c, d};
+  return bits<h8_t>(v);
 }
 
-// Split-K hand-off: writes this workgroup's sums (row b of the call goes to
-// partial row prow[b] of ptotal), takes a ticket, and returns true in the
-// last workgroup of the column group, with z = f16(sum over splits, in split
-// order) in zf[b*128 + col] as f32.
-template <int B>
-__device__ __forceinline__ bool gemv_splitk_last(const float *sums, float *zf, float *partial,
-                                                 uint32_t *ticket, int ksplit, int ks, int nrows,
-                                                 const int (&prow)[B], size_t ptotal, size_t out,
-                                                 int col0) {
+// Four MFMAs of one step: columns a (acc0) and a+8 (acc1), rows 0-7 then 8-15.
+__device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_t ahi, f4_t &acc0,
+                                          f4_t &acc1) {
+  acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, frag(p[0], p[4], p[8], p[12]), acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, frag(p[2], p[6], p[10], p[14]), acc1, 0, 0, 0);
+  acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, frag(p[1], p[5], p[9], p[13]), acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, frag(p[3], p[7], p[11], p[15]), acc1, 0, 0, 0);
+}
+
+// Split-K hand-off over zf[nrows][128] (this workgroup's f32 sums): returns
+// true in the last workgroup of the column group with z = f16(sum over
+// splits, in split order) in zf.  The partial sums and the ticket are
+// agent-scope atomics, coherent across the XCDs' L2s on their own, so no
+// fence is needed, only order: each wave waits for its stores to be
+// acknowledged before the barrier, and the last workgroup loads after its
+// ticket returned.  (A device fence would write back and invalidate the L2
+// in every workgroup.)
+__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a, int nrows,
+                                                 const GemvRow *rows, uint32_t *ticket, int ks,
+                                                 size_t out, int col0) {
   __shared__ int s_last;
-  if (ksplit == 1) {
-    for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) zf[e] = h2f(f2h(sums[e]));
+  if (a.ksplit == 1) {
+    for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
     __syncthreads();
     return true;
   }
-  // The partial sums and the ticket are agent-scope atomics (coherent across
-  // the XCDs' L2s on their own), so no fence is needed, only order: each
-  // wave waits for its stores to be acknowledged before the barrier, and the
-  // last workgroup's loads are issued after its ticket returned.  (A device
-  // fence here would write back and invalidate the L2 in every workgroup.)
-  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+  const size_t stride = a.ptotal * out;
+  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    if (b < nrows) st_agent(partial + ((size_t)ks * ptotal + prow[b]) * out + col0 + col, sums[e]);
+    st_agent(a.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, zf[e]);
   }
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)ksplit - 1u) ? 1 : 0;
+    s_last = (prev == (uint32_t)a.ksplit - 1u) ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return false;
-  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
+    const float *p = a.partial + (size_t)rows[b].prow * out + col0 + col;
     float s = 0.0f;
-    if (b < nrows)
-      for (int k = 0; k < ksplit; ++k)
-        s = s + ld_agent(partial + ((size_t)k * ptotal + prow[b]) * out + col0 + col);
+    int k = 0;
+    for (; k + 8 <= a.ksplit; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = ld_agent(p + (size_t)(k + j) * stride);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s = s + v[j];
+    }
+    for (; k < a.ksplit; ++k) s = s + ld_agent(p + (size_t)k * stride);
     zf[e] = h2f(f2h(s));
   }
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -377,102 +377,153 @@ __device__ __forceinline__ bool gemv_splitk_last(const float *sums, float *zf, f
   return true;
 }
 
-// The finish over zf[B][128] (f32 holding f16 values): rotation, * 1/sqrt(128),
-// * svh, f16, output dtype at element offset yoff[b] + col; or z itself as
-// f16 into zout when y is null.
-template <int B>
-__device__ __forceinline__ void gemv_finish(float *zf, const uint16_t *__restrict__ svh, void *y,
-                                            int ydt, uint16_t *zout, int nrows,
-                                            const size_t (&yoff)[B], int col0) {
-  if (y == nullptr) {
-    for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+// The finish over zf[nrows][128] (f32 holding f16 values): rotation,
+// * 1/sqrt(128), * svh, f16, output dtype; or z itself when y is null.
+__device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, int expert, int nrows,
+                                            const GemvRow *rows, size_t out, int col0) {
+  if (a.y == nullptr) {
+    for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
       const int b = e >> 7, col = e & 127;
-      if (b < nrows) zout[yoff[b] + col0 + col] = f2h(zf[e]);
+      a.zout[(size_t)rows[b].out_off + col0 + col] = f2h(zf[e]);
     }
     return;
   }
-  had128_lds(zf, B, threadIdx.x, GEMV_THREADS);
-  for (int e = threadIdx.x; e < B * 128; e += GEMV_THREADS) {
+  had128_lds(zf, nrows, threadIdx.x, GEMV_THREADS);
+  const uint16_t *sv = a.svh + (size_t)expert * out + col0;
+  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    if (b < nrows) {
-      const float sc = zf[e] * HAD_SCALE;
-      store_out(y, yoff[b] + col0 + col, f2h(sc * h2f(svh[col0 + col])), ydt);
+    const float sc = zf[e] * HAD_SCALE;
+    store_out(a.y, (size_t)rows[b].out_off + col0 + col, f2h(sc * h2f(sv[col])), a.ydt);
+  }
+}
+
+// One workgroup of the GEMV: expert `expert` of the bank, nrows <= 16 rows
+// (table `rows` in LDS), column group cg, split ks.
+template <int K, int CB>
+__device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows,
+                                        const GemvRow *rows, uint32_t *ticket, int cg, int ks,
+                                        char *smem, int rows_alloc) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const size_t out = (size_t)a.out_tiles * 16;
+  const int tk0 = ks * a.tps;
+  const int ntk = min(a.tps, a.in_tiles - tk0);  // a multiple of 8
+  const int kr = a.tps * 16 + 8;
+  uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
+  float *zf = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);
+  const int nw = a.n >> 1;
+  const int g = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+  const size_t tn = (size_t)cg * 8 + 2 * wave + t;
+  const uint32_t *twe = a.tw + (size_t)expert * a.expert_words;
+  const int iters = ntk >> 2;
+
+  // weights of step 0 in flight while the rows are prepared
+  uint32_t nxt[K > 0 ? K : 1];
+  if constexpr (K > 0) {
+    const uint32_t *p0 = twe + ((size_t)(tk0 + g) * a.out_tiles + tn) * nw + c * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) nxt[i] = p0[i];
+  }
+  gemv_prepare(a, expert, nrows, rows, xs, kr, tk0, ntk, wave, lane);
+  __syncthreads();
+
+  const int arow = min(lane & 15, nrows - 1);
+  const uint16_t *xa = xs + arow * kr + g * 16;
+  f4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (K > 0) {
+    const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    for (int it = 0; it < iters; ++it) {
+      uint32_t wd[K + 1];
+#pragma unroll
+      for (int i = 0; i < K; ++i) wd[i + 1] = nxt[i];
+      if (it + 1 < iters) {
+        const uint32_t *pn =
+            twe + ((size_t)(tk0 + 4 * (it + 1) + g) * a.out_tiles + tn) * nw + c * K;
+#pragma unroll
+        for (int i = 0; i < K; ++i) nxt[i] = pn[i];
+      }
+      wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wd[K]);
+      const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
+      const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
+      uint32_t p[16];
+      static_for<16>([&](auto P) {
+        constexpr int q = decltype(P)::value;
+        p[q] = chunk_pair<K, CB, q>(wd, a.mask);
+      });
+      gemv_mfma(p, alo, ahi, acc0, acc1);
+    }
+  } else {
+    // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
+    uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
+                                                   (size_t)rows_alloc * 128 * 4) +
+                      wave * 512;
+    for (int it = 0; it < iters; ++it) {
+      for (int i = lane; i < 8 * nw; i += 64) {
+        const int seg = i / (2 * nw), off = i - seg * 2 * nw;
+        stage[i] = twe[((size_t)(tk0 + 4 * it + seg) * a.out_tiles + cg * 8 + 2 * wave) * nw + off];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t *mine = stage + (g * 2 + t) * nw;
+      const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
+      const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
+      uint32_t p[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint32_t cw = 32u * c + 2u * q;
+        p[q] = decode_pair<CB>(tile_window(mine, a.n, cw), tile_window(mine, a.n, cw + 1u), a.mask);
+      }
+      gemv_mfma(p, alo, ahi, acc0, acc1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
+
+  // C of a 16x16 MFMA: lane l holds rows 4(l/16)+i, column l%16.
+  const int col = (2 * wave + t) * 16 + c;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * g + i;
+    if (m < nrows) {
+      zf[m * 128 + col] = acc0[i];
+      zf[m * 128 + col + 8] = acc1[i];
+    }
+  }
+  __syncthreads();
+  if (!gemv_splitk_last(zf, a, nrows, rows, ticket, ks, out, cg * 128)) return;
+  gemv_finish(zf, a, expert, nrows, rows, out, cg * 128);
 }
 
-// The whole GEMV for one (column group, k-split) workgroup over nrows <= B
-// rows: activations at dword offsets xoff[b] of xp, partial rows prow[b] of
-// ptotal, outputs at element offsets yoff[b].
-template <int K, int B, int CB>
-__device__ __forceinline__ void gemv_body(const uint32_t *__restrict__ tw,
-                                          const uint32_t *__restrict__ xp,
-                                          const uint16_t *__restrict__ svh, void *y, int ydt,
-                                          uint16_t *zout, float *partial, uint32_t *ticket,
-                                          int nrows, const int (&xoff)[B], const int (&prow)[B],
-                                          size_t ptotal, const size_t (&yoff)[B], int in_tiles,
-                                          int out_tiles, int n, int ksplit, int tps, uint32_t mask,
-                                          int cg, int ks, float *red, uint32_t *stage) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tn = cg * 8 + (lane >> 3), c = lane & 7;
-  float acc[B][2];
-#pragma unroll
-  for (int b = 0; b < B; ++b) acc[b][0] = acc[b][1] = 0.0f;
-  const int tk0 = ks * tps + wave;
-  const int tk_end = min(in_tiles, (ks + 1) * tps);
-  const int nw = n >> 1;
-  const size_t row_words = (size_t)out_tiles * nw;  // dwords per k-tile row
-  if constexpr (K > 0) {
-    const int src = (((lane & ~7) | ((lane + 7) & 7)) << 2);
-    gemv_accum<K, B, CB>(tw + (size_t)tn * (8 * K) + c * K, row_words, xp, xoff, tk0, tk_end, mask,
-                         src, acc);
-  } else {
-    gemv_accum_generic<B, CB>(tw + (size_t)cg * 8 * nw, row_words, n, xp, xoff, tk0, tk_end, mask,
-                              lane, stage + wave * 512, acc);
+template <int K, int CB>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a, int rows,
+                                                            uint32_t *__restrict__ ticket) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
+  if (threadIdx.x < GEMV_ROWS) {
+    const int b = min((int)threadIdx.x, rows - 1);
+    ri[threadIdx.x] = GemvRow{b * a.in_tiles * 16, b * a.out_tiles * 16, b, 0};
   }
-  gemv_wave_reduce<B>(acc, red, wave, lane);
-  float *sums = red + 4 * B * 128;
-  float *zf = red;
-  const size_t out = (size_t)out_tiles * 16;
-  if (!gemv_splitk_last<B>(sums, zf, partial, ticket, ksplit, ks, nrows, prow, ptotal, out, cg * 128))
-    return;
-  gemv_finish<B>(zf, svh, y, ydt, zout, nrows, yoff, cg * 128);
+  __syncthreads();
+  gemv_wg<K, CB>(a, 0, rows, ri, ticket + blockIdx.x, blockIdx.x, blockIdx.y, smem + 256, rows);
 }
 
-template <int K, int B, int CB>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
-    const uint32_t *__restrict__ tw, const uint32_t *__restrict__ xp,
-    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    float *__restrict__ partial, uint32_t *__restrict__ ticket, int rows, int in_tiles,
-    int out_tiles, int n, int ksplit, int tps, uint32_t mask) {
-  __shared__ float red[5 * B * 128];
-  __shared__ uint32_t stage[K == 0 ? 4 * 512 : 1];
-  const int in2 = in_tiles * 8;
-  const size_t out = (size_t)out_tiles * 16;
-  int xoff[B], prow[B];
-  size_t yoff[B];
-#pragma unroll
-  for (int b = 0; b < B; ++b) {
-    const int r = b < rows ? b : 0;
-    xoff[b] = r * in2;
-    prow[b] = r;
-    yoff[b] = (size_t)r * out;
-  }
-  gemv_body<K, B, CB>(tw, xp, svh, y, ydt, zout, partial, ticket + blockIdx.x, rows, xoff, prow,
-                      (size_t)rows, yoff, in_tiles, out_tiles, n, ksplit, tps, mask, blockIdx.x,
-                      blockIdx.y, red, stage);
+// k-splits of a GEMV: whole input Hadamard blocks per split, at most
+// GEMV_TPS_MAX k-tile rows, ~1024 workgroups over `groups` column groups.
+void gemv_plan(int in, int out, int groups, int *ksplit, int *tps) {
+  const int nb = in / 128;
+  const int cgs = std::max(1, out / 128) * std::max(1, groups);
+  int ks = std::min(nb, std::max(1, (1024 + cgs - 1) / cgs));
+  int bps = std::min(GEMV_TPS_MAX / 8, (nb + ks - 1) / ks);  // blocks per split
+  *tps = 8 * bps;
+  *ksplit = (nb + bps - 1) / bps;
 }
 
 int gemv_ksplit(int in, int out, int groups) {
-  const int in_tiles = in / 16;
-  const int cgs = std::max(1, out / 128) * std::max(1, groups);
-  // Aim for ~4 workgroups (16 waves) per CU on 256 CUs, with at least 8
-  // k-tile rows (2 per wave) per split.
-  int ks = std::max(1, 1024 / cgs);
-  ks = std::min(ks, std::max(1, in_tiles / 8));
-  const int tps = (in_tiles + ks - 1) / ks;
-  return (in_tiles + tps - 1) / tps;
+  int ks, tps;
+  gemv_plan(in, out, groups, &ks, &tps);
+  return ks;
 }
 
 void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t *tickets) {
@@ -481,81 +532,64 @@ void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t
   *tickets = (size_t)out / 128;
 }
 
-template <int K, int B, int CB>
-static void gemv_go(dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
-                    const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
-                    uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
-                    int tps, uint32_t mask) {
-  hipLaunchKernelGGL((gemv_kernel<K, B, CB>), grid, dim3(GEMV_THREADS), 0, s, tw, xp, svh, y, ydt,
-                     zout, partial, ticket, rows, in_tiles, out_tiles, n, ksplit, tps, mask);
-}
-
-template <int B, int CB>
-static void gemv_rate(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
-                      const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
-                      uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
-                      int tps, uint32_t mask) {
+template <int CB>
+static void gemv_launch_cb(int kk, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &a,
+                           int rows, uint32_t *ticket) {
   switch (kk) {
-#define EXL3_GV(KK)                                                                               \
-  case KK:                                                                                        \
-    gemv_go<KK, B, CB>(grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles,      \
-                       out_tiles, n, ksplit, tps, mask);                                          \
+#define EXL3_GV(KK)                                                                          \
+  case KK:                                                                                   \
+    hipLaunchKernelGGL((gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), lds, s, a, rows,   \
+                       ticket);                                                              \
     break;
     EXL3_GV(1) EXL3_GV(2) EXL3_GV(3) EXL3_GV(4) EXL3_GV(5) EXL3_GV(6) EXL3_GV(7) EXL3_GV(8)
 #undef EXL3_GV
     default:
-      gemv_go<0, B, CB>(grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles,
-                        out_tiles, n, ksplit, tps, mask);
+      hipLaunchKernelGGL((gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), lds, s, a, rows, ticket);
   }
 }
 
-template <int CB>
-static void gemv_rows(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint32_t *xp,
-                      const uint16_t *svh, void *y, int ydt, uint16_t *zout, float *partial,
-                      uint32_t *ticket, int rows, int in_tiles, int out_tiles, int n, int ksplit,
-                      int tps, uint32_t mask) {
-#define EXL3_GR(BB)                                                                        \
-  gemv_rate<BB, CB>(kk, grid, s, tw, xp, svh, y, ydt, zout, partial, ticket, rows, in_tiles, \
-                    out_tiles, n, ksplit, tps, mask)
-  switch (rows) {
-    case 1: EXL3_GR(1); break;
-    case 2: EXL3_GR(2); break;
-    case 3: EXL3_GR(3); break;
-    case 4: EXL3_GR(4); break;
-    case 5: EXL3_GR(5); break;
-    case 6: EXL3_GR(6); break;
-    case 7: EXL3_GR(7); break;
-    default: EXL3_GR(8); break;
-  }
-#undef EXL3_GR
-}
-
-hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const uint16_t *xp,
-                       const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
-                       int out, Scratch &sc, hipStream_t s) {
+hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,
+                       bool prepared, const uint16_t *suh, const uint16_t *svh, void *y, int ydt,
+                       uint16_t *zout, int rows, int in, int out, Scratch &sc, hipStream_t s) {
   if (rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
   if (in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
   if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
   if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
-  const int in_tiles = in / 16, out_tiles = out / 16;
-  const int ksplit = gemv_ksplit(in, out, 1);
-  const int tps = (in_tiles + ksplit - 1) / ksplit;
-  if (ksplit > 65535 || out / 128 > 2147483647) return hipErrorInvalidValue;
+  if ((int64_t)rows * std::max(in, out) >= (int64_t)1 << 31) return hipErrorInvalidValue;
+  int ksplit, tps;
+  gemv_plan(in, out, 1, &ksplit, &tps);
+  if (ksplit > 65535) return hipErrorInvalidValue;
   if (ksplit > 1) {
     if (sc.partial == nullptr || sc.partial_floats < (size_t)ksplit * rows * out)
       return hipErrorInvalidValue;
     if (sc.ticket == nullptr || sc.tickets < (size_t)out / 128) return hipErrorInvalidValue;
   }
-  const dim3 grid(out / 128, ksplit);
+  GemvArgs a{};
+  a.tw = reinterpret_cast<const uint32_t *>(trellis);
+  a.expert_words = 0;
+  a.x = x;
+  a.xdt = xdt;
+  a.prepared = prepared ? 1 : 0;
+  a.suh = suh;
+  a.svh = svh;
+  a.y = y;
+  a.ydt = ydt;
+  a.zout = zout;
+  a.partial = sc.partial;
+  a.ptotal = (size_t)rows;
+  a.in_tiles = in / 16;
+  a.out_tiles = out / 16;
+  a.n = f.n;
+  a.ksplit = ksplit;
+  a.tps = tps;
+  a.mask = f.mask();
   const int kk = f.integer_rate() ? f.n / 16 : 0;
-  const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
-  const uint32_t *xw = reinterpret_cast<const uint32_t *>(xp);
+  const size_t lds = gemv_lds_bytes(rows, tps, kk == 0);
+  const dim3 grid(out / 128, ksplit);
   if (f.codebook == CB_MCG)
-    gemv_rows<CB_MCG>(kk, grid, s, tw, xw, svh, y, ydt, zout, sc.partial, sc.ticket, rows, in_tiles,
-                      out_tiles, f.n, ksplit, tps, f.mask());
+    gemv_launch_cb<CB_MCG>(kk, grid, lds, s, a, rows, sc.ticket);
   else
-    gemv_rows<CB_MUL1>(kk, grid, s, tw, xw, svh, y, ydt, zout, sc.partial, sc.ticket, rows,
-                       in_tiles, out_tiles, f.n, ksplit, tps, f.mask());
+    gemv_launch_cb<CB_MUL1>(kk, grid, lds, s, a, rows, sc.ticket);
   return hipGetLastError();
 }
 
@@ -749,16 +783,16 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
 //   1. route: one workgroup counts the (row, k) slots per expert, orders the
 //      slots by expert (within an expert in any order: every slot's
 //      arithmetic is independent of its position) and emits work items of
-//      up to 8 slots of one expert;
-//   2. prepare: per slot, x[row] * suh_gate[e] and x[row] * suh_up[e] rotated;
-//   3. grouped GEMV (gate and up in one launch): each work item is a GEMV over
-//      its expert's packed weights for its slots, split-K with the fused
-//      finish, giving g and u (f16) per slot;
-//   4. mid: h = silu(g) * u in f32 (limit > 0: g <= limit, |u| <= limit,
+//      up to 16 slots of one expert;
+//   2. grouped GEMV, gate and up in one launch: each work item is the GEMV
+//      workgroup above over its expert's packed weights for its slots, the
+//      prepare (x[row] * suh[e]) fused, split-K with the fused finish,
+//      giving g and u (f16) per slot;
+//   3. mid: h = silu(g) * u in f32 (limit > 0: g <= limit, |u| <= limit,
 //      turboexl3_ds41/src/exl3/kernels/exl3/q3_exl3_prep_gu_epi.metal:47-56),
 //      then the down projection's prepare with suh_down[e];
-//   5. grouped GEMV down, finished per slot (f16);
-//   6. combine: y[row] = sum_k score[row, k] * d[slot(row, k)] in f32, in k
+//   4. grouped GEMV down on the prepared rows, finished per slot (f16);
+//   5. combine: y[row] = sum_k score[row, k] * d[slot(row, k)] in f32, in k
 //      order, then the output dtype.
 
 struct MoeItem {
@@ -766,7 +800,7 @@ struct MoeItem {
 };
 
 constexpr int MOE_ROUTE_THREADS = 1024;
-constexpr int MOE_ITEM_ROWS = 8;
+constexpr int MOE_ITEM_ROWS = GEMV_ROWS;
 
 // Exclusive prefix sum over the 1024 threads of a block; *total gets the sum.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp,
@@ -829,39 +863,6 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(
   if (t == 0) *n_items = total;
 }
 
-// Per slot s (row s / topk, expert inds[s]): the gate and up prepares.
-__global__ __launch_bounds__(64) void moe_prepare2_kernel(
-    const void *__restrict__ x, int xdt, const uint32_t *__restrict__ inds, int topk, int experts,
-    const uint16_t *__restrict__ suh_g, const uint16_t *__restrict__ suh_u,
-    uint16_t *__restrict__ xg, uint16_t *__restrict__ xu, int hidden) {
-  const int lane = threadIdx.x;
-  const size_t slot = blockIdx.y;
-  const uint32_t e = inds ? inds[slot] : 0u;
-  if (e >= (uint32_t)experts) return;
-  const size_t row = slot / topk;
-  const int i0 = blockIdx.x * 128 + lane;
-  const float x0 = h2f(f2h(load_act(x, row * hidden + i0, xdt)));
-  const float x1 = h2f(f2h(load_act(x, row * hidden + i0 + 64, xdt)));
-#pragma unroll
-  for (int which = 0; which < 2; ++which) {
-    const uint16_t *su = (which ? suh_u : suh_g) + (size_t)e * hidden;
-    float v0 = x0 * h2f(su[i0]);
-    float v1 = x1 * h2f(su[i0 + 64]);
-#pragma unroll
-    for (int bit = 1; bit <= 32; bit <<= 1) {
-      const float p0 = __shfl_xor(v0, bit, 64);
-      const float p1 = __shfl_xor(v1, bit, 64);
-      const bool lower = (lane & bit) == 0;
-      v0 = lower ? v0 + p0 : p0 - v0;
-      v1 = lower ? v1 + p1 : p1 - v1;
-    }
-    const float a = v0 + v1, b = v0 - v1;
-    uint16_t *dst = (which ? xu : xg) + slot * hidden;
-    dst[i0] = f2h(a * HAD_SCALE);
-    dst[i0 + 64] = f2h(b * HAD_SCALE);
-  }
-}
-
 // h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e].
 __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u,
@@ -884,7 +885,7 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
       uv = uv > -limit ? uv : -limit;
       uv = uv < limit ? uv : limit;
     }
-    const float h = (gv / (1.0f + expf(-gv))) * uv;
+    const float h = f32_value(gv / (1.0f + expf(-gv))) * uv;
     v[j] = h2f(f2h(h)) * h2f(suh_d[(size_t)e * inter + i]);
   }
 #pragma unroll
@@ -900,61 +901,29 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
   xd[slot * inter + i0 + 64] = f2h(b * HAD_SCALE);
 }
 
-// Grouped GEMV: blockIdx.z = item * nsel + which; each item is up to 8 slots
-// of one expert (slot ids sorted[start .. start+count)).
-struct MoeGemvSide {
-  const uint32_t *tw;   // bank trellis, dwords
-  const uint16_t *svh;  // [E][out]
-  const uint32_t *xp;   // [slots][in] prepared, as dwords
-  uint16_t *y;          // [slots][out] f16
-  float *partial;       // [ksplit][slots][out]
-  uint32_t *ticket;     // [max_items][out/128]
-};
-
-template <int K, int B, int CB>
-__device__ __forceinline__ void moe_gemv_item(const MoeGemvSide &sd, const uint32_t *sorted,
-                                              const MoeItem &it, int slots, int in_tiles,
-                                              int out_tiles, int n, int ksplit, int tps,
-                                              uint32_t mask, int item, float *red,
-                                              uint32_t *stage) {
-  const int in2 = in_tiles * 8;
-  const size_t out = (size_t)out_tiles * 16;
-  int xoff[B], prow[B];
-  size_t yoff[B];
-  const int nrows = (int)it.count;
-#pragma unroll
-  for (int b = 0; b < B; ++b) {
-    const int slot = (int)sorted[it.start + (b < nrows ? b : 0)];
-    xoff[b] = slot * in2;
-    prow[b] = slot;
-    yoff[b] = (size_t)slot * out;
-  }
-  const size_t per_expert = (size_t)in_tiles * out_tiles * (n >> 1);
-  gemv_body<K, B, CB>(sd.tw + per_expert * it.expert, sd.xp, sd.svh + out * it.expert, sd.y,
-                      OUT_F16, nullptr, sd.partial, sd.ticket + (size_t)item * (out_tiles / 8) + blockIdx.x,
-                      nrows, xoff, prow, (size_t)slots, yoff, in_tiles, out_tiles, n, ksplit, tps,
-                      mask, blockIdx.x, blockIdx.y, red, stage);
-}
-
+// Grouped GEMV: blockIdx.z = item * nsel + which.  Raw inputs are rows
+// slot / topk of x; prepared inputs are rows slot.
 template <int K, int CB>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
-    MoeGemvSide s0, MoeGemvSide s1, int nsel, const uint32_t *__restrict__ sorted,
-    const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, int slots,
-    int in_tiles, int out_tiles, int n, int ksplit, int tps, uint32_t mask) {
-  __shared__ float red[5 * MOE_ITEM_ROWS * 128];
-  __shared__ uint32_t stage[K == 0 ? 4 * 512 : 1];
-  const int item = blockIdx.z / nsel, which = blockIdx.z % nsel;
+    GemvArgs s0, GemvArgs s1, int nsel, const uint32_t *__restrict__ sorted,
+    const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, int topk,
+    uint32_t *__restrict__ t0, uint32_t *__restrict__ t1) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int item = blockIdx.z / nsel, which = blockIdx.z - item * nsel;
   if ((uint32_t)item >= *n_items) return;
   const MoeItem it = items[item];
-  const MoeGemvSide &sd = which ? s1 : s0;
-  if (it.count <= 1)
-    moe_gemv_item<K, 1, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
-  else if (it.count <= 2)
-    moe_gemv_item<K, 2, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
-  else if (it.count <= 4)
-    moe_gemv_item<K, 4, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
-  else
-    moe_gemv_item<K, 8, CB>(sd, sorted, it, slots, in_tiles, out_tiles, n, ksplit, tps, mask, item, red, stage);
+  const GemvArgs &a = which ? s1 : s0;
+  GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
+  if (threadIdx.x < GEMV_ROWS) {
+    const int b = min((int)threadIdx.x, (int)it.count - 1);
+    const int slot = (int)sorted[it.start + b];
+    const int in = a.in_tiles * 16, out = a.out_tiles * 16;
+    ri[threadIdx.x] = GemvRow{(a.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
+  }
+  __syncthreads();
+  uint32_t *ticket = (which ? t1 : t0) + (size_t)item * (a.out_tiles / 8) + blockIdx.x;
+  gemv_wg<K, CB>(a, (int)it.expert, (int)it.count, ri, ticket, blockIdx.x, blockIdx.y, smem + 256,
+                 MOE_ITEM_ROWS);
 }
 
 // y[row] = sum_k score * d[slot] (f32, k order), in the output dtype.
@@ -972,7 +941,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
     const uint32_t e = inds ? inds[slot] : 0u;
     if (e >= (uint32_t)experts) continue;
     const float w = scores ? load_act(scores, slot, sdt) : 1.0f;
-    acc = acc + w * h2f(d[slot * hidden + i]);
+    acc = acc + f32_value(w * h2f(d[slot * hidden + i]));
   }
   if (ydt == OUT_F16)
     ((uint16_t *)y)[row * hidden + i] = f2h(acc);
@@ -985,7 +954,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
 namespace {
 
 struct MoeLayout {
-  size_t sorted, items, n_items, xg, xu, g, u, xd, d, pgu, pd, total;
+  size_t sorted, items, n_items, g, u, xd, d, pgu, pd, total;
   size_t tickets;  // in the separate ticket buffer: gate, up, down
   int slots, max_items, ks_gu, ks_d, tps_gu, tps_d;
 };
@@ -998,10 +967,8 @@ MoeLayout moe_layout(const MoeArgs &a) {
   L.slots = slots;
   L.max_items = std::min(a.experts, slots) + (slots + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
   const int groups = std::max(1, std::min(a.experts, slots));
-  L.ks_gu = gemv_ksplit(a.hidden, a.inter, 2 * groups);
-  L.ks_d = gemv_ksplit(a.inter, a.hidden, groups);
-  L.tps_gu = (a.hidden / 16 + L.ks_gu - 1) / L.ks_gu;
-  L.tps_d = (a.inter / 16 + L.ks_d - 1) / L.ks_d;
+  gemv_plan(a.hidden, a.inter, 2 * groups, &L.ks_gu, &L.tps_gu);
+  gemv_plan(a.inter, a.hidden, groups, &L.ks_d, &L.tps_d);
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -1011,8 +978,6 @@ MoeLayout moe_layout(const MoeArgs &a) {
   L.sorted = take((size_t)slots * 4);
   L.items = take((size_t)L.max_items * sizeof(MoeItem));
   L.n_items = take(4);
-  L.xg = take((size_t)slots * a.hidden * 2);
-  L.xu = take((size_t)slots * a.hidden * 2);
   L.g = take((size_t)slots * a.inter * 2);
   L.u = take((size_t)slots * a.inter * 2);
   L.xd = take((size_t)slots * a.inter * 2);
@@ -1025,34 +990,45 @@ MoeLayout moe_layout(const MoeArgs &a) {
 }
 
 template <int CB>
-void moe_gemv_launch(int kk, dim3 grid, hipStream_t s, const MoeGemvSide &s0, const MoeGemvSide &s1,
-                     int nsel, const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
-                     int slots, int in_tiles, int out_tiles, int n, int ksplit, int tps,
-                     uint32_t mask) {
+void moe_gemv_launch(int kk, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &s0,
+                     const GemvArgs &s1, int nsel, const uint32_t *sorted, const MoeItem *items,
+                     const uint32_t *n_items, int topk, uint32_t *t0, uint32_t *t1) {
   switch (kk) {
 #define EXL3_MG(KK)                                                                            \
   case KK:                                                                                     \
-    hipLaunchKernelGGL((moe_gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), 0, s, s0, s1, nsel, \
-                       sorted, items, n_items, slots, in_tiles, out_tiles, n, ksplit, tps, mask); \
+    hipLaunchKernelGGL((moe_gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), lds, s, s0, s1,   \
+                       nsel, sorted, items, n_items, topk, t0, t1);                            \
     break;
     EXL3_MG(1) EXL3_MG(2) EXL3_MG(3) EXL3_MG(4) EXL3_MG(5) EXL3_MG(6) EXL3_MG(7) EXL3_MG(8)
 #undef EXL3_MG
     default:
-      hipLaunchKernelGGL((moe_gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), 0, s, s0, s1, nsel,
-                         sorted, items, n_items, slots, in_tiles, out_tiles, n, ksplit, tps, mask);
+      hipLaunchKernelGGL((moe_gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), lds, s, s0, s1, nsel,
+                         sorted, items, n_items, topk, t0, t1);
   }
 }
 
-void moe_gemv(const Format &f, dim3 grid, hipStream_t s, const MoeGemvSide &s0,
-              const MoeGemvSide &s1, int nsel, const uint32_t *sorted, const MoeItem *items,
-              const uint32_t *n_items, int slots, int in, int out, int ksplit, int tps) {
-  const int kk = f.integer_rate() ? f.n / 16 : 0;
-  if (f.codebook == CB_MCG)
-    moe_gemv_launch<CB_MCG>(kk, grid, s, s0, s1, nsel, sorted, items, n_items, slots, in / 16,
-                            out / 16, f.n, ksplit, tps, f.mask());
-  else
-    moe_gemv_launch<CB_MUL1>(kk, grid, s, s0, s1, nsel, sorted, items, n_items, slots, in / 16,
-                             out / 16, f.n, ksplit, tps, f.mask());
+GemvArgs moe_side(const MoeBank &b, const void *x, int xdt, bool prepared, uint16_t *y,
+                  float *partial, size_t slots, int ksplit, int tps) {
+  GemvArgs a{};
+  a.tw = reinterpret_cast<const uint32_t *>(b.trellis);
+  a.expert_words = (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2);
+  a.x = x;
+  a.xdt = xdt;
+  a.prepared = prepared ? 1 : 0;
+  a.suh = b.suh;
+  a.svh = b.svh;
+  a.y = y;
+  a.ydt = OUT_F16;
+  a.zout = nullptr;
+  a.partial = partial;
+  a.ptotal = slots;
+  a.in_tiles = b.in / 16;
+  a.out_tiles = b.out / 16;
+  a.n = b.f.n;
+  a.ksplit = ksplit;
+  a.tps = tps;
+  a.mask = b.f.mask();
+  return a;
 }
 
 }  // namespace
@@ -1073,38 +1049,46 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
-  if (gate.f.n != up.f.n || gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden ||
-      gate.out != a.inter || up.out != a.inter || down.in != a.inter)
+  if (gate.f.n != up.f.n || gate.f.codebook != up.f.codebook || gate.f.window != up.f.window ||
+      gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden || gate.out != a.inter ||
+      up.out != a.inter || down.in != a.inter)
     return hipErrorInvalidValue;
   const MoeLayout L = moe_layout(a);
   if (scratch_bytes < L.total || ntickets < L.tickets || L.slots > 65535 ||
-      L.max_items * 2 > 65535)
+      L.max_items * 2 > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
     return hipErrorInvalidValue;
   char *base = (char *)scratch;
   uint32_t *sorted = (uint32_t *)(base + L.sorted);
   MoeItem *items = (MoeItem *)(base + L.items);
   uint32_t *n_items = (uint32_t *)(base + L.n_items);
-  uint16_t *xg = (uint16_t *)(base + L.xg), *xu = (uint16_t *)(base + L.xu);
   uint16_t *g = (uint16_t *)(base + L.g), *u = (uint16_t *)(base + L.u);
   uint16_t *xd = (uint16_t *)(base + L.xd), *d = (uint16_t *)(base + L.d);
   float *pgu = (float *)(base + L.pgu), *pd = (float *)(base + L.pd);
-  uint32_t *tgu = tickets, *td = tickets + (size_t)2 * L.max_items * (a.inter / 128);
+  uint32_t *tg = tickets, *tu = tickets + (size_t)L.max_items * (a.inter / 128);
+  uint32_t *td = tickets + (size_t)2 * L.max_items * (a.inter / 128);
 
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
                      a.experts, sorted, items, n_items);
-  hipLaunchKernelGGL(moe_prepare2_kernel, dim3(a.hidden / 128, L.slots), dim3(64), 0, s, a.x, a.xdt,
-                     a.inds, a.topk, a.experts, gate.suh, up.suh, xg, xu, a.hidden);
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
-  MoeGemvSide sg{(const uint32_t *)gate.trellis, gate.svh, (const uint32_t *)xg, g, pgu, tgu};
-  MoeGemvSide su{(const uint32_t *)up.trellis, up.svh, (const uint32_t *)xu, u, pgu + gu_part,
-                 tgu + (size_t)L.max_items * (a.inter / 128)};
-  moe_gemv(gate.f, dim3(a.inter / 128, L.ks_gu, L.max_items * 2), s, sg, su, 2, sorted, items,
-           n_items, L.slots, a.hidden, a.inter, L.ks_gu, L.tps_gu);
+  const GemvArgs sg = moe_side(gate, a.x, a.xdt, false, g, pgu, L.slots, L.ks_gu, L.tps_gu);
+  const GemvArgs su = moe_side(up, a.x, a.xdt, false, u, pgu + gu_part, L.slots, L.ks_gu, L.tps_gu);
+  const int kg = gate.f.integer_rate() ? gate.f.n / 16 : 0;
+  const size_t lds_gu = gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, kg == 0);
+  const dim3 ggu(a.inter / 128, L.ks_gu, L.max_items * 2);
+  if (gate.f.codebook == CB_MCG)
+    moe_gemv_launch<CB_MCG>(kg, ggu, lds_gu, s, sg, su, 2, sorted, items, n_items, a.topk, tg, tu);
+  else
+    moe_gemv_launch<CB_MUL1>(kg, ggu, lds_gu, s, sg, su, 2, sorted, items, n_items, a.topk, tg, tu);
   hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
                      a.experts, down.suh, xd, a.inter, a.limit);
-  MoeGemvSide sd{(const uint32_t *)down.trellis, down.svh, (const uint32_t *)xd, d, pd, td};
-  moe_gemv(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items), s, sd, sd, 1, sorted, items, n_items,
-           L.slots, a.inter, a.hidden, L.ks_d, L.tps_d);
+  const GemvArgs sd = moe_side(down, xd, OUT_F16, true, d, pd, L.slots, L.ks_d, L.tps_d);
+  const int kd = down.f.integer_rate() ? down.f.n / 16 : 0;
+  const size_t lds_d = gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, kd == 0);
+  const dim3 gd(a.hidden / 128, L.ks_d, L.max_items);
+  if (down.f.codebook == CB_MCG)
+    moe_gemv_launch<CB_MCG>(kd, gd, lds_d, s, sd, sd, 1, sorted, items, n_items, a.topk, td, td);
+  else
+    moe_gemv_launch<CB_MUL1>(kd, gd, lds_d, s, sd, sd, 1, sorted, items, n_items, a.topk, td, td);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();
