@@ -7,9 +7,11 @@ HBM GB/s at bs=1" is quoted on): a decode pass at batch 1 over the linears of
 a 36-layer Qwen3-8B-shaped decoder (per layer q/o 4096->4096, k/v
 4096->1024, gate/up 4096->12288, down 12288->4096), EXL3 K=4 mul1 weights,
 uniform-random trellis words, suh +-1, svh f16(+-U[0.5,1.5]*0.02), f16
-N(0,1) activations.  One step = one matmul (one kernel: prepare + decode GEMV + finish)
-per linear, 252 linears, 3.47 GB of distinct packed weights (beyond the 256 MB
-Infinity Cache, so every step reads HBM).  The step is captured once into a
+N(0,1) activations.  One step = every linear once (one kernel per launch: prepare + decode GEMV +
+finish), the linears that read the same rows in one launch as a decoder layer
+issues them (q+k+v, o, gate+up, down: exl3_matmul_shared; --per-linear: one
+launch each), 252 linears, 3.47 GB of distinct packed weights (beyond the
+256 MB Infinity Cache, so every step reads HBM).  The step is captured once into a
 HIP graph and replayed.
 
 `value` = packed-weight bytes per step * steps / timed seconds (GB/s).
@@ -139,6 +141,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--per-linear", action="store_true",
+                    help="one launch per linear instead of one per shared-input group")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the EXL3 path has no multi-GPU leg); "
@@ -153,10 +157,27 @@ def main() -> int:
     step_bytes = sum(packed_bytes(i, o) for _, i, o, _ in lins)
     xs = {i: torch.randn(1, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
     ys = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+    # launches of one step: the linears that read the same rows go together
+    # (q,k,v and gate,up), as a decoder layer issues them
+    groups = []
+    if args.per_linear:
+        groups = [[j] for j in range(len(lins))]
+    else:
+        per = len(SHAPES)
+        for l0 in range(0, len(lins), per):
+            groups += [[l0, l0 + 1, l0 + 2], [l0 + 3], [l0 + 4, l0 + 5], [l0 + 6]]
+
+    def launch(g):
+        if len(g) == 1:
+            name, i, o, lin = lins[g[0]]
+            lin(xs[i], out=ys[g[0]])
+        else:
+            i = lins[g[0]][1]
+            X.matmul_shared([lins[j][3].weight for j in g], xs[i], outs=[ys[j] for j in g])
 
     def step():
-        for (name, i, o, lin), y in zip(lins, ys):
-            lin(xs[i], out=y)
+        for g in groups:
+            launch(g)
 
     # Warm up on the stream the graph is captured on: the library keeps its
     # scratch per stream and sizes it at the first call, outside the capture.
@@ -194,14 +215,15 @@ def main() -> int:
     log("roofline leg")
     torch.cuda.synchronize()
     pairs = []
-    torch.cuda._sleep(int(2.4e9 * 0.05))
+    torch.cuda._sleep(int(2.4e9 * 0.2))
     for _ in range(3):
-        for (name, i, o, lin), y in zip(lins, ys):
+        for g in groups:
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            lin(xs[i], out=y)
+            launch(g)
             b.record()
-            pairs.append((name, packed_bytes(i, o), a, b))
+            name = "+".join(lins[j][0] for j in g)
+            pairs.append((name, sum(packed_bytes(lins[j][1], lins[j][2]) for j in g), a, b))
     torch.cuda.synchronize()
     kbytes = sum(p[1] for p in pairs)
     kms = sum(a.elapsed_time(b) for _, _, a, b in pairs)
@@ -236,10 +258,11 @@ def main() -> int:
         "config": {"workload": f"decode GEMV pass, batch 1, EXL3 K={K_BITS} mul1, "
                                f"{args.layers}-layer Qwen3-8B-shaped linears (q,k,v,o,gate,up,down)",
                    "layers": args.layers, "batch": 1, "K": K_BITS, "packed_bytes_per_step": step_bytes,
-                   "linears_per_step": len(lins)},
+                   "linears_per_step": len(lins), "launches_per_step": len(groups),
+                   "launch_groups": "per linear" if args.per_linear else "q+k+v, o, gate+up, down"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "exl3::gemv_kernel<4,0> (mul1, K=4)", "launches": len(pairs),
+                     "kernel": "exl3::gemv_kernel<4,0,false> (mul1, K=4, window 16)", "launches": len(pairs),
                      "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -219,6 +219,15 @@ void exl3_release(exl3_weight *w);
  * caller's buffer, which must have x's dtype and the result's shape. */
 exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3_array *out);
 
+/* Up to four linears that read the same rows, in one launch: outs[i] =
+ * x @ W_i^T, each in x's dtype (turboexl3's linearShared,
+ * sushi_ds41/src/sushi/exl3/linear.zig:34-60: q/k/v, gate/up).  The weights
+ * must share the input width, rate, codebook and window (else refused:
+ * the caller runs exl3_matmul per weight).  Output ownership per outs[i] as
+ * exl3_matmul.  Not a QuantTable entry. */
+exl3_verdict exl3_matmul_shared(const exl3_weight *const *ws, uint32_t count, exl3_array x,
+                                exl3_stream s, exl3_array *outs);
+
 /* QuantTable.moe (quant.zig:43-45): turboexl3_ds41 refuses it ("routed
  * experts run through swiglu", turboexl3_ds41/plugin.zig:263-265); so does
  * this library, with the same reason. */

@@ -153,6 +153,54 @@ __device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1], uint3
   return decode_pair<CB>(chunk_window<K, 2 * P>(w), chunk_window<K, 2 * P + 1>(w), mask);
 }
 
+// Codeword I of a chunk as a zero-extended 16-bit value, with the cheapest
+// extraction its window allows: v_bfe_u32 when the window lies in one dword,
+// v_perm_b32 when it straddles two dwords on a byte boundary, else
+// v_alignbit_b32 and a mask.  (Stream bit b is bit 31 - b%32 of its dword:
+// a window starting at bit o of a dword, o <= 16, is bits 31-o .. 16-o.)
+template <int K, int I>
+__device__ __forceinline__ uint32_t chunk_cw(const uint32_t (&w)[K + 1]) {
+  constexpr int E = 32 + (I + 1) * K;
+  constexpr int S = E - 16;
+  constexpr int J0 = S >> 5, J1 = (E - 1) >> 5;
+  static_assert(J0 >= 0 && J1 <= K && J1 - J0 <= 1, "window outside the chunk buffer");
+  if constexpr (J0 == J1) {
+    return __builtin_amdgcn_ubfe(w[J0], 16 - (S & 31), 16);
+  } else if constexpr ((S & 31) == 24) {
+    // the last byte of dword J0, then the first (most significant) of J1
+    return __builtin_amdgcn_perm(w[J0], w[J1], 0x0C0C0403u);
+  } else {
+    return __builtin_amdgcn_alignbit(w[J0], w[J1], 31 - ((E - 1) & 31)) & 0xFFFFu;
+  }
+}
+
+// decode_pair on zero-extended codewords; MASKED applies a window below 16.
+template <int CB, bool MASKED>
+__device__ __forceinline__ uint32_t decode_pair_cw(uint32_t c0, uint32_t c1, uint32_t mask) {
+  if constexpr (MASKED) {
+    c0 &= mask;
+    c1 &= mask;
+  }
+  if constexpr (CB == CB_MUL1) {
+    uint32_t h = __builtin_amdgcn_sad_u8(c0 * MUL1_MULT, 0u, 0x64006400u);
+    h = __builtin_amdgcn_sad_hi_u8(c1 * MUL1_MULT, 0u, h);
+    const h2_t inv = {bits<_Float16>(MUL1_INV), bits<_Float16>(MUL1_INV)};
+    const h2_t bias = {bits<_Float16>(MUL1_BIAS), bits<_Float16>(MUL1_BIAS)};
+    return bits<uint32_t>(__builtin_elementwise_fma(bits<h2_t>(h), inv, bias));
+  } else {
+    const uint32_t p0 = 0x3B603B60u ^ ((c0 * MCG_MULT) & 0x8FFF8FFFu);
+    const uint32_t p1 = 0x3B603B60u ^ ((c1 * MCG_MULT) & 0x8FFF8FFFu);
+    const uint32_t lo = __builtin_amdgcn_perm(p1, p0, 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(p1, p0, 0x07060302u);
+    return bits<uint32_t>(bits<h2_t>(lo) + bits<h2_t>(hi));
+  }
+}
+
+template <int K, int CB, bool MASKED, int P>
+__device__ __forceinline__ uint32_t chunk_pair_cw(const uint32_t (&w)[K + 1], uint32_t mask) {
+  return decode_pair_cw<CB, MASKED>(chunk_cw<K, 2 * P>(w), chunk_cw<K, 2 * P + 1>(w), mask);
+}
+
 // ------------------------------------------------------------ generic rate
 
 // Codeword t (0..255) of a tile of n halfwords whose n/2 dwords are in `tw`

@@ -493,54 +493,95 @@ static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t las
   return ok();
 }
 
-// One linear over `rows` rows: x raw (xdt, prepared in the kernels) or
-// already prepared (f16), to the finished y (ydt) or, with y null, the inner
-// product z (f16).  Up to 16 rows take the GEMV, one launch per 16 rows; wider
-// calls of an integer rate take the GEMM after a prepare launch (other rates
-// take the GEMV 16 rows at a time).
-static hipError_t run_linear(const exl3_weight *w, const WeightPriv *pv, const void *x, int xdt,
-                             bool prepared, void *y, int ydt, uint16_t *zout, int64_t rows,
-                             StreamScratch *ss, hipStream_t s) {
-  const int in = (int)pv->in, outf = (int)pv->out;
-  const uint16_t *trellis = (const uint16_t *)w->w.data;
-  const uint16_t *suh = (const uint16_t *)w->scales.data;
-  const uint16_t *svh = (const uint16_t *)w->biases.data;
+// Scratch of one GEMV launch over `count` linears of widths outs[] for
+// `rows` rows: partial sums and (zeroed) tickets, split per linear.
+static hipError_t gemv_scratch(StreamScratch *ss, const int *outs, int count, int in, int rows,
+                               bool generic, exl3::Scratch *sc, hipStream_t s) {
+  int total = 0;
+  for (int i = 0; i < count; ++i) total += outs[i];
+  int ksplit, tps;
+  exl3::gemv_multi_plan(in, total, generic, &ksplit, &tps);
+  hipError_t e = grow(&ss->partial, &ss->partial_bytes, (size_t)ksplit * rows * total * 4, s, false);
+  if (e != hipSuccess) return e;
+  e = grow(&ss->ticket, &ss->ticket_bytes, (size_t)(total / 128) * 4, s, true);
+  if (e != hipSuccess) return e;
+  size_t po = 0, to = 0;
+  for (int i = 0; i < count; ++i) {
+    sc[i].partial = (float *)ss->partial + po;
+    sc[i].partial_floats = (size_t)ksplit * rows * outs[i];
+    sc[i].ticket = (uint32_t *)ss->ticket + to;
+    sc[i].tickets = (size_t)outs[i] / 128;
+    po += sc[i].partial_floats;
+    to += sc[i].tickets;
+  }
+  return hipSuccess;
+}
+
+// Linears ws[0..count) over `rows` rows of the same input: x raw (xdt,
+// prepared in the kernels) or already prepared (f16), to finished outputs
+// ys[i] (ydt) or, with ys null, inner products zs[i] (f16).  Up to 16 rows
+// take the GEMV, one launch per 16 rows for all the linears; wider calls of
+// an integer rate take the GEMM per linear after one prepare launch (other
+// rates take the GEMV 16 rows at a time).
+static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *const *pvs, int count,
+                              const void *x, int xdt, bool prepared, void *const *ys, int ydt,
+                              uint16_t *const *zs, int64_t rows, StreamScratch *ss, hipStream_t s) {
+  const WeightPriv *p0 = pvs[0];
+  const int in = (int)p0->in;
   const size_t xsz = prepared ? 2 : (xdt == exl3::ACT_F32 ? 4 : 2);
   const size_t ysz = ydt == exl3::ACT_F32 ? 4 : 2;
-  if (rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate()) {
-    const uint16_t *xp = (const uint16_t *)x;
-    if (!prepared) {
-      hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, false);
-      if (e != hipSuccess) return e;
-      for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
-        const int r = (int)std::min<int64_t>(65535, rows - r0);
-        e = exl3::launch_prepare((const char *)x + (size_t)r0 * in * xsz, xdt, suh,
-                                 (uint16_t *)ss->xp + (size_t)r0 * in, r, in, s);
+  if (rows > exl3::GEMV_ROWS_MAX && p0->f.integer_rate()) {
+    for (int i = 0; i < count; ++i) {
+      const uint16_t *xp = (const uint16_t *)x;
+      if (!prepared) {
+        hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, false);
         if (e != hipSuccess) return e;
+        for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+          const int r = (int)std::min<int64_t>(65535, rows - r0);
+          e = exl3::launch_prepare((const char *)x + (size_t)r0 * in * xsz, xdt,
+                                   (const uint16_t *)ws[i]->scales.data,
+                                   (uint16_t *)ss->xp + (size_t)r0 * in, r, in, s);
+          if (e != hipSuccess) return e;
+        }
+        xp = (const uint16_t *)ss->xp;
       }
-      xp = (const uint16_t *)ss->xp;
+      hipError_t e = exl3::launch_gemm((const uint16_t *)ws[i]->w.data, pvs[i]->f, xp,
+                                       (const uint16_t *)ws[i]->biases.data, ys ? ys[i] : nullptr,
+                                       ydt, zs ? zs[i] : nullptr, (int)rows, in, (int)pvs[i]->out, s);
+      if (e != hipSuccess) return e;
     }
-    return exl3::launch_gemm(trellis, pv->f, xp, svh, y, ydt, zout, (int)rows, in, outf, s);
+    return hipSuccess;
   }
+  int outs[4];
+  for (int i = 0; i < count; ++i) outs[i] = (int)pvs[i]->out;
   for (int64_t r0 = 0; r0 < rows; r0 += exl3::GEMV_ROWS_MAX) {
     const int r = (int)std::min<int64_t>(exl3::GEMV_ROWS_MAX, rows - r0);
-    size_t pf = 0, tk = 0;
-    exl3::gemv_scratch_need(r, in, outf, &pf, &tk);
-    hipError_t e = grow(&ss->partial, &ss->partial_bytes, pf * sizeof(float), s, false);
+    exl3::Scratch sc[4];
+    hipError_t e = gemv_scratch(ss, outs, count, in, r, !p0->f.integer_rate(), sc, s);
     if (e != hipSuccess) return e;
-    e = grow(&ss->ticket, &ss->ticket_bytes, tk * sizeof(uint32_t), s, true);
-    if (e != hipSuccess) return e;
-    exl3::Scratch sc;
-    sc.partial = (float *)ss->partial;
-    sc.partial_floats = ss->partial_bytes / sizeof(float);
-    sc.ticket = (uint32_t *)ss->ticket;
-    sc.tickets = ss->ticket_bytes / sizeof(uint32_t);
-    e = exl3::launch_gemv(trellis, pv->f, (const char *)x + (size_t)r0 * in * xsz, xdt, prepared,
-                          suh, svh, y ? (char *)y + (size_t)r0 * outf * ysz : nullptr, ydt,
-                          zout ? zout + (size_t)r0 * outf : nullptr, r, in, outf, sc, s);
+    exl3::GemvLinear ls[4];
+    for (int i = 0; i < count; ++i) {
+      ls[i].trellis = (const uint16_t *)ws[i]->w.data;
+      ls[i].suh = (const uint16_t *)ws[i]->scales.data;
+      ls[i].svh = (const uint16_t *)ws[i]->biases.data;
+      ls[i].y = ys ? (char *)ys[i] + (size_t)r0 * outs[i] * ysz : nullptr;
+      ls[i].zout = zs ? zs[i] + (size_t)r0 * outs[i] : nullptr;
+      ls[i].out = outs[i];
+    }
+    e = exl3::launch_gemv_multi(ls, count, p0->f, (const char *)x + (size_t)r0 * in * xsz, xdt,
+                                prepared, ydt, r, in, sc, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+static hipError_t run_linear(const exl3_weight *w, const WeightPriv *pv, const void *x, int xdt,
+                             bool prepared, void *y, int ydt, uint16_t *zout, int64_t rows,
+                             StreamScratch *ss, hipStream_t s) {
+  void *ys[1] = {y};
+  uint16_t *zs[1] = {zout};
+  return run_linears(&w, &pv, 1, x, xdt, prepared, y ? ys : nullptr, ydt, zout ? zs : nullptr, rows,
+                     ss, s);
 }
 
 exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
@@ -560,6 +601,40 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(g_scratch_mu);
   hipError_t e = run_linear(w, pv, x.data, xdt, false, out->data, xdt, nullptr, rows, ss, s);
+  if (e != hipSuccess) return hip_failed(e);
+  return ok();
+}
+
+exl3_verdict exl3_matmul_shared(const exl3_weight *const *ws, uint32_t count, exl3_array x,
+                                exl3_stream stream, exl3_array *outs) {
+  if (!ws || !outs || count < 1 || count > 4) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  const WeightPriv *pvs[4];
+  for (uint32_t i = 0; i < count; ++i) {
+    pvs[i] = priv_of(ws[i]);
+    if (!pvs[i]) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+    if (pvs[i]->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
+    if (pvs[i]->in != pvs[0]->in || pvs[i]->f.n != pvs[0]->f.n ||
+        pvs[i]->f.codebook != pvs[0]->f.codebook || pvs[i]->f.window != pvs[0]->f.window ||
+        pvs[i]->device != pvs[0]->device)
+      return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: shared linears differ in input, rate or codebook");
+  }
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  const int64_t in = pvs[0]->in;
+  if (x.ndim < 1 || x.ndim > EXL3_MAX_DIMS || !x.data || x.shape[x.ndim - 1] != in) return kShape;
+  const int64_t rows = numel(x) / in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pvs[0]->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  void *ys[4];
+  for (uint32_t i = 0; i < count; ++i) {
+    exl3_verdict v = output_for(&outs[i], x, pvs[i]->out, rows);
+    if (v.code != EXL3_OK) return v;
+    ys[i] = outs[i].data;
+  }
+  StreamScratch *ss = scratch_for(pvs[0]->device, s);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  hipError_t e = run_linears(ws, pvs, (int)count, x.data, xdt, false, ys, xdt, nullptr, rows, ss, s);
   if (e != hipSuccess) return hip_failed(e);
   return ok();
 }
@@ -638,7 +713,8 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   StreamScratch *ss = scratch_for(pg->device, s);
   std::lock_guard<std::mutex> g(g_scratch_mu);
   size_t ntick = 0;
-  const size_t need = exl3::moe_scratch_bytes(a, &ntick);
+  const size_t need =
+      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &ntick);
   hipError_t e = grow(&ss->moe, &ss->moe_bytes, need, s, false);
   if (e != hipSuccess) return hip_failed(e);
   e = grow(&ss->moe_ticket, &ss->moe_ticket_bytes, ntick * 4, s, true);

@@ -59,12 +59,27 @@ constexpr int GEMV_ROWS_MAX = 16;
 hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,
                        bool prepared, const uint16_t *suh, const uint16_t *svh, void *y, int ydt,
                        uint16_t *zout, int rows, int in, int out, Scratch &sc, hipStream_t s);
+// Up to four linears that read the same rows (same in, rate, codebook and
+// window), one launch; sc[i] is linear i's scratch.
+struct GemvLinear {
+  const uint16_t *trellis;
+  const uint16_t *suh;
+  const uint16_t *svh;
+  void *y;
+  uint16_t *zout;
+  int out;
+};
+hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
+                             int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
+                             hipStream_t s);
 // GEMM (any rows): the same contract through LDS-staged decode and MFMA.
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
                        int out, hipStream_t s);
-// Scratch the GEMV needs for (rows, in, out): partial floats and tickets.
-void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t *tickets);
+// The split of one GEMV launch over weights of total output width
+// total_out: a linear of width out needs ksplit * rows * out partial floats
+// and out / 128 tickets.
+void gemv_multi_plan(int in, int total_out, bool generic, int *ksplit, int *tps);
 
 // ------------------------------------------------------------------- MoE
 
@@ -94,7 +109,7 @@ struct MoeArgs {
 };
 // Scratch bytes for a call, and (in *tickets) the count of u32 tickets it
 // needs in a separate buffer that starts zeroed and is left zeroed.
-size_t moe_scratch_bytes(const MoeArgs &a, size_t *tickets);
+size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic, size_t *tickets);
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                       const MoeBank &down, void *scratch, size_t scratch_bytes, uint32_t *tickets,
                       size_t ntickets, hipStream_t s);

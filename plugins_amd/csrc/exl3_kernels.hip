@@ -223,29 +223,33 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 
 // ===================================================================== GEMV
 //
-// One launch per matmul of up to 16 rows.  A workgroup (4 waves) owns one
-// 128-column group (8 output tiles: one Hadamard block of the output) and one
-// k-split of tps k-tile rows (a multiple of 8, so the split is whole input
-// Hadamard blocks):
+// One launch per matmul of up to 16 rows, and one launch for up to four
+// weights that read the same rows (q/k/v, gate/up: the reference's
+// linearShared, sushi_ds41/src/sushi/exl3/linear.zig:34-60), their column
+// groups side by side in the grid.  A workgroup (8 waves) owns one
+// 128-column group (8 output tiles: one Hadamard block of the output) of one
+// weight and one k-split of tps k-tile rows (whole input Hadamard blocks):
 //  1. it prepares its rows' input slice in LDS (x * suh, Hadamard-128, f16:
 //     the reference's prepare, run per split instead of as its own launch);
-//  2. wave w owns tiles 2w, 2w+1 of the group; lane l = 16g + 8t + c takes
-//     chunk c of tile 2w+t in k-tile row 4i+g of the split at step i, loads
-//     its K dwords (+ the history dword from lane l-1 of its tile through
-//     ds_bpermute), decodes its 32 codewords in registers into four 8 x f16
-//     MFMA B operands (column a / a+8, rows 0-7 / 8-15 of the tile), and
-//     v_mfma_f32_16x16x32_f16 sums them against the rows' activations (MFMA
-//     A operands from LDS) over the 4 k-tile rows of the step.  MFMA rows are
-//     the call's rows, so 1..16 rows cost the same decode;
-//  3. the per-row f32 sums go to scratch; the last workgroup of the column
-//     group (a ticket counter) adds the splits in split order, rounds z to
-//     f16 and runs the finish (Hadamard-128, * svh) on its 128 columns.
-// Codewords 32a..32a+31 of a tile are columns a and a+8 over all 16 rows, so
-// a lane's decoded weights are already whole B-operand columns.
+//  2. wave w takes tiles 2q, 2q+1 (q = w % 4) of the group over k-part w / 4
+//     of the split; lane l = 16g + 8t + c takes chunk c of tile 2q+t in
+//     k-tile row 4i+g of its part at step i, loads its K dwords (+ the
+//     history dword of lane l-1 of its tile, by ds_bpermute), decodes its 32
+//     codewords in registers into four 8 x f16 MFMA B operands (column a /
+//     a+8, rows 0-7 / 8-15), and v_mfma_f32_16x16x32_f16 sums them against
+//     the rows' activations (A operands from LDS) over the step's 4 k-tile
+//     rows.  MFMA rows are the call's rows: 1..16 rows cost one decode;
+//  3. the two k-parts add in LDS; the per-row sums go to scratch, and the
+//     last workgroup of the column group (a ticket counter) adds the splits
+//     in split order, rounds z to f16 and runs the finish (Hadamard-128,
+//     * svh) on its 128 columns.  Every sum is in a fixed order that does not
+//     depend on how many rows share the call.
 
-constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_THREADS = 512;
 constexpr int GEMV_ROWS = 16;
 constexpr int GEMV_TPS_MAX = 64;
+constexpr int GEMV_KSPLIT_MAX = 64;
+constexpr int GEMV_MAXW = 4;
 
 struct GemvRow {
   int in_off;   // element offset of the row's activations
@@ -254,38 +258,47 @@ struct GemvRow {
   int pad;
 };
 
-struct GemvArgs {
+struct GemvWeight {
   const uint32_t *tw;   // trellis dwords (a bank's expert 0)
-  size_t expert_words;  // dwords per expert
-  const void *x;        // activations (ACT_*), or prepared rows (f16) when prepared
-  int xdt;
-  int prepared;
-  const uint16_t *suh;  // [E][in]; unused when prepared
+  const uint16_t *suh;  // [E][in]
   const uint16_t *svh;  // [E][out]
-  void *y;              // finished output, or nullptr:
-  int ydt;
+  void *y;              // finished output in ydt, or nullptr:
   uint16_t *zout;       // the inner product z (f16) instead
   float *partial;       // [ksplit][ptotal][out]
+  uint32_t *ticket;     // [groups][out/128], zero between calls
+  size_t expert_words;  // dwords per expert
+  int out_tiles;
+  int cg0;              // first grid column group of this weight
+};
+
+struct GemvArgs {
+  GemvWeight w[GEMV_MAXW];
+  int nweights;
+  const void *x;  // activations (ACT_*), or prepared rows (f16) when prepared
+  int xdt;
+  int prepared;
+  int ydt;
   size_t ptotal;
-  int in_tiles, out_tiles, n, ksplit, tps;
+  int in_tiles, n, ksplit, tps;
   uint32_t mask;
 };
 
-// Dynamic LDS of a GEMV workgroup: row table, prepared rows, z tile, and
-// (generic rate) a word stage per wave.
+// Dynamic LDS of a GEMV workgroup: row table, prepared rows, the two
+// k-parts' z tiles, and (generic rate) a word stage per wave.
 __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, bool generic) {
-  return 256 + (size_t)rows_alloc * (tps * 16 + 8) * 2 + (size_t)rows_alloc * 128 * 4 +
-         (generic ? 4 * 512 * 4 : 0);
+  return 256 + (size_t)rows_alloc * (tps * 16 + 8) * 2 +
+         (size_t)2 * (rows_alloc > 2 ? rows_alloc : 2) * 128 * 4 +
+         (generic ? (size_t)(GEMV_THREADS / 64) * 512 * 4 : 0);
 }
 
 // The rows' input slice [tk0*16, tk0*16 + ntk*16) prepared into xs (row
 // stride kr halfs): one wave per (row, 128-block).
-__device__ __forceinline__ void gemv_prepare(const GemvArgs &a, int expert, int nrows,
-                                             const GemvRow *rows, uint16_t *xs, int kr, int tk0,
-                                             int ntk, int wave, int lane) {
+__device__ __forceinline__ void gemv_prepare(const GemvArgs &a, const GemvWeight &W, int expert,
+                                             int nrows, const GemvRow *rows, uint16_t *xs, int kr,
+                                             int tk0, int ntk, int wave, int lane) {
   const int nb = ntk >> 3;
   const int in = a.in_tiles * 16;
-  for (int it = wave; it < nrows * nb; it += 4) {
+  for (int it = wave; it < nrows * nb; it += GEMV_THREADS / 64) {
     const int r = it / nb, blk = it - r * nb;
     const int k = tk0 * 16 + blk * 128 + lane;
     uint16_t *dst = xs + r * kr + blk * 128 + lane;
@@ -295,7 +308,7 @@ __device__ __forceinline__ void gemv_prepare(const GemvArgs &a, int expert, int 
       dst[64] = src[64];
       continue;
     }
-    const uint16_t *su = a.suh + (size_t)expert * in + k;
+    const uint16_t *su = W.suh + (size_t)expert * in + k;
     float v0 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k, a.xdt))) * h2f(su[0]);
     float v1 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k + 64, a.xdt))) * h2f(su[64]);
 #pragma unroll
@@ -333,20 +346,23 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 // fence is needed, only order: each wave waits for its stores to be
 // acknowledged before the barrier, and the last workgroup loads after its
 // ticket returned.  (A device fence would write back and invalidate the L2
-// in every workgroup.)
-__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a, int nrows,
+// in every workgroup.)  The last workgroup issues all of an element's loads
+// before it adds them.
+__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
+                                                 const GemvWeight &W, int nrows,
                                                  const GemvRow *rows, uint32_t *ticket, int ks,
                                                  size_t out, int col0) {
   __shared__ int s_last;
+  const int E = nrows * 128;
   if (a.ksplit == 1) {
-    for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
+    for (int e = threadIdx.x; e < E; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
     __syncthreads();
     return true;
   }
   const size_t stride = a.ptotal * out;
-  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
+  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    st_agent(a.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, zf[e]);
+    st_agent(W.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, zf[e]);
   }
   wait_stores();
   __syncthreads();
@@ -357,19 +373,17 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a, i
   }
   __syncthreads();
   if (!s_last) return false;
-  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
+  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    const float *p = a.partial + (size_t)rows[b].prow * out + col0 + col;
+    const float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
+    float v[GEMV_KSPLIT_MAX];
+#pragma unroll
+    for (int k = 0; k < GEMV_KSPLIT_MAX; ++k)
+      if (k < a.ksplit) v[k] = ld_agent(p + (size_t)k * stride);
     float s = 0.0f;
-    int k = 0;
-    for (; k + 8 <= a.ksplit; k += 8) {
-      float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = ld_agent(p + (size_t)(k + j) * stride);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s = s + v[j];
-    }
-    for (; k < a.ksplit; ++k) s = s + ld_agent(p + (size_t)k * stride);
+    for (int k = 0; k < GEMV_KSPLIT_MAX; ++k)
+      if (k < a.ksplit) s = s + v[k];
     zf[e] = h2f(f2h(s));
   }
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -379,56 +393,61 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a, i
 
 // The finish over zf[nrows][128] (f32 holding f16 values): rotation,
 // * 1/sqrt(128), * svh, f16, output dtype; or z itself when y is null.
-__device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, int expert, int nrows,
-                                            const GemvRow *rows, size_t out, int col0) {
-  if (a.y == nullptr) {
+__device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const GemvWeight &W,
+                                            int expert, int nrows, const GemvRow *rows, size_t out,
+                                            int col0) {
+  if (W.y == nullptr) {
     for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
       const int b = e >> 7, col = e & 127;
-      a.zout[(size_t)rows[b].out_off + col0 + col] = f2h(zf[e]);
+      W.zout[(size_t)rows[b].out_off + col0 + col] = f2h(zf[e]);
     }
     return;
   }
   had128_lds(zf, nrows, threadIdx.x, GEMV_THREADS);
-  const uint16_t *sv = a.svh + (size_t)expert * out + col0;
+  const uint16_t *sv = W.svh + (size_t)expert * out + col0;
   for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
     const float sc = zf[e] * HAD_SCALE;
-    store_out(a.y, (size_t)rows[b].out_off + col0 + col, f2h(sc * h2f(sv[col])), a.ydt);
+    store_out(W.y, (size_t)rows[b].out_off + col0 + col, f2h(sc * h2f(sv[col])), a.ydt);
   }
 }
 
-// One workgroup of the GEMV: expert `expert` of the bank, nrows <= 16 rows
-// (table `rows` in LDS), column group cg, split ks.
-template <int K, int CB>
-__device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows,
-                                        const GemvRow *rows, uint32_t *ticket, int cg, int ks,
-                                        char *smem, int rows_alloc) {
+// One workgroup of the GEMV: expert `expert` of weight W, nrows <= 16 rows
+// (table `rows` in LDS), column group cg of W, split ks.
+template <int K, int CB, bool MASKED>
+__device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, int expert,
+                                        int nrows, const GemvRow *rows, uint32_t *ticket, int cg,
+                                        int ks, char *smem, int rows_alloc) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const size_t out = (size_t)a.out_tiles * 16;
+  const int q = wave & 3, kp = wave >> 2;
+  const size_t out = (size_t)W.out_tiles * 16;
   const int tk0 = ks * a.tps;
   const int ntk = min(a.tps, a.in_tiles - tk0);  // a multiple of 8
   const int kr = a.tps * 16 + 8;
   uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
-  float *zf = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);
+  const int zrows = rows_alloc > 2 ? rows_alloc : 2;
+  float *zp = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);  // [2][zrows][128]
   const int nw = a.n >> 1;
   const int g = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
-  const size_t tn = (size_t)cg * 8 + 2 * wave + t;
-  const uint32_t *twe = a.tw + (size_t)expert * a.expert_words;
-  const int iters = ntk >> 2;
+  const size_t tn = (size_t)cg * 8 + 2 * q + t;
+  const uint32_t *twe = W.tw + (size_t)expert * W.expert_words;
+  const int part = ntk >> 1;  // k-tile rows per k-part, a multiple of 4
+  const int kb = tk0 + kp * part;
+  const int iters = part >> 2;
 
   // weights of step 0 in flight while the rows are prepared
   uint32_t nxt[K > 0 ? K : 1];
   if constexpr (K > 0) {
-    const uint32_t *p0 = twe + ((size_t)(tk0 + g) * a.out_tiles + tn) * nw + c * K;
+    const uint32_t *p0 = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
 #pragma unroll
     for (int i = 0; i < K; ++i) nxt[i] = p0[i];
   }
-  gemv_prepare(a, expert, nrows, rows, xs, kr, tk0, ntk, wave, lane);
+  gemv_prepare(a, W, expert, nrows, rows, xs, kr, tk0, ntk, wave, lane);
   __syncthreads();
 
   const int arow = min(lane & 15, nrows - 1);
-  const uint16_t *xa = xs + arow * kr + g * 16;
+  const uint16_t *xa = xs + arow * kr + (kp * part + g) * 16;
   f4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (K > 0) {
     const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
@@ -437,8 +456,7 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows
 #pragma unroll
       for (int i = 0; i < K; ++i) wd[i + 1] = nxt[i];
       if (it + 1 < iters) {
-        const uint32_t *pn =
-            twe + ((size_t)(tk0 + 4 * (it + 1) + g) * a.out_tiles + tn) * nw + c * K;
+        const uint32_t *pn = twe + ((size_t)(kb + 4 * (it + 1) + g) * W.out_tiles + tn) * nw + c * K;
 #pragma unroll
         for (int i = 0; i < K; ++i) nxt[i] = pn[i];
       }
@@ -447,20 +465,20 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows
       const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
       uint32_t p[16];
       static_for<16>([&](auto P) {
-        constexpr int q = decltype(P)::value;
-        p[q] = chunk_pair<K, CB, q>(wd, a.mask);
+        constexpr int pq = decltype(P)::value;
+        p[pq] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
       });
       gemv_mfma(p, alo, ahi, acc0, acc1);
     }
   } else {
     // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
     uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
-                                                   (size_t)rows_alloc * 128 * 4) +
+                                                   (size_t)2 * zrows * 128 * 4) +
                       wave * 512;
     for (int it = 0; it < iters; ++it) {
       for (int i = lane; i < 8 * nw; i += 64) {
         const int seg = i / (2 * nw), off = i - seg * 2 * nw;
-        stage[i] = twe[((size_t)(tk0 + 4 * it + seg) * a.out_tiles + cg * 8 + 2 * wave) * nw + off];
+        stage[i] = twe[((size_t)(kb + 4 * it + seg) * W.out_tiles + cg * 8 + 2 * q) * nw + off];
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -470,9 +488,9 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows
       const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
       uint32_t p[16];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const uint32_t cw = 32u * c + 2u * q;
-        p[q] = decode_pair<CB>(tile_window(mine, a.n, cw), tile_window(mine, a.n, cw + 1u), a.mask);
+      for (int pq = 0; pq < 16; ++pq) {
+        const uint32_t cw = 32u * c + 2u * pq;
+        p[pq] = decode_pair<CB>(tile_window(mine, a.n, cw), tile_window(mine, a.n, cw + 1u), a.mask);
       }
       gemv_mfma(p, alo, ahi, acc0, acc1);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -482,40 +500,57 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, int expert, int nrows
   }
 
   // C of a 16x16 MFMA: lane l holds rows 4(l/16)+i, column l%16.
-  const int col = (2 * wave + t) * 16 + c;
+  const int col = (2 * q + t) * 16 + c;
+  float *zk = zp + kp * zrows * 128;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * g + i;
     if (m < nrows) {
-      zf[m * 128 + col] = acc0[i];
-      zf[m * 128 + col + 8] = acc1[i];
+      zk[m * 128 + col] = acc0[i];
+      zk[m * 128 + col + 8] = acc1[i];
     }
   }
   __syncthreads();
-  if (!gemv_splitk_last(zf, a, nrows, rows, ticket, ks, out, cg * 128)) return;
-  gemv_finish(zf, a, expert, nrows, rows, out, cg * 128);
+  float *zf = zp;
+  for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
+  __syncthreads();
+  if (!gemv_splitk_last(zf, a, W, nrows, rows, ticket, ks, out, cg * 128)) return;
+  gemv_finish(zf, a, W, expert, nrows, rows, out, cg * 128);
 }
 
-template <int K, int CB>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a, int rows,
-                                                            uint32_t *__restrict__ ticket) {
+// The weight of grid column group `gx` (weights' groups side by side).
+__device__ __forceinline__ int gemv_weight_of(const GemvArgs &a, int gx) {
+  int wi = 0;
+#pragma unroll
+  for (int i = 1; i < GEMV_MAXW; ++i)
+    if (i < a.nweights && gx >= a.w[i].cg0) wi = i;
+  return wi;
+}
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a, int rows) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wi = gemv_weight_of(a, blockIdx.x);
+  const GemvWeight &W = a.w[wi];
+  const int cg = blockIdx.x - W.cg0;
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, rows - 1);
-    ri[threadIdx.x] = GemvRow{b * a.in_tiles * 16, b * a.out_tiles * 16, b, 0};
+    ri[threadIdx.x] = GemvRow{b * a.in_tiles * 16, b * W.out_tiles * 16, b, 0};
   }
   __syncthreads();
-  gemv_wg<K, CB>(a, 0, rows, ri, ticket + blockIdx.x, blockIdx.x, blockIdx.y, smem + 256, rows);
+  gemv_wg<K, CB, MASKED>(a, W, 0, rows, ri, W.ticket + cg, cg, blockIdx.y, smem + 256, rows);
 }
 
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
-// GEMV_TPS_MAX k-tile rows, ~1024 workgroups over `groups` column groups.
+// GEMV_TPS_MAX k-tile rows (32 for the generic rate) and GEMV_KSPLIT_MAX
+// splits, ~512 workgroups over `groups` column groups.
 void gemv_plan(int in, int out, int groups, int *ksplit, int *tps) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
-  int ks = std::min(nb, std::max(1, (1024 + cgs - 1) / cgs));
+  int ks = std::min(nb, std::max(1, (512 + cgs - 1) / cgs));
   int bps = std::min(GEMV_TPS_MAX / 8, (nb + ks - 1) / ks);  // blocks per split
+  bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
   *tps = 8 * bps;
   *ksplit = (nb + bps - 1) / bps;
 }
@@ -526,71 +561,105 @@ int gemv_ksplit(int in, int out, int groups) {
   return ks;
 }
 
-void gemv_scratch_need(int rows, int in, int out, size_t *partial_floats, size_t *tickets) {
-  const int ks = gemv_ksplit(in, out, 1);
-  *partial_floats = (size_t)ks * rows * out;
-  *tickets = (size_t)out / 128;
+void gemv_multi_plan(int in, int total_out, bool generic, int *ksplit, int *tps) {
+  gemv_plan(in, total_out, 1, ksplit, tps);
+  if (generic && *tps > 32) {
+    *tps = 32;
+    *ksplit = (in / 16 + 31) / 32;
+  }
 }
 
-template <int CB>
-static void gemv_launch_cb(int kk, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &a,
-                           int rows, uint32_t *ticket) {
+template <int CB, bool MASKED, typename F>
+static void gemv_dispatch_k(int kk, F &&launch) {
   switch (kk) {
-#define EXL3_GV(KK)                                                                          \
-  case KK:                                                                                   \
-    hipLaunchKernelGGL((gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), lds, s, a, rows,   \
-                       ticket);                                                              \
-    break;
-    EXL3_GV(1) EXL3_GV(2) EXL3_GV(3) EXL3_GV(4) EXL3_GV(5) EXL3_GV(6) EXL3_GV(7) EXL3_GV(8)
-#undef EXL3_GV
-    default:
-      hipLaunchKernelGGL((gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), lds, s, a, rows, ticket);
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 3: launch(std::integral_constant<int, 3>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    case 5: launch(std::integral_constant<int, 5>{}); break;
+    case 6: launch(std::integral_constant<int, 6>{}); break;
+    case 7: launch(std::integral_constant<int, 7>{}); break;
+    case 8: launch(std::integral_constant<int, 8>{}); break;
+    default: launch(std::integral_constant<int, 0>{});
   }
+}
+
+hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
+                             int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
+                             hipStream_t s) {
+  if (count < 1 || count > GEMV_MAXW || rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
+  if (in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
+  if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
+  const bool generic = !f.integer_rate();
+  int maxout = 0, totcg = 0;
+  for (int i = 0; i < count; ++i) {
+    if (ls[i].out <= 0 || ls[i].out % 128 != 0) return hipErrorInvalidValue;
+    if (ls[i].y == nullptr && ls[i].zout == nullptr) return hipErrorInvalidValue;
+    maxout = std::max(maxout, ls[i].out);
+    totcg += ls[i].out / 128;
+  }
+  if ((int64_t)rows * std::max(in, maxout) >= (int64_t)1 << 31) return hipErrorInvalidValue;
+  int ksplit, tps;
+  gemv_multi_plan(in, 128 * totcg, generic, &ksplit, &tps);
+  if (ksplit > GEMV_KSPLIT_MAX || totcg > 65535) return hipErrorInvalidValue;
+  GemvArgs a{};
+  a.nweights = count;
+  int cg0 = 0;
+  for (int i = 0; i < count; ++i) {
+    GemvWeight &w = a.w[i];
+    w.tw = reinterpret_cast<const uint32_t *>(ls[i].trellis);
+    w.suh = ls[i].suh;
+    w.svh = ls[i].svh;
+    w.y = ls[i].y;
+    w.zout = ls[i].zout;
+    w.expert_words = 0;
+    w.out_tiles = ls[i].out / 16;
+    w.cg0 = cg0;
+    cg0 += ls[i].out / 128;
+    if (ksplit > 1) {
+      if (sc[i].partial == nullptr || sc[i].partial_floats < (size_t)ksplit * rows * ls[i].out)
+        return hipErrorInvalidValue;
+      if (sc[i].ticket == nullptr || sc[i].tickets < (size_t)ls[i].out / 128)
+        return hipErrorInvalidValue;
+    }
+    w.partial = sc[i].partial;
+    w.ticket = sc[i].ticket;
+  }
+  a.x = x;
+  a.xdt = xdt;
+  a.prepared = prepared ? 1 : 0;
+  a.ydt = ydt;
+  a.ptotal = (size_t)rows;
+  a.in_tiles = in / 16;
+  a.n = f.n;
+  a.ksplit = ksplit;
+  a.tps = tps;
+  a.mask = f.mask();
+  const size_t lds = gemv_lds_bytes(rows, tps, generic);
+  const dim3 grid(totcg, ksplit);
+  auto go = [&](auto KC) {
+    constexpr int K = decltype(KC)::value;
+    if (f.codebook == CB_MCG) {
+      if (f.window < 16)
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+      else
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+    } else {
+      if (f.window < 16)
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+      else
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, false>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+    }
+  };
+  gemv_dispatch_k<0, false>(generic ? 0 : f.n / 16, go);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,
                        bool prepared, const uint16_t *suh, const uint16_t *svh, void *y, int ydt,
                        uint16_t *zout, int rows, int in, int out, Scratch &sc, hipStream_t s) {
-  if (rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
-  if (in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
-  if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
-  if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
-  if ((int64_t)rows * std::max(in, out) >= (int64_t)1 << 31) return hipErrorInvalidValue;
-  int ksplit, tps;
-  gemv_plan(in, out, 1, &ksplit, &tps);
-  if (ksplit > 65535) return hipErrorInvalidValue;
-  if (ksplit > 1) {
-    if (sc.partial == nullptr || sc.partial_floats < (size_t)ksplit * rows * out)
-      return hipErrorInvalidValue;
-    if (sc.ticket == nullptr || sc.tickets < (size_t)out / 128) return hipErrorInvalidValue;
-  }
-  GemvArgs a{};
-  a.tw = reinterpret_cast<const uint32_t *>(trellis);
-  a.expert_words = 0;
-  a.x = x;
-  a.xdt = xdt;
-  a.prepared = prepared ? 1 : 0;
-  a.suh = suh;
-  a.svh = svh;
-  a.y = y;
-  a.ydt = ydt;
-  a.zout = zout;
-  a.partial = sc.partial;
-  a.ptotal = (size_t)rows;
-  a.in_tiles = in / 16;
-  a.out_tiles = out / 16;
-  a.n = f.n;
-  a.ksplit = ksplit;
-  a.tps = tps;
-  a.mask = f.mask();
-  const int kk = f.integer_rate() ? f.n / 16 : 0;
-  const size_t lds = gemv_lds_bytes(rows, tps, kk == 0);
-  const dim3 grid(out / 128, ksplit);
-  if (f.codebook == CB_MCG)
-    gemv_launch_cb<CB_MCG>(kk, grid, lds, s, a, rows, sc.ticket);
-  else
-    gemv_launch_cb<CB_MUL1>(kk, grid, lds, s, a, rows, sc.ticket);
-  return hipGetLastError();
+  GemvLinear l{trellis, suh, svh, y, zout, out};
+  return launch_gemv_multi(&l, 1, f, x, xdt, prepared, ydt, rows, in, &sc, s);
 }
 
 // ===================================================================== GEMM
@@ -901,29 +970,31 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
   xd[slot * inter + i0 + 64] = f2h(b * HAD_SCALE);
 }
 
-// Grouped GEMV: blockIdx.z = item * nsel + which.  Raw inputs are rows
+// Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
+// launch's weights (gate and up side by side, or down).  Raw inputs are rows
 // slot / topk of x; prepared inputs are rows slot.
-template <int K, int CB>
+template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
-    GemvArgs s0, GemvArgs s1, int nsel, const uint32_t *__restrict__ sorted,
-    const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, int topk,
-    uint32_t *__restrict__ t0, uint32_t *__restrict__ t1) {
+    GemvArgs a, const uint32_t *__restrict__ sorted, const MoeItem *__restrict__ items,
+    const uint32_t *__restrict__ n_items, int topk) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int item = blockIdx.z / nsel, which = blockIdx.z - item * nsel;
+  const int item = blockIdx.z;
   if ((uint32_t)item >= *n_items) return;
   const MoeItem it = items[item];
-  const GemvArgs &a = which ? s1 : s0;
+  const int wi = gemv_weight_of(a, blockIdx.x);
+  const GemvWeight &W = a.w[wi];
+  const int cg = blockIdx.x - W.cg0;
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, (int)it.count - 1);
     const int slot = (int)sorted[it.start + b];
-    const int in = a.in_tiles * 16, out = a.out_tiles * 16;
+    const int in = a.in_tiles * 16, out = W.out_tiles * 16;
     ri[threadIdx.x] = GemvRow{(a.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
   }
   __syncthreads();
-  uint32_t *ticket = (which ? t1 : t0) + (size_t)item * (a.out_tiles / 8) + blockIdx.x;
-  gemv_wg<K, CB>(a, (int)it.expert, (int)it.count, ri, ticket, blockIdx.x, blockIdx.y, smem + 256,
-                 MOE_ITEM_ROWS);
+  uint32_t *ticket = W.ticket + (size_t)item * (W.out_tiles / 8) + cg;
+  gemv_wg<K, CB, MASKED>(a, W, (int)it.expert, (int)it.count, ri, ticket, cg, blockIdx.y,
+                         smem + 256, MOE_ITEM_ROWS);
 }
 
 // y[row] = sum_k score * d[slot] (f32, k order), in the output dtype.
@@ -961,7 +1032,7 @@ struct MoeLayout {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-MoeLayout moe_layout(const MoeArgs &a) {
+MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   MoeLayout L{};
   const int slots = a.rows * a.topk;
   L.slots = slots;
@@ -969,6 +1040,14 @@ MoeLayout moe_layout(const MoeArgs &a) {
   const int groups = std::max(1, std::min(a.experts, slots));
   gemv_plan(a.hidden, a.inter, 2 * groups, &L.ks_gu, &L.tps_gu);
   gemv_plan(a.inter, a.hidden, groups, &L.ks_d, &L.tps_d);
+  if (generic_gu && L.tps_gu > 32) {
+    L.tps_gu = 32;
+    L.ks_gu = (a.hidden / 16 + 31) / 32;
+  }
+  if (generic_d && L.tps_d > 32) {
+    L.tps_d = 32;
+    L.ks_d = (a.inter / 16 + 31) / 32;
+  }
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -989,56 +1068,69 @@ MoeLayout moe_layout(const MoeArgs &a) {
   return L;
 }
 
-template <int CB>
-void moe_gemv_launch(int kk, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &s0,
-                     const GemvArgs &s1, int nsel, const uint32_t *sorted, const MoeItem *items,
-                     const uint32_t *n_items, int topk, uint32_t *t0, uint32_t *t1) {
-  switch (kk) {
-#define EXL3_MG(KK)                                                                            \
-  case KK:                                                                                     \
-    hipLaunchKernelGGL((moe_gemv_kernel<KK, CB>), grid, dim3(GEMV_THREADS), lds, s, s0, s1,   \
-                       nsel, sorted, items, n_items, topk, t0, t1);                            \
-    break;
-    EXL3_MG(1) EXL3_MG(2) EXL3_MG(3) EXL3_MG(4) EXL3_MG(5) EXL3_MG(6) EXL3_MG(7) EXL3_MG(8)
-#undef EXL3_MG
-    default:
-      hipLaunchKernelGGL((moe_gemv_kernel<0, CB>), grid, dim3(GEMV_THREADS), lds, s, s0, s1, nsel,
-                         sorted, items, n_items, topk, t0, t1);
-  }
+void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &a,
+                     const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
+                     int topk) {
+  auto go = [&](auto KC) {
+    constexpr int K = decltype(KC)::value;
+    if (f.codebook == CB_MCG) {
+      if (f.window < 16)
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, a,
+                           sorted, items, n_items, topk);
+      else
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s, a,
+                           sorted, items, n_items, topk);
+    } else {
+      if (f.window < 16)
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s, a,
+                           sorted, items, n_items, topk);
+      else
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, dim3(GEMV_THREADS), lds, s,
+                           a, sorted, items, n_items, topk);
+    }
+  };
+  gemv_dispatch_k<0, false>(f.integer_rate() ? f.n / 16 : 0, go);
 }
 
-GemvArgs moe_side(const MoeBank &b, const void *x, int xdt, bool prepared, uint16_t *y,
-                  float *partial, size_t slots, int ksplit, int tps) {
+GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, uint32_t *ticket, int cg0) {
+  GemvWeight w{};
+  w.tw = reinterpret_cast<const uint32_t *>(b.trellis);
+  w.suh = b.suh;
+  w.svh = b.svh;
+  w.y = y;
+  w.zout = nullptr;
+  w.partial = partial;
+  w.ticket = ticket;
+  w.expert_words = (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2);
+  w.out_tiles = b.out / 16;
+  w.cg0 = cg0;
+  return w;
+}
+
+GemvArgs moe_args(const void *x, int xdt, bool prepared, size_t slots, int in, const Format &f,
+                  int ksplit, int tps) {
   GemvArgs a{};
-  a.tw = reinterpret_cast<const uint32_t *>(b.trellis);
-  a.expert_words = (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2);
   a.x = x;
   a.xdt = xdt;
   a.prepared = prepared ? 1 : 0;
-  a.suh = b.suh;
-  a.svh = b.svh;
-  a.y = y;
   a.ydt = OUT_F16;
-  a.zout = nullptr;
-  a.partial = partial;
   a.ptotal = slots;
-  a.in_tiles = b.in / 16;
-  a.out_tiles = b.out / 16;
-  a.n = b.f.n;
+  a.in_tiles = in / 16;
+  a.n = f.n;
   a.ksplit = ksplit;
   a.tps = tps;
-  a.mask = b.f.mask();
+  a.mask = f.mask();
   return a;
 }
 
 }  // namespace
 
-size_t moe_scratch_bytes(const MoeArgs &a, size_t *tickets) {
+size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic, size_t *tickets) {
   if (a.rows <= 0 || a.topk <= 0) {
     *tickets = 1;
     return 256;
   }
-  const MoeLayout L = moe_layout(a);
+  const MoeLayout L = moe_layout(a, gu_generic, d_generic);
   *tickets = L.tickets;
   return L.total;
 }
@@ -1053,9 +1145,10 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
       gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden || gate.out != a.inter ||
       up.out != a.inter || down.in != a.inter)
     return hipErrorInvalidValue;
-  const MoeLayout L = moe_layout(a);
+  const bool gu_generic = !gate.f.integer_rate(), d_generic = !down.f.integer_rate();
+  const MoeLayout L = moe_layout(a, gu_generic, d_generic);
   if (scratch_bytes < L.total || ntickets < L.tickets || L.slots > 65535 ||
-      L.max_items * 2 > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
+      L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
     return hipErrorInvalidValue;
   char *base = (char *)scratch;
   uint32_t *sorted = (uint32_t *)(base + L.sorted);
@@ -1070,25 +1163,21 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
                      a.experts, sorted, items, n_items);
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
-  const GemvArgs sg = moe_side(gate, a.x, a.xdt, false, g, pgu, L.slots, L.ks_gu, L.tps_gu);
-  const GemvArgs su = moe_side(up, a.x, a.xdt, false, u, pgu + gu_part, L.slots, L.ks_gu, L.tps_gu);
-  const int kg = gate.f.integer_rate() ? gate.f.n / 16 : 0;
-  const size_t lds_gu = gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, kg == 0);
-  const dim3 ggu(a.inter / 128, L.ks_gu, L.max_items * 2);
-  if (gate.f.codebook == CB_MCG)
-    moe_gemv_launch<CB_MCG>(kg, ggu, lds_gu, s, sg, su, 2, sorted, items, n_items, a.topk, tg, tu);
-  else
-    moe_gemv_launch<CB_MUL1>(kg, ggu, lds_gu, s, sg, su, 2, sorted, items, n_items, a.topk, tg, tu);
+  GemvArgs agu = moe_args(a.x, a.xdt, false, L.slots, a.hidden, gate.f, L.ks_gu, L.tps_gu);
+  agu.nweights = 2;
+  agu.w[0] = moe_weight(gate, g, pgu, tg, 0);
+  agu.w[1] = moe_weight(up, u, pgu + gu_part, tu, a.inter / 128);
+  moe_gemv_launch(gate.f, dim3(2 * (a.inter / 128), L.ks_gu, L.max_items),
+                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, agu, sorted, items,
+                  n_items, a.topk);
   hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
                      a.experts, down.suh, xd, a.inter, a.limit);
-  const GemvArgs sd = moe_side(down, xd, OUT_F16, true, d, pd, L.slots, L.ks_d, L.tps_d);
-  const int kd = down.f.integer_rate() ? down.f.n / 16 : 0;
-  const size_t lds_d = gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, kd == 0);
-  const dim3 gd(a.hidden / 128, L.ks_d, L.max_items);
-  if (down.f.codebook == CB_MCG)
-    moe_gemv_launch<CB_MCG>(kd, gd, lds_d, s, sd, sd, 1, sorted, items, n_items, a.topk, td, td);
-  else
-    moe_gemv_launch<CB_MUL1>(kd, gd, lds_d, s, sd, sd, 1, sorted, items, n_items, a.topk, td, td);
+  GemvArgs ad = moe_args(xd, OUT_F16, true, L.slots, a.inter, down.f, L.ks_d, L.tps_d);
+  ad.nweights = 1;
+  ad.w[0] = moe_weight(down, d, pd, td, 0);
+  moe_gemv_launch(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items),
+                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, ad, sorted, items, n_items,
+                  a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();

@@ -115,6 +115,7 @@ SIGNATURES = {
     "exl3_load_bank": (Verdict, [POINTER(LoadCtx), Str, c_uint32, POINTER(Weight)]),
     "exl3_release": (None, [POINTER(Weight)]),
     "exl3_matmul": (Verdict, [POINTER(Weight), Array, c_void_p, POINTER(Array)]),
+    "exl3_matmul_shared": (Verdict, [POINTER(POINTER(Weight)), c_uint32, Array, c_void_p, POINTER(Array)]),
     "exl3_moe": (Verdict, [POINTER(Weight), Array, Array, Array, c_bool, c_void_p, POINTER(Array)]),
     "exl3_swiglu": (Verdict, [POINTER(Weight), POINTER(Weight), POINTER(Weight), Array, Array, Array,
                               POINTER(SwigluOpts), c_void_p, POINTER(Array)]),
@@ -312,6 +313,16 @@ def matmul(w: Weight, x, out=None, stream=None):
     check(lib().exl3_matmul(ctypes.byref(w), array(x), stream_handle(stream), ctypes.byref(a)),
           "matmul")
     return y
+
+
+def matmul_shared(ws, x, outs=None, stream=None):
+    """Several linears reading the same rows in one launch (outs[i] = x @ W_i^T)."""
+    n = len(ws)
+    ptrs = (POINTER(Weight) * n)(*[ctypes.pointer(w) for w in ws])
+    ys = outs if outs is not None else [_out_tensor(x, w.biases.shape[w.biases.ndim - 1]) for w in ws]
+    arr = (Array * n)(*[array(y) for y in ys])
+    check(lib().exl3_matmul_shared(ptrs, n, array(x), stream_handle(stream), arr), "matmul_shared")
+    return ys
 
 
 def moe(bank: Weight, x, lhs=None, rhs=None, sorted_: bool = False, stream=None) -> Verdict:

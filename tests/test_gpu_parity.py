@@ -313,3 +313,33 @@ def test_swiglu_dense_shared_expert():
                         (td[None], sd[None], vd[None]), np.zeros((4, 1), np.int32),
                         np.ones((4, 1), np.float32), hidden, inter, n)
     assert S.rel_fro(y, want) < 1e-3
+
+
+# ------------------------------------------------------- shared-input linears
+
+@pytest.mark.parametrize("rows", [1, 3, 16, 40])
+def test_matmul_shared_against_oracle(rows):
+    # q/k/v-like linears reading the same rows in one launch
+    # (sushi_ds41/src/sushi/exl3/linear.zig:34-60)
+    rng = np.random.default_rng(600 + rows)
+    in_f, n = 512, 48
+    outs = (256, 128, 384)
+    lins, parts = [], []
+    for o in outs:
+        lin, t, u, v = make(rng, in_f, o, n)
+        lins.append(lin)
+        parts.append((t, u, v, o))
+    x = S.activations(rng, rows, in_f)
+    ys = X.matmul_shared([l.weight for l in lins], dev_f16(x))
+    for y, (t, u, v, o) in zip(ys, parts):
+        yo = S.h2f(O.project(x.astype(np.float32), t, u, v, in_f, o, n))
+        assert y.shape == (rows, o)
+        assert S.rel_fro(y.float().cpu().numpy(), yo) < 1e-3
+
+
+def test_matmul_shared_refuses_mixed_rates():
+    rng = np.random.default_rng(601)
+    a, *_ = make(rng, 256, 128, 48)
+    b, *_ = make(rng, 256, 128, 64)
+    with pytest.raises(X.Exl3Error, match="differ"):
+        X.matmul_shared([a.weight, b.weight], dev_f16(S.activations(rng, 1, 256)))
