@@ -376,14 +376,16 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
   for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
     const float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
-    float v[GEMV_KSPLIT_MAX];
-#pragma unroll
-    for (int k = 0; k < GEMV_KSPLIT_MAX; ++k)
-      if (k < a.ksplit) v[k] = ld_agent(p + (size_t)k * stride);
     float s = 0.0f;
+    for (int k0 = 0; k0 < a.ksplit; k0 += 8) {
+      float v[8];
 #pragma unroll
-    for (int k = 0; k < GEMV_KSPLIT_MAX; ++k)
-      if (k < a.ksplit) s = s + v[k];
+      for (int j = 0; j < 8; ++j)
+        if (k0 + j < a.ksplit) v[j] = ld_agent(p + (size_t)(k0 + j) * stride);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + j < a.ksplit) s = s + v[j];
+    }
     zf[e] = h2f(f2h(s));
   }
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
