@@ -292,25 +292,58 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 }
 
 // The rows' input slice [tk0*16, tk0*16 + ntk*16) prepared into xs (row
-// stride kr halfs): one wave per (row, 128-block).
-__device__ __forceinline__ void gemv_prepare(const GemvArgs &a, const GemvWeight &W, int expert,
-                                             int nrows, const GemvRow *rows, uint16_t *xs, int kr,
-                                             int tk0, int ntk, int wave, int lane) {
-  const int nb = ntk >> 3;
+// stride kr halfs): one wave per (row, 128-block) item.  Loads and
+// arithmetic are split so a workgroup can issue the first items' loads
+// before its weight loads (the prepare is on the critical path; the weights
+// are not needed until it is done).
+constexpr int PREP_BATCH = 2;  // items per wave per batch
+
+struct PrepRegs {
+  float x0[PREP_BATCH], x1[PREP_BATCH], s0[PREP_BATCH], s1[PREP_BATCH];
+};
+
+__device__ __forceinline__ void gemv_prep_load(const GemvArgs &a, const GemvWeight &W, int expert,
+                                               const GemvRow *rows, int nitems, int nb, int tk0,
+                                               int base, int wave, int lane, PrepRegs &r) {
   const int in = a.in_tiles * 16;
-  for (int it = wave; it < nrows * nb; it += GEMV_THREADS / 64) {
-    const int r = it / nb, blk = it - r * nb;
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = base + wave + j * (GEMV_THREADS / 64);
+    if (it >= nitems) break;
+    const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + lane;
-    uint16_t *dst = xs + r * kr + blk * 128 + lane;
+    const size_t xo = (size_t)rows[row].in_off + k;
     if (a.prepared) {
-      const uint16_t *src = (const uint16_t *)a.x + rows[r].in_off + k;
-      dst[0] = src[0];
-      dst[64] = src[64];
+      r.x0[j] = h2f(((const uint16_t *)a.x)[xo]);
+      r.x1[j] = h2f(((const uint16_t *)a.x)[xo + 64]);
+    } else {
+      const uint16_t *su = W.suh + (size_t)expert * in + k;
+      r.x0[j] = load_act(a.x, xo, a.xdt);
+      r.x1[j] = load_act(a.x, xo + 64, a.xdt);
+      r.s0[j] = h2f(su[0]);
+      r.s1[j] = h2f(su[64]);
+    }
+  }
+}
+
+__device__ __forceinline__ void gemv_prep_store(const GemvArgs &a, int nitems, int nb, int base,
+                                                int wave, int lane, uint16_t *xs, int kr,
+                                                const PrepRegs &r) {
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = base + wave + j * (GEMV_THREADS / 64);
+    if (it >= nitems) break;
+    const int row = it / nb, blk = it - row * nb;
+    uint16_t *dst = xs + row * kr + blk * 128 + lane;
+    if (a.prepared) {
+      dst[0] = f2h(r.x0[j]);
+      dst[64] = f2h(r.x1[j]);
       continue;
     }
-    const uint16_t *su = W.suh + (size_t)expert * in + k;
-    float v0 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k, a.xdt))) * h2f(su[0]);
-    float v1 = h2f(f2h(load_act(a.x, (size_t)rows[r].in_off + k + 64, a.xdt))) * h2f(su[64]);
+    // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
+    // (expert_exl3.zig:490-501; expert_exl3_kernels.zig:902-936)
+    float v0 = h2f(f2h(r.x0[j])) * r.s0[j];
+    float v1 = h2f(f2h(r.x1[j])) * r.s1[j];
 #pragma unroll
     for (int bit = 1; bit <= 32; bit <<= 1) {
       const float p0 = __shfl_xor(v0, bit, 64);
@@ -394,7 +427,8 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
 }
 
 // The finish over zf[nrows][128] (f32 holding f16 values): rotation,
-// * 1/sqrt(128), * svh, f16, output dtype; or z itself when y is null.
+// * 1/sqrt(128), * svh, f16, output dtype (one wave per row, the butterfly in
+// registers and lane exchanges); or z itself when y is null.
 __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const GemvWeight &W,
                                             int expert, int nrows, const GemvRow *rows, size_t out,
                                             int col0) {
@@ -405,12 +439,23 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const 
     }
     return;
   }
-  had128_lds(zf, nrows, threadIdx.x, GEMV_THREADS);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint16_t *sv = W.svh + (size_t)expert * out + col0;
-  for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
-    const int b = e >> 7, col = e & 127;
-    const float sc = zf[e] * HAD_SCALE;
-    store_out(W.y, (size_t)rows[b].out_off + col0 + col, f2h(sc * h2f(sv[col])), a.ydt);
+  const float sv0 = h2f(sv[lane]), sv1 = h2f(sv[lane + 64]);
+  for (int b = wave; b < nrows; b += GEMV_THREADS / 64) {
+    float v0 = zf[b * 128 + lane], v1 = zf[b * 128 + lane + 64];
+#pragma unroll
+    for (int bit = 1; bit <= 32; bit <<= 1) {
+      const float p0 = __shfl_xor(v0, bit, 64);
+      const float p1 = __shfl_xor(v1, bit, 64);
+      const bool lower = (lane & bit) == 0;
+      v0 = lower ? v0 + p0 : p0 - v0;
+      v1 = lower ? v1 + p1 : p1 - v1;
+    }
+    const float s0 = (v0 + v1) * HAD_SCALE, s1 = (v0 - v1) * HAD_SCALE;
+    const size_t yo = (size_t)rows[b].out_off + col0;
+    store_out(W.y, yo + lane, f2h(s0 * sv0), a.ydt);
+    store_out(W.y, yo + lane + 64, f2h(s1 * sv1), a.ydt);
   }
 }
 
@@ -438,14 +483,28 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
   const int kb = tk0 + kp * part;
   const int iters = part >> 2;
 
-  // weights of step 0 in flight while the rows are prepared
-  uint32_t nxt[K > 0 ? K : 1];
+  // the first prepare items' loads, then the first two steps' weights, so
+  // the weights are in flight while the rows are prepared
+  const int nb = ntk >> 3, nitems = nrows * nb;
+  PrepRegs pr;
+  gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
+  uint32_t nx0[K > 0 ? K : 1], nx1[K > 0 ? K : 1];
   if constexpr (K > 0) {
     const uint32_t *p0 = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
 #pragma unroll
-    for (int i = 0; i < K; ++i) nxt[i] = p0[i];
+    for (int i = 0; i < K; ++i) nx0[i] = p0[i];
+    if (iters > 1) {
+      const uint32_t *p1 = p0 + (size_t)4 * W.out_tiles * nw;
+#pragma unroll
+      for (int i = 0; i < K; ++i) nx1[i] = p1[i];
+    }
   }
-  gemv_prepare(a, W, expert, nrows, rows, xs, kr, tk0, ntk, wave, lane);
+  gemv_prep_store(a, nitems, nb, 0, wave, lane, xs, kr, pr);
+  for (int base = PREP_BATCH * (GEMV_THREADS / 64); base < nitems;
+       base += PREP_BATCH * (GEMV_THREADS / 64)) {
+    gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, base, wave, lane, pr);
+    gemv_prep_store(a, nitems, nb, base, wave, lane, xs, kr, pr);
+  }
   __syncthreads();
 
   const int arow = min(lane & 15, nrows - 1);
@@ -456,11 +515,14 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
     for (int it = 0; it < iters; ++it) {
       uint32_t wd[K + 1];
 #pragma unroll
-      for (int i = 0; i < K; ++i) wd[i + 1] = nxt[i];
-      if (it + 1 < iters) {
-        const uint32_t *pn = twe + ((size_t)(kb + 4 * (it + 1) + g) * W.out_tiles + tn) * nw + c * K;
+      for (int i = 0; i < K; ++i) {
+        wd[i + 1] = nx0[i];
+        nx0[i] = nx1[i];
+      }
+      if (it + 2 < iters) {
+        const uint32_t *pn = twe + ((size_t)(kb + 4 * (it + 2) + g) * W.out_tiles + tn) * nw + c * K;
 #pragma unroll
-        for (int i = 0; i < K; ++i) nxt[i] = pn[i];
+        for (int i = 0; i < K; ++i) nx1[i] = pn[i];
       }
       wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wd[K]);
       const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
