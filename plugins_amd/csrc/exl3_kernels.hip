@@ -428,9 +428,10 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
 
 // The finish over zf[nrows][128] (f32 holding f16 values): rotation,
 // * 1/sqrt(128), * svh, f16, output dtype (one wave per row, the butterfly in
-// registers and lane exchanges); or z itself when y is null.
+// registers and lane exchanges); or z itself when y is null.  sv holds this
+// lane's svh values (columns lane and lane + 64), loaded at the start.
 __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const GemvWeight &W,
-                                            int expert, int nrows, const GemvRow *rows, size_t out,
+                                            int nrows, const GemvRow *rows, const float (&sv)[2],
                                             int col0) {
   if (W.y == nullptr) {
     for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
@@ -440,8 +441,6 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const 
     return;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint16_t *sv = W.svh + (size_t)expert * out + col0;
-  const float sv0 = h2f(sv[lane]), sv1 = h2f(sv[lane + 64]);
   for (int b = wave; b < nrows; b += GEMV_THREADS / 64) {
     float v0 = zf[b * 128 + lane], v1 = zf[b * 128 + lane + 64];
 #pragma unroll
@@ -454,8 +453,8 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const 
     }
     const float s0 = (v0 + v1) * HAD_SCALE, s1 = (v0 - v1) * HAD_SCALE;
     const size_t yo = (size_t)rows[b].out_off + col0;
-    store_out(W.y, yo + lane, f2h(s0 * sv0), a.ydt);
-    store_out(W.y, yo + lane + 64, f2h(s1 * sv1), a.ydt);
+    store_out(W.y, yo + lane, f2h(s0 * sv[0]), a.ydt);
+    store_out(W.y, yo + lane + 64, f2h(s1 * sv[1]), a.ydt);
   }
 }
 
@@ -483,8 +482,15 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
   const int kb = tk0 + kp * part;
   const int iters = part >> 2;
 
-  // the first prepare items' loads, then the first two steps' weights, so
-  // the weights are in flight while the rows are prepared
+  // svh of the group's columns for the finish, the first prepare items'
+  // loads, then the first two steps' weights, so the weights are in flight
+  // while the rows are prepared
+  float sv[2] = {0.0f, 0.0f};
+  if (W.y != nullptr) {
+    const uint16_t *svp = W.svh + (size_t)expert * out + cg * 128;
+    sv[0] = h2f(svp[lane]);
+    sv[1] = h2f(svp[lane + 64]);
+  }
   const int nb = ntk >> 3, nitems = nrows * nb;
   PrepRegs pr;
   gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
@@ -579,7 +585,7 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   __syncthreads();
   if (!gemv_splitk_last(zf, a, W, nrows, rows, ticket, ks, out, cg * 128)) return;
-  gemv_finish(zf, a, W, expert, nrows, rows, out, cg * 128);
+  gemv_finish(zf, a, W, nrows, rows, sv, cg * 128);
 }
 
 // The weight of grid column group `gx` (weights' groups side by side).
