@@ -26,6 +26,8 @@ DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # the first kernel parameters arrive in SGPRs at wave launch (gfx950)
+    "-mllvm", "-amdgpu-kernarg-preload-count=8",
 ]
 HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 

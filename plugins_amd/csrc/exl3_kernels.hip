@@ -271,16 +271,22 @@ struct GemvWeight {
   int cg0;              // first grid column group of this weight
 };
 
-struct GemvArgs {
-  GemvWeight w[GEMV_MAXW];
-  int nweights;
+// The scalars of a launch, copied into SGPRs at kernel entry with the chosen
+// weight's fields (one round trip of argument loads).
+struct GemvCfg {
   const void *x;  // activations (ACT_*), or prepared rows (f16) when prepared
+  size_t ptotal;
   int xdt;
   int prepared;
   int ydt;
-  size_t ptotal;
   int in_tiles, n, ksplit, tps;
   uint32_t mask;
+};
+
+struct GemvArgs {
+  GemvCfg c;
+  GemvWeight w[GEMV_MAXW];
+  int nweights;
 };
 
 // Dynamic LDS of a GEMV workgroup: row table, prepared rows, the two
@@ -298,11 +304,27 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 // are not needed until it is done).
 constexpr int PREP_BATCH = 2;  // items per wave per batch
 
+// Raw bits as loaded (converted only when the rows are prepared, so the
+// loads do not wait): x holds the two elements (one dword for f16/bf16, two
+// for f32), su the two suh values.
 struct PrepRegs {
-  float x0[PREP_BATCH], x1[PREP_BATCH], s0[PREP_BATCH], s1[PREP_BATCH];
+  uint32_t x0[PREP_BATCH], x1[PREP_BATCH], su[PREP_BATCH];
 };
 
-__device__ __forceinline__ void gemv_prep_load(const GemvArgs &a, const GemvWeight &W, int expert,
+__device__ __forceinline__ void prep_unpack(uint32_t x0, uint32_t x1, int dt, float &a, float &b) {
+  if (dt == OUT_F32) {
+    a = bits<float>(x0);
+    b = bits<float>(x1);
+  } else if (dt == OUT_BF16) {
+    a = bf2f((uint16_t)(x0 & 0xFFFFu));
+    b = bf2f((uint16_t)(x0 >> 16));
+  } else {
+    a = h2f((uint16_t)(x0 & 0xFFFFu));
+    b = h2f((uint16_t)(x0 >> 16));
+  }
+}
+
+__device__ __forceinline__ void gemv_prep_load(const GemvCfg &a, const GemvWeight &W, int expert,
                                                const GemvRow *rows, int nitems, int nb, int tk0,
                                                int base, int wave, int lane, PrepRegs &r) {
   const int in = a.in_tiles * 16;
@@ -311,22 +333,39 @@ __device__ __forceinline__ void gemv_prep_load(const GemvArgs &a, const GemvWeig
     const int it = base + wave + j * (GEMV_THREADS / 64);
     if (it >= nitems) break;
     const int row = it / nb, blk = it - row * nb;
-    const int k = tk0 * 16 + blk * 128 + lane;
+    const int k = tk0 * 16 + blk * 128 + 2 * lane;
     const size_t xo = (size_t)rows[row].in_off + k;
-    if (a.prepared) {
-      r.x0[j] = h2f(((const uint16_t *)a.x)[xo]);
-      r.x1[j] = h2f(((const uint16_t *)a.x)[xo + 64]);
+    if (a.prepared || a.xdt != OUT_F32) {
+      r.x0[j] = *reinterpret_cast<const uint32_t *>((const uint16_t *)a.x + xo);
     } else {
-      const uint16_t *su = W.suh + (size_t)expert * in + k;
-      r.x0[j] = load_act(a.x, xo, a.xdt);
-      r.x1[j] = load_act(a.x, xo + 64, a.xdt);
-      r.s0[j] = h2f(su[0]);
-      r.s1[j] = h2f(su[64]);
+      const u2_t v = *reinterpret_cast<const u2_t *>((const float *)a.x + xo);
+      r.x0[j] = v[0];
+      r.x1[j] = v[1];
     }
+    if (!a.prepared)
+      r.su[j] = *reinterpret_cast<const uint32_t *>(W.suh + (size_t)expert * in + k);
   }
 }
 
-__device__ __forceinline__ void gemv_prep_store(const GemvArgs &a, int nitems, int nb, int base,
+// Element i of a 128-block sits in lane i/2, register i%2: the butterfly's
+// stage on index bit 0 is in-register, bits 1..6 exchange across lanes; each
+// stage is (lo + hi, lo - hi), in bit order, as the reference's kernels
+// compute it (expert_exl3_kernels.zig:902-970).
+__device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
+  const float a = v0 + v1, b = v0 - v1;
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int bit = 1; bit <= 32; bit <<= 1) {
+    const float p0 = __shfl_xor(v0, bit, 64);
+    const float p1 = __shfl_xor(v1, bit, 64);
+    const bool lower = (lane & bit) == 0;
+    v0 = lower ? v0 + p0 : p0 - v0;
+    v1 = lower ? v1 + p1 : p1 - v1;
+  }
+}
+
+__device__ __forceinline__ void gemv_prep_store(const GemvCfg &a, int nitems, int nb, int base,
                                                 int wave, int lane, uint16_t *xs, int kr,
                                                 const PrepRegs &r) {
 #pragma unroll
@@ -334,27 +373,19 @@ __device__ __forceinline__ void gemv_prep_store(const GemvArgs &a, int nitems, i
     const int it = base + wave + j * (GEMV_THREADS / 64);
     if (it >= nitems) break;
     const int row = it / nb, blk = it - row * nb;
-    uint16_t *dst = xs + row * kr + blk * 128 + lane;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
     if (a.prepared) {
-      dst[0] = f2h(r.x0[j]);
-      dst[64] = f2h(r.x1[j]);
+      *dst = r.x0[j];
       continue;
     }
     // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
-    // (expert_exl3.zig:490-501; expert_exl3_kernels.zig:902-936)
-    float v0 = h2f(f2h(r.x0[j])) * r.s0[j];
-    float v1 = h2f(f2h(r.x1[j])) * r.s1[j];
-#pragma unroll
-    for (int bit = 1; bit <= 32; bit <<= 1) {
-      const float p0 = __shfl_xor(v0, bit, 64);
-      const float p1 = __shfl_xor(v1, bit, 64);
-      const bool lower = (lane & bit) == 0;
-      v0 = lower ? v0 + p0 : p0 - v0;
-      v1 = lower ? v1 + p1 : p1 - v1;
-    }
-    const float s0 = v0 + v1, s1 = v0 - v1;
-    dst[0] = f2h(s0 * HAD_SCALE);
-    dst[64] = f2h(s1 * HAD_SCALE);
+    // (expert_exl3.zig:490-501)
+    float x0, x1;
+    prep_unpack(r.x0[j], r.x1[j], a.xdt, x0, x1);
+    float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
+    float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
+    had128_pair(v0, v1, lane);
+    *dst = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
   }
 }
 
@@ -381,7 +412,7 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 // ticket returned.  (A device fence would write back and invalidate the L2
 // in every workgroup.)  The last workgroup issues all of an element's loads
 // before it adds them.
-__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
+__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
                                                  const GemvWeight &W, int nrows,
                                                  const GemvRow *rows, uint32_t *ticket, int ks,
                                                  size_t out, int col0) {
@@ -426,12 +457,27 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvArgs &a,
   return true;
 }
 
+// Stores two consecutive finished f16 values in the output dtype.
+__device__ __forceinline__ void store_out2(void *p, size_t i, uint16_t y0, uint16_t y1, int dt) {
+  if (dt == OUT_F16) {
+    *reinterpret_cast<uint32_t *>((uint16_t *)p + i) = (uint32_t)y0 | ((uint32_t)y1 << 16);
+  } else if (dt == OUT_BF16) {
+    *reinterpret_cast<uint32_t *>((uint16_t *)p + i) =
+        (uint32_t)f2bf(h2f(y0)) | ((uint32_t)f2bf(h2f(y1)) << 16);
+  } else {
+    float2 v;
+    v.x = h2f(y0);
+    v.y = h2f(y1);
+    *reinterpret_cast<float2 *>((float *)p + i) = v;
+  }
+}
+
 // The finish over zf[nrows][128] (f32 holding f16 values): rotation,
-// * 1/sqrt(128), * svh, f16, output dtype (one wave per row, the butterfly in
-// registers and lane exchanges); or z itself when y is null.  sv holds this
-// lane's svh values (columns lane and lane + 64), loaded at the start.
-__device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const GemvWeight &W,
-                                            int nrows, const GemvRow *rows, const float (&sv)[2],
+// * 1/sqrt(128), * svh, f16, output dtype (one wave per row, element i in
+// lane i/2); or z itself when y is null.  sv holds svh of this lane's two
+// columns (2 lane, 2 lane + 1), loaded at the start.
+__device__ __forceinline__ void gemv_finish(float *zf, const GemvCfg &a, const GemvWeight &W,
+                                            int nrows, const GemvRow *rows, uint32_t sv,
                                             int col0) {
   if (W.y == nullptr) {
     for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
@@ -441,27 +487,19 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvArgs &a, const 
     return;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float sv0 = h2f((uint16_t)(sv & 0xFFFFu)), sv1 = h2f((uint16_t)(sv >> 16));
   for (int b = wave; b < nrows; b += GEMV_THREADS / 64) {
-    float v0 = zf[b * 128 + lane], v1 = zf[b * 128 + lane + 64];
-#pragma unroll
-    for (int bit = 1; bit <= 32; bit <<= 1) {
-      const float p0 = __shfl_xor(v0, bit, 64);
-      const float p1 = __shfl_xor(v1, bit, 64);
-      const bool lower = (lane & bit) == 0;
-      v0 = lower ? v0 + p0 : p0 - v0;
-      v1 = lower ? v1 + p1 : p1 - v1;
-    }
-    const float s0 = (v0 + v1) * HAD_SCALE, s1 = (v0 - v1) * HAD_SCALE;
-    const size_t yo = (size_t)rows[b].out_off + col0;
-    store_out(W.y, yo + lane, f2h(s0 * sv[0]), a.ydt);
-    store_out(W.y, yo + lane + 64, f2h(s1 * sv[1]), a.ydt);
+    float v0 = zf[b * 128 + 2 * lane], v1 = zf[b * 128 + 2 * lane + 1];
+    had128_pair(v0, v1, lane);
+    const float s0 = v0 * HAD_SCALE, s1 = v1 * HAD_SCALE;
+    store_out2(W.y, (size_t)rows[b].out_off + col0 + 2 * lane, f2h(s0 * sv0), f2h(s1 * sv1), a.ydt);
   }
 }
 
 // One workgroup of the GEMV: expert `expert` of weight W, nrows <= 16 rows
 // (table `rows` in LDS), column group cg of W, split ks.
 template <int K, int CB, bool MASKED>
-__device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, int expert,
+__device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, int expert,
                                         int nrows, const GemvRow *rows, uint32_t *ticket, int cg,
                                         int ks, char *smem, int rows_alloc) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -485,12 +523,9 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
   // svh of the group's columns for the finish, the first prepare items'
   // loads, then the first two steps' weights, so the weights are in flight
   // while the rows are prepared
-  float sv[2] = {0.0f, 0.0f};
-  if (W.y != nullptr) {
-    const uint16_t *svp = W.svh + (size_t)expert * out + cg * 128;
-    sv[0] = h2f(svp[lane]);
-    sv[1] = h2f(svp[lane + 64]);
-  }
+  uint32_t sv = 0;
+  if (W.y != nullptr)
+    sv = *reinterpret_cast<const uint32_t *>(W.svh + (size_t)expert * out + cg * 128 + 2 * lane);
   const int nb = ntk >> 3, nitems = nrows * nb;
   PrepRegs pr;
   gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
@@ -588,28 +623,29 @@ __device__ __forceinline__ void gemv_wg(const GemvArgs &a, const GemvWeight &W, 
   gemv_finish(zf, a, W, nrows, rows, sv, cg * 128);
 }
 
-// The weight of grid column group `gx` (weights' groups side by side).
-__device__ __forceinline__ int gemv_weight_of(const GemvArgs &a, int gx) {
-  int wi = 0;
-#pragma unroll
-  for (int i = 1; i < GEMV_MAXW; ++i)
-    if (i < a.nweights && gx >= a.w[i].cg0) wi = i;
-  return wi;
+// The weight of grid column group `gx` (weights' groups side by side): the
+// first column groups of weights 1..3 (0 when absent) come as separate
+// kernel parameters, which gfx950 preloads into SGPRs at wave launch, so
+// choosing the weight costs no load and its fields arrive in one round trip.
+__device__ __forceinline__ int gemv_weight_of(int gx, int cg1, int cg2, int cg3) {
+  return (cg1 > 0 && gx >= cg1) + (cg2 > 0 && gx >= cg2) + (cg3 > 0 && gx >= cg3);
 }
 
 template <int K, int CB, bool MASKED>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a, int rows) {
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(int rows, int cg1, int cg2, int cg3,
+                                                            GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int wi = gemv_weight_of(a, blockIdx.x);
-  const GemvWeight &W = a.w[wi];
+  const int wi = gemv_weight_of(blockIdx.x, cg1, cg2, cg3);
+  const GemvCfg c = a.c;
+  const GemvWeight W = a.w[wi];
   const int cg = blockIdx.x - W.cg0;
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, rows - 1);
-    ri[threadIdx.x] = GemvRow{b * a.in_tiles * 16, b * W.out_tiles * 16, b, 0};
+    ri[threadIdx.x] = GemvRow{b * c.in_tiles * 16, b * W.out_tiles * 16, b, 0};
   }
   __syncthreads();
-  gemv_wg<K, CB, MASKED>(a, W, 0, rows, ri, W.ticket + cg, cg, blockIdx.y, smem + 256, rows);
+  gemv_wg<K, CB, MASKED>(c, W, 0, rows, ri, W.ticket + cg, cg, blockIdx.y, smem + 256, rows);
 }
 
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
@@ -695,30 +731,36 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     w.partial = sc[i].partial;
     w.ticket = sc[i].ticket;
   }
-  a.x = x;
-  a.xdt = xdt;
-  a.prepared = prepared ? 1 : 0;
-  a.ydt = ydt;
-  a.ptotal = (size_t)rows;
-  a.in_tiles = in / 16;
-  a.n = f.n;
-  a.ksplit = ksplit;
-  a.tps = tps;
-  a.mask = f.mask();
+  a.c.x = x;
+  a.c.xdt = xdt;
+  a.c.prepared = prepared ? 1 : 0;
+  a.c.ydt = ydt;
+  a.c.ptotal = (size_t)rows;
+  a.c.in_tiles = in / 16;
+  a.c.n = f.n;
+  a.c.ksplit = ksplit;
+  a.c.tps = tps;
+  a.c.mask = f.mask();
   const size_t lds = gemv_lds_bytes(rows, tps, generic);
   const dim3 grid(totcg, ksplit);
+  const int cg1 = count > 1 ? a.w[1].cg0 : 0, cg2 = count > 2 ? a.w[2].cg0 : 0;
+  const int cg3 = count > 3 ? a.w[3].cg0 : 0;
   auto go = [&](auto KC) {
     constexpr int K = decltype(KC)::value;
     if (f.codebook == CB_MCG) {
       if (f.window < 16)
-        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, rows,
+                           cg1, cg2, cg3, a);
       else
-        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s, rows,
+                           cg1, cg2, cg3, a);
     } else {
       if (f.window < 16)
-        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s, rows,
+                           cg1, cg2, cg3, a);
       else
-        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, false>), grid, dim3(GEMV_THREADS), lds, s, a, rows);
+        hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, false>), grid, dim3(GEMV_THREADS), lds, s, rows,
+                           cg1, cg2, cg3, a);
     }
   };
   gemv_dispatch_k<0, false>(generic ? 0 : f.n / 16, go);
@@ -1045,25 +1087,26 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
 // slot / topk of x; prepared inputs are rows slot.
 template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
-    GemvArgs a, const uint32_t *__restrict__ sorted, const MoeItem *__restrict__ items,
-    const uint32_t *__restrict__ n_items, int topk) {
+    int cg1, int topk, const uint32_t *__restrict__ sorted, const MoeItem *__restrict__ items,
+    const uint32_t *__restrict__ n_items, GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.z;
   if ((uint32_t)item >= *n_items) return;
   const MoeItem it = items[item];
-  const int wi = gemv_weight_of(a, blockIdx.x);
-  const GemvWeight &W = a.w[wi];
+  const int wi = gemv_weight_of(blockIdx.x, cg1, 0, 0);
+  const GemvCfg c = a.c;
+  const GemvWeight W = a.w[wi];
   const int cg = blockIdx.x - W.cg0;
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, (int)it.count - 1);
     const int slot = (int)sorted[it.start + b];
-    const int in = a.in_tiles * 16, out = W.out_tiles * 16;
-    ri[threadIdx.x] = GemvRow{(a.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
+    const int in = c.in_tiles * 16, out = W.out_tiles * 16;
+    ri[threadIdx.x] = GemvRow{(c.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
   }
   __syncthreads();
   uint32_t *ticket = W.ticket + (size_t)item * (W.out_tiles / 8) + cg;
-  gemv_wg<K, CB, MASKED>(a, W, (int)it.expert, (int)it.count, ri, ticket, cg, blockIdx.y,
+  gemv_wg<K, CB, MASKED>(c, W, (int)it.expert, (int)it.count, ri, ticket, cg, blockIdx.y,
                          smem + 256, MOE_ITEM_ROWS);
 }
 
@@ -1141,22 +1184,23 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
 void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &a,
                      const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
                      int topk) {
+  const int cg1 = a.nweights > 1 ? a.w[1].cg0 : 0;
   auto go = [&](auto KC) {
     constexpr int K = decltype(KC)::value;
     if (f.codebook == CB_MCG) {
       if (f.window < 16)
-        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, a,
-                           sorted, items, n_items, topk);
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, dim3(GEMV_THREADS), lds, s, cg1,
+                           topk, sorted, items, n_items, a);
       else
-        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s, a,
-                           sorted, items, n_items, topk);
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, dim3(GEMV_THREADS), lds, s,
+                           cg1, topk, sorted, items, n_items, a);
     } else {
       if (f.window < 16)
-        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s, a,
-                           sorted, items, n_items, topk);
+        hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, dim3(GEMV_THREADS), lds, s,
+                           cg1, topk, sorted, items, n_items, a);
       else
         hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, dim3(GEMV_THREADS), lds, s,
-                           a, sorted, items, n_items, topk);
+                           cg1, topk, sorted, items, n_items, a);
     }
   };
   gemv_dispatch_k<0, false>(f.integer_rate() ? f.n / 16 : 0, go);
@@ -1180,16 +1224,16 @@ GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, uint32_t *t
 GemvArgs moe_args(const void *x, int xdt, bool prepared, size_t slots, int in, const Format &f,
                   int ksplit, int tps) {
   GemvArgs a{};
-  a.x = x;
-  a.xdt = xdt;
-  a.prepared = prepared ? 1 : 0;
-  a.ydt = OUT_F16;
-  a.ptotal = slots;
-  a.in_tiles = in / 16;
-  a.n = f.n;
-  a.ksplit = ksplit;
-  a.tps = tps;
-  a.mask = f.mask();
+  a.c.x = x;
+  a.c.xdt = xdt;
+  a.c.prepared = prepared ? 1 : 0;
+  a.c.ydt = OUT_F16;
+  a.c.ptotal = slots;
+  a.c.in_tiles = in / 16;
+  a.c.n = f.n;
+  a.c.ksplit = ksplit;
+  a.c.tps = tps;
+  a.c.mask = f.mask();
   return a;
 }
 
