@@ -143,7 +143,18 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--per-linear", action="store_true",
                     help="one launch per linear instead of one per shared-input group")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only copy a buffer of this many MiB 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.copy_mib:
+        import torch
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_mib": args.copy_mib, "copies": 5}))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the EXL3 path has no multi-GPU leg); "
               "run with --gpus 1", file=sys.stderr)
