@@ -262,6 +262,14 @@ def main() -> int:
         log("cpu baseline")
         cpu = cpu_baseline(args.cpu_seconds)
 
+    # HBM traffic per launch of this workload, measured by the FETCH_SIZE /
+    # WRITE_SIZE counter runs of profiles/gemv_k4_qwen3_8b_decode.md (each
+    # scaled by its plain-copy calibration); null when that file is absent.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemv_k4_qwen3_8b_decode.json")
+    if args.layers == LAYERS and not args.per_linear and os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("traffic_bytes_per_launch")
+
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
@@ -273,7 +281,9 @@ def main() -> int:
                    "linears_per_step": len(lins), "launches_per_step": len(groups),
                    "launch_groups": "per linear" if args.per_linear else "q+k+v, o, gate+up, down"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_unit": "bytes per launch (profiles/gemv_k4_qwen3_8b_decode.md)",
+                     "algorithmic_bytes_per_launch": round(kbytes / len(pairs)),
                      "kernel": "exl3::gemv_kernel<4,0,false> (mul1, K=4, window 16)", "launches": len(pairs),
                      "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
         "cpu_baseline": cpu,
