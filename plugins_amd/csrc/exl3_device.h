@@ -153,11 +153,26 @@ __device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1], uint3
   return decode_pair<CB>(chunk_window<K, 2 * P>(w), chunk_window<K, 2 * P + 1>(w), mask);
 }
 
+// Number of a chunk's codewords whose window straddles dwords J and J+1.
+__host__ __device__ constexpr int chunk_crossings(int K, int J) {
+  int n = 0;
+  for (int i = 0; i < 32; ++i) {
+    const int e = 32 + (i + 1) * K, s = e - 16;
+    if ((s >> 5) == J && ((e - 1) >> 5) == J + 1) ++n;
+  }
+  return n;
+}
+
 // Codeword I of a chunk as a zero-extended 16-bit value, with the cheapest
-// extraction its window allows: v_bfe_u32 when the window lies in one dword,
-// v_perm_b32 when it straddles two dwords on a byte boundary, else
-// v_alignbit_b32 and a mask.  (Stream bit b is bit 31 - b%32 of its dword:
+// extraction its window allows.  (Stream bit b is bit 31 - b%32 of its dword:
 // a window starting at bit o of a dword, o <= 16, is bits 31-o .. 16-o.)
+//  * inside one dword: one v_bfe_u32 (a shift or an and at o = 0, 16);
+//  * straddling dwords J, J+1 where several windows do: the middle dword
+//    T = v_alignbit(w[J], w[J+1], 16) (stream bits 32J+16 .. 32J+47) holds
+//    every such window whole, so each is one v_bfe_u32 of T, and T is
+//    computed once per boundary;
+//  * the only straddling window of its boundary: v_perm_b32 when it starts
+//    on a byte boundary, else v_alignbit_b32 and a mask.
 template <int K, int I>
 __device__ __forceinline__ uint32_t chunk_cw(const uint32_t (&w)[K + 1]) {
   constexpr int E = 32 + (I + 1) * K;
@@ -166,6 +181,10 @@ __device__ __forceinline__ uint32_t chunk_cw(const uint32_t (&w)[K + 1]) {
   static_assert(J0 >= 0 && J1 <= K && J1 - J0 <= 1, "window outside the chunk buffer");
   if constexpr (J0 == J1) {
     return __builtin_amdgcn_ubfe(w[J0], 16 - (S & 31), 16);
+  } else if constexpr (chunk_crossings(K, J0) > 1) {
+    constexpr int o = (S & 31) - 16;  // 1..15: start of the window in T
+    const uint32_t T = __builtin_amdgcn_alignbit(w[J0], w[J1], 16);
+    return __builtin_amdgcn_ubfe(T, 16 - o, 16);
   } else if constexpr ((S & 31) == 24) {
     // the last byte of dword J0, then the first (most significant) of J1
     return __builtin_amdgcn_perm(w[J0], w[J1], 0x0C0C0403u);
@@ -200,6 +219,24 @@ template <int K, int CB, bool MASKED, int P>
 __device__ __forceinline__ uint32_t chunk_pair_cw(const uint32_t (&w)[K + 1], uint32_t mask) {
   return decode_pair_cw<CB, MASKED>(chunk_cw<K, 2 * P>(w), chunk_cw<K, 2 * P + 1>(w), mask);
 }
+
+// mul1 before its affine step: the f16 pair h = (1024 + s1, 1024 + s0), exact
+// integers, with w = f16(h * f16(0x1EEE) + f16(0xC931)).  A dot product over
+// these feeds the affine step afterwards:  sum x (h a + b) = a sum x h +
+// b sum x  (MUL1_A, MUL1_B below).
+template <bool MASKED, int K, int P>
+__device__ __forceinline__ uint32_t chunk_pair_mul1_h(const uint32_t (&w)[K + 1], uint32_t mask) {
+  uint32_t c0 = chunk_cw<K, 2 * P>(w), c1 = chunk_cw<K, 2 * P + 1>(w);
+  if constexpr (MASKED) {
+    c0 &= mask;
+    c1 &= mask;
+  }
+  const uint32_t h = __builtin_amdgcn_sad_u8(c0 * MUL1_MULT, 0u, 0x64006400u);
+  return __builtin_amdgcn_sad_hi_u8(c1 * MUL1_MULT, 0u, h);
+}
+// f16(0x1EEE) and f16(0xC931) as f32 (exact).
+constexpr float MUL1_A = 0.00676727294921875f;
+constexpr float MUL1_B = -10.3828125f;
 
 // ------------------------------------------------------------ generic rate
 

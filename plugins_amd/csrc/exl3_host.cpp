@@ -140,26 +140,24 @@ exl3_array make_array(void *data, int dt, std::initializer_list<int64_t> shape, 
 
 // -------------------------------------------------------------- scratch
 
-// Device scratch per (device, stream): prepared rows, split-K partials and
-// tickets, MoE staging.  Grown on demand (after draining the stream); the
-// tickets are zeroed once and each use leaves them zero.
+// Device scratch per (device, stream): prepared rows, split-K partial-sum
+// slots (GEMV and MoE alike), MoE staging.  Grown on demand (after draining
+// the stream); the slots are set to all-ones bytes (the kernels' empty mark)
+// when allocated, and each use leaves them so.
 struct StreamScratch {
   void *xp = nullptr;
   size_t xp_bytes = 0;
   void *partial = nullptr;
   size_t partial_bytes = 0;
-  void *ticket = nullptr;
-  size_t ticket_bytes = 0;
   void *moe = nullptr;
   size_t moe_bytes = 0;
-  void *moe_ticket = nullptr;
-  size_t moe_ticket_bytes = 0;
 };
 
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, StreamScratch> g_scratch;
 
-hipError_t grow(void **p, size_t *have, size_t need, hipStream_t s, bool zero) {
+// fill: the byte every new allocation is set to, or -1 for none.
+hipError_t grow(void **p, size_t *have, size_t need, hipStream_t s, int fill) {
   if (*have >= need && *p != nullptr) return hipSuccess;
   if (*p != nullptr) {
     hipError_t e = hipStreamSynchronize(s);
@@ -171,8 +169,8 @@ hipError_t grow(void **p, size_t *have, size_t need, hipStream_t s, bool zero) {
   size_t bytes = std::max<size_t>(need, 256);
   hipError_t e = hipMalloc(p, bytes);
   if (e != hipSuccess) return e;
-  if (zero) {
-    e = hipMemsetAsync(*p, 0, bytes, s);
+  if (fill >= 0) {
+    e = hipMemsetAsync(*p, fill, bytes, s);
     if (e != hipSuccess) return e;
   }
   *have = bytes;
@@ -494,25 +492,20 @@ static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t las
 }
 
 // Scratch of one GEMV launch over `count` linears of widths outs[] for
-// `rows` rows: partial sums and (zeroed) tickets, split per linear.
+// `rows` rows: partial-sum slots, split per linear.
 static hipError_t gemv_scratch(StreamScratch *ss, const int *outs, int count, int in, int rows,
                                bool generic, exl3::Scratch *sc, hipStream_t s) {
   int total = 0;
   for (int i = 0; i < count; ++i) total += outs[i];
   int ksplit, tps;
   exl3::gemv_multi_plan(in, total, generic, &ksplit, &tps);
-  hipError_t e = grow(&ss->partial, &ss->partial_bytes, (size_t)ksplit * rows * total * 4, s, false);
+  hipError_t e = grow(&ss->partial, &ss->partial_bytes, (size_t)ksplit * rows * total * 4, s, 0xFF);
   if (e != hipSuccess) return e;
-  e = grow(&ss->ticket, &ss->ticket_bytes, (size_t)(total / 128) * 4, s, true);
-  if (e != hipSuccess) return e;
-  size_t po = 0, to = 0;
+  size_t po = 0;
   for (int i = 0; i < count; ++i) {
     sc[i].partial = (float *)ss->partial + po;
     sc[i].partial_floats = (size_t)ksplit * rows * outs[i];
-    sc[i].ticket = (uint32_t *)ss->ticket + to;
-    sc[i].tickets = (size_t)outs[i] / 128;
     po += sc[i].partial_floats;
-    to += sc[i].tickets;
   }
   return hipSuccess;
 }
@@ -534,7 +527,7 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
     for (int i = 0; i < count; ++i) {
       const uint16_t *xp = (const uint16_t *)x;
       if (!prepared) {
-        hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, false);
+        hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, -1);
         if (e != hipSuccess) return e;
         for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
           const int r = (int)std::min<int64_t>(65535, rows - r0);
@@ -712,15 +705,15 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
                    (const uint16_t *)down->biases.data, pd->f, (int)pd->in, (int)pd->out};
   StreamScratch *ss = scratch_for(pg->device, s);
   std::lock_guard<std::mutex> g(g_scratch_mu);
-  size_t ntick = 0;
+  size_t nslots = 0;
   const size_t need =
-      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &ntick);
-  hipError_t e = grow(&ss->moe, &ss->moe_bytes, need, s, false);
+      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &nslots);
+  hipError_t e = grow(&ss->moe, &ss->moe_bytes, need, s, -1);
   if (e != hipSuccess) return hip_failed(e);
-  e = grow(&ss->moe_ticket, &ss->moe_ticket_bytes, ntick * 4, s, true);
+  e = grow(&ss->partial, &ss->partial_bytes, nslots * 4, s, 0xFF);
   if (e != hipSuccess) return hip_failed(e);
-  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, (uint32_t *)ss->moe_ticket,
-                       ss->moe_ticket_bytes / 4, s);
+  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, (float *)ss->partial,
+                       ss->partial_bytes / 4, s);
   if (e != hipSuccess) {
     if (e == hipErrorInvalidValue) return kShape;
     return hip_failed(e);

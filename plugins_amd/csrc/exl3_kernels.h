@@ -22,15 +22,13 @@ struct Format {
   bool integer_rate() const { return n % 16 == 0 && n >= 16 && n <= 128; }
 };
 
-// Device scratch a matmul uses: split-K partial sums and per-column-group
-// tickets (zero between calls: the last workgroup of a group resets its own).
+// Device scratch a matmul uses: split-K partial-sum slots, each holding the
+// empty mark (all-ones bytes) between calls: every call leaves the slots it
+// used empty again, so one slot buffer serves any sequence of calls on one
+// stream whatever their shapes.
 struct Scratch {
   float *partial = nullptr;
   size_t partial_floats = 0;
-  uint32_t *ticket = nullptr;
-  size_t tickets = 0;
-  void *bytes = nullptr;  // generic staging (MoE routing, prepared rows)
-  size_t nbytes = 0;
 };
 
 // Output / activation element types understood by the kernels.
@@ -77,8 +75,7 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
                        int out, hipStream_t s);
 // The split of one GEMV launch over weights of total output width
-// total_out: a linear of width out needs ksplit * rows * out partial floats
-// and out / 128 tickets.
+// total_out: a linear of width out needs ksplit * rows * out partial floats.
 void gemv_multi_plan(int in, int total_out, bool generic, int *ksplit, int *tps);
 
 // ------------------------------------------------------------------- MoE
@@ -107,11 +104,12 @@ struct MoeArgs {
   void *y;
   int ydt;
 };
-// Scratch bytes for a call, and (in *tickets) the count of u32 tickets it
-// needs in a separate buffer that starts zeroed and is left zeroed.
-size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic, size_t *tickets);
+// Staging bytes for a call, and (in *partial_floats) the partial-sum slots
+// it needs (a Scratch slot buffer: empty between calls, left empty).
+size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
+                         size_t *partial_floats);
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
-                      const MoeBank &down, void *scratch, size_t scratch_bytes, uint32_t *tickets,
-                      size_t ntickets, hipStream_t s);
+                      const MoeBank &down, void *scratch, size_t scratch_bytes, float *partial,
+                      size_t partial_floats, hipStream_t s);
 
 }  // namespace exl3

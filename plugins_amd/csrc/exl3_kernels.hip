@@ -239,11 +239,14 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 //     a+8, rows 0-7 / 8-15), and v_mfma_f32_16x16x32_f16 sums them against
 //     the rows' activations (A operands from LDS) over the step's 4 k-tile
 //     rows.  MFMA rows are the call's rows: 1..16 rows cost one decode;
-//  3. the two k-parts add in LDS; the per-row sums go to scratch, and the
-//     last workgroup of the column group (a ticket counter) adds the splits
-//     in split order, rounds z to f16 and runs the finish (Hadamard-128,
-//     * svh) on its 128 columns.  Every sum is in a fixed order that does not
-//     depend on how many rows share the call.
+//  3. the two k-parts add in LDS; the other splits' per-row sums go to
+//     scratch slots, and the workgroup of the last split (the highest
+//     workgroup index of the column group) adds the splits in split order,
+//     rounds z to f16 and runs the finish (Hadamard-128, * svh) on its 128
+//     columns.  Every sum is in a fixed order that does not depend on how
+//     many rows share the call.
+//  With mul1 at an integer rate the MFMAs take the codebook value before its
+//  affine step (chunk_pair_mul1_h) and the step is applied to the sums.
 
 constexpr int GEMV_THREADS = 512;
 constexpr int GEMV_ROWS = 16;
@@ -264,8 +267,7 @@ struct GemvWeight {
   const uint16_t *svh;  // [E][out]
   void *y;              // finished output in ydt, or nullptr:
   uint16_t *zout;       // the inner product z (f16) instead
-  float *partial;       // [ksplit][ptotal][out]
-  uint32_t *ticket;     // [groups][out/128], zero between calls
+  float *partial;       // [ksplit][ptotal][out] slots, empty between calls
   size_t expert_words;  // dwords per expert
   int out_tiles;
   int cg0;              // first grid column group of this weight
@@ -290,10 +292,12 @@ struct GemvArgs {
 };
 
 // Dynamic LDS of a GEMV workgroup: row table, prepared rows, the two
-// k-parts' z tiles, and (generic rate) a word stage per wave.
+// k-parts' z tiles, the prepared rows' sums per 64 elements, and (generic
+// rate) a word stage per wave.
 __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, bool generic) {
   return 256 + (size_t)rows_alloc * (tps * 16 + 8) * 2 +
          (size_t)2 * (rows_alloc > 2 ? rows_alloc : 2) * 128 * 4 +
+         (size_t)rows_alloc * (tps / 4) * 4 +
          (generic ? (size_t)(GEMV_THREADS / 64) * 512 * 4 : 0);
 }
 
@@ -365,27 +369,38 @@ __device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
   }
 }
 
+// Stores the prepared pairs; with hsum (row stride nb * 2) also the sum of
+// each 64 prepared elements (lanes 0-31 and 32-63 of an item), added in a
+// fixed butterfly order.
 __device__ __forceinline__ void gemv_prep_store(const GemvCfg &a, int nitems, int nb, int base,
                                                 int wave, int lane, uint16_t *xs, int kr,
-                                                const PrepRegs &r) {
+                                                const PrepRegs &r, float *hsum) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
     const int it = base + wave + j * (GEMV_THREADS / 64);
     if (it >= nitems) break;
     const int row = it / nb, blk = it - row * nb;
     uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
+    uint32_t y;
     if (a.prepared) {
-      *dst = r.x0[j];
-      continue;
+      y = r.x0[j];
+    } else {
+      // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
+      // (expert_exl3.zig:490-501)
+      float x0, x1;
+      prep_unpack(r.x0[j], r.x1[j], a.xdt, x0, x1);
+      float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
+      float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
+      had128_pair(v0, v1, lane);
+      y = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
     }
-    // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
-    // (expert_exl3.zig:490-501)
-    float x0, x1;
-    prep_unpack(r.x0[j], r.x1[j], a.xdt, x0, x1);
-    float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
-    float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
-    had128_pair(v0, v1, lane);
-    *dst = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+    *dst = y;
+    if (hsum != nullptr) {
+      float s = h2f((uint16_t)(y & 0xFFFFu)) + h2f((uint16_t)(y >> 16));
+#pragma unroll
+      for (int m = 1; m < 32; m <<= 1) s = s + __shfl_xor(s, m, 64);
+      if ((lane & 31) == 0) hsum[row * nb * 2 + blk * 2 + (lane >> 5)] = s;
+    }
   }
 }
 
@@ -404,19 +419,26 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 }
 
 // Split-K hand-off over zf[nrows][128] (this workgroup's f32 sums): returns
-// true in the last workgroup of the column group with z = f16(sum over
-// splits, in split order) in zf.  The partial sums and the ticket are
-// agent-scope atomics, coherent across the XCDs' L2s on their own, so no
-// fence is needed, only order: each wave waits for its stores to be
-// acknowledged before the barrier, and the last workgroup loads after its
-// ticket returned.  (A device fence would write back and invalidate the L2
-// in every workgroup.)  The last workgroup issues all of an element's loads
-// before it adds them.
+// true in the workgroup of the last split, with z = f16(sum over splits, in
+// split order) in zf.  Partial-sum slots hold PARTIAL_EMPTY (a NaN bit
+// pattern no arithmetic produces) between calls.  The other splits store
+// their sums and exit; the last split's workgroup reads their slots,
+// re-reading each one until its store has landed, then puts PARTIAL_EMPTY
+// back.  It never waits on a workgroup that has not started: the last split
+// has the highest workgroup index of its column group, and workgroups are
+// dispatched in index order, so every slot it waits for belongs to a
+// workgroup already running, whose stores land within a memory round trip
+// (PARTIAL_POLL_MAX bounds the wait regardless: a slot still empty then
+// makes the sum NaN).  Slots are agent-scope atomics, coherent across the
+// XCDs' L2s, so no fence is needed.  (A device fence would write back and
+// invalidate the L2 in every workgroup.)
+constexpr uint32_t PARTIAL_EMPTY = 0xFFFFFFFFu;
+constexpr int PARTIAL_POLL_MAX = 1 << 20;
+
 __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
                                                  const GemvWeight &W, int nrows,
-                                                 const GemvRow *rows, uint32_t *ticket, int ks,
-                                                 size_t out, int col0) {
-  __shared__ int s_last;
+                                                 const GemvRow *rows, int ks, size_t out,
+                                                 int col0) {
   const int E = nrows * 128;
   if (a.ksplit == 1) {
     for (int e = threadIdx.x; e < E; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
@@ -424,35 +446,39 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
     return true;
   }
   const size_t stride = a.ptotal * out;
-  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
-    const int b = e >> 7, col = e & 127;
-    st_agent(W.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, zf[e]);
-  }
-  wait_stores();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)a.ksplit - 1u) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return false;
-  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
-    const int b = e >> 7, col = e & 127;
-    const float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
-    float s = 0.0f;
-    for (int k0 = 0; k0 < a.ksplit; k0 += 8) {
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (k0 + j < a.ksplit) v[j] = ld_agent(p + (size_t)(k0 + j) * stride);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (k0 + j < a.ksplit) s = s + v[j];
+  if (ks != a.ksplit - 1) {
+    for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
+      const int b = e >> 7, col = e & 127;
+      float v = zf[e];
+      if (v != v) v = bits<float>(0x7FC00000u);  // never PARTIAL_EMPTY
+      st_agent(W.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, v);
     }
-    zf[e] = h2f(f2h(s));
+    return false;
   }
-  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float empty = bits<float>(PARTIAL_EMPTY);
+  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
+    const int b = e >> 7, col = e & 127;
+    float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
+    float s = 0.0f;
+    for (int k0 = 0; k0 < ks; k0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (k0 + j < ks) v[j] = ld_agent(p + (size_t)(k0 + j) * stride);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (k0 + j >= ks) break;
+        float *slot = p + (size_t)(k0 + j) * stride;
+        for (int n = 0; bits<uint32_t>(v[j]) == PARTIAL_EMPTY && n < PARTIAL_POLL_MAX; ++n) {
+          __builtin_amdgcn_s_sleep(2);
+          v[j] = ld_agent(slot);
+        }
+        st_agent(slot, empty);
+        s = s + v[j];
+      }
+    }
+    zf[e] = h2f(f2h(s + zf[e]));
+  }
   __syncthreads();
   return true;
 }
@@ -500,7 +526,7 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvCfg &a, const G
 // (table `rows` in LDS), column group cg of W, split ks.
 template <int K, int CB, bool MASKED>
 __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, int expert,
-                                        int nrows, const GemvRow *rows, uint32_t *ticket, int cg,
+                                        int nrows, const GemvRow *rows, int cg,
                                         int ks, char *smem, int rows_alloc) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -512,6 +538,12 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
   uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
   const int zrows = rows_alloc > 2 ? rows_alloc : 2;
   float *zp = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);  // [2][zrows][128]
+  // mul1 at an integer rate: the MFMAs take h (the codebook value before its
+  // affine step, chunk_pair_mul1_h), and z = a * acc + b * (sum of the
+  // k-part's prepared activations) afterwards, from the 64-element sums
+  // hsum[row][ntk / 4] that the prepare leaves
+  constexpr bool FOLD = K > 0 && CB == CB_MUL1;
+  float *hsum = zp + 2 * zrows * 128;
   const int nw = a.n >> 1;
   const int g = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
   const size_t tn = (size_t)cg * 8 + 2 * q + t;
@@ -529,22 +561,29 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
   const int nb = ntk >> 3, nitems = nrows * nb;
   PrepRegs pr;
   gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
-  uint32_t nx0[K > 0 ? K : 1], nx1[K > 0 ? K : 1];
+  // three steps' weights in flight: step i uses buffer i % 3 and then loads
+  // step i + 3 into it
+  constexpr int KB = K > 0 ? K : 1;
+  uint32_t b0[KB], b1[KB], b2[KB];
+  const uint32_t *wp = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
+  const size_t wstep = (size_t)4 * W.out_tiles * nw;  // dwords per step
   if constexpr (K > 0) {
-    const uint32_t *p0 = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
 #pragma unroll
-    for (int i = 0; i < K; ++i) nx0[i] = p0[i];
+    for (int i = 0; i < K; ++i) b0[i] = wp[i];
     if (iters > 1) {
-      const uint32_t *p1 = p0 + (size_t)4 * W.out_tiles * nw;
 #pragma unroll
-      for (int i = 0; i < K; ++i) nx1[i] = p1[i];
+      for (int i = 0; i < K; ++i) b1[i] = wp[wstep + i];
+    }
+    if (iters > 2) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) b2[i] = wp[2 * wstep + i];
     }
   }
-  gemv_prep_store(a, nitems, nb, 0, wave, lane, xs, kr, pr);
+  gemv_prep_store(a, nitems, nb, 0, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
   for (int base = PREP_BATCH * (GEMV_THREADS / 64); base < nitems;
        base += PREP_BATCH * (GEMV_THREADS / 64)) {
     gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, base, wave, lane, pr);
-    gemv_prep_store(a, nitems, nb, base, wave, lane, xs, kr, pr);
+    gemv_prep_store(a, nitems, nb, base, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
   }
   __syncthreads();
 
@@ -553,32 +592,51 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
   f4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (K > 0) {
     const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
-    for (int it = 0; it < iters; ++it) {
+    auto step = [&](uint32_t(&b)[KB], int it) {
       uint32_t wd[K + 1];
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        wd[i + 1] = nx0[i];
-        nx0[i] = nx1[i];
-      }
-      if (it + 2 < iters) {
-        const uint32_t *pn = twe + ((size_t)(kb + 4 * (it + 2) + g) * W.out_tiles + tn) * nw + c * K;
-#pragma unroll
-        for (int i = 0; i < K; ++i) nx1[i] = pn[i];
-      }
-      wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wd[K]);
+      for (int i = 0; i < K; ++i) wd[i + 1] = b[i];
+      wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)b[K - 1]);
       const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
       const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
-      uint32_t p[16];
-      static_for<16>([&](auto P) {
-        constexpr int pq = decltype(P)::value;
-        p[pq] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
+      // one B operand at a time (pairs f, f+4, f+8, f+12: rows 0-7 or 8-15 of
+      // column a or a+8), each consumed by its MFMA before the next is made
+      static_for<4>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
+        uint32_t q[4];
+        static_for<4>([&](auto J) {
+          constexpr int pq = p0 + 4 * decltype(J)::value;
+          if constexpr (FOLD)
+            q[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.mask);
+          else
+            q[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
+        });
+        const h8_t bf = frag(q[0], q[1], q[2], q[3]);
+        if constexpr (f == 0) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc0, 0, 0, 0);
+        if constexpr (f == 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc1, 0, 0, 0);
+        if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
+        if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
       });
-      gemv_mfma(p, alo, ahi, acc0, acc1);
+      if (it + 3 < iters) {
+        const uint32_t *pn = wp + (size_t)(it + 3) * wstep;
+#pragma unroll
+        for (int i = 0; i < K; ++i) b[i] = pn[i];
+      }
+    };
+    int it = 0;
+    for (; it + 3 <= iters; it += 3) {
+      step(b0, it);
+      step(b1, it + 1);
+      step(b2, it + 2);
     }
+    if (it < iters) step(b0, it);
+    if (it + 1 < iters) step(b1, it + 1);
   } else {
     // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
     uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
-                                                   (size_t)2 * zrows * 128 * 4) +
+                                                   (size_t)2 * zrows * 128 * 4 +
+                                                   (size_t)rows_alloc * (a.tps / 4) * 4) +
                       wave * 512;
     for (int it = 0; it < iters; ++it) {
       for (int i = lane; i < 8 * nw; i += 64) {
@@ -611,15 +669,25 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * g + i;
     if (m < nrows) {
-      zk[m * 128 + col] = acc0[i];
-      zk[m * 128 + col + 8] = acc1[i];
+      float z0 = acc0[i], z1 = acc1[i];
+      if constexpr (FOLD) {
+        // the k-part's 64-element sums of row m, in k order
+        const float *hs = hsum + m * nb * 2 + kp * (part >> 2);
+        float sx = 0.0f;
+        for (int h = 0; h < (part >> 2); ++h) sx = sx + hs[h];
+        const float bx = MUL1_B * sx;
+        z0 = MUL1_A * z0 + bx;
+        z1 = MUL1_A * z1 + bx;
+      }
+      zk[m * 128 + col] = z0;
+      zk[m * 128 + col + 8] = z1;
     }
   }
   __syncthreads();
   float *zf = zp;
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   __syncthreads();
-  if (!gemv_splitk_last(zf, a, W, nrows, rows, ticket, ks, out, cg * 128)) return;
+  if (!gemv_splitk_last(zf, a, W, nrows, rows, ks, out, cg * 128)) return;
   gemv_finish(zf, a, W, nrows, rows, sv, cg * 128);
 }
 
@@ -632,7 +700,7 @@ __device__ __forceinline__ int gemv_weight_of(int gx, int cg1, int cg2, int cg3)
 }
 
 template <int K, int CB, bool MASKED>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(int rows, int cg1, int cg2, int cg3,
+__global__ __launch_bounds__(GEMV_THREADS, 8) void gemv_kernel(int rows, int cg1, int cg2, int cg3,
                                                             GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int wi = gemv_weight_of(blockIdx.x, cg1, cg2, cg3);
@@ -645,7 +713,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(int rows, int cg1, i
     ri[threadIdx.x] = GemvRow{b * c.in_tiles * 16, b * W.out_tiles * 16, b, 0};
   }
   __syncthreads();
-  gemv_wg<K, CB, MASKED>(c, W, 0, rows, ri, W.ticket + cg, cg, blockIdx.y, smem + 256, rows);
+  gemv_wg<K, CB, MASKED>(c, W, 0, rows, ri, cg, blockIdx.y, smem + 256, rows);
 }
 
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
@@ -725,11 +793,8 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     if (ksplit > 1) {
       if (sc[i].partial == nullptr || sc[i].partial_floats < (size_t)ksplit * rows * ls[i].out)
         return hipErrorInvalidValue;
-      if (sc[i].ticket == nullptr || sc[i].tickets < (size_t)ls[i].out / 128)
-        return hipErrorInvalidValue;
     }
     w.partial = sc[i].partial;
-    w.ticket = sc[i].ticket;
   }
   a.c.x = x;
   a.c.xdt = xdt;
@@ -776,18 +841,21 @@ hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, 
 
 // ===================================================================== GEMM
 //
-// Workgroup tile 128 rows x 128 columns (one Hadamard block of the output),
-// 4 waves in a 2x2 grid of 64x64 sub-tiles, each 2x2 v_mfma_f32_32x32x16_f16
-// tiles with f32 accumulators.  The k loop runs in stages of 32 (two k-tile
-// rows of 8 output tiles = 16 tiles = 128 chunks); every thread decodes half
-// a chunk (16 codewords) of the next stage into the other LDS buffer while the
-// MFMAs consume the current one.  The B^T tile sits in LDS as [n][k] with k
-// contiguous (a chunk's column is 16 consecutive k), so an MFMA B operand (8
-// consecutive k of one column) is one ds_read_b128; A operands (prepared
-// activations, row-major f16) load straight from global memory in operand
-// layout.  The epilogue rounds z to f16 in LDS and runs the finish per row.
+// Workgroup tile 256 rows x 128 columns (one Hadamard block of the output),
+// 8 waves in a 4 x 2 grid of 64 x 64 sub-tiles, each 2 x 2
+// v_mfma_f32_32x32x16_f16 tiles with f32 accumulators.  The k loop runs in
+// stages of 64 (four k-tile rows of 8 output tiles = 32 tiles = 256 chunks);
+// every thread decodes half a chunk (16 codewords) of the next stage into the
+// other LDS buffer after the MFMAs of the current one are issued, so the
+// decode's VALU work overlaps the matrix cores.  The B^T tile sits in LDS as
+// [n][k] with k contiguous (a chunk's column is 16 consecutive k), so an
+// MFMA B operand (8 consecutive k of one column) is one ds_read_b128.  A
+// operands (prepared activations, row-major f16) load straight from global
+// memory in operand layout, two stages ahead, as do the packed words.  The
+// epilogue rounds z to f16 in LDS and runs the finish per row.  Each decoded
+// weight serves 256 rows.
 
-constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_THREADS = 256;
+constexpr int GM_BM = 256, GM_BN = 128, GM_BK = 64, GM_THREADS = 512;
 constexpr int GM_LDK = GM_BK + 8;  // k stride (halfs) of a B^T column in LDS
 constexpr int GM_ZLD = GM_BN + 8;  // column stride (halfs) of the z tile
 constexpr int GM_LDS_HALFS =
@@ -795,12 +863,12 @@ constexpr int GM_LDS_HALFS =
 
 // Decodes this thread's half chunk (codewords 16h..16h+15: pairs 8h..8h+7)
 // into bt (LDS).  h is uniform per wave, so only one arm runs.
-template <int K, int CB, int H>
+template <int K, int CB, bool MASKED, int H>
 __device__ __forceinline__ void gemm_decode_half(const uint32_t (&wd)[K + 1], uint32_t *btw,
                                                  int tkl, int tnl, int c, uint32_t mask) {
   static_for<8>([&](auto Q) {
     constexpr int p = decltype(Q)::value + 8 * H;
-    const uint32_t v = chunk_pair<K, CB, p>(wd, mask);
+    const uint32_t v = chunk_pair_cw<K, CB, MASKED, p>(wd, mask);
     constexpr int r = chunk_row(2 * p);
     constexpr int ch = chunk_colhalf(2 * p);
     const int nl = tnl * 16 + c + 8 * ch;
@@ -809,45 +877,110 @@ __device__ __forceinline__ void gemm_decode_half(const uint32_t (&wd)[K + 1], ui
   });
 }
 
-template <int K, int CB>
-__device__ __forceinline__ void gemm_decode_stage(const uint32_t (&wd)[K + 1], uint16_t *bt,
-                                                  int tkl, int tnl, int c, int h, uint32_t mask) {
-  uint32_t *btw = reinterpret_cast<uint32_t *>(bt);
-  if (h)
-    gemm_decode_half<K, CB, 1>(wd, btw, tkl, tnl, c, mask);
-  else
-    gemm_decode_half<K, CB, 0>(wd, btw, tkl, tnl, c, mask);
-}
-
+// The K dwords of this thread's chunk, and (first half) the history dword:
+// the last dword of the previous chunk of the tile, circularly.  Codewords
+// 16..31 of a chunk never reach the history dword.
 template <int K>
-__device__ __forceinline__ void gemm_load_words(const uint32_t *__restrict__ tw, size_t tbase,
-                                                int c, int h, uint32_t (&wd)[K + 1]) {
-  const uint32_t *tp = tw + tbase;
+__device__ __forceinline__ void gemm_load_words(const uint32_t *__restrict__ tp, int c, int h,
+                                                uint32_t (&wd)[K + 1]) {
 #pragma unroll
   for (int i = 0; i < K; ++i) wd[i + 1] = tp[c * K + i];
-  // codewords 16..31 of a chunk never reach the history dword
   wd[0] = h ? 0u : tp[((c + 7) & 7) * K + (K - 1)];
 }
 
-template <int K, int CB>
+// A operands of one stage: a[kk][i] = rows (lane & 31) + 32 i of the wave's
+// 64, k = 16 kk + 8 (lane / 32) .. +7 of the stage.  Rows past M read row 0
+// instead (their results are not stored; rows of an MFMA are independent),
+// so the loads need no branch.
+__device__ __forceinline__ void gemm_load_a(const uint16_t *ap0, const uint16_t *ap1, int k0,
+                                            h8_t (&a)[4][2]) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    a[kk][0] = *reinterpret_cast<const h8_t *>(ap0 + k0 + kk * 16);
+    a[kk][1] = *reinterpret_cast<const h8_t *>(ap1 + k0 + kk * 16);
+  }
+}
+
+// The main loop of one wave: decoder half H (uniform per wave, so the loop
+// body has no branch and the scheduler can interleave the decode's VALU work
+// and the A loads between the MFMAs: one basic block per stage).  Loads past
+// the last stage re-read the last stage (in bounds, unused).
+template <int K, int CB, bool MASKED, int H>
+__device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
+                                          const uint32_t *twc, size_t wstage,
+                                          const uint16_t *ap0, const uint16_t *ap1, int bn0,
+                                          int stages, int tkl, int tnl, int c, uint32_t mask) {
+  h8_t aA[4][2], aB[4][2];
+  uint32_t wdA[K + 1], wdB[K + 1];
+  {
+    uint32_t wd0[K + 1];
+    gemm_load_words<K>(twc, c, H, wd0);
+    gemm_load_a(ap0, ap1, 0, aA);
+    gemm_load_words<K>(twc + wstage, c, H, wdB);
+    gemm_load_a(ap0, ap1, GM_BK, aB);
+    gemm_load_words<K>(twc + (size_t)min(2, stages - 1) * wstage, c, H, wdA);
+    gemm_decode_half<K, CB, MASKED, H>(wd0, reinterpret_cast<uint32_t *>(lds), tkl, tnl, c, mask);
+  }
+  __syncthreads();
+
+  // stage st: MFMAs on buffer st & 1 with operands a, then A of stage st + 2
+  // into a, the decode of stage st + 1 (words in wd) into the other buffer,
+  // and the words of stage st + 3 into wd
+  auto stage = [&](h8_t(&a)[4][2], uint32_t(&wd)[K + 1], int st) {
+    const uint16_t *cur = lds + (st & 1) * (GM_BN * GM_LDK);
+    uint16_t *nxt = lds + ((st + 1) & 1) * (GM_BN * GM_LDK);
+    h8_t b[4][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      b[kk][0] = *reinterpret_cast<const h8_t *>(cur + bn0 + kk * 16);
+      b[kk][1] = *reinterpret_cast<const h8_t *>(cur + bn0 + 32 * GM_LDK + kk * 16);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][0], b[kk][0], acc[0][0], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][1], b[kk][0], acc[1][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][0], b[kk][1], acc[0][1], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][1], b[kk][1], acc[1][1], 0, 0, 0);
+    }
+    gemm_load_a(ap0, ap1, min(st + 2, stages - 1) * GM_BK, a);
+    gemm_decode_half<K, CB, MASKED, H>(wd, reinterpret_cast<uint32_t *>(nxt), tkl, tnl, c, mask);
+    gemm_load_words<K>(twc + (size_t)min(st + 3, stages - 1) * wstage, c, H, wd);
+    // B operands first, then each MFMA followed by a share of the VALU work
+    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x0002, 5, 0);  // VALU
+      if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+    }
+    __syncthreads();
+  };
+  for (int st = 0; st < stages; st += 2) {
+    stage(aA, wdB, st);
+    stage(aB, wdA, st + 1);
+  }
+}
+
+template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
     int M, int in_tiles, int out_tiles, uint32_t mask) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_HALFS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 1, wc = wave & 1;
   const int cg = blockIdx.x;
   const int m0 = blockIdx.y * GM_BM;
   const int in = in_tiles * 16;
   const size_t out = (size_t)out_tiles * 16;
   const int nw = 8 * K;
-  // decoder role: 16 tiles (2 k-tile rows x 8 output tiles) x 8 chunks = 128
+  // decoder role: 32 tiles (4 k-tile rows x 8 output tiles) x 8 chunks = 256
   // chunks; waves 2q and 2q+1 take chunks 64q..64q+63, halves 0 and 1.
-  const int h = __builtin_amdgcn_readfirstlane(wave & 1);
   const int chunk_id = (wave >> 1) * 64 + lane;
   const int tl = chunk_id >> 3, tkl = tl >> 3, tnl = tl & 7, c = chunk_id & 7;
-  const size_t tcol = (size_t)cg * 8 + tnl;
+  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + (size_t)cg * 8 + tnl) * nw;
+  const size_t wstage = (size_t)4 * out_tiles * nw;  // dwords per stage
 
   f16v_t acc[2][2];
 #pragma unroll
@@ -860,42 +993,15 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
   // A operand rows of this lane (rows past M read as zero)
   const int arow0 = m0 + wr * 64 + (lane & 31);
   const int akoff = 8 * (lane >> 5);
-  const bool aok0 = arow0 < M, aok1 = arow0 + 32 < M;
-  const uint16_t *ap0 = xp + (size_t)(aok0 ? arow0 : 0) * in + akoff;
-  const uint16_t *ap1 = xp + (size_t)(aok1 ? arow0 + 32 : 0) * in + akoff;
-
-  const int stages = in_tiles / 2;
-  uint32_t wd[K + 1];
-  gemm_load_words<K>(tw, ((size_t)tkl * out_tiles + tcol) * nw, c, h, wd);
-  gemm_decode_stage<K, CB>(wd, lds, tkl, tnl, c, h, mask);
-  __syncthreads();
-
-  for (int st = 0; st < stages; ++st) {
-    uint16_t *cur = lds + (st & 1) * (GM_BN * GM_LDK);
-    uint16_t *nxt = lds + ((st + 1) & 1) * (GM_BN * GM_LDK);
-    const bool more = st + 1 < stages;
-    if (more) gemm_load_words<K>(tw, ((size_t)(2 * (st + 1) + tkl) * out_tiles + tcol) * nw, c, h, wd);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int k0 = st * GM_BK + kk * 16;
-      h8_t a0 = {}, a1 = {};
-      if (aok0) a0 = *reinterpret_cast<const h8_t *>(ap0 + k0);
-      if (aok1) a1 = *reinterpret_cast<const h8_t *>(ap1 + k0);
-      h8_t b[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int nl = wc * 64 + j * 32 + (lane & 31);
-        b[j] = *reinterpret_cast<const h8_t *>(cur + nl * GM_LDK + kk * 16 + akoff);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b[j], acc[0][j], 0, 0, 0);
-        acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b[j], acc[1][j], 0, 0, 0);
-      }
-    }
-    if (more) gemm_decode_stage<K, CB>(wd, nxt, tkl, tnl, c, h, mask);
-    __syncthreads();
-  }
+  const uint16_t *ap0 = xp + (size_t)(arow0 < M ? arow0 : 0) * in + akoff;
+  const uint16_t *ap1 = xp + (size_t)(arow0 + 32 < M ? arow0 + 32 : 0) * in + akoff;
+  // B operand columns of this lane in a stage buffer
+  const int bn0 = (wc * 64 + (lane & 31)) * GM_LDK + akoff;
+  const int stages = in_tiles / 4;  // even: in is a multiple of 128
+  if (wave & 1)
+    gemm_main<K, CB, MASKED, 1>(acc, lds, twc, wstage, ap0, ap1, bn0, stages, tkl, tnl, c, mask);
+  else
+    gemm_main<K, CB, MASKED, 0>(acc, lds, twc, wstage, ap0, ap1, bn0, stages, tkl, tnl, c, mask);
 
   // z = f16(acc) into the z tile: D[i][j] of a 32x32 MFMA sits in lane
   // l = j + 32 * ((i / 4) % 2), register 4 * (i / 8) + i % 4.
@@ -910,7 +1016,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
         lds[row * GM_ZLD + col] = f2h(acc[i][j][r]);
       }
   __syncthreads();
-  for (int row = wave; row < GM_BM; row += 4) {
+  for (int row = wave; row < GM_BM; row += GM_THREADS / 64) {
     const int m = m0 + row;
     if (m >= M) break;
     const uint16_t *zr = lds + row * GM_ZLD;
@@ -923,15 +1029,15 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
   }
 }
 
-template <int CB>
+template <int CB, bool MASKED>
 static void gemm_cb(int kk, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
                     const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
                     int out_tiles, uint32_t mask) {
   switch (kk) {
-#define EXL3_GM(KK)                                                                          \
-  case KK:                                                                                   \
-    hipLaunchKernelGGL((gemm_kernel<KK, CB>), grid, dim3(GM_THREADS), 0, s, tw, xp, svh, y, \
-                       ydt, zout, M, in_tiles, out_tiles, mask);                             \
+#define EXL3_GM(KK)                                                                     \
+  case KK:                                                                              \
+    hipLaunchKernelGGL((gemm_kernel<KK, CB, MASKED>), grid, dim3(GM_THREADS), 0, s, tw, \
+                       xp, svh, y, ydt, zout, M, in_tiles, out_tiles, mask);            \
     break;
     EXL3_GM(1) EXL3_GM(2) EXL3_GM(3) EXL3_GM(4) EXL3_GM(5) EXL3_GM(6) EXL3_GM(7) EXL3_GM(8)
 #undef EXL3_GM
@@ -950,10 +1056,19 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
   if (mblocks > 65535) return hipErrorInvalidValue;
   const dim3 grid(out / 128, mblocks);
   const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
-  if (f.codebook == CB_MCG)
-    gemm_cb<CB_MCG>(f.n / 16, grid, s, tw, xp, svh, y, ydt, zout, rows, in / 16, out / 16, f.mask());
-  else
-    gemm_cb<CB_MUL1>(f.n / 16, grid, s, tw, xp, svh, y, ydt, zout, rows, in / 16, out / 16, f.mask());
+  const int kk = f.n / 16, it = in / 16, ot = out / 16;
+  const uint32_t m = f.mask();
+  if (f.codebook == CB_MCG) {
+    if (f.window < 16)
+      gemm_cb<CB_MCG, true>(kk, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, m);
+    else
+      gemm_cb<CB_MCG, false>(kk, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, m);
+  } else {
+    if (f.window < 16)
+      gemm_cb<CB_MUL1, true>(kk, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, m);
+    else
+      gemm_cb<CB_MUL1, false>(kk, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, m);
+  }
   return hipGetLastError();
 }
 
@@ -1105,8 +1220,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     ri[threadIdx.x] = GemvRow{(c.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
   }
   __syncthreads();
-  uint32_t *ticket = W.ticket + (size_t)item * (W.out_tiles / 8) + cg;
-  gemv_wg<K, CB, MASKED>(c, W, (int)it.expert, (int)it.count, ri, ticket, cg, blockIdx.y,
+  gemv_wg<K, CB, MASKED>(c, W, (int)it.expert, (int)it.count, ri, cg, blockIdx.y,
                          smem + 256, MOE_ITEM_ROWS);
 }
 
@@ -1138,8 +1252,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
 namespace {
 
 struct MoeLayout {
-  size_t sorted, items, n_items, g, u, xd, d, pgu, pd, total;
-  size_t tickets;  // in the separate ticket buffer: gate, up, down
+  size_t sorted, items, n_items, g, u, xd, d, total;
+  size_t partial_floats;  // slots in the separate slot buffer: gate, up, down
   int slots, max_items, ks_gu, ks_d, tps_gu, tps_d;
 };
 
@@ -1174,10 +1288,8 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   L.u = take((size_t)slots * a.inter * 2);
   L.xd = take((size_t)slots * a.inter * 2);
   L.d = take((size_t)slots * a.hidden * 2);
-  L.pgu = take((size_t)2 * L.ks_gu * slots * a.inter * 4);
-  L.pd = take((size_t)L.ks_d * slots * a.hidden * 4);
   L.total = o;
-  L.tickets = (size_t)L.max_items * (2 * (a.inter / 128) + a.hidden / 128);
+  L.partial_floats = (size_t)2 * L.ks_gu * slots * a.inter + (size_t)L.ks_d * slots * a.hidden;
   return L;
 }
 
@@ -1206,7 +1318,7 @@ void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, cons
   gemv_dispatch_k<0, false>(f.integer_rate() ? f.n / 16 : 0, go);
 }
 
-GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, uint32_t *ticket, int cg0) {
+GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, int cg0) {
   GemvWeight w{};
   w.tw = reinterpret_cast<const uint32_t *>(b.trellis);
   w.suh = b.suh;
@@ -1214,7 +1326,6 @@ GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, uint32_t *t
   w.y = y;
   w.zout = nullptr;
   w.partial = partial;
-  w.ticket = ticket;
   w.expert_words = (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2);
   w.out_tiles = b.out / 16;
   w.cg0 = cg0;
@@ -1239,19 +1350,20 @@ GemvArgs moe_args(const void *x, int xdt, bool prepared, size_t slots, int in, c
 
 }  // namespace
 
-size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic, size_t *tickets) {
+size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
+                         size_t *partial_floats) {
   if (a.rows <= 0 || a.topk <= 0) {
-    *tickets = 1;
+    *partial_floats = 1;
     return 256;
   }
   const MoeLayout L = moe_layout(a, gu_generic, d_generic);
-  *tickets = L.tickets;
+  *partial_floats = L.partial_floats;
   return L.total;
 }
 
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
-                      const MoeBank &down, void *scratch, size_t scratch_bytes, uint32_t *tickets,
-                      size_t ntickets, hipStream_t s) {
+                      const MoeBank &down, void *scratch, size_t scratch_bytes, float *partial,
+                      size_t partial_floats, hipStream_t s) {
   if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
@@ -1261,7 +1373,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     return hipErrorInvalidValue;
   const bool gu_generic = !gate.f.integer_rate(), d_generic = !down.f.integer_rate();
   const MoeLayout L = moe_layout(a, gu_generic, d_generic);
-  if (scratch_bytes < L.total || ntickets < L.tickets || L.slots > 65535 ||
+  if (scratch_bytes < L.total || partial_floats < L.partial_floats || L.slots > 65535 ||
       L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
     return hipErrorInvalidValue;
   char *base = (char *)scratch;
@@ -1270,17 +1382,15 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   uint32_t *n_items = (uint32_t *)(base + L.n_items);
   uint16_t *g = (uint16_t *)(base + L.g), *u = (uint16_t *)(base + L.u);
   uint16_t *xd = (uint16_t *)(base + L.xd), *d = (uint16_t *)(base + L.d);
-  float *pgu = (float *)(base + L.pgu), *pd = (float *)(base + L.pd);
-  uint32_t *tg = tickets, *tu = tickets + (size_t)L.max_items * (a.inter / 128);
-  uint32_t *td = tickets + (size_t)2 * L.max_items * (a.inter / 128);
+  float *pgu = partial, *pd = partial + (size_t)2 * L.ks_gu * L.slots * a.inter;
 
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
                      a.experts, sorted, items, n_items);
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   GemvArgs agu = moe_args(a.x, a.xdt, false, L.slots, a.hidden, gate.f, L.ks_gu, L.tps_gu);
   agu.nweights = 2;
-  agu.w[0] = moe_weight(gate, g, pgu, tg, 0);
-  agu.w[1] = moe_weight(up, u, pgu + gu_part, tu, a.inter / 128);
+  agu.w[0] = moe_weight(gate, g, pgu, 0);
+  agu.w[1] = moe_weight(up, u, pgu + gu_part, a.inter / 128);
   moe_gemv_launch(gate.f, dim3(2 * (a.inter / 128), L.ks_gu, L.max_items),
                   gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, agu, sorted, items,
                   n_items, a.topk);
@@ -1288,7 +1398,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                      a.experts, down.suh, xd, a.inter, a.limit);
   GemvArgs ad = moe_args(xd, OUT_F16, true, L.slots, a.inter, down.f, L.ks_d, L.tps_d);
   ad.nweights = 1;
-  ad.w[0] = moe_weight(down, d, pd, td, 0);
+  ad.w[0] = moe_weight(down, d, pd, 0);
   moe_gemv_launch(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items),
                   gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, ad, sorted, items, n_items,
                   a.topk);

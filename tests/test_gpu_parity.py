@@ -200,9 +200,20 @@ def test_matmul_dtypes_and_leading_dims(dtype):
     y = lin(x.to(DEV))
     assert y.shape == (2, 3, 256) and y.dtype == dtype
     yo = O.project(x.float().numpy().reshape(6, 256), trellis, suh, svh, 256, 256, 64)
-    # the output is y16 then the output dtype: compare in that dtype
-    want = torch.from_numpy(S.h2f(yo)).to(dtype).float().numpy()
-    assert S.rel_fro(y.float().cpu().numpy().reshape(6, 256), want) < 1e-3
+    got = y.float().cpu().numpy().reshape(6, 256)
+    if dtype == torch.bfloat16:
+        # y16 then bf16: one bf16 rounding of a value within the f16 bar, so
+        # each element is within one bf16 ulp (plus the f16 bar's absolute
+        # share) of the oracle's y16 in bf16
+        want = torch.from_numpy(S.h2f(yo)).to(dtype).float().numpy()
+        ulp = np.spacing(np.abs(want)).astype(np.float64) * 2.0**16
+        slack = 1e-3 * np.sqrt(np.mean(want.astype(np.float64) ** 2))
+        err = np.abs(got - want) - ulp - slack
+        i = np.unravel_index(np.argmax(err), err.shape)
+        assert err[i] <= 0, (i, got[i], want[i], S.h2f(yo)[i])
+        assert S.rel_fro(got, S.h2f(yo)) < 4e-3
+    else:
+        assert S.rel_fro(got, S.h2f(yo)) < 1e-3
 
 
 def test_matmul_is_row_invariant():
