@@ -841,124 +841,49 @@ hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, 
 
 // ===================================================================== GEMM
 //
-// Workgroup tile 256 rows x 128 columns (one Hadamard block of the output),
-// 8 waves in a 4 x 2 grid of 64 x 64 sub-tiles, each 2 x 2
-// v_mfma_f32_32x32x16_f16 tiles with f32 accumulators.  The k loop runs in
-// stages of 64 (four k-tile rows of 8 output tiles = 32 tiles = 256 chunks);
-// every thread decodes half a chunk (16 codewords) of the next stage into the
-// other LDS buffer after the MFMAs of the current one are issued, so the
-// decode's VALU work overlaps the matrix cores.  The B^T tile sits in LDS as
-// [n][k] with k contiguous (a chunk's column is 16 consecutive k), so an
-// MFMA B operand (8 consecutive k of one column) is one ds_read_b128.  A
-// operands (prepared activations, row-major f16) load straight from global
-// memory in operand layout, two stages ahead, as do the packed words.  The
-// epilogue rounds z to f16 in LDS and runs the finish per row.  Each decoded
-// weight serves 256 rows.
+// Workgroup tile 256 rows x 256 columns (two Hadamard blocks of the output),
+// 4 waves, each a 128 x 128 sub-tile of 4 x 4 v_mfma_f32_32x32x16_f16 tiles
+// (256 f32 accumulators per lane).  The k loop runs in stages of 32 (two
+// k-tile rows).  While the MFMAs consume the current stage from LDS, every
+// thread decodes one chunk of the next stage (the 256 chunks of 2 k-tile rows
+// x 16 output tiles) into four MFMA B fragments (8 consecutive k of one
+// column each) and stores them into the other LDS buffer as B^T [n][k] rows,
+// stores its four 16-byte pieces of the next A tile (prepared rows, f16), and
+// loads the pieces and packed words of the stage three ahead into the
+// register set it just freed (three sets in flight); the decode's VALU work
+// and the memory operations are interleaved between the MFMAs.  LDS rows are padded to 40 halfs (80
+// bytes), so the 16-byte operand reads of 16 consecutive rows hit distinct
+// banks.  The MFMAs take the weights as their first operand, so the
+// accumulators hold z^T: a lane holds one row of z and 16 of its columns.
+// That is the operand layout of a second MFMA, which applies the finish's
+// Hadamard stages on column bits 0-4 (H_32, +-1 entries: exact products,
+// f32 sums) to f16(z); stages 5 and 6 are the reference's butterflies across
+// the four 32-column blocks, in registers, then * 1/sqrt(128) * svh.  No LDS
+// round trip.  Each decoded weight serves 256 rows and each staged activation
+// 256 columns.
 
-constexpr int GM_BM = 256, GM_BN = 128, GM_BK = 64, GM_THREADS = 512;
-constexpr int GM_LDK = GM_BK + 8;  // k stride (halfs) of a B^T column in LDS
-constexpr int GM_ZLD = GM_BN + 8;  // column stride (halfs) of the z tile
-constexpr int GM_LDS_HALFS =
-    (2 * GM_BN * GM_LDK > GM_BM * GM_ZLD) ? 2 * GM_BN * GM_LDK : GM_BM * GM_ZLD;
+constexpr int GM_BM = 256, GM_BN = 256, GM_BK = 32, GM_THREADS = 256;
+constexpr int GM_LD = GM_BK + 8;      // halfs per LDS row of A / column of B^T
+constexpr int GM_TILE = 256 * GM_LD;  // halfs per operand buffer
+constexpr int GM_LDS_HALFS = 4 * GM_TILE;  // A and B^T, two stages
 
-// Decodes this thread's half chunk (codewords 16h..16h+15: pairs 8h..8h+7)
-// into bt (LDS).  h is uniform per wave, so only one arm runs.
-template <int K, int CB, bool MASKED, int H>
-__device__ __forceinline__ void gemm_decode_half(const uint32_t (&wd)[K + 1], uint32_t *btw,
-                                                 int tkl, int tnl, int c, uint32_t mask) {
-  static_for<8>([&](auto Q) {
-    constexpr int p = decltype(Q)::value + 8 * H;
-    const uint32_t v = chunk_pair_cw<K, CB, MASKED, p>(wd, mask);
-    constexpr int r = chunk_row(2 * p);
-    constexpr int ch = chunk_colhalf(2 * p);
-    const int nl = tnl * 16 + c + 8 * ch;
-    const int kl = tkl * 16 + r;
-    btw[(nl * GM_LDK + kl) >> 1] = v;
+// A chunk's 32 codewords as four MFMA B fragments of 8 consecutive k of one
+// column: f = 0: column a, tile rows 0-7; 1: column a+8, rows 0-7; 2: column
+// a, rows 8-15; 3: column a+8, rows 8-15 (pairs p, p+4, p+8, p+12 for p = 0,
+// 2, 1, 3), stored to B^T at column n0 (+8) and k k0 (+8).
+template <int K, int CB, bool MASKED>
+__device__ __forceinline__ void gemm_decode_chunk(const uint32_t (&wd)[K + 1], uint16_t *bt, int n0,
+                                                  int k0, uint32_t mask) {
+  static_for<4>([&](auto F) {
+    constexpr int f = decltype(F)::value;
+    constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
+    uint32_t q[4];
+    static_for<4>([&](auto J) {
+      q[J] = chunk_pair_cw<K, CB, MASKED, p0 + 4 * decltype(J)::value>(wd, mask);
+    });
+    const u4_t v = {q[0], q[1], q[2], q[3]};
+    *reinterpret_cast<u4_t *>(bt + (n0 + 8 * (f & 1)) * GM_LD + k0 + 8 * (f >> 1)) = v;
   });
-}
-
-// The K dwords of this thread's chunk, and (first half) the history dword:
-// the last dword of the previous chunk of the tile, circularly.  Codewords
-// 16..31 of a chunk never reach the history dword.
-template <int K>
-__device__ __forceinline__ void gemm_load_words(const uint32_t *__restrict__ tp, int c, int h,
-                                                uint32_t (&wd)[K + 1]) {
-#pragma unroll
-  for (int i = 0; i < K; ++i) wd[i + 1] = tp[c * K + i];
-  wd[0] = h ? 0u : tp[((c + 7) & 7) * K + (K - 1)];
-}
-
-// A operands of one stage: a[kk][i] = rows (lane & 31) + 32 i of the wave's
-// 64, k = 16 kk + 8 (lane / 32) .. +7 of the stage.  Rows past M read row 0
-// instead (their results are not stored; rows of an MFMA are independent),
-// so the loads need no branch.
-__device__ __forceinline__ void gemm_load_a(const uint16_t *ap0, const uint16_t *ap1, int k0,
-                                            h8_t (&a)[4][2]) {
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    a[kk][0] = *reinterpret_cast<const h8_t *>(ap0 + k0 + kk * 16);
-    a[kk][1] = *reinterpret_cast<const h8_t *>(ap1 + k0 + kk * 16);
-  }
-}
-
-// The main loop of one wave: decoder half H (uniform per wave, so the loop
-// body has no branch and the scheduler can interleave the decode's VALU work
-// and the A loads between the MFMAs: one basic block per stage).  Loads past
-// the last stage re-read the last stage (in bounds, unused).
-template <int K, int CB, bool MASKED, int H>
-__device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
-                                          const uint32_t *twc, size_t wstage,
-                                          const uint16_t *ap0, const uint16_t *ap1, int bn0,
-                                          int stages, int tkl, int tnl, int c, uint32_t mask) {
-  h8_t aA[4][2], aB[4][2];
-  uint32_t wdA[K + 1], wdB[K + 1];
-  {
-    uint32_t wd0[K + 1];
-    gemm_load_words<K>(twc, c, H, wd0);
-    gemm_load_a(ap0, ap1, 0, aA);
-    gemm_load_words<K>(twc + wstage, c, H, wdB);
-    gemm_load_a(ap0, ap1, GM_BK, aB);
-    gemm_load_words<K>(twc + (size_t)min(2, stages - 1) * wstage, c, H, wdA);
-    gemm_decode_half<K, CB, MASKED, H>(wd0, reinterpret_cast<uint32_t *>(lds), tkl, tnl, c, mask);
-  }
-  __syncthreads();
-
-  // stage st: MFMAs on buffer st & 1 with operands a, then A of stage st + 2
-  // into a, the decode of stage st + 1 (words in wd) into the other buffer,
-  // and the words of stage st + 3 into wd
-  auto stage = [&](h8_t(&a)[4][2], uint32_t(&wd)[K + 1], int st) {
-    const uint16_t *cur = lds + (st & 1) * (GM_BN * GM_LDK);
-    uint16_t *nxt = lds + ((st + 1) & 1) * (GM_BN * GM_LDK);
-    h8_t b[4][2];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      b[kk][0] = *reinterpret_cast<const h8_t *>(cur + bn0 + kk * 16);
-      b[kk][1] = *reinterpret_cast<const h8_t *>(cur + bn0 + 32 * GM_LDK + kk * 16);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][0], b[kk][0], acc[0][0], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][1], b[kk][0], acc[1][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][0], b[kk][1], acc[0][1], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][1], b[kk][1], acc[1][1], 0, 0, 0);
-    }
-    gemm_load_a(ap0, ap1, min(st + 2, stages - 1) * GM_BK, a);
-    gemm_decode_half<K, CB, MASKED, H>(wd, reinterpret_cast<uint32_t *>(nxt), tkl, tnl, c, mask);
-    gemm_load_words<K>(twc + (size_t)min(st + 3, stages - 1) * wstage, c, H, wd);
-    // B operands first, then each MFMA followed by a share of the VALU work
-    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x0002, 5, 0);  // VALU
-      if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
-    }
-    __syncthreads();
-  };
-  for (int st = 0; st < stages; st += 2) {
-    stage(aA, wdB, st);
-    stage(aB, wdA, st + 1);
-  }
 }
 
 template <int K, int CB, bool MASKED>
@@ -970,63 +895,198 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 1, wc = wave & 1;
-  const int cg = blockIdx.x;
-  const int m0 = blockIdx.y * GM_BM;
+  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking
+  // the row block as n % (row blocks) lets an XCD's workgroups share a few
+  // row blocks of A in its L2.  (Only the speed depends on this.)
+  const int mblocks = gridDim.y;
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int cp = lin / mblocks;  // columns 256 cp ..
+  const int m0 = (lin % mblocks) * GM_BM;
   const int in = in_tiles * 16;
   const size_t out = (size_t)out_tiles * 16;
   const int nw = 8 * K;
-  // decoder role: 32 tiles (4 k-tile rows x 8 output tiles) x 8 chunks = 256
-  // chunks; waves 2q and 2q+1 take chunks 64q..64q+63, halves 0 and 1.
-  const int chunk_id = (wave >> 1) * 64 + lane;
-  const int tl = chunk_id >> 3, tkl = tl >> 3, tnl = tl & 7, c = chunk_id & 7;
-  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + (size_t)cg * 8 + tnl) * nw;
-  const size_t wstage = (size_t)4 * out_tiles * nw;  // dwords per stage
 
-  f16v_t acc[2][2];
+  // decoder role: chunk c of output tile tnl of k-tile row tkl of the stage;
+  // the 8 chunks of a tile sit in 8 consecutive lanes.  Tiles past the last
+  // column (the second half of an odd last pair) decode tile 0 instead and
+  // their results are not stored.
+  const int tkl = tid >> 7, tnl = (tid >> 3) & 15, c = tid & 7;
+  const int tcol = cp * 16 + tnl < out_tiles ? cp * 16 + tnl : 0;
+  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + tcol) * nw + c * K;
+  const size_t wstage = (size_t)2 * out_tiles * nw;  // dwords per stage
+  const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of chunk c-1
+  const int bn0 = tnl * 16 + c, bk0 = tkl * 16;
+
+  // A staging: pieces t + 256 i (i = 0..3) of the 256 x 4 16-byte pieces of
+  // a stage: row (t >> 2) + 64 i, piece t & 3.  Rows past M read row M - 1
+  // (not stored; rows of an MFMA are independent), so no load branches.
+  const int arow = tid >> 2, apc = tid & 3;
+  const uint16_t *ap[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
+    ap[i] = xp + (size_t)min(m0 + arow + 64 * i, M - 1) * in + apc * 8;
+  const int ast = arow * GM_LD + apc * 8;
+
+  // operand fragments of this lane in a stage buffer
+  const int am = (wr * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
+  const int bn = (wc * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
+
+  f16v_t acc[4][4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // A operand rows of this lane (rows past M read as zero)
-  const int arow0 = m0 + wr * 64 + (lane & 31);
-  const int akoff = 8 * (lane >> 5);
-  const uint16_t *ap0 = xp + (size_t)(arow0 < M ? arow0 : 0) * in + akoff;
-  const uint16_t *ap1 = xp + (size_t)(arow0 + 32 < M ? arow0 + 32 : 0) * in + akoff;
-  // B operand columns of this lane in a stage buffer
-  const int bn0 = (wc * 64 + (lane & 31)) * GM_LDK + akoff;
-  const int stages = in_tiles / 4;  // even: in is a multiple of 128
-  if (wave & 1)
-    gemm_main<K, CB, MASKED, 1>(acc, lds, twc, wstage, ap0, ap1, bn0, stages, tkl, tnl, c, mask);
-  else
-    gemm_main<K, CB, MASKED, 0>(acc, lds, twc, wstage, ap0, ap1, bn0, stages, tkl, tnl, c, mask);
-
-  // z = f16(acc) into the z tile: D[i][j] of a 32x32 MFMA sits in lane
-  // l = j + 32 * ((i / 4) % 2), register 4 * (i / 8) + i % 4.
+  h8_t ar[3][4];
+  uint32_t wn[3][K];
+  const int stages = in_tiles / 2;  // >= 4: in is a multiple of 128
+  // register set S <- stage st (clamped to the last stage: in bounds, unused)
+  auto load_stage = [&](auto S, int st) {
+    constexpr int q = decltype(S)::value;
+    st = min(st, stages - 1);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i) ar[q][i] = *reinterpret_cast<const h8_t *>(ap[i] + st * GM_BK);
+    const uint32_t *p = twc + (size_t)st * wstage;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < K; ++j) wn[q][j] = p[j];
+  };
+  // register set S -> LDS buffer at off (A pieces, decoded chunk)
+  auto store_stage = [&](auto S, int off) {
+    constexpr int q = decltype(S)::value;
+    uint16_t *as = lds + off, *bs = lds + off + GM_TILE;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int col = wc * 64 + j * 32 + (lane & 31);
-        lds[row * GM_ZLD + col] = f2h(acc[i][j][r]);
-      }
-  __syncthreads();
-  for (int row = wave; row < GM_BM; row += GM_THREADS / 64) {
-    const int m = m0 + row;
-    if (m >= M) break;
-    const uint16_t *zr = lds + row * GM_ZLD;
-    if (y == nullptr) {
-      zout[(size_t)m * out + cg * 128 + lane] = zr[lane];
-      zout[(size_t)m * out + cg * 128 + lane + 64] = zr[lane + 64];
-    } else {
-      finish_row_wave(zr, svh + cg * 128, y, ydt, (size_t)m * out + cg * 128, lane);
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t *>(as + ast + i * 64 * GM_LD) = ar[q][i];
+    uint32_t wd[K + 1];
+#pragma unroll
+    for (int j = 0; j < K; ++j) wd[j + 1] = wn[q][j];
+    wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
+    gemm_decode_chunk<K, CB, MASKED>(wd, bs, bn0, bk0, mask);
+  };
+  // stage st: MFMAs on buffer st & 1; set S (stage st + 1) into the other
+  // buffer, then set S <- stage st + 4
+  auto stage = [&](auto S, int st) {
+    const int cur = (st & 1) * 2 * GM_TILE, nxt = 2 * GM_TILE - cur;
+    const uint16_t *ac = lds + cur, *bc = lds + cur + GM_TILE;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      h8_t a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const h8_t *>(ac + am + i * 32 * GM_LD + kk * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const h8_t *>(bc + bn + j * 32 * GM_LD + kk * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[j][i], 0, 0, 0);
     }
+    store_stage(S, nxt);
+    load_stage(S, st + 4);
+    // operands of the first slab, then each MFMA followed by a share of the
+    // VALU work and of the memory operations
+    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);  // VALU
+      if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
+      if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+    }
+    __syncthreads();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  load_stage(I0{}, 0);
+  load_stage(I1{}, 1);
+  load_stage(I2{}, 2);
+  store_stage(I0{}, 0);
+  load_stage(I0{}, 3);
+  __syncthreads();
+  int st = 0;
+  for (; st + 3 <= stages; st += 3) {
+    stage(I1{}, st);
+    stage(I2{}, st + 1);
+    stage(I0{}, st + 2);
   }
+  if (st < stages) stage(I1{}, st);
+  if (st + 1 < stages) stage(I2{}, st + 1);
+
+  // acc[j][i] = z^T for columns 32 j .. of the wave's column group and rows
+  // 32 i .. of its 128: lane l holds row (l & 31), register r column
+  // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
+  const int cg = cp * 2 + wc;
+  if (cg * 8 >= out_tiles) return;  // the odd half of the last pair
+  const int rb = m0 + wr * 128 + (lane & 31);
+  if (y == nullptr) {
+    static_for<4>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (rb + 32 * i < M) {
+        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 4 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[j][i][r]);
+      }
+    });
+    return;
+  }
+  // H_32 as the second operand: element e of fragment kk pairs with column
+  // 16 kk + 8 (e / 4) + 4 (l / 32) + e % 4 of a 32-column block (the
+  // registers 8 kk + e above), output column (l & 31).
+  h8_t hb[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int nl = 16 * kk + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      hb[kk][e] = (__builtin_popcount(nl & lane & 31) & 1) ? -1.0f16 : 1.0f16;
+    }
+  float sv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sv[j] = h2f(svh[cg * 128 + 32 * j + (lane & 31)]);
+  static_for<4>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    // D2_j = f16(z block j) H_32: lane l holds output column (l & 31),
+    // register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the 32
+    f16v_t d2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h8_t a0, a1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a0[e] = bits<_Float16>(f2h(acc[j][i][e]));
+        a1[e] = bits<_Float16>(f2h(acc[j][i][8 + e]));
+      }
+      f16v_t zero = {};
+      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
+      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wr * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi)
+      const float t0 = d2[0][r] + d2[1][r], t1 = d2[0][r] - d2[1][r];
+      const float t2 = d2[2][r] + d2[3][r], t3 = d2[2][r] - d2[3][r];
+      const float u[4] = {t0 + t2, t1 + t3, t0 - t2, t1 - t3};
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          store_out(y, (size_t)m * out + cg * 128 + 32 * j + (lane & 31),
+                    f2h((u[j] * HAD_SCALE) * sv[j]), ydt);
+      }
+    }
+  });
 }
 
 template <int CB, bool MASKED>
@@ -1054,7 +1114,7 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
   if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
   const int mblocks = (rows + GM_BM - 1) / GM_BM;
   if (mblocks > 65535) return hipErrorInvalidValue;
-  const dim3 grid(out / 128, mblocks);
+  const dim3 grid((out + 255) / 256, mblocks);
   const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
   const int kk = f.n / 16, it = in / 16, ot = out / 16;
   const uint32_t m = f.mask();
