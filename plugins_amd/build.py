@@ -31,10 +31,13 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
+# (source, object name, flags): exl3_rate.hip once per rate K (0 = any even
+# n), so the rates' kernels compile in parallel.
 SOURCES = [
-    ("exl3_kernels.hip", DEVICE_FLAGS),
-    ("exl3_host.cpp", HOST_FLAGS),
-    ("exl3_json.cpp", HOST_FLAGS),
+    ("exl3_kernels.hip", "exl3_kernels", DEVICE_FLAGS),
+    *[("exl3_rate.hip", f"exl3_rate_k{k}", DEVICE_FLAGS + [f"-DEXL3_INST_K={k}"]) for k in range(9)],
+    ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
+    ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
 ]
 
 
@@ -45,8 +48,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the EXL3 library cannot be built")
 
 
-def _compile(src: str, flags: list[str]) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+def _compile(src: str, name: str, flags: list[str]) -> str:
+    obj = os.path.join(BUILD, name + ".o")
     cmd = [_hipcc(), *flags, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(line for line in (r.stdout + r.stderr).splitlines()
@@ -62,7 +65,8 @@ def build(verbose: bool = True) -> str:
     """Compiles every source and links the shared library; returns its path."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda sf: _compile(*sf), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]

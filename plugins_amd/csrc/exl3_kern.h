@@ -1,0 +1,926 @@
+// exl3_kern.h -- the rate-templated EXL3 kernels (GEMV, GEMM, grouped MoE
+// GEMV) and their per-rate launchers, for MI355X (gfx950, wave64).
+//
+// Included by exl3_kernels.hip (dispatchers; it sees the launchers as
+// extern instantiations) and by exl3_rate.hip, which the build compiles once
+// per rate K with EXL3_INST_K = K to instantiate that rate's kernels, so the
+// rates compile in parallel.  Paths in citations are relative to
+// /root/reference/plugins/.
+#pragma once
+
+#include <algorithm>
+#include <utility>
+
+#include "exl3_device.h"
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+template <int... Is, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F &&f) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+// Agent-scope (all XCDs) loads and stores for the split-K hand-off.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0): this wave's outstanding vector-memory operations,
+// stores included on gfx9-family parts, have completed.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ===================================================================== GEMV
+//
+// One launch per matmul of up to 16 rows, and one launch for up to four
+// weights that read the same rows (q/k/v, gate/up: the reference's
+// linearShared, sushi_ds41/src/sushi/exl3/linear.zig:34-60), their column
+// groups side by side in the grid.  A workgroup (8 waves) owns one
+// 128-column group (8 output tiles: one Hadamard block of the output) of one
+// weight and one k-split of tps k-tile rows (whole input Hadamard blocks):
+//  1. it prepares its rows' input slice in LDS (x * suh, Hadamard-128, f16:
+//     the reference's prepare, run per split instead of as its own launch);
+//  2. wave w takes tiles 2q, 2q+1 (q = w % 4) of the group over k-part w / 4
+//     of the split; lane l = 16g + 8t + c takes chunk c of tile 2q+t in
+//     k-tile row 4i+g of its part at step i, loads its K dwords (+ the
+//     history dword of lane l-1 of its tile, by ds_bpermute), decodes its 32
+//     codewords in registers into four 8 x f16 MFMA B operands (column a /
+//     a+8, rows 0-7 / 8-15), and v_mfma_f32_16x16x32_f16 sums them against
+//     the rows' activations (A operands from LDS) over the step's 4 k-tile
+//     rows.  MFMA rows are the call's rows: 1..16 rows cost one decode;
+//  3. the two k-parts add in LDS; the other splits' per-row sums go to
+//     scratch slots, and the workgroup of the last split (the highest
+//     workgroup index of the column group) adds the splits in split order,
+//     rounds z to f16 and runs the finish (Hadamard-128, * svh) on its 128
+//     columns.  Every sum is in a fixed order that does not depend on how
+//     many rows share the call.
+//  With mul1 at an integer rate the MFMAs take the codebook value before its
+//  affine step (chunk_pair_mul1_h) and the step is applied to the sums.
+
+constexpr int GEMV_THREADS = 512;
+constexpr int GEMV_ROWS = 16;
+constexpr int GEMV_TPS_MAX = 64;
+constexpr int GEMV_KSPLIT_MAX = 64;
+constexpr int GEMV_MAXW = 4;
+
+struct GemvRow {
+  int in_off;   // element offset of the row's activations
+  int out_off;  // element offset of the row's output
+  int prow;     // row of the split-K partial buffer
+  int pad;
+};
+
+struct GemvWeight {
+  const uint32_t *tw;   // trellis dwords (a bank's expert 0)
+  const uint16_t *suh;  // [E][in]
+  const uint16_t *svh;  // [E][out]
+  void *y;              // finished output in ydt, or nullptr:
+  uint16_t *zout;       // the inner product z (f16) instead
+  float *partial;       // [ksplit][ptotal][out] slots, empty between calls
+  size_t expert_words;  // dwords per expert
+  int out_tiles;
+  int cg0;              // first grid column group of this weight
+};
+
+// The scalars of a launch, copied into SGPRs at kernel entry with the chosen
+// weight's fields (one round trip of argument loads).
+struct GemvCfg {
+  const void *x;  // activations (ACT_*), or prepared rows (f16) when prepared
+  size_t ptotal;
+  int xdt;
+  int prepared;
+  int ydt;
+  int in_tiles, n, ksplit, tps;
+  uint32_t mask;
+};
+
+struct GemvArgs {
+  GemvCfg c;
+  GemvWeight w[GEMV_MAXW];
+  int nweights;
+};
+
+// Dynamic LDS of a GEMV workgroup: row table, prepared rows, the two
+// k-parts' z tiles, the prepared rows' sums per 64 elements, and (generic
+// rate) a word stage per wave.
+__host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, bool generic) {
+  return 256 + (size_t)rows_alloc * (tps * 16 + 8) * 2 +
+         (size_t)2 * (rows_alloc > 2 ? rows_alloc : 2) * 128 * 4 +
+         (size_t)rows_alloc * (tps / 4) * 4 +
+         (generic ? (size_t)(GEMV_THREADS / 64) * 512 * 4 : 0);
+}
+
+// The rows' input slice [tk0*16, tk0*16 + ntk*16) prepared into xs (row
+// stride kr halfs): one wave per (row, 128-block) item.  Loads and
+// arithmetic are split so a workgroup can issue the first items' loads
+// before its weight loads (the prepare is on the critical path; the weights
+// are not needed until it is done).
+constexpr int PREP_BATCH = 2;  // items per wave per batch
+
+// Raw bits as loaded (converted only when the rows are prepared, so the
+// loads do not wait): x holds the two elements (one dword for f16/bf16, two
+// for f32), su the two suh values.
+struct PrepRegs {
+  uint32_t x0[PREP_BATCH], x1[PREP_BATCH], su[PREP_BATCH];
+};
+
+__device__ __forceinline__ void prep_unpack(uint32_t x0, uint32_t x1, int dt, float &a, float &b) {
+  if (dt == OUT_F32) {
+    a = bits<float>(x0);
+    b = bits<float>(x1);
+  } else if (dt == OUT_BF16) {
+    a = bf2f((uint16_t)(x0 & 0xFFFFu));
+    b = bf2f((uint16_t)(x0 >> 16));
+  } else {
+    a = h2f((uint16_t)(x0 & 0xFFFFu));
+    b = h2f((uint16_t)(x0 >> 16));
+  }
+}
+
+__device__ __forceinline__ void gemv_prep_load(const GemvCfg &a, const GemvWeight &W, int expert,
+                                               const GemvRow *rows, int nitems, int nb, int tk0,
+                                               int base, int wave, int lane, PrepRegs &r) {
+  const int in = a.in_tiles * 16;
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = base + wave + j * (GEMV_THREADS / 64);
+    if (it >= nitems) break;
+    const int row = it / nb, blk = it - row * nb;
+    const int k = tk0 * 16 + blk * 128 + 2 * lane;
+    const size_t xo = (size_t)rows[row].in_off + k;
+    if (a.prepared || a.xdt != OUT_F32) {
+      r.x0[j] = *reinterpret_cast<const uint32_t *>((const uint16_t *)a.x + xo);
+    } else {
+      const u2_t v = *reinterpret_cast<const u2_t *>((const float *)a.x + xo);
+      r.x0[j] = v[0];
+      r.x1[j] = v[1];
+    }
+    if (!a.prepared)
+      r.su[j] = *reinterpret_cast<const uint32_t *>(W.suh + (size_t)expert * in + k);
+  }
+}
+
+// Element i of a 128-block sits in lane i/2, register i%2: the butterfly's
+// stage on index bit 0 is in-register, bits 1..6 exchange across lanes; each
+// stage is (lo + hi, lo - hi), in bit order, as the reference's kernels
+// compute it (expert_exl3_kernels.zig:902-970).
+__device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
+  const float a = v0 + v1, b = v0 - v1;
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int bit = 1; bit <= 32; bit <<= 1) {
+    const float p0 = __shfl_xor(v0, bit, 64);
+    const float p1 = __shfl_xor(v1, bit, 64);
+    const bool lower = (lane & bit) == 0;
+    v0 = lower ? v0 + p0 : p0 - v0;
+    v1 = lower ? v1 + p1 : p1 - v1;
+  }
+}
+
+// Stores the prepared pairs; with hsum (row stride nb * 2) also the sum of
+// each 64 prepared elements (lanes 0-31 and 32-63 of an item), added in a
+// fixed butterfly order.
+__device__ __forceinline__ void gemv_prep_store(const GemvCfg &a, int nitems, int nb, int base,
+                                                int wave, int lane, uint16_t *xs, int kr,
+                                                const PrepRegs &r, float *hsum) {
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = base + wave + j * (GEMV_THREADS / 64);
+    if (it >= nitems) break;
+    const int row = it / nb, blk = it - row * nb;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
+    uint32_t y;
+    if (a.prepared) {
+      y = r.x0[j];
+    } else {
+      // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
+      // (expert_exl3.zig:490-501)
+      float x0, x1;
+      prep_unpack(r.x0[j], r.x1[j], a.xdt, x0, x1);
+      float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
+      float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
+      had128_pair(v0, v1, lane);
+      y = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+    }
+    *dst = y;
+    if (hsum != nullptr) {
+      float s = h2f((uint16_t)(y & 0xFFFFu)) + h2f((uint16_t)(y >> 16));
+#pragma unroll
+      for (int m = 1; m < 32; m <<= 1) s = s + __shfl_xor(s, m, 64);
+      if ((lane & 31) == 0) hsum[row * nb * 2 + blk * 2 + (lane >> 5)] = s;
+    }
+  }
+}
+
+__device__ __forceinline__ h8_t frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u4_t v = {a, b, c, d};
+  return bits<h8_t>(v);
+}
+
+// Four MFMAs of one step: columns a (acc0) and a+8 (acc1), rows 0-7 then 8-15.
+__device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_t ahi, f4_t &acc0,
+                                          f4_t &acc1) {
+  acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, frag(p[0], p[4], p[8], p[12]), acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, frag(p[2], p[6], p[10], p[14]), acc1, 0, 0, 0);
+  acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, frag(p[1], p[5], p[9], p[13]), acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, frag(p[3], p[7], p[11], p[15]), acc1, 0, 0, 0);
+}
+
+// Split-K hand-off over zf[nrows][128] (this workgroup's f32 sums): returns
+// true in the workgroup of the last split, with z = f16(sum over splits, in
+// split order) in zf.  Partial-sum slots hold PARTIAL_EMPTY (a NaN bit
+// pattern no arithmetic produces) between calls.  The other splits store
+// their sums and exit; the last split's workgroup reads their slots,
+// re-reading each one until its store has landed, then puts PARTIAL_EMPTY
+// back.  It never waits on a workgroup that has not started: the last split
+// has the highest workgroup index of its column group, and workgroups are
+// dispatched in index order, so every slot it waits for belongs to a
+// workgroup already running, whose stores land within a memory round trip
+// (PARTIAL_POLL_MAX bounds the wait regardless: a slot still empty then
+// makes the sum NaN).  Slots are agent-scope atomics, coherent across the
+// XCDs' L2s, so no fence is needed.  (A device fence would write back and
+// invalidate the L2 in every workgroup.)
+constexpr uint32_t PARTIAL_EMPTY = 0xFFFFFFFFu;
+constexpr int PARTIAL_POLL_MAX = 1 << 20;
+
+__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
+                                                 const GemvWeight &W, int nrows,
+                                                 const GemvRow *rows, int ks, size_t out,
+                                                 int col0) {
+  const int E = nrows * 128;
+  if (a.ksplit == 1) {
+    for (int e = threadIdx.x; e < E; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
+    __syncthreads();
+    return true;
+  }
+  const size_t stride = a.ptotal * out;
+  if (ks != a.ksplit - 1) {
+    for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
+      const int b = e >> 7, col = e & 127;
+      float v = zf[e];
+      if (v != v) v = bits<float>(0x7FC00000u);  // never PARTIAL_EMPTY
+      st_agent(W.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, v);
+    }
+    return false;
+  }
+  const float empty = bits<float>(PARTIAL_EMPTY);
+  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
+    const int b = e >> 7, col = e & 127;
+    float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
+    float s = 0.0f;
+    for (int k0 = 0; k0 < ks; k0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (k0 + j < ks) v[j] = ld_agent(p + (size_t)(k0 + j) * stride);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (k0 + j >= ks) break;
+        float *slot = p + (size_t)(k0 + j) * stride;
+        for (int n = 0; bits<uint32_t>(v[j]) == PARTIAL_EMPTY && n < PARTIAL_POLL_MAX; ++n) {
+          __builtin_amdgcn_s_sleep(2);
+          v[j] = ld_agent(slot);
+        }
+        st_agent(slot, empty);
+        s = s + v[j];
+      }
+    }
+    zf[e] = h2f(f2h(s + zf[e]));
+  }
+  __syncthreads();
+  return true;
+}
+
+// Stores two consecutive finished f16 values in the output dtype.
+__device__ __forceinline__ void store_out2(void *p, size_t i, uint16_t y0, uint16_t y1, int dt) {
+  if (dt == OUT_F16) {
+    *reinterpret_cast<uint32_t *>((uint16_t *)p + i) = (uint32_t)y0 | ((uint32_t)y1 << 16);
+  } else if (dt == OUT_BF16) {
+    *reinterpret_cast<uint32_t *>((uint16_t *)p + i) =
+        (uint32_t)f2bf(h2f(y0)) | ((uint32_t)f2bf(h2f(y1)) << 16);
+  } else {
+    float2 v;
+    v.x = h2f(y0);
+    v.y = h2f(y1);
+    *reinterpret_cast<float2 *>((float *)p + i) = v;
+  }
+}
+
+// The finish over zf[nrows][128] (f32 holding f16 values): rotation,
+// * 1/sqrt(128), * svh, f16, output dtype (one wave per row, element i in
+// lane i/2); or z itself when y is null.  sv holds svh of this lane's two
+// columns (2 lane, 2 lane + 1), loaded at the start.
+__device__ __forceinline__ void gemv_finish(float *zf, const GemvCfg &a, const GemvWeight &W,
+                                            int nrows, const GemvRow *rows, uint32_t sv,
+                                            int col0) {
+  if (W.y == nullptr) {
+    for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
+      const int b = e >> 7, col = e & 127;
+      W.zout[(size_t)rows[b].out_off + col0 + col] = f2h(zf[e]);
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float sv0 = h2f((uint16_t)(sv & 0xFFFFu)), sv1 = h2f((uint16_t)(sv >> 16));
+  for (int b = wave; b < nrows; b += GEMV_THREADS / 64) {
+    float v0 = zf[b * 128 + 2 * lane], v1 = zf[b * 128 + 2 * lane + 1];
+    had128_pair(v0, v1, lane);
+    const float s0 = v0 * HAD_SCALE, s1 = v1 * HAD_SCALE;
+    store_out2(W.y, (size_t)rows[b].out_off + col0 + 2 * lane, f2h(s0 * sv0), f2h(s1 * sv1), a.ydt);
+  }
+}
+
+// One workgroup of the GEMV: expert `expert` of weight W, nrows <= 16 rows
+// (table `rows` in LDS), column group cg of W, split ks.
+template <int K, int CB, bool MASKED>
+__device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, int expert,
+                                        int nrows, const GemvRow *rows, int cg,
+                                        int ks, char *smem, int rows_alloc) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = wave & 3, kp = wave >> 2;
+  const size_t out = (size_t)W.out_tiles * 16;
+  const int tk0 = ks * a.tps;
+  const int ntk = min(a.tps, a.in_tiles - tk0);  // a multiple of 8
+  const int kr = a.tps * 16 + 8;
+  uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
+  const int zrows = rows_alloc > 2 ? rows_alloc : 2;
+  float *zp = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);  // [2][zrows][128]
+  // mul1 at an integer rate: the MFMAs take h (the codebook value before its
+  // affine step, chunk_pair_mul1_h), and z = a * acc + b * (sum of the
+  // k-part's prepared activations) afterwards, from the 64-element sums
+  // hsum[row][ntk / 4] that the prepare leaves
+  constexpr bool FOLD = K > 0 && CB == CB_MUL1;
+  float *hsum = zp + 2 * zrows * 128;
+  const int nw = a.n >> 1;
+  const int g = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+  const size_t tn = (size_t)cg * 8 + 2 * q + t;
+  const uint32_t *twe = W.tw + (size_t)expert * W.expert_words;
+  const int part = ntk >> 1;  // k-tile rows per k-part, a multiple of 4
+  const int kb = tk0 + kp * part;
+  const int iters = part >> 2;
+
+  // svh of the group's columns for the finish, the first prepare items'
+  // loads, then the first two steps' weights, so the weights are in flight
+  // while the rows are prepared
+  uint32_t sv = 0;
+  if (W.y != nullptr)
+    sv = *reinterpret_cast<const uint32_t *>(W.svh + (size_t)expert * out + cg * 128 + 2 * lane);
+  const int nb = ntk >> 3, nitems = nrows * nb;
+  PrepRegs pr;
+  gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
+  // three steps' weights in flight: step i uses buffer i % 3 and then loads
+  // step i + 3 into it
+  constexpr int KB = K > 0 ? K : 1;
+  uint32_t b0[KB], b1[KB], b2[KB];
+  const uint32_t *wp = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
+  const size_t wstep = (size_t)4 * W.out_tiles * nw;  // dwords per step
+  if constexpr (K > 0) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) b0[i] = wp[i];
+    if (iters > 1) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) b1[i] = wp[wstep + i];
+    }
+    if (iters > 2) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) b2[i] = wp[2 * wstep + i];
+    }
+  }
+  gemv_prep_store(a, nitems, nb, 0, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
+  for (int base = PREP_BATCH * (GEMV_THREADS / 64); base < nitems;
+       base += PREP_BATCH * (GEMV_THREADS / 64)) {
+    gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, base, wave, lane, pr);
+    gemv_prep_store(a, nitems, nb, base, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
+  }
+  __syncthreads();
+
+  const int arow = min(lane & 15, nrows - 1);
+  const uint16_t *xa = xs + arow * kr + (kp * part + g) * 16;
+  f4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (K > 0) {
+    const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    auto step = [&](uint32_t(&b)[KB], int it) {
+      uint32_t wd[K + 1];
+#pragma unroll
+      for (int i = 0; i < K; ++i) wd[i + 1] = b[i];
+      wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)b[K - 1]);
+      const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
+      const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
+      // one B operand at a time (pairs f, f+4, f+8, f+12: rows 0-7 or 8-15 of
+      // column a or a+8), each consumed by its MFMA before the next is made
+      static_for<4>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
+        uint32_t q[4];
+        static_for<4>([&](auto J) {
+          constexpr int pq = p0 + 4 * decltype(J)::value;
+          if constexpr (FOLD)
+            q[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.mask);
+          else
+            q[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
+        });
+        const h8_t bf = frag(q[0], q[1], q[2], q[3]);
+        if constexpr (f == 0) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc0, 0, 0, 0);
+        if constexpr (f == 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc1, 0, 0, 0);
+        if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
+        if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
+      });
+      if (it + 3 < iters) {
+        const uint32_t *pn = wp + (size_t)(it + 3) * wstep;
+#pragma unroll
+        for (int i = 0; i < K; ++i) b[i] = pn[i];
+      }
+    };
+    int it = 0;
+    for (; it + 3 <= iters; it += 3) {
+      step(b0, it);
+      step(b1, it + 1);
+      step(b2, it + 2);
+    }
+    if (it < iters) step(b0, it);
+    if (it + 1 < iters) step(b1, it + 1);
+  } else {
+    // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
+    uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
+                                                   (size_t)2 * zrows * 128 * 4 +
+                                                   (size_t)rows_alloc * (a.tps / 4) * 4) +
+                      wave * 512;
+    for (int it = 0; it < iters; ++it) {
+      for (int i = lane; i < 8 * nw; i += 64) {
+        const int seg = i / (2 * nw), off = i - seg * 2 * nw;
+        stage[i] = twe[((size_t)(kb + 4 * it + seg) * W.out_tiles + cg * 8 + 2 * q) * nw + off];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t *mine = stage + (g * 2 + t) * nw;
+      const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
+      const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
+      uint32_t p[16];
+#pragma unroll
+      for (int pq = 0; pq < 16; ++pq) {
+        const uint32_t cw = 32u * c + 2u * pq;
+        p[pq] = decode_pair<CB>(tile_window(mine, a.n, cw), tile_window(mine, a.n, cw + 1u), a.mask);
+      }
+      gemv_mfma(p, alo, ahi, acc0, acc1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // C of a 16x16 MFMA: lane l holds rows 4(l/16)+i, column l%16.
+  const int col = (2 * q + t) * 16 + c;
+  float *zk = zp + kp * zrows * 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * g + i;
+    if (m < nrows) {
+      float z0 = acc0[i], z1 = acc1[i];
+      if constexpr (FOLD) {
+        // the k-part's 64-element sums of row m, in k order
+        const float *hs = hsum + m * nb * 2 + kp * (part >> 2);
+        float sx = 0.0f;
+        for (int h = 0; h < (part >> 2); ++h) sx = sx + hs[h];
+        const float bx = MUL1_B * sx;
+        z0 = MUL1_A * z0 + bx;
+        z1 = MUL1_A * z1 + bx;
+      }
+      zk[m * 128 + col] = z0;
+      zk[m * 128 + col + 8] = z1;
+    }
+  }
+  __syncthreads();
+  float *zf = zp;
+  for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
+  __syncthreads();
+  if (!gemv_splitk_last(zf, a, W, nrows, rows, ks, out, cg * 128)) return;
+  gemv_finish(zf, a, W, nrows, rows, sv, cg * 128);
+}
+
+// The weight of grid column group `gx` (weights' groups side by side): the
+// first column groups of weights 1..3 (0 when absent) come as separate
+// kernel parameters, which gfx950 preloads into SGPRs at wave launch, so
+// choosing the weight costs no load and its fields arrive in one round trip.
+__device__ __forceinline__ int gemv_weight_of(int gx, int cg1, int cg2, int cg3) {
+  return (cg1 > 0 && gx >= cg1) + (cg2 > 0 && gx >= cg2) + (cg3 > 0 && gx >= cg3);
+}
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GEMV_THREADS, 8) void gemv_kernel(int rows, int cg1, int cg2, int cg3,
+                                                            GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int wi = gemv_weight_of(blockIdx.x, cg1, cg2, cg3);
+  const GemvCfg c = a.c;
+  const GemvWeight W = a.w[wi];
+  const int cg = blockIdx.x - W.cg0;
+  GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
+  if (threadIdx.x < GEMV_ROWS) {
+    const int b = min((int)threadIdx.x, rows - 1);
+    ri[threadIdx.x] = GemvRow{b * c.in_tiles * 16, b * W.out_tiles * 16, b, 0};
+  }
+  __syncthreads();
+  gemv_wg<K, CB, MASKED>(c, W, 0, rows, ri, cg, blockIdx.y, smem + 256, rows);
+}
+
+
+// ===================================================================== GEMM
+//
+// Workgroup tile 256 rows x 256 columns (two Hadamard blocks of the output),
+// 4 waves, each a 128 x 128 sub-tile of 4 x 4 v_mfma_f32_32x32x16_f16 tiles
+// (256 f32 accumulators per lane).  The k loop runs in stages of 32 (two
+// k-tile rows).  While the MFMAs consume the current stage from LDS, every
+// thread decodes one chunk of the next stage (the 256 chunks of 2 k-tile rows
+// x 16 output tiles) into four MFMA B fragments (8 consecutive k of one
+// column each) and stores them into the other LDS buffer as B^T [n][k] rows,
+// stores its four 16-byte pieces of the next A tile (prepared rows, f16), and
+// loads the pieces and packed words of the stage three ahead into the
+// register set it just freed (three sets in flight); the decode's VALU work
+// and the memory operations are interleaved between the MFMAs.  LDS rows are padded to 40 halfs (80
+// bytes), so the 16-byte operand reads of 16 consecutive rows hit distinct
+// banks.  The MFMAs take the weights as their first operand, so the
+// accumulators hold z^T: a lane holds one row of z and 16 of its columns.
+// That is the operand layout of a second MFMA, which applies the finish's
+// Hadamard stages on column bits 0-4 (H_32, +-1 entries: exact products,
+// f32 sums) to f16(z); stages 5 and 6 are the reference's butterflies across
+// the four 32-column blocks, in registers, then * 1/sqrt(128) * svh.  No LDS
+// round trip.  Each decoded weight serves 256 rows and each staged activation
+// 256 columns.
+
+constexpr int GM_BM = 256, GM_BN = 256, GM_BK = 32, GM_THREADS = 256;
+constexpr int GM_LD = GM_BK + 8;      // halfs per LDS row of A / column of B^T
+constexpr int GM_TILE = 256 * GM_LD;  // halfs per operand buffer
+constexpr int GM_LDS_HALFS = 4 * GM_TILE;  // A and B^T, two stages
+
+// A chunk's 32 codewords as four MFMA B fragments of 8 consecutive k of one
+// column: f = 0: column a, tile rows 0-7; 1: column a+8, rows 0-7; 2: column
+// a, rows 8-15; 3: column a+8, rows 8-15 (pairs p, p+4, p+8, p+12 for p = 0,
+// 2, 1, 3), stored to B^T at column n0 (+8) and k k0 (+8).
+template <int K, int CB, bool MASKED>
+__device__ __forceinline__ void gemm_decode_chunk(const uint32_t (&wd)[K + 1], uint16_t *bt, int n0,
+                                                  int k0, uint32_t mask) {
+  static_for<4>([&](auto F) {
+    constexpr int f = decltype(F)::value;
+    constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
+    uint32_t q[4];
+    static_for<4>([&](auto J) {
+      q[J] = chunk_pair_cw<K, CB, MASKED, p0 + 4 * decltype(J)::value>(wd, mask);
+    });
+    const u4_t v = {q[0], q[1], q[2], q[3]};
+    *reinterpret_cast<u4_t *>(bt + (n0 + 8 * (f & 1)) * GM_LD + k0 + 8 * (f >> 1)) = v;
+  });
+}
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
+    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
+    int M, int in_tiles, int out_tiles, uint32_t mask) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_HALFS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking
+  // the row block as n % (row blocks) lets an XCD's workgroups share a few
+  // row blocks of A in its L2.  (Only the speed depends on this.)
+  const int mblocks = gridDim.y;
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int cp = lin / mblocks;  // columns 256 cp ..
+  const int m0 = (lin % mblocks) * GM_BM;
+  const int in = in_tiles * 16;
+  const size_t out = (size_t)out_tiles * 16;
+  const int nw = 8 * K;
+
+  // decoder role: chunk c of output tile tnl of k-tile row tkl of the stage;
+  // the 8 chunks of a tile sit in 8 consecutive lanes.  Tiles past the last
+  // column (the second half of an odd last pair) decode tile 0 instead and
+  // their results are not stored.
+  const int tkl = tid >> 7, tnl = (tid >> 3) & 15, c = tid & 7;
+  const int tcol = cp * 16 + tnl < out_tiles ? cp * 16 + tnl : 0;
+  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + tcol) * nw + c * K;
+  const size_t wstage = (size_t)2 * out_tiles * nw;  // dwords per stage
+  const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of chunk c-1
+  const int bn0 = tnl * 16 + c, bk0 = tkl * 16;
+
+  // A staging: pieces t + 256 i (i = 0..3) of the 256 x 4 16-byte pieces of
+  // a stage: row (t >> 2) + 64 i, piece t & 3.  Rows past M read row M - 1
+  // (not stored; rows of an MFMA are independent), so no load branches.
+  const int arow = tid >> 2, apc = tid & 3;
+  const uint16_t *ap[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    ap[i] = xp + (size_t)min(m0 + arow + 64 * i, M - 1) * in + apc * 8;
+  const int ast = arow * GM_LD + apc * 8;
+
+  // operand fragments of this lane in a stage buffer
+  const int am = (wr * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
+  const int bn = (wc * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
+
+  f16v_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  h8_t ar[3][4];
+  uint32_t wn[3][K];
+  const int stages = in_tiles / 2;  // >= 4: in is a multiple of 128
+  // register set S <- stage st (clamped to the last stage: in bounds, unused)
+  auto load_stage = [&](auto S, int st) {
+    constexpr int q = decltype(S)::value;
+    st = min(st, stages - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ar[q][i] = *reinterpret_cast<const h8_t *>(ap[i] + st * GM_BK);
+    const uint32_t *p = twc + (size_t)st * wstage;
+#pragma unroll
+    for (int j = 0; j < K; ++j) wn[q][j] = p[j];
+  };
+  // register set S -> LDS buffer at off (A pieces, decoded chunk)
+  auto store_stage = [&](auto S, int off) {
+    constexpr int q = decltype(S)::value;
+    uint16_t *as = lds + off, *bs = lds + off + GM_TILE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t *>(as + ast + i * 64 * GM_LD) = ar[q][i];
+    uint32_t wd[K + 1];
+#pragma unroll
+    for (int j = 0; j < K; ++j) wd[j + 1] = wn[q][j];
+    wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
+    gemm_decode_chunk<K, CB, MASKED>(wd, bs, bn0, bk0, mask);
+  };
+  // stage st: MFMAs on buffer st & 1; set S (stage st + 1) into the other
+  // buffer, then set S <- stage st + 4
+  auto stage = [&](auto S, int st) {
+    const int cur = (st & 1) * 2 * GM_TILE, nxt = 2 * GM_TILE - cur;
+    const uint16_t *ac = lds + cur, *bc = lds + cur + GM_TILE;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      h8_t a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const h8_t *>(ac + am + i * 32 * GM_LD + kk * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const h8_t *>(bc + bn + j * 32 * GM_LD + kk * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[j][i], 0, 0, 0);
+    }
+    store_stage(S, nxt);
+    load_stage(S, st + 4);
+    // operands of the first slab, then each MFMA followed by a share of the
+    // VALU work and of the memory operations
+    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);  // VALU
+      if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
+      if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
+    }
+    __syncthreads();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  load_stage(I0{}, 0);
+  load_stage(I1{}, 1);
+  load_stage(I2{}, 2);
+  store_stage(I0{}, 0);
+  load_stage(I0{}, 3);
+  __syncthreads();
+  int st = 0;
+  for (; st + 3 <= stages; st += 3) {
+    stage(I1{}, st);
+    stage(I2{}, st + 1);
+    stage(I0{}, st + 2);
+  }
+  if (st < stages) stage(I1{}, st);
+  if (st + 1 < stages) stage(I2{}, st + 1);
+
+  // acc[j][i] = z^T for columns 32 j .. of the wave's column group and rows
+  // 32 i .. of its 128: lane l holds row (l & 31), register r column
+  // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
+  const int cg = cp * 2 + wc;
+  if (cg * 8 >= out_tiles) return;  // the odd half of the last pair
+  const int rb = m0 + wr * 128 + (lane & 31);
+  if (y == nullptr) {
+    static_for<4>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (rb + 32 * i < M) {
+        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 4 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[j][i][r]);
+      }
+    });
+    return;
+  }
+  // H_32 as the second operand: element e of fragment kk pairs with column
+  // 16 kk + 8 (e / 4) + 4 (l / 32) + e % 4 of a 32-column block (the
+  // registers 8 kk + e above), output column (l & 31).
+  h8_t hb[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int nl = 16 * kk + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      hb[kk][e] = (__builtin_popcount(nl & lane & 31) & 1) ? -1.0f16 : 1.0f16;
+    }
+  float sv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sv[j] = h2f(svh[cg * 128 + 32 * j + (lane & 31)]);
+  static_for<4>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    // D2_j = f16(z block j) H_32: lane l holds output column (l & 31),
+    // register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the 32
+    f16v_t d2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h8_t a0, a1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a0[e] = bits<_Float16>(f2h(acc[j][i][e]));
+        a1[e] = bits<_Float16>(f2h(acc[j][i][8 + e]));
+      }
+      f16v_t zero = {};
+      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
+      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wr * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi)
+      const float t0 = d2[0][r] + d2[1][r], t1 = d2[0][r] - d2[1][r];
+      const float t2 = d2[2][r] + d2[3][r], t3 = d2[2][r] - d2[3][r];
+      const float u[4] = {t0 + t2, t1 + t3, t0 - t2, t1 - t3};
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          store_out(y, (size_t)m * out + cg * 128 + 32 * j + (lane & 31),
+                    f2h((u[j] * HAD_SCALE) * sv[j]), ydt);
+      }
+    }
+  });
+}
+
+// ==================================================== grouped MoE GEMV
+
+// A work item of the routed MoE: up to GEMV_ROWS slots of one expert.
+struct MoeItem {
+  uint32_t expert, start, count, pad;
+};
+
+constexpr int MOE_ITEM_ROWS = GEMV_ROWS;
+
+// Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
+// launch's weights (gate and up side by side, or down).  Raw inputs are rows
+// slot / topk of x; prepared inputs are rows slot.
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
+    int cg1, int topk, const uint32_t *__restrict__ sorted, const MoeItem *__restrict__ items,
+    const uint32_t *__restrict__ n_items, GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int item = blockIdx.z;
+  if ((uint32_t)item >= *n_items) return;
+  const MoeItem it = items[item];
+  const int wi = gemv_weight_of(blockIdx.x, cg1, 0, 0);
+  const GemvCfg c = a.c;
+  const GemvWeight W = a.w[wi];
+  const int cg = blockIdx.x - W.cg0;
+  GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
+  if (threadIdx.x < GEMV_ROWS) {
+    const int b = min((int)threadIdx.x, (int)it.count - 1);
+    const int slot = (int)sorted[it.start + b];
+    const int in = c.in_tiles * 16, out = W.out_tiles * 16;
+    ri[threadIdx.x] = GemvRow{(c.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
+  }
+  __syncthreads();
+  gemv_wg<K, CB, MASKED>(c, W, (int)it.expert, (int)it.count, ri, cg, blockIdx.y,
+                         smem + 256, MOE_ITEM_ROWS);
+}
+
+
+// ====================================================== per-rate launchers
+//
+// K = 1..8: an integer rate (n = 16K) with compile-time windows; K = 0: any
+// even n (GEMV only).
+
+template <int K>
+void gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, int rows, int cg1, int cg2,
+             int cg3, const GemvArgs &a) {
+  const dim3 blk(GEMV_THREADS);
+  if (f.codebook == CB_MCG) {
+    if (f.window < 16)
+      hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+    else
+      hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+  } else {
+    if (f.window < 16)
+      hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+    else
+      hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, rows, cg1, cg2, cg3,
+                         a);
+  }
+}
+
+template <int K>
+void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, int cg1, int topk,
+                 const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
+                 const GemvArgs &a) {
+  const dim3 blk(GEMV_THREADS);
+  if (f.codebook == CB_MCG) {
+    if (f.window < 16)
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, cg1, topk, sorted,
+                         items, n_items, a);
+    else
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, cg1, topk, sorted,
+                         items, n_items, a);
+  } else {
+    if (f.window < 16)
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, cg1, topk, sorted,
+                         items, n_items, a);
+    else
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, cg1, topk, sorted,
+                         items, n_items, a);
+  }
+}
+
+template <int K>
+void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
+             const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
+             int out_tiles) {
+  static_assert(K > 0, "the GEMM serves integer rates");
+  const dim3 blk(GM_THREADS);
+  const uint32_t m = f.mask();
+  if (f.codebook == CB_MCG) {
+    if (f.window < 16)
+      hipLaunchKernelGGL((gemm_kernel<K, CB_MCG, true>), grid, blk, 0, s, tw, xp, svh, y, ydt, zout,
+                         M, in_tiles, out_tiles, m);
+    else
+      hipLaunchKernelGGL((gemm_kernel<K, CB_MCG, false>), grid, blk, 0, s, tw, xp, svh, y, ydt,
+                         zout, M, in_tiles, out_tiles, m);
+  } else {
+    if (f.window < 16)
+      hipLaunchKernelGGL((gemm_kernel<K, CB_MUL1, true>), grid, blk, 0, s, tw, xp, svh, y, ydt,
+                         zout, M, in_tiles, out_tiles, m);
+    else
+      hipLaunchKernelGGL((gemm_kernel<K, CB_MUL1, false>), grid, blk, 0, s, tw, xp, svh, y, ydt,
+                         zout, M, in_tiles, out_tiles, m);
+  }
+}
+
+// Declarations of one rate's launcher instantiations.
+#define EXL3_GEMV_GO(KK) \
+  void gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, int, int, int, int, const GemvArgs &)
+#define EXL3_MOE_GEMV_GO(KK)                                                                   \
+  void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, int, int, const uint32_t *, \
+                       const MoeItem *, const uint32_t *, const GemvArgs &)
+#define EXL3_GEMM_GO(KK)                                                                    \
+  void gemm_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
+                   const uint16_t *, void *, int, uint16_t *, int, int, int)
+
+#ifndef EXL3_INST_K
+// instantiated in the per-rate units only
+#define EXL3_EXTERN_RATE(KK)            \
+  extern template EXL3_GEMV_GO(KK);     \
+  extern template EXL3_MOE_GEMV_GO(KK);
+EXL3_EXTERN_RATE(0)
+EXL3_EXTERN_RATE(1)
+EXL3_EXTERN_RATE(2)
+EXL3_EXTERN_RATE(3)
+EXL3_EXTERN_RATE(4)
+EXL3_EXTERN_RATE(5)
+EXL3_EXTERN_RATE(6)
+EXL3_EXTERN_RATE(7)
+EXL3_EXTERN_RATE(8)
+#undef EXL3_EXTERN_RATE
+extern template EXL3_GEMM_GO(1);
+extern template EXL3_GEMM_GO(2);
+extern template EXL3_GEMM_GO(3);
+extern template EXL3_GEMM_GO(4);
+extern template EXL3_GEMM_GO(5);
+extern template EXL3_GEMM_GO(6);
+extern template EXL3_GEMM_GO(7);
+extern template EXL3_GEMM_GO(8);
+#endif
+
+}  // namespace exl3
