@@ -35,6 +35,16 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 // s_waitcnt vmcnt(0): this wave's outstanding vector-memory operations,
 // stores included on gfx9-family parts, have completed.
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Workgroup barrier that orders LDS only: the fences name the local address
+// space, so the barrier waits for this wave's LDS operations (lgkmcnt) but
+// not for its global loads in flight (a __syncthreads() fence also covers
+// global memory and so waits for every outstanding load, prefetches
+// included).  Global memory shared between waves is ordered explicitly.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // ===================================================================== GEMV
 //
@@ -62,12 +72,22 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 //     many rows share the call.
 //  With mul1 at an integer rate the MFMAs take the codebook value before its
 //  affine step (chunk_pair_mul1_h) and the step is applied to the sums.
+//
+//  Every memory round trip is on the critical path of a launch this small
+//  (a q/o linear at K=4 is 8 MiB: about 1 us of HBM time), so the trellis
+//  and activation pointers and the launch geometry are kernel arguments that
+//  gfx950 preloads into SGPRs: a workgroup issues its weight and activation
+//  loads at its first instructions, with no kernel-argument load before them.
 
 constexpr int GEMV_THREADS = 512;
 constexpr int GEMV_ROWS = 16;
 constexpr int GEMV_TPS_MAX = 64;
 constexpr int GEMV_KSPLIT_MAX = 64;
 constexpr int GEMV_MAXW = 4;
+// Prepare items (one row's 128-block) per wave per batch, and per batch of
+// the workgroup.
+constexpr int PREP_BATCH = 2;
+constexpr int PREP_ITEMS = PREP_BATCH * (GEMV_THREADS / 64);
 
 struct GemvRow {
   int in_off;   // element offset of the row's activations
@@ -76,34 +96,65 @@ struct GemvRow {
   int pad;
 };
 
+// Per weight, read from the kernel-argument segment after the loads are out.
 struct GemvWeight {
-  const uint32_t *tw;   // trellis dwords (a bank's expert 0)
   const uint16_t *suh;  // [E][in]
   const uint16_t *svh;  // [E][out]
   void *y;              // finished output in ydt, or nullptr:
   uint16_t *zout;       // the inner product z (f16) instead
   float *partial;       // [ksplit][ptotal][out] slots, empty between calls
-  size_t expert_words;  // dwords per expert
-  int out_tiles;
-  int cg0;              // first grid column group of this weight
+  size_t expert_words;  // trellis dwords per expert
 };
 
-// The scalars of a launch, copied into SGPRs at kernel entry with the chosen
-// weight's fields (one round trip of argument loads).
 struct GemvCfg {
-  const void *x;  // activations (ACT_*), or prepared rows (f16) when prepared
-  size_t ptotal;
-  int xdt;
-  int prepared;
+  size_t ptotal;  // rows of the partial-sum slots
   int ydt;
-  int in_tiles, n, ksplit, tps;
+  int ksplit;
   uint32_t mask;
+  int nw;  // trellis dwords per tile (n / 2)
 };
 
 struct GemvArgs {
   GemvCfg c;
   GemvWeight w[GEMV_MAXW];
-  int nweights;
+};
+
+// Launch geometry in three words (preloaded SGPRs, so that no launch value
+// costs a load; gridDim itself is a load from the implicit arguments):
+//   g0 = cg1 | cg2 << 16     first column groups of weights 1, 2 (0: absent)
+//   g1 = cg3 | cgend << 16   ... of weight 3, and the end of the last weight
+//   g2 = in_tiles | tps << 16 | rows << 23 | xdt << 28 | prepared << 30
+struct GemvGeo {
+  int cg1, cg2, cg3, cgend, in_tiles, tps, rows, xdt, prepared;
+  __host__ __device__ static GemvGeo unpack(uint32_t g0, uint32_t g1, uint32_t g2) {
+    GemvGeo g;
+    g.cg1 = (int)(g0 & 0xFFFFu);
+    g.cg2 = (int)(g0 >> 16);
+    g.cg3 = (int)(g1 & 0xFFFFu);
+    g.cgend = (int)(g1 >> 16);
+    g.in_tiles = (int)(g2 & 0xFFFFu);
+    g.tps = (int)((g2 >> 16) & 0x7Fu);
+    g.rows = (int)((g2 >> 23) & 0x1Fu);
+    g.xdt = (int)((g2 >> 28) & 3u);
+    g.prepared = (int)((g2 >> 30) & 1u);
+    return g;
+  }
+};
+inline void gemv_geo_pack(const GemvGeo &g, uint32_t *g0, uint32_t *g1, uint32_t *g2) {
+  *g0 = (uint32_t)g.cg1 | ((uint32_t)g.cg2 << 16);
+  *g1 = (uint32_t)g.cg3 | ((uint32_t)g.cgend << 16);
+  *g2 = (uint32_t)g.in_tiles | ((uint32_t)g.tps << 16) | ((uint32_t)g.rows << 23) |
+        ((uint32_t)g.xdt << 28) | ((uint32_t)g.prepared << 30);
+}
+
+// Row b of a workgroup: its activations, output and partial-sum row.  A
+// table in LDS (the MoE's slots) or, without one, row b of the call.
+struct RowMap {
+  const GemvRow *t;
+  int in, out;
+  __device__ __forceinline__ int in_off(int b) const { return t ? t[b].in_off : b * in; }
+  __device__ __forceinline__ int out_off(int b) const { return t ? t[b].out_off : b * out; }
+  __device__ __forceinline__ int prow(int b) const { return t ? t[b].prow : b; }
 };
 
 // Dynamic LDS of a GEMV workgroup: row table, prepared rows, the two
@@ -118,10 +169,8 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 
 // The rows' input slice [tk0*16, tk0*16 + ntk*16) prepared into xs (row
 // stride kr halfs): one wave per (row, 128-block) item.  Loads and
-// arithmetic are split so a workgroup can issue the first items' loads
-// before its weight loads (the prepare is on the critical path; the weights
-// are not needed until it is done).
-constexpr int PREP_BATCH = 2;  // items per wave per batch
+// arithmetic are split so a workgroup issues its first items' loads with its
+// weight loads.
 
 // Raw bits as loaded (converted only when the rows are prepared, so the
 // loads do not wait): x holds the two elements (one dword for f16/bf16, two
@@ -130,39 +179,54 @@ struct PrepRegs {
   uint32_t x0[PREP_BATCH], x1[PREP_BATCH], su[PREP_BATCH];
 };
 
+// Branch-free: all three readings are formed and one is selected, so no
+// control flow joins while the weight loads are in flight.
 __device__ __forceinline__ void prep_unpack(uint32_t x0, uint32_t x1, int dt, float &a, float &b) {
-  if (dt == OUT_F32) {
-    a = bits<float>(x0);
-    b = bits<float>(x1);
-  } else if (dt == OUT_BF16) {
-    a = bf2f((uint16_t)(x0 & 0xFFFFu));
-    b = bf2f((uint16_t)(x0 >> 16));
-  } else {
-    a = h2f((uint16_t)(x0 & 0xFFFFu));
-    b = h2f((uint16_t)(x0 >> 16));
-  }
+  const float fa = h2f((uint16_t)(x0 & 0xFFFFu)), fb = h2f((uint16_t)(x0 >> 16));
+  const float ba = bits<float>(x0 << 16), bb = bits<float>(x0 & 0xFFFF0000u);
+  const float sa = bits<float>(x0), sb = bits<float>(x1);
+  a = dt == OUT_F32 ? sa : dt == OUT_BF16 ? ba : fa;
+  b = dt == OUT_F32 ? sb : dt == OUT_BF16 ? bb : fb;
 }
 
-__device__ __forceinline__ void gemv_prep_load(const GemvCfg &a, const GemvWeight &W, int expert,
-                                               const GemvRow *rows, int nitems, int nb, int tk0,
-                                               int base, int wave, int lane, PrepRegs &r) {
-  const int in = a.in_tiles * 16;
+// Items past the last one load (and later store) the last item again: the
+// same values to the same place.  Every lane issues the same loads whatever
+// the dtype (f16/bf16 read their dword twice; prepared rows read x in place
+// of suh), so the batch has no branches around its loads and the waits for
+// them do not also wait for the weight loads in flight.  The activations
+// need only preloaded arguments; suh needs its pointer from the argument
+// segment, so it is a second call.
+__device__ __forceinline__ void gemv_prep_load_x(const void *x, int xdt, int prepared,
+                                                 const RowMap &rm, int nitems, int nb, int tk0,
+                                                 int base, int wave, int lane, PrepRegs &r) {
+  const int esz = (!prepared && xdt == OUT_F32) ? 4 : 2;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    const int it = base + wave + j * (GEMV_THREADS / 64);
-    if (it >= nitems) break;
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
-    const size_t xo = (size_t)rows[row].in_off + k;
-    if (a.prepared || a.xdt != OUT_F32) {
-      r.x0[j] = *reinterpret_cast<const uint32_t *>((const uint16_t *)a.x + xo);
-    } else {
-      const u2_t v = *reinterpret_cast<const u2_t *>((const float *)a.x + xo);
-      r.x0[j] = v[0];
-      r.x1[j] = v[1];
-    }
-    if (!a.prepared)
-      r.su[j] = *reinterpret_cast<const uint32_t *>(W.suh + (size_t)expert * in + k);
+    const char *pa = (const char *)x + ((size_t)rm.in_off(row) + k) * esz;
+    r.x0[j] = *reinterpret_cast<const uint32_t *>(pa);
+    r.x1[j] = *reinterpret_cast<const uint32_t *>(pa + (esz - 2) * 2);
+  }
+}
+// A load through the global address space (a pointer that passed through
+// inline asm is otherwise generic, and a flat load is waited for as both a
+// vector-memory and an LDS operation).
+__device__ __forceinline__ uint32_t ld_global_u32(const void *p) {
+  return *(const __attribute__((address_space(1))) uint32_t *)p;
+}
+
+__device__ __forceinline__ void gemv_prep_load_su(const void *x, int prepared, const uint16_t *suh,
+                                                  int nitems, int nb, int tk0, int base, int wave,
+                                                  int lane, PrepRegs &r) {
+  const uint16_t *sup = prepared ? (const uint16_t *)x : suh;
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
+    const int blk = it % nb;
+    const int k = tk0 * 16 + blk * 128 + 2 * lane;
+    r.su[j] = ld_global_u32(sup + k);
   }
 }
 
@@ -187,28 +251,24 @@ __device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
 // Stores the prepared pairs; with hsum (row stride nb * 2) also the sum of
 // each 64 prepared elements (lanes 0-31 and 32-63 of an item), added in a
 // fixed butterfly order.
-__device__ __forceinline__ void gemv_prep_store(const GemvCfg &a, int nitems, int nb, int base,
-                                                int wave, int lane, uint16_t *xs, int kr,
+__device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitems, int nb,
+                                                int base, int wave, int lane, uint16_t *xs, int kr,
                                                 const PrepRegs &r, float *hsum) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    const int it = base + wave + j * (GEMV_THREADS / 64);
-    if (it >= nitems) break;
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
-    uint32_t y;
-    if (a.prepared) {
-      y = r.x0[j];
-    } else {
-      // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
-      // (expert_exl3.zig:490-501)
-      float x0, x1;
-      prep_unpack(r.x0[j], r.x1[j], a.xdt, x0, x1);
-      float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
-      float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
-      had128_pair(v0, v1, lane);
-      y = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
-    }
+    // f16(x) * suh in f32, the butterfly, * 1/sqrt(128), f16
+    // (expert_exl3.zig:490-501); prepared rows are taken as they are (the
+    // rotation is formed regardless and not used: no branch)
+    float x0, x1;
+    prep_unpack(r.x0[j], r.x1[j], xdt, x0, x1);
+    float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
+    float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
+    had128_pair(v0, v1, lane);
+    const uint32_t rot = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+    const uint32_t y = prepared ? r.x0[j] : rot;
     *dst = y;
     if (hsum != nullptr) {
       float s = h2f((uint16_t)(y & 0xFFFFu)) + h2f((uint16_t)(y >> 16));
@@ -250,14 +310,13 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 constexpr uint32_t PARTIAL_EMPTY = 0xFFFFFFFFu;
 constexpr int PARTIAL_POLL_MAX = 1 << 20;
 
-__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
-                                                 const GemvWeight &W, int nrows,
-                                                 const GemvRow *rows, int ks, size_t out,
+__device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, float *partial,
+                                                 int nrows, const RowMap &rm, int ks, size_t out,
                                                  int col0) {
   const int E = nrows * 128;
   if (a.ksplit == 1) {
     for (int e = threadIdx.x; e < E; e += GEMV_THREADS) zf[e] = h2f(f2h(zf[e]));
-    __syncthreads();
+    lds_barrier();
     return true;
   }
   const size_t stride = a.ptotal * out;
@@ -266,14 +325,14 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
       const int b = e >> 7, col = e & 127;
       float v = zf[e];
       if (v != v) v = bits<float>(0x7FC00000u);  // never PARTIAL_EMPTY
-      st_agent(W.partial + ks * stride + (size_t)rows[b].prow * out + col0 + col, v);
+      st_agent(partial + ks * stride + (size_t)rm.prow(b) * out + col0 + col, v);
     }
     return false;
   }
   const float empty = bits<float>(PARTIAL_EMPTY);
   for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    float *p = W.partial + (size_t)rows[b].prow * out + col0 + col;
+    float *p = partial + (size_t)rm.prow(b) * out + col0 + col;
     float s = 0.0f;
     for (int k0 = 0; k0 < ks; k0 += 16) {
       float v[16];
@@ -294,7 +353,7 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a,
     }
     zf[e] = h2f(f2h(s + zf[e]));
   }
-  __syncthreads();
+  lds_barrier();
   return true;
 }
 
@@ -317,13 +376,12 @@ __device__ __forceinline__ void store_out2(void *p, size_t i, uint16_t y0, uint1
 // * 1/sqrt(128), * svh, f16, output dtype (one wave per row, element i in
 // lane i/2); or z itself when y is null.  sv holds svh of this lane's two
 // columns (2 lane, 2 lane + 1), loaded at the start.
-__device__ __forceinline__ void gemv_finish(float *zf, const GemvCfg &a, const GemvWeight &W,
-                                            int nrows, const GemvRow *rows, uint32_t sv,
-                                            int col0) {
-  if (W.y == nullptr) {
+__device__ __forceinline__ void gemv_finish(float *zf, int ydt, void *y, uint16_t *zout, int nrows,
+                                            const RowMap &rm, uint32_t sv, int col0) {
+  if (y == nullptr) {
     for (int e = threadIdx.x; e < nrows * 128; e += GEMV_THREADS) {
       const int b = e >> 7, col = e & 127;
-      W.zout[(size_t)rows[b].out_off + col0 + col] = f2h(zf[e]);
+      zout[(size_t)rm.out_off(b) + col0 + col] = f2h(zf[e]);
     }
     return;
   }
@@ -333,23 +391,29 @@ __device__ __forceinline__ void gemv_finish(float *zf, const GemvCfg &a, const G
     float v0 = zf[b * 128 + 2 * lane], v1 = zf[b * 128 + 2 * lane + 1];
     had128_pair(v0, v1, lane);
     const float s0 = v0 * HAD_SCALE, s1 = v1 * HAD_SCALE;
-    store_out2(W.y, (size_t)rows[b].out_off + col0 + 2 * lane, f2h(s0 * sv0), f2h(s1 * sv1), a.ydt);
+    store_out2(y, (size_t)rm.out_off(b) + col0 + 2 * lane, f2h(s0 * sv0), f2h(s1 * sv1), ydt);
   }
 }
 
-// One workgroup of the GEMV: expert `expert` of weight W, nrows <= 16 rows
-// (table `rows` in LDS), column group cg of W, split ks.
-template <int K, int CB, bool MASKED>
-__device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, int expert,
-                                        int nrows, const GemvRow *rows, int cg,
-                                        int ks, char *smem, int rows_alloc) {
+// One workgroup of the GEMV: expert `expert` of the weight with trellis
+// words `twe` (that expert's) and out_tiles output tiles, nrows <= 16 rows
+// (row map rm), column group cg, split ks.  ONEB: the rows' items fit one
+// prepare batch (nrows * tps / 8 <= PREP_ITEMS).
+template <int K, int CB, bool MASKED, bool ONEB>
+__device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, const void *x,
+                                        const GemvGeo &geo, const GemvCfg &a,
+                                        const GemvWeight &W, int expert, int nrows,
+                                        const RowMap &rm, int cg, int ks, char *smem,
+                                        int rows_alloc) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = wave & 3, kp = wave >> 2;
-  const size_t out = (size_t)W.out_tiles * 16;
-  const int tk0 = ks * a.tps;
-  const int ntk = min(a.tps, a.in_tiles - tk0);  // a multiple of 8
-  const int kr = a.tps * 16 + 8;
+  const size_t out = (size_t)out_tiles * 16;
+  const int tps = geo.tps, in_tiles = geo.in_tiles;
+  const int in = in_tiles * 16;
+  const int tk0 = ks * tps;
+  const int ntk = min(tps, in_tiles - tk0);  // a multiple of 8
+  const int kr = tps * 16 + 8;
   uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
   const int zrows = rows_alloc > 2 ? rows_alloc : 2;
   float *zp = reinterpret_cast<float *>(smem + (size_t)rows_alloc * kr * 2);  // [2][zrows][128]
@@ -359,48 +423,61 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
   // hsum[row][ntk / 4] that the prepare leaves
   constexpr bool FOLD = K > 0 && CB == CB_MUL1;
   float *hsum = zp + 2 * zrows * 128;
-  const int nw = a.n >> 1;
+  const int nw = K > 0 ? 8 * K : a.nw;  // trellis dwords per tile
   const int g = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
   const size_t tn = (size_t)cg * 8 + 2 * q + t;
-  const uint32_t *twe = W.tw + (size_t)expert * W.expert_words;
   const int part = ntk >> 1;  // k-tile rows per k-part, a multiple of 4
   const int kb = tk0 + kp * part;
   const int iters = part >> 2;
 
-  // svh of the group's columns for the finish, the first prepare items'
-  // loads, then the first two steps' weights, so the weights are in flight
-  // while the rows are prepared
-  uint32_t sv = 0;
-  if (W.y != nullptr)
-    sv = *reinterpret_cast<const uint32_t *>(W.svh + (size_t)expert * out + cg * 128 + 2 * lane);
-  const int nb = ntk >> 3, nitems = nrows * nb;
-  PrepRegs pr;
-  gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, 0, wave, lane, pr);
-  // three steps' weights in flight: step i uses buffer i % 3 and then loads
-  // step i + 3 into it
+  // Loads of the workgroup's start, all in flight at once, in the order
+  // their data is needed (vector loads complete in issue order): the first
+  // prepare items' activations, the first step's weights, suh of those items,
+  // the next two steps' weights (steps past the last reload the last one: in
+  // bounds and unused, so no branches and the waits stay exact), svh for the
+  // finish.
   constexpr int KB = K > 0 ? K : 1;
   uint32_t b0[KB], b1[KB], b2[KB];
-  const uint32_t *wp = twe + ((size_t)(kb + g) * W.out_tiles + tn) * nw + c * K;
-  const size_t wstep = (size_t)4 * W.out_tiles * nw;  // dwords per step
+  const uint32_t *wp = twe + ((size_t)(kb + g) * out_tiles + tn) * nw + c * K;
+  const size_t wstep = (size_t)4 * out_tiles * nw;  // dwords per step
+  const int nb = ntk >> 3, nitems = nrows * nb;
+  PrepRegs pr;
+  gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
   if constexpr (K > 0) {
 #pragma unroll
     for (int i = 0; i < K; ++i) b0[i] = wp[i];
-    if (iters > 1) {
+  }
+  // The loads above use preloaded arguments only.  W.suh comes from the
+  // argument segment (a scalar load issued at entry); passing it through an
+  // empty asm statement that also orders memory keeps the wait for that
+  // scalar load after the loads above are issued.
+  const uint16_t *suh0 = W.suh;
+  asm volatile("" : "+s"(suh0)::"memory");
+  const uint16_t *suh = suh0 + (size_t)expert * in;
+  gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
+  if constexpr (K > 0) {
+    const uint32_t *p1 = wp + (size_t)min(1, iters - 1) * wstep;
+    const uint32_t *p2 = wp + (size_t)min(2, iters - 1) * wstep;
 #pragma unroll
-      for (int i = 0; i < K; ++i) b1[i] = wp[wstep + i];
-    }
-    if (iters > 2) {
+    for (int i = 0; i < K; ++i) b1[i] = p1[i];
 #pragma unroll
-      for (int i = 0; i < K; ++i) b2[i] = wp[2 * wstep + i];
+    for (int i = 0; i < K; ++i) b2[i] = p2[i];
+  }
+  // svh of this lane's two columns (read whether or not the finish runs: a
+  // load without a branch around it)
+  const uint16_t *svp = W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : suh;
+  const uint32_t sv = ld_global_u32(svp + 2 * lane);
+  gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
+                  FOLD ? hsum : nullptr);
+  if constexpr (!ONEB) {
+    for (int base = PREP_ITEMS; base < nitems; base += PREP_ITEMS) {
+      gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, base, wave, lane, pr);
+      gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, base, wave, lane, pr);
+      gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, base, wave, lane, xs, kr, pr,
+                      FOLD ? hsum : nullptr);
     }
   }
-  gemv_prep_store(a, nitems, nb, 0, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
-  for (int base = PREP_BATCH * (GEMV_THREADS / 64); base < nitems;
-       base += PREP_BATCH * (GEMV_THREADS / 64)) {
-    gemv_prep_load(a, W, expert, rows, nitems, nb, tk0, base, wave, lane, pr);
-    gemv_prep_store(a, nitems, nb, base, wave, lane, xs, kr, pr, FOLD ? hsum : nullptr);
-  }
-  __syncthreads();
+  lds_barrier();
 
   const int arow = min(lane & 15, nrows - 1);
   const uint16_t *xa = xs + arow * kr + (kp * part + g) * 16;
@@ -419,25 +496,23 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
       static_for<4>([&](auto F) {
         constexpr int f = decltype(F)::value;
         constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
-        uint32_t q[4];
+        uint32_t qv[4];
         static_for<4>([&](auto J) {
           constexpr int pq = p0 + 4 * decltype(J)::value;
           if constexpr (FOLD)
-            q[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.mask);
+            qv[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.mask);
           else
-            q[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
+            qv[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
         });
-        const h8_t bf = frag(q[0], q[1], q[2], q[3]);
+        const h8_t bf = frag(qv[0], qv[1], qv[2], qv[3]);
         if constexpr (f == 0) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc0, 0, 0, 0);
         if constexpr (f == 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc1, 0, 0, 0);
         if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
         if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
       });
-      if (it + 3 < iters) {
-        const uint32_t *pn = wp + (size_t)(it + 3) * wstep;
+      const uint32_t *pn = wp + (size_t)min(it + 3, iters - 1) * wstep;
 #pragma unroll
-        for (int i = 0; i < K; ++i) b[i] = pn[i];
-      }
+      for (int i = 0; i < K; ++i) b[i] = pn[i];
     };
     int it = 0;
     for (; it + 3 <= iters; it += 3) {
@@ -451,12 +526,13 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
     // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
     uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
                                                    (size_t)2 * zrows * 128 * 4 +
-                                                   (size_t)rows_alloc * (a.tps / 4) * 4) +
+                                                   (size_t)rows_alloc * (tps / 4) * 4) +
                       wave * 512;
+    const int n = 2 * nw;
     for (int it = 0; it < iters; ++it) {
       for (int i = lane; i < 8 * nw; i += 64) {
         const int seg = i / (2 * nw), off = i - seg * 2 * nw;
-        stage[i] = twe[((size_t)(kb + 4 * it + seg) * W.out_tiles + cg * 8 + 2 * q) * nw + off];
+        stage[i] = twe[((size_t)(kb + 4 * it + seg) * out_tiles + cg * 8 + 2 * q) * nw + off];
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -468,7 +544,7 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
 #pragma unroll
       for (int pq = 0; pq < 16; ++pq) {
         const uint32_t cw = 32u * c + 2u * pq;
-        p[pq] = decode_pair<CB>(tile_window(mine, a.n, cw), tile_window(mine, a.n, cw + 1u), a.mask);
+        p[pq] = decode_pair<CB>(tile_window(mine, n, cw), tile_window(mine, n, cw + 1u), a.mask);
       }
       gemv_mfma(p, alo, ahi, acc0, acc1);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -498,39 +574,41 @@ __device__ __forceinline__ void gemv_wg(const GemvCfg &a, const GemvWeight &W, i
       zk[m * 128 + col + 8] = z1;
     }
   }
-  __syncthreads();
+  lds_barrier();
   float *zf = zp;
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
-  __syncthreads();
-  if (!gemv_splitk_last(zf, a, W, nrows, rows, ks, out, cg * 128)) return;
-  gemv_finish(zf, a, W, nrows, rows, sv, cg * 128);
+  lds_barrier();
+  if (!gemv_splitk_last(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) return;
+  gemv_finish(zf, a.ydt, W.y, W.zout, nrows, rm, sv, cg * 128);
 }
 
-// The weight of grid column group `gx` (weights' groups side by side): the
-// first column groups of weights 1..3 (0 when absent) come as separate
-// kernel parameters, which gfx950 preloads into SGPRs at wave launch, so
-// choosing the weight costs no load and its fields arrive in one round trip.
-__device__ __forceinline__ int gemv_weight_of(int gx, int cg1, int cg2, int cg3) {
-  return (cg1 > 0 && gx >= cg1) + (cg2 > 0 && gx >= cg2) + (cg3 > 0 && gx >= cg3);
+// The weight of grid column group `gx` (weights' groups side by side) and
+// its first and end column groups.
+struct WeightSpan {
+  int wi, c0, c1;
+};
+__device__ __forceinline__ WeightSpan gemv_weight_of(int gx, int cg1, int cg2, int cg3, int gend) {
+  const int wi = (cg1 > 0 && gx >= cg1) + (cg2 > 0 && gx >= cg2) + (cg3 > 0 && gx >= cg3);
+  const int c0 = wi == 0 ? 0 : wi == 1 ? cg1 : wi == 2 ? cg2 : cg3;
+  const int n1 = wi == 0 ? cg1 : wi == 1 ? cg2 : wi == 2 ? cg3 : 0;
+  return WeightSpan{wi, c0, n1 > 0 ? n1 : gend};
 }
 
-template <int K, int CB, bool MASKED>
-__global__ __launch_bounds__(GEMV_THREADS, 8) void gemv_kernel(int rows, int cg1, int cg2, int cg3,
-                                                            GemvArgs a) {
+// Dense GEMV over up to four weights: the trellis pointers, the activations
+// and the geometry are the first kernel arguments (preloaded SGPRs).
+template <int K, int CB, bool MASKED, bool ONEB>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
+    const uint32_t *tw0, const uint32_t *tw1, const uint32_t *tw2, const uint32_t *tw3,
+    const void *x, uint32_t g0, uint32_t g1, uint32_t g2, GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int wi = gemv_weight_of(blockIdx.x, cg1, cg2, cg3);
-  const GemvCfg c = a.c;
-  const GemvWeight W = a.w[wi];
-  const int cg = blockIdx.x - W.cg0;
-  GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
-  if (threadIdx.x < GEMV_ROWS) {
-    const int b = min((int)threadIdx.x, rows - 1);
-    ri[threadIdx.x] = GemvRow{b * c.in_tiles * 16, b * W.out_tiles * 16, b, 0};
-  }
-  __syncthreads();
-  gemv_wg<K, CB, MASKED>(c, W, 0, rows, ri, cg, blockIdx.y, smem + 256, rows);
+  const GemvGeo geo = GemvGeo::unpack(g0, g1, g2);
+  const WeightSpan ws = gemv_weight_of(blockIdx.x, geo.cg1, geo.cg2, geo.cg3, geo.cgend);
+  const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
+  const int out_tiles = 8 * (ws.c1 - ws.c0);
+  const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
+  gemv_wg<K, CB, MASKED, ONEB>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
+                               blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
 }
-
 
 // ===================================================================== GEMM
 //
@@ -796,71 +874,87 @@ constexpr int MOE_ITEM_ROWS = GEMV_ROWS;
 // slot / topk of x; prepared inputs are rows slot.
 template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
-    int cg1, int topk, const uint32_t *__restrict__ sorted, const MoeItem *__restrict__ items,
-    const uint32_t *__restrict__ n_items, GemvArgs a) {
+    const uint32_t *tw0, const uint32_t *tw1, const void *x, uint32_t g0, uint32_t g1,
+    uint32_t g2, int topk, const uint32_t *__restrict__ sorted,
+    const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.z;
   if ((uint32_t)item >= *n_items) return;
   const MoeItem it = items[item];
-  const int wi = gemv_weight_of(blockIdx.x, cg1, 0, 0);
-  const GemvCfg c = a.c;
-  const GemvWeight W = a.w[wi];
-  const int cg = blockIdx.x - W.cg0;
+  const GemvGeo geo = GemvGeo::unpack(g0, g1, g2);
+  const WeightSpan ws = gemv_weight_of(blockIdx.x, geo.cg1, 0, 0, geo.cgend);
+  const uint32_t *tw = ws.wi == 0 ? tw0 : tw1;
+  const int out_tiles = 8 * (ws.c1 - ws.c0);
+  const GemvWeight &W = a.w[ws.wi];
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, (int)it.count - 1);
     const int slot = (int)sorted[it.start + b];
-    const int in = c.in_tiles * 16, out = W.out_tiles * 16;
-    ri[threadIdx.x] = GemvRow{(c.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
+    const int in = geo.in_tiles * 16, out = out_tiles * 16;
+    ri[threadIdx.x] = GemvRow{(geo.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
   }
-  __syncthreads();
-  gemv_wg<K, CB, MASKED>(c, W, (int)it.expert, (int)it.count, ri, cg, blockIdx.y,
-                         smem + 256, MOE_ITEM_ROWS);
+  lds_barrier();
+  const RowMap rm{ri, 0, 0};
+  gemv_wg<K, CB, MASKED, false>(tw + (size_t)it.expert * W.expert_words, out_tiles, x, geo, a.c,
+                                W, (int)it.expert, (int)it.count, rm, blockIdx.x - ws.c0,
+                                blockIdx.y, smem + 256, MOE_ITEM_ROWS);
 }
-
 
 // ====================================================== per-rate launchers
 //
 // K = 1..8: an integer rate (n = 16K) with compile-time windows; K = 0: any
 // even n (GEMV only).
 
+// Dense GEMV over up to four weights (tw[i] their trellis words).
 template <int K>
-void gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, int rows, int cg1, int cg2,
-             int cg3, const GemvArgs &a) {
+void gemv_go(const Format &f, bool oneb, dim3 grid, size_t lds, hipStream_t s,
+             const uint32_t *const *tw, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
+             const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
+  auto go = [&](auto CBC, auto MC, auto OC) {
+    constexpr int CB = decltype(CBC)::value;
+    constexpr bool M = decltype(MC)::value, O = decltype(OC)::value;
+    hipLaunchKernelGGL((gemv_kernel<K, CB, M, O>), grid, blk, lds, s, tw[0], tw[1], tw[2], tw[3], x,
+                       g0, g1, g2, a);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  using MUL1 = std::integral_constant<int, CB_MUL1>;
+  using MCG = std::integral_constant<int, CB_MCG>;
+  const bool masked = f.window < 16;
   if (f.codebook == CB_MCG) {
-    if (f.window < 16)
-      hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+    if (masked)
+      oneb ? go(MCG{}, T{}, T{}) : go(MCG{}, T{}, F{});
     else
-      hipLaunchKernelGGL((gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+      oneb ? go(MCG{}, F{}, T{}) : go(MCG{}, F{}, F{});
   } else {
-    if (f.window < 16)
-      hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, rows, cg1, cg2, cg3, a);
+    if (masked)
+      oneb ? go(MUL1{}, T{}, T{}) : go(MUL1{}, T{}, F{});
     else
-      hipLaunchKernelGGL((gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, rows, cg1, cg2, cg3,
-                         a);
+      oneb ? go(MUL1{}, F{}, T{}) : go(MUL1{}, F{}, F{});
   }
 }
 
 template <int K>
-void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, int cg1, int topk,
-                 const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
+void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, const uint32_t *tw0,
+                 const uint32_t *tw1, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
+                 int topk, const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
                  const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
   if (f.codebook == CB_MCG) {
     if (f.window < 16)
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, cg1, topk, sorted,
-                         items, n_items, a);
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, tw0, tw1, x, g0, g1,
+                         g2, topk, sorted, items, n_items, a);
     else
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, cg1, topk, sorted,
-                         items, n_items, a);
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, tw0, tw1, x, g0,
+                         g1, g2, topk, sorted, items, n_items, a);
   } else {
     if (f.window < 16)
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, cg1, topk, sorted,
-                         items, n_items, a);
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, tw0, tw1, x, g0,
+                         g1, g2, topk, sorted, items, n_items, a);
     else
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, cg1, topk, sorted,
-                         items, n_items, a);
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, tw0, tw1, x, g0,
+                         g1, g2, topk, sorted, items, n_items, a);
   }
 }
 
@@ -889,11 +983,13 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
 }
 
 // Declarations of one rate's launcher instantiations.
-#define EXL3_GEMV_GO(KK) \
-  void gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, int, int, int, int, const GemvArgs &)
-#define EXL3_MOE_GEMV_GO(KK)                                                                   \
-  void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, int, int, const uint32_t *, \
-                       const MoeItem *, const uint32_t *, const GemvArgs &)
+#define EXL3_GEMV_GO(KK)                                                                 \
+  void gemv_go<KK>(const Format &, bool, dim3, size_t, hipStream_t, const uint32_t *const *, \
+                   const void *, uint32_t, uint32_t, uint32_t, const GemvArgs &)
+#define EXL3_MOE_GEMV_GO(KK)                                                                    \
+  void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, const uint32_t *,            \
+                       const uint32_t *, const void *, uint32_t, uint32_t, uint32_t, int,       \
+                       const uint32_t *, const MoeItem *, const uint32_t *, const GemvArgs &)
 #define EXL3_GEMM_GO(KK)                                                                    \
   void gemm_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
                    const uint16_t *, void *, int, uint16_t *, int, int, int)

@@ -260,19 +260,20 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   int ksplit, tps;
   gemv_multi_plan(in, 128 * totcg, generic, &ksplit, &tps);
   if (ksplit > GEMV_KSPLIT_MAX || totcg > 65535) return hipErrorInvalidValue;
+  if (in / 16 > 65535) return hipErrorInvalidValue;
   GemvArgs a{};
-  a.nweights = count;
+  const uint32_t *tw[GEMV_MAXW] = {nullptr, nullptr, nullptr, nullptr};
+  int cgs[GEMV_MAXW] = {0, 0, 0, 0};
   int cg0 = 0;
   for (int i = 0; i < count; ++i) {
     GemvWeight &w = a.w[i];
-    w.tw = reinterpret_cast<const uint32_t *>(ls[i].trellis);
+    tw[i] = reinterpret_cast<const uint32_t *>(ls[i].trellis);
     w.suh = ls[i].suh;
     w.svh = ls[i].svh;
     w.y = ls[i].y;
     w.zout = ls[i].zout;
     w.expert_words = 0;
-    w.out_tiles = ls[i].out / 16;
-    w.cg0 = cg0;
+    cgs[i] = cg0;
     cg0 += ls[i].out / 128;
     if (ksplit > 1) {
       if (sc[i].partial == nullptr || sc[i].partial_floats < (size_t)ksplit * rows * ls[i].out)
@@ -280,22 +281,28 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     }
     w.partial = sc[i].partial;
   }
-  a.c.x = x;
-  a.c.xdt = xdt;
-  a.c.prepared = prepared ? 1 : 0;
   a.c.ydt = ydt;
   a.c.ptotal = (size_t)rows;
-  a.c.in_tiles = in / 16;
-  a.c.n = f.n;
   a.c.ksplit = ksplit;
-  a.c.tps = tps;
   a.c.mask = f.mask();
+  a.c.nw = f.n / 2;
+  GemvGeo geo{};
+  geo.cg1 = cgs[1];
+  geo.cg2 = cgs[2];
+  geo.cg3 = cgs[3];
+  geo.cgend = totcg;
+  geo.rows = rows;
+  geo.xdt = xdt;
+  geo.prepared = prepared ? 1 : 0;
+  geo.in_tiles = in / 16;
+  geo.tps = tps;
+  uint32_t g0, g1, g2;
+  gemv_geo_pack(geo, &g0, &g1, &g2);
   const size_t lds = gemv_lds_bytes(rows, tps, generic);
   const dim3 grid(totcg, ksplit);
-  const int cg1 = count > 1 ? a.w[1].cg0 : 0, cg2 = count > 2 ? a.w[2].cg0 : 0;
-  const int cg3 = count > 3 ? a.w[3].cg0 : 0;
+  const bool oneb = rows * (tps / 8) <= PREP_ITEMS;
   rate_dispatch(generic ? 0 : f.n / 16, [&](auto KC) {
-    gemv_go<decltype(KC)::value>(f, grid, lds, s, rows, cg1, cg2, cg3, a);
+    gemv_go<decltype(KC)::value>(f, oneb, grid, lds, s, tw, x, g0, g1, g2, a);
   });
   return hipGetLastError();
 }
@@ -516,43 +523,64 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   return L;
 }
 
-void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const GemvArgs &a,
+// One grouped GEMV launch over `nweights` banks (gate and up side by side,
+// or down); x holds raw rows (slot / topk) or prepared rows (slot).
+struct MoeGemv {
+  const uint32_t *tw[2];
+  int nweights;
+  const void *x;
+  int xdt;
+  bool prepared;
+  int in, out, ksplit, tps;
+  GemvArgs a;
+};
+
+void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const MoeGemv &m,
                      const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
                      int topk) {
-  const int cg1 = a.nweights > 1 ? a.w[1].cg0 : 0;
+  GemvGeo geo{};
+  geo.cg1 = m.nweights > 1 ? m.out / 128 : 0;
+  geo.cgend = (int)grid.x;
+  geo.rows = MOE_ITEM_ROWS;
+  geo.xdt = m.xdt;
+  geo.prepared = m.prepared ? 1 : 0;
+  geo.in_tiles = m.in / 16;
+  geo.tps = m.tps;
+  uint32_t g0, g1, g2;
+  gemv_geo_pack(geo, &g0, &g1, &g2);
   rate_dispatch(f.integer_rate() ? f.n / 16 : 0, [&](auto KC) {
-    moe_gemv_go<decltype(KC)::value>(f, grid, lds, s, cg1, topk, sorted, items, n_items, a);
+    moe_gemv_go<decltype(KC)::value>(f, grid, lds, s, m.tw[0], m.tw[1], m.x, g0, g1, g2, topk,
+                                     sorted, items, n_items, m.a);
   });
 }
 
-GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial, int cg0) {
+GemvWeight moe_weight(const MoeBank &b, uint16_t *y, float *partial) {
   GemvWeight w{};
-  w.tw = reinterpret_cast<const uint32_t *>(b.trellis);
   w.suh = b.suh;
   w.svh = b.svh;
   w.y = y;
   w.zout = nullptr;
   w.partial = partial;
   w.expert_words = (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2);
-  w.out_tiles = b.out / 16;
-  w.cg0 = cg0;
   return w;
 }
 
-GemvArgs moe_args(const void *x, int xdt, bool prepared, size_t slots, int in, const Format &f,
-                  int ksplit, int tps) {
-  GemvArgs a{};
-  a.c.x = x;
-  a.c.xdt = xdt;
-  a.c.prepared = prepared ? 1 : 0;
-  a.c.ydt = OUT_F16;
-  a.c.ptotal = slots;
-  a.c.in_tiles = in / 16;
-  a.c.n = f.n;
-  a.c.ksplit = ksplit;
-  a.c.tps = tps;
-  a.c.mask = f.mask();
-  return a;
+MoeGemv moe_gemv(const void *x, int xdt, bool prepared, size_t slots, int in, int out,
+                 const Format &f, int ksplit, int tps) {
+  MoeGemv m{};
+  m.x = x;
+  m.xdt = xdt;
+  m.prepared = prepared;
+  m.in = in;
+  m.out = out;
+  m.ksplit = ksplit;
+  m.tps = tps;
+  m.a.c.ydt = OUT_F16;
+  m.a.c.ptotal = slots;
+  m.a.c.ksplit = ksplit;
+  m.a.c.mask = f.mask();
+  m.a.c.nw = f.n / 2;
+  return m;
 }
 
 }  // namespace
@@ -574,6 +602,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
+  if (a.hidden / 16 > 65535 || a.inter / 16 > 65535) return hipErrorInvalidValue;
   if (gate.f.n != up.f.n || gate.f.codebook != up.f.codebook || gate.f.window != up.f.window ||
       gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden || gate.out != a.inter ||
       up.out != a.inter || down.in != a.inter)
@@ -594,20 +623,23 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
                      a.experts, sorted, items, n_items);
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
-  GemvArgs agu = moe_args(a.x, a.xdt, false, L.slots, a.hidden, gate.f, L.ks_gu, L.tps_gu);
-  agu.nweights = 2;
-  agu.w[0] = moe_weight(gate, g, pgu, 0);
-  agu.w[1] = moe_weight(up, u, pgu + gu_part, a.inter / 128);
+  MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
+  mgu.nweights = 2;
+  mgu.tw[0] = reinterpret_cast<const uint32_t *>(gate.trellis);
+  mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
+  mgu.a.w[0] = moe_weight(gate, g, pgu);
+  mgu.a.w[1] = moe_weight(up, u, pgu + gu_part);
   moe_gemv_launch(gate.f, dim3(2 * (a.inter / 128), L.ks_gu, L.max_items),
-                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, agu, sorted, items,
+                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu, sorted, items,
                   n_items, a.topk);
   hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
                      a.experts, down.suh, xd, a.inter, a.limit);
-  GemvArgs ad = moe_args(xd, OUT_F16, true, L.slots, a.inter, down.f, L.ks_d, L.tps_d);
-  ad.nweights = 1;
-  ad.w[0] = moe_weight(down, d, pd, 0);
+  MoeGemv md = moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d, L.tps_d);
+  md.nweights = 1;
+  md.tw[0] = md.tw[1] = reinterpret_cast<const uint32_t *>(down.trellis);
+  md.a.w[0] = moe_weight(down, d, pd);
   moe_gemv_launch(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items),
-                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, ad, sorted, items, n_items,
+                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted, items, n_items,
                   a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
