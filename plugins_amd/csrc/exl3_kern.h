@@ -612,202 +612,310 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
 
 // ===================================================================== GEMM
 //
-// Workgroup tile 256 rows x 256 columns (two Hadamard blocks of the output),
-// 4 waves, each a 128 x 128 sub-tile of 4 x 4 v_mfma_f32_32x32x16_f16 tiles
-// (256 f32 accumulators per lane).  The k loop runs in stages of 32 (two
-// k-tile rows).  While the MFMAs consume the current stage from LDS, every
-// thread decodes one chunk of the next stage (the 256 chunks of 2 k-tile rows
-// x 16 output tiles) into four MFMA B fragments (8 consecutive k of one
-// column each) and stores them into the other LDS buffer as B^T [n][k] rows,
-// stores its four 16-byte pieces of the next A tile (prepared rows, f16), and
-// loads the pieces and packed words of the stage three ahead into the
-// register set it just freed (three sets in flight); the decode's VALU work
-// and the memory operations are interleaved between the MFMAs.  LDS rows are padded to 40 halfs (80
-// bytes), so the 16-byte operand reads of 16 consecutive rows hit distinct
-// banks.  The MFMAs take the weights as their first operand, so the
-// accumulators hold z^T: a lane holds one row of z and 16 of its columns.
-// That is the operand layout of a second MFMA, which applies the finish's
-// Hadamard stages on column bits 0-4 (H_32, +-1 entries: exact products,
-// f32 sums) to f16(z); stages 5 and 6 are the reference's butterflies across
-// the four 32-column blocks, in registers, then * 1/sqrt(128) * svh.  No LDS
-// round trip.  Each decoded weight serves 256 rows and each staged activation
-// 256 columns.
+// Workgroup tile 256 rows x 128 columns (one Hadamard block of the output),
+// 8 waves, two per SIMD (on gfx950 one wave issues at most one VALU
+// instruction every 8 cycles, so the weight decode needs more than one wave
+// per SIMD to keep pace with the MFMAs).  Wave w owns rows 64 (w / 2) .. + 63
+// and columns 64 (w % 2) .. + 63 as 2 x 2 v_mfma_f32_32x32x16_f16 tiles (64
+// f32 accumulators per lane).  The k loop runs in stages of 64 (four k-tile
+// rows), double-buffered in LDS.  Per stage:
+//  * the next stage's 256 chunks (4 k-tile rows x 8 output tiles x 8 chunks)
+//    are decoded into MFMA B fragments and stored as B^T [n][k]: waves 0-3
+//    decode rows 0-7 of each chunk's two columns, waves 4-7 rows 8-15
+//    (uniform code per wave);
+//  * the activations (prepared rows, f16) are loaded coalesced (8 lanes per
+//    128-byte row piece: an MFMA-layout load that puts 32 rows in one
+//    instruction runs at a quarter of the rate) three stages ahead and
+//    stored into LDS as A [m][k] the stage before they are used;
+//  * both operands are read from LDS in MFMA layout (rows padded to 72
+//    halfs, so the 16-byte reads of 16 consecutive rows hit distinct banks);
+//    within a stage, MFMA step kk contracts k = 32 h + 8 kk + e over lane
+//    half h and element e, the same order for both operands;
+//  * the 16 MFMAs of a wave are issued one per slot, and each slot also
+//    issues a share of the decode, the LDS traffic and the global loads, in
+//    an order fixed at compile time (scheduling barriers between slots);
+//  * one barrier, after the stores into the next buffer and the last reads
+//    of the current one; the next stage's first fragments are read right
+//    after it, under the stage's last MFMAs.
+// The MFMAs take the weights as their first operand, so the accumulators
+// hold z^T: a lane holds one row of z and 16 of its columns.  That is the
+// operand layout of a second MFMA, which applies the finish's Hadamard
+// stages on column bits 0-4 (H_32, +-1 entries: exact products, f32 sums) to
+// f16(z); the 128-column block spans two waves, so stages 5 and 6 go through
+// LDS, then * 1/sqrt(128) * svh.  Each decoded weight serves 256 rows.  Tiles
+// of 128 columns keep the grid a multiple of the 256 CUs at the Qwen3-8B
+// shapes (M = 2048: 256 tiles for 4096 outputs, 768 for 12288).
 
-constexpr int GM_BM = 256, GM_BN = 256, GM_BK = 32, GM_THREADS = 256;
-constexpr int GM_LD = GM_BK + 8;      // halfs per LDS row of A / column of B^T
-constexpr int GM_TILE = 256 * GM_LD;  // halfs per operand buffer
-constexpr int GM_LDS_HALFS = 4 * GM_TILE;  // A and B^T, two stages
+constexpr int GM_BM = 256, GM_BN = 128, GM_BK = 64, GM_THREADS = 512;
+constexpr int GM_LD = GM_BK + 8;         // halfs per LDS row of A / column of B^T
+constexpr int GM_ATILE = GM_BM * GM_LD;  // halfs of A per stage buffer
+constexpr int GM_BTILE = GM_BN * GM_LD;  // halfs of B^T per stage buffer
+constexpr int GM_STAGE = GM_ATILE + GM_BTILE;
+constexpr int GM_LDS_BYTES = 2 * GM_STAGE * 2;  // two stage buffers (108 KiB)
+// finish exchange: 64 rows of the 128 columns after the H_32 step (f32),
+// rows padded to 132 floats (33 KiB: within the two stage buffers)
+constexpr int GM_FLD = 132;
+static_assert(64 * GM_FLD * 4 <= GM_LDS_BYTES, "finish exchange exceeds the stage buffers");
 
-// A chunk's 32 codewords as four MFMA B fragments of 8 consecutive k of one
-// column: f = 0: column a, tile rows 0-7; 1: column a+8, rows 0-7; 2: column
-// a, rows 8-15; 3: column a+8, rows 8-15 (pairs p, p+4, p+8, p+12 for p = 0,
-// 2, 1, 3), stored to B^T at column n0 (+8) and k k0 (+8).
-template <int K, int CB, bool MASKED>
-__device__ __forceinline__ void gemm_decode_chunk(const uint32_t (&wd)[K + 1], uint16_t *bt, int n0,
-                                                  int k0, uint32_t mask) {
-  static_for<4>([&](auto F) {
-    constexpr int f = decltype(F)::value;
-    constexpr int p0 = (f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3;
-    uint32_t q[4];
-    static_for<4>([&](auto J) {
-      q[J] = chunk_pair_cw<K, CB, MASKED, p0 + 4 * decltype(J)::value>(wd, mask);
-    });
-    const u4_t v = {q[0], q[1], q[2], q[3]};
-    *reinterpret_cast<u4_t *>(bt + (n0 + 8 * (f & 1)) * GM_LD + k0 + 8 * (f >> 1)) = v;
-  });
+// Pair place in fragment order: fragment f (0: column a, rows 0-7; 1: column
+// a+8, rows 0-7; 2: column a, rows 8-15; 3: column a+8, rows 8-15) holds
+// pairs p0(f) + 4J, J = 0..3.
+__host__ __device__ constexpr int gm_pair(int f, int J) {
+  return ((f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3) + 4 * J;
 }
 
-template <int K, int CB, bool MASKED>
-__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
-    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
-    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    int M, int in_tiles, int out_tiles, uint32_t mask) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_HALFS];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
-  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking
-  // the row block as n % (row blocks) lets an XCD's workgroups share a few
-  // row blocks of A in its L2.  (Only the speed depends on this.)
-  const int mblocks = gridDim.y;
-  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
-  const int cp = lin / mblocks;  // columns 256 cp ..
-  const int m0 = (lin % mblocks) * GM_BM;
-  const int in = in_tiles * 16;
-  const size_t out = (size_t)out_tiles * 16;
-  const int nw = 8 * K;
+// The main loop of one wave; HALF = 0: the wave decodes fragments 0 and 1 of
+// its chunk, 1: fragments 2 and 3.  aoff: element offsets of this thread's
+// four activation pieces (rows 64 u apart) in xp; ast: the first piece's
+// place in an A buffer; ard / brd: the wave's A / B fragment reads.
+//
+// Everything a stage waits for was issued stages earlier: the packed words
+// of stage x are loaded GM_WL stages ahead (a few registers each, so deep:
+// the history exchange of stage x, two stages before its use, then never
+// waits on HBM latency), the activations of stage x three stages ahead
+// (stored into LDS during stage x - 1).
+template <int K>
+constexpr int gm_wl() { return K <= 4 ? 6 : 3; }  // word sets (divides the 6-stage trip)
 
-  // decoder role: chunk c of output tile tnl of k-tile row tkl of the stage;
-  // the 8 chunks of a tile sit in 8 consecutive lanes.  Tiles past the last
-  // column (the second half of an odd last pair) decode tile 0 instead and
-  // their results are not stored.
-  const int tkl = tid >> 7, tnl = (tid >> 3) & 15, c = tid & 7;
-  const int tcol = cp * 16 + tnl < out_tiles ? cp * 16 + tnl : 0;
-  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + tcol) * nw + c * K;
-  const size_t wstage = (size_t)2 * out_tiles * nw;  // dwords per stage
-  const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of chunk c-1
-  const int bn0 = tnl * 16 + c, bk0 = tkl * 16;
+template <int K, int CB, bool MASKED, int HALF>
+__device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
+                                          const uint32_t *twc, size_t wstage, int src, int bst,
+                                          const uint16_t *xp, const int (&aoff)[4], int ast,
+                                          int ard, int brd, int NS, uint32_t mask) {
+  constexpr int WL = gm_wl<K>();
+  u4_t ra[3][4];       // activation pieces of stage x in set x % 3
+  uint32_t wn[WL][K];  // packed words of stage x in set x % WL
+  uint32_t hist[2];    // history dword of the chunk of stage x in hist[x % 2]
+  h8_t af[2][2];       // A fragments of a step (step % 2) [row block]
+  h8_t bf[2][2];       // B fragments of a step (step % 2) [column block]
 
-  // A staging: pieces t + 256 i (i = 0..3) of the 256 x 4 16-byte pieces of
-  // a stage: row (t >> 2) + 64 i, piece t & 3.  Rows past M read row M - 1
-  // (not stored; rows of an MFMA are independent), so no load branches.
-  const int arow = tid >> 2, apc = tid & 3;
-  const uint16_t *ap[4];
+  auto load_a = [&](auto R, int st) {
+    constexpr int r = decltype(R)::value;
+    st = min(st, NS - 1);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    ap[i] = xp + (size_t)min(m0 + arow + 64 * i, M - 1) * in + apc * 8;
-  const int ast = arow * GM_LD + apc * 8;
-
-  // operand fragments of this lane in a stage buffer
-  const int am = (wr * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
-  const int bn = (wc * 128 + (lane & 31)) * GM_LD + 8 * (lane >> 5);
-
-  f16v_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  h8_t ar[3][4];
-  uint32_t wn[3][K];
-  const int stages = in_tiles / 2;  // >= 4: in is a multiple of 128
-  // register set S <- stage st (clamped to the last stage: in bounds, unused)
-  auto load_stage = [&](auto S, int st) {
+    for (int u = 0; u < 4; ++u)
+      ra[r][u] = *reinterpret_cast<const u4_t *>(xp + aoff[u] + st * GM_BK);
+  };
+  auto store_a = [&](auto R, int buf, int u) {
+    constexpr int r = decltype(R)::value;
+    *reinterpret_cast<u4_t *>(lds + buf * GM_STAGE + ast + 64 * u * GM_LD) = ra[r][u];
+  };
+  auto load_w = [&](auto S, int st) {
     constexpr int q = decltype(S)::value;
-    st = min(st, stages - 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ar[q][i] = *reinterpret_cast<const h8_t *>(ap[i] + st * GM_BK);
-    const uint32_t *p = twc + (size_t)st * wstage;
+    const uint32_t *p = twc + (size_t)min(st, NS - 1) * wstage;
 #pragma unroll
     for (int j = 0; j < K; ++j) wn[q][j] = p[j];
   };
-  // register set S -> LDS buffer at off (A pieces, decoded chunk)
-  auto store_stage = [&](auto S, int off) {
-    constexpr int q = decltype(S)::value;
-    uint16_t *as = lds + off, *bs = lds + off + GM_TILE;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t *>(as + ast + i * 64 * GM_LD) = ar[q][i];
+  auto read_af = [&](auto Q, int buf, int kk, int i) {
+    constexpr int q = decltype(Q)::value;
+    af[q][i] = *reinterpret_cast<const h8_t *>(lds + buf * GM_STAGE + ard + i * 32 * GM_LD + 8 * kk);
+  };
+  auto read_bf = [&](auto Q, int buf, int kk, int j) {
+    constexpr int q = decltype(Q)::value;
+    bf[q][j] = *reinterpret_cast<const h8_t *>(lds + buf * GM_STAGE + GM_ATILE + brd +
+                                               j * 32 * GM_LD + 8 * kk);
+  };
+  auto bperm = [&](auto S, auto HS) {
+    constexpr int q = decltype(S)::value, hq = decltype(HS)::value;
+    hist[hq] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
+  };
+  // pair P of the chunk held in word set S (history hist[HS])
+  auto pair = [&](auto S, auto HS, auto P) -> uint32_t {
+    constexpr int q = decltype(S)::value, hq = decltype(HS)::value, p = decltype(P)::value;
     uint32_t wd[K + 1];
+    wd[0] = hist[hq];
 #pragma unroll
     for (int j = 0; j < K; ++j) wd[j + 1] = wn[q][j];
-    wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
-    gemm_decode_chunk<K, CB, MASKED>(wd, bs, bn0, bk0, mask);
+    return chunk_pair_cw<K, CB, MASKED, p>(wd, mask);
   };
-  // stage st: MFMAs on buffer st & 1; set S (stage st + 1) into the other
-  // buffer, then set S <- stage st + 4
-  auto stage = [&](auto S, int st) {
-    const int cur = (st & 1) * 2 * GM_TILE, nxt = 2 * GM_TILE - cur;
-    const uint16_t *ac = lds + cur, *bc = lds + cur + GM_TILE;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      h8_t a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const h8_t *>(ac + am + i * 32 * GM_LD + kk * 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const h8_t *>(bc + bn + j * 32 * GM_LD + kk * 16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[j][i], 0, 0, 0);
-    }
-    store_stage(S, nxt);
-    load_stage(S, st + 4);
-    // operands of the first slab, then each MFMA followed by a share of the
-    // VALU work and of the memory operations
-    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x0002, 6, 0);  // VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);  // DS read
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);  // VALU
-      if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);  // DS write
-      if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);  // VMEM read
-    }
-    __syncthreads();
+  auto store_frag = [&](int buf, int f, const uint32_t (&v4)[4]) {
+    const u4_t v = {v4[0], v4[1], v4[2], v4[3]};
+    *reinterpret_cast<u4_t *>(lds + buf * GM_STAGE + GM_ATILE + bst + 8 * (f & 1) * GM_LD +
+                              8 * (f >> 1)) = v;
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  load_stage(I0{}, 0);
-  load_stage(I1{}, 1);
-  load_stage(I2{}, 2);
-  store_stage(I0{}, 0);
-  load_stage(I0{}, 3);
-  __syncthreads();
-  int st = 0;
-  for (; st + 3 <= stages; st += 3) {
-    stage(I1{}, st);
-    stage(I2{}, st + 1);
-    stage(I0{}, st + 2);
-  }
-  if (st < stages) stage(I1{}, st);
-  if (st + 1 < stages) stage(I2{}, st + 1);
+  using IC0 = std::integral_constant<int, 0>;
+  using IC1 = std::integral_constant<int, 1>;
 
-  // acc[j][i] = z^T for columns 32 j .. of the wave's column group and rows
-  // 32 i .. of its 128: lane l holds row (l & 31), register r column
+  // Stage st (PH = st % 6; buffer st % 2): stores the activations of stage
+  // st + 1 and decodes its words into the other buffer, loads the words of
+  // stage st + WL and the activations of stage st + 3 (into the sets of
+  // stage st, consumed), reads the next stage's first fragments after the
+  // barrier, and forms the history of stage st + 2.
+  auto stage = [&](auto PH, int st) {
+    constexpr int ph = decltype(PH)::value;
+    using A1 = std::integral_constant<int, (ph + 1) % 3>;   // activations of st + 1
+    using A0 = std::integral_constant<int, ph % 3>;         // ... of st, then st + 3
+    using W0 = std::integral_constant<int, ph % WL>;        // words of st, then st + WL
+    using W1 = std::integral_constant<int, (ph + 1) % WL>;  // words of st + 1
+    using W2 = std::integral_constant<int, (ph + 2) % WL>;  // words of st + 2
+    using H1 = std::integral_constant<int, (ph + 1) & 1>;
+    using H2 = std::integral_constant<int, ph & 1>;
+    const int cur = st & 1, nxt = cur ^ 1;
+    uint32_t fr[4];
+    static_for<16>([&](auto SL) {
+      constexpr int s = decltype(SL)::value;
+      constexpr int kk = s >> 2, i = (s >> 1) & 1, j = s & 1;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk & 1][j], af[kk & 1][i], acc[i][j],
+                                                          0, 0, 0);
+      // the next step's fragments, under this step's MFMAs (the last step's
+      // two per slot, so that they are in before the barrier)
+      if constexpr (kk < 2) {
+        using QN = std::integral_constant<int, (kk + 1) & 1>;
+        if constexpr ((s & 3) < 2) read_af(QN{}, cur, kk + 1, s & 1);
+        if constexpr ((s & 3) >= 2) read_bf(QN{}, cur, kk + 1, s & 1);
+      }
+      if constexpr (s == 8) {
+        read_af(IC1{}, cur, 3, 0);
+        read_af(IC1{}, cur, 3, 1);
+      }
+      if constexpr (s == 9) {
+        read_bf(IC1{}, cur, 3, 0);
+        read_bf(IC1{}, cur, 3, 1);
+      }
+      // the next stage's activations into the other buffer
+      if constexpr (s < 4) store_a(A1{}, nxt, s);
+      // decode of the next stage: one pair per slot, a fragment store after
+      // every fourth
+      if constexpr (s >= 1 && s <= 8) {
+        constexpr int fl = (s - 1) >> 2, J = (s - 1) & 3;
+        constexpr int f = 2 * HALF + fl;
+        fr[J] = pair(W1{}, H1{}, std::integral_constant<int, gm_pair(f, J)>{});
+        if constexpr (J == 3) store_frag(nxt, f, fr);
+      }
+      if constexpr (s == 9) {
+        load_w(W0{}, st + WL);
+        load_a(A0{}, st + 3);
+      }
+      // the next buffer is complete and this one is read (the last step's
+      // fragments are in registers): one barrier, then the next stage's
+      // first fragments
+      if constexpr (s == 10) lds_barrier();
+      if constexpr (s == 12) {
+        read_af(IC0{}, nxt, 0, 0);
+        read_af(IC0{}, nxt, 0, 1);
+      }
+      if constexpr (s == 13) {
+        read_bf(IC0{}, nxt, 0, 0);
+        read_bf(IC0{}, nxt, 0, 1);
+      }
+      if constexpr (s == 15) bperm(W2{}, H2{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // prologue: words of stages 0 .. WL-1, activations of stages 0-2 in
+  // flight; stage 0 decoded and stored into buffer 0, the first fragments
+  // read, the history of stage 1 formed
+  static_for<WL>([&](auto W) { load_w(W, decltype(W)::value); });
+  load_a(IC0{}, 0);
+  load_a(IC1{}, 1);
+  load_a(std::integral_constant<int, 2>{}, 2);
+  bperm(IC0{}, IC0{});
+  static_for<2>([&](auto FL) {
+    constexpr int f = 2 * HALF + decltype(FL)::value;
+    uint32_t v4[4];
+    static_for<4>([&](auto J) {
+      v4[J] = pair(IC0{}, IC0{}, std::integral_constant<int, gm_pair(f, decltype(J)::value)>{});
+    });
+    store_frag(0, f, v4);
+  });
+#pragma unroll
+  for (int u = 0; u < 4; ++u) store_a(IC0{}, 0, u);
+  bperm(IC1{}, IC1{});
+  lds_barrier();
+  read_af(IC0{}, 0, 0, 0);
+  read_af(IC0{}, 0, 0, 1);
+  read_bf(IC0{}, 0, 0, 0);
+  read_bf(IC0{}, 0, 0, 1);
+
+  // six stages per trip (word sets cycle by WL, activations by 3, the rest by 2)
+  int st = 0;
+  for (; st + 6 <= NS; st += 6) {
+    static_for<6>([&](auto PH) { stage(PH, st + decltype(PH)::value); });
+  }
+  // NS is even: 0, 2 or 4 stages left
+  if (st < NS) {
+    stage(std::integral_constant<int, 0>{}, st);
+    stage(std::integral_constant<int, 1>{}, st + 1);
+    if (st + 2 < NS) {
+      stage(std::integral_constant<int, 2>{}, st + 2);
+      stage(std::integral_constant<int, 3>{}, st + 3);
+    }
+  }
+}
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
+    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
+    int M, int in_tiles, int out_tiles, uint32_t mask) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_BYTES / 2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wc = wave & 1;
+  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking the
+  // row block as n % (row blocks) gives each XCD a few row blocks of the
+  // activations to keep in its L2.  (Only the speed depends on this.)
+  const int mblocks = gridDim.y;
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int cg = lin / mblocks;  // output columns 128 cg ..
+  const int m0 = (lin % mblocks) * GM_BM;
+  const int in = in_tiles * 16;
+  const size_t out = (size_t)out_tiles * 16;
+  constexpr int NW = 8 * K;     // trellis dwords per tile
+  const int NS = in_tiles / 4;  // stages (even, >= 2: in is a multiple of 128)
+
+  // decoder role: chunk c of output tile tnl of k-tile row tkl of a stage
+  // (threads t and t + 256 take the same chunk); the 8 chunks of a tile sit
+  // in 8 consecutive lanes
+  const int dt = tid & 255;
+  const int tkl = dt >> 6, tnl = (dt >> 3) & 7, c = dt & 7;
+  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
+  const size_t wstage = (size_t)4 * out_tiles * NW;  // dwords per stage
+  const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of chunk c-1
+  const int bst = (tnl * 16 + c) * GM_LD + tkl * 16;     // fragment 0's LDS place
+
+  // activation loads: 16-byte piece (tid & 7) of rows (tid >> 3) + 64 u of
+  // the tile; rows past M read row M - 1 (not stored: rows of an MFMA are
+  // independent)
+  int aoff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) aoff[u] = min(m0 + (tid >> 3) + 64 * u, M - 1) * in + (tid & 7) * 8;
+  const int ast = (tid >> 3) * GM_LD + (tid & 7) * 8;
+  // fragment reads: row 64 wm + 32 i + (lane & 31) / column
+  // 64 wc + 32 j + (lane & 31), k 32 h + 8 kk with h = lane / 32
+  const int h = lane >> 5;
+  const int ard = (64 * wm + (lane & 31)) * GM_LD + 32 * h;
+  const int brd = (64 * wc + (lane & 31)) * GM_LD + 32 * h;
+
+  f16v_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if (wave < 4)
+    gemm_main<K, CB, MASKED, 0>(acc, lds, twc, wstage, src, bst, xp, aoff, ast, ard, brd, NS,
+                                mask);
+  else
+    gemm_main<K, CB, MASKED, 1>(acc, lds, twc, wstage, src, bst, xp, aoff, ast, ard, brd, NS,
+                                mask);
+
+  // acc[i][j] = z^T for columns 64 wc + 32 j .. and rows 64 wm + 32 i .. of
+  // the tile: lane l holds row (l & 31), register r column
   // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
-  const int cg = cp * 2 + wc;
-  if (cg * 8 >= out_tiles) return;  // the odd half of the last pair
-  const int rb = m0 + wr * 128 + (lane & 31);
+  const int rb = m0 + 64 * wm + (lane & 31);
   if (y == nullptr) {
-    static_for<4>([&](auto I) {
+    static_for<2>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if (rb + 32 * i < M) {
-        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 4 * (lane >> 5);
+        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[j][i][r]);
+          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[i][j][r]);
       }
     });
     return;
@@ -823,38 +931,51 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(
       const int nl = 16 * kk + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
       hb[kk][e] = (__builtin_popcount(nl & lane & 31) & 1) ? -1.0f16 : 1.0f16;
     }
-  float sv[4];
+  // The stage buffers are free now: the H_32 outputs go through them as f32
+  // [64 rows][GM_FLD], in four passes of 64 rows (row block i of the waves
+  // with wm / 2 == g), so the butterflies across the four 32-column blocks
+  // (two waves) can pair them.
+  float *fx = reinterpret_cast<float *>(lds);
+  static_for<4>([&](auto P) {
+    constexpr int i = decltype(P)::value & 1, g = decltype(P)::value >> 1;
+    lds_barrier();  // the previous use of the buffers is done
+    if ((wm >> 1) == g) {
+      // D2_j = f16(z block j) H_32: lane l holds output column (l & 31) of
+      // block 2 wc + j, register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the
+      // wave's rows 32 i ..
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sv[j] = h2f(svh[cg * 128 + 32 * j + (lane & 31)]);
-  static_for<4>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    // D2_j = f16(z block j) H_32: lane l holds output column (l & 31),
-    // register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the 32
-    f16v_t d2[4];
+      for (int j = 0; j < 2; ++j) {
+        h8_t a0, a1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      h8_t a0, a1;
+        for (int e = 0; e < 8; ++e) {
+          a0[e] = bits<_Float16>(f2h(acc[i][j][e]));
+          a1[e] = bits<_Float16>(f2h(acc[i][j][8 + e]));
+        }
+        f16v_t zero = {};
+        f16v_t d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2, 0, 0, 0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        a0[e] = bits<_Float16>(f2h(acc[j][i][e]));
-        a1[e] = bits<_Float16>(f2h(acc[j][i][8 + e]));
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * (wm & 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          fx[row * GM_FLD + 32 * (2 * wc + j) + (lane & 31)] = d2[r];
+        }
       }
-      f16v_t zero = {};
-      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
-      d2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2[j], 0, 0, 0);
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wr * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi)
-      const float t0 = d2[0][r] + d2[1][r], t1 = d2[0][r] - d2[1][r];
-      const float t2 = d2[2][r] + d2[3][r], t3 = d2[2][r] - d2[3][r];
+    lds_barrier();
+    // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi),
+    // then * 1/sqrt(128) * svh
+    for (int e = tid; e < 64 * 32; e += GM_THREADS) {
+      const int row = e >> 5, cl = e & 31;
+      const float *fr = fx + row * GM_FLD + cl;
+      const float t0 = fr[0] + fr[32], t1 = fr[0] - fr[32];
+      const float t2 = fr[64] + fr[96], t3 = fr[64] - fr[96];
       const float u[4] = {t0 + t2, t1 + t3, t0 - t2, t1 - t3};
+      const int m = m0 + 64 * (2 * g + (row >> 5)) + 32 * i + (row & 31);
       if (m < M) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          store_out(y, (size_t)m * out + cg * 128 + 32 * j + (lane & 31),
-                    f2h((u[j] * HAD_SCALE) * sv[j]), ydt);
+          store_out(y, (size_t)m * out + cg * 128 + 32 * j + cl,
+                    f2h((u[j] * HAD_SCALE) * h2f(svh[cg * 128 + 32 * j + cl])), ydt);
       }
     }
   });

@@ -27,31 +27,27 @@ namespace exl3 {
 
 // =================================================================== prepare
 
-// One wave per 128-block of one row: element i of the block lives in lane
-// i%64, register i/64.  Stages on index bits 0..5 exchange across lanes,
-// bit 6 is in-register; each stage is (lo + hi, lo - hi).
-__global__ __launch_bounds__(64) void prepare_kernel(const void *__restrict__ x, int xdt,
-                                                     const uint16_t *__restrict__ suh,
-                                                     uint16_t *__restrict__ xp, int in) {
-  const int lane = threadIdx.x;
-  const size_t row = blockIdx.y;
-  const int i0 = blockIdx.x * 128 + lane;
-  const size_t base = row * (size_t)in;
+// One wave per 128-block of one row, four blocks per workgroup: element i
+// of the block lives in lane i/2, register i%2 (had128_pair: the stage on
+// index bit 0 in-register, bits 1..6 across lanes; each stage (lo + hi,
+// lo - hi) in bit order, as the reference computes it).
+__global__ __launch_bounds__(256) void prepare_kernel(const void *__restrict__ x, int xdt,
+                                                      const uint16_t *__restrict__ suh,
+                                                      uint16_t *__restrict__ xp, int in,
+                                                      int nblk) {
+  const int lane = threadIdx.x & 63;
+  const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nblk) return;  // whole waves
+  const size_t base = (size_t)blockIdx.y * in;
+  const int k = blk * 128 + 2 * lane;
   // f16(x) * suh in f32 (expert_exl3.zig:490-493; the kernel's
   // float(x) * float(suh), expert_exl3_kernels.zig:908-912).
-  float v0 = h2f(f2h(load_act(x, base + i0, xdt))) * h2f(suh[i0]);
-  float v1 = h2f(f2h(load_act(x, base + i0 + 64, xdt))) * h2f(suh[i0 + 64]);
-#pragma unroll
-  for (int bit = 1; bit <= 32; bit <<= 1) {
-    const float p0 = __shfl_xor(v0, bit, 64);
-    const float p1 = __shfl_xor(v1, bit, 64);
-    const bool lower = (lane & bit) == 0;
-    v0 = lower ? v0 + p0 : p0 - v0;
-    v1 = lower ? v1 + p1 : p1 - v1;
-  }
-  const float a = v0 + v1, b = v0 - v1;
-  xp[base + i0] = f2h(a * HAD_SCALE);
-  xp[base + i0 + 64] = f2h(b * HAD_SCALE);
+  const uint32_t su = *reinterpret_cast<const uint32_t *>(suh + k);
+  float v0 = h2f(f2h(load_act(x, base + k, xdt))) * h2f((uint16_t)(su & 0xFFFFu));
+  float v1 = h2f(f2h(load_act(x, base + k + 1, xdt))) * h2f((uint16_t)(su >> 16));
+  had128_pair(v0, v1, lane);
+  *reinterpret_cast<uint32_t *>(xp + base + k) =
+      (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
 }
 
 // The same rotation on an f16 [rows, 128-block] of inner products, then
@@ -86,7 +82,9 @@ hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t 
                           int in, hipStream_t s) {
   if (rows <= 0 || in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
   if (rows > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(prepare_kernel, dim3(in / 128, rows), dim3(64), 0, s, x, xdt, suh, xp, in);
+  const int nblk = in / 128;
+  hipLaunchKernelGGL(prepare_kernel, dim3((nblk + 3) / 4, rows), dim3(256), 0, s, x, xdt, suh, xp,
+                     in, nblk);
   return hipGetLastError();
 }
 
