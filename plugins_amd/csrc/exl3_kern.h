@@ -433,11 +433,13 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // Loads of the workgroup's start, all in flight at once, in the order
   // their data is needed (vector loads complete in issue order): the first
   // prepare items' activations, the first step's weights, suh of those items,
-  // the next two steps' weights (steps past the last reload the last one: in
-  // bounds and unused, so no branches and the waits stay exact), svh for the
-  // finish.
+  // the next NBUF - 1 steps' weights (steps past the last reload the last one:
+  // in bounds and unused, so no branches and the waits stay exact), svh for
+  // the finish.
   constexpr int KB = K > 0 ? K : 1;
-  uint32_t b0[KB], b1[KB], b2[KB];
+  // steps in flight per wave: as many as a few registers allow
+  constexpr int NBUF = K <= 0 ? 1 : 3;
+  uint32_t bw[NBUF][KB];
   const uint32_t *wp = twe + ((size_t)(kb + g) * out_tiles + tn) * nw + c * K;
   const size_t wstep = (size_t)4 * out_tiles * nw;  // dwords per step
   const int nb = ntk >> 3, nitems = nrows * nb;
@@ -445,7 +447,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
   if constexpr (K > 0) {
 #pragma unroll
-    for (int i = 0; i < K; ++i) b0[i] = wp[i];
+    for (int i = 0; i < K; ++i) bw[0][i] = wp[i];
   }
   // The loads above use preloaded arguments only.  W.suh comes from the
   // argument segment (a scalar load issued at entry); passing it through an
@@ -456,12 +458,12 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   const uint16_t *suh = suh0 + (size_t)expert * in;
   gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
   if constexpr (K > 0) {
-    const uint32_t *p1 = wp + (size_t)min(1, iters - 1) * wstep;
-    const uint32_t *p2 = wp + (size_t)min(2, iters - 1) * wstep;
 #pragma unroll
-    for (int i = 0; i < K; ++i) b1[i] = p1[i];
+    for (int b = 1; b < NBUF; ++b) {
+      const uint32_t *pb = wp + (size_t)min(b, iters - 1) * wstep;
 #pragma unroll
-    for (int i = 0; i < K; ++i) b2[i] = p2[i];
+      for (int i = 0; i < K; ++i) bw[b][i] = pb[i];
+    }
   }
   // svh of this lane's two columns (read whether or not the finish runs: a
   // load without a branch around it)
@@ -510,18 +512,16 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
         if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
         if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
       });
-      const uint32_t *pn = wp + (size_t)min(it + 3, iters - 1) * wstep;
+      const uint32_t *pn = wp + (size_t)min(it + NBUF, iters - 1) * wstep;
 #pragma unroll
       for (int i = 0; i < K; ++i) b[i] = pn[i];
     };
     int it = 0;
-    for (; it + 3 <= iters; it += 3) {
-      step(b0, it);
-      step(b1, it + 1);
-      step(b2, it + 2);
-    }
-    if (it < iters) step(b0, it);
-    if (it + 1 < iters) step(b1, it + 1);
+    for (; it + NBUF <= iters; it += NBUF)
+      static_for<NBUF>([&](auto B) { step(bw[decltype(B)::value], it + decltype(B)::value); });
+    static_for<NBUF - 1>([&](auto B) {
+      if (it + decltype(B)::value < iters) step(bw[decltype(B)::value], it + decltype(B)::value);
+    });
   } else {
     // any even n: the wave stages its 4 k-tile rows x 2 tiles of dwords
     uint32_t *stage = reinterpret_cast<uint32_t *>(smem + (size_t)rows_alloc * kr * 2 +
