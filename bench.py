@@ -132,6 +132,41 @@ def gemm_tflops(torch, X, iters: int = 10):
                                               "includes": "prepare + LDS-decode MFMA GEMM + finish"}}
 
 
+def decode_tok_s(torch, batches=(1, 16), ctx=2048, steps=8):
+    """a 36-layer Qwen3-8B-shaped decoder decode step (EXL3
+    K=4 linears incl. lm_head, f16 attention over a random KV cache at context
+    `ctx`), captured in a HIP graph; tokens per second per batch size."""
+    from plugins_amd import qwen3 as Q
+    res = {}
+    for B in batches:
+        m = Q.Qwen3Decoder(Q.Qwen3Config(), B, ctx, seed=21)
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            m.step(stream=cap)
+            m.step(stream=cap)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap, capture_error_mode="thread_local"):
+            m.step(stream=cap)
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        el = (time.perf_counter() - t0) / steps
+        wb, kvb = m.weight_bytes(), m.kv_bytes()
+        res[f"batch{B}"] = {"tok_s": round(B / el, 1), "ms_per_step": round(el * 1e3, 3),
+                            "weight_bytes": wb, "kv_bytes": kvb,
+                            "gbs": round((wb + kvb) / el / 1e9, 1)}
+        del g, m
+        torch.cuda.empty_cache()
+    res["config"] = ("36 layers, hidden 4096, 32/8 heads x 128, SwiGLU 12288, vocab 151936, EXL3 K=4 "
+                     f"mul1 (lm_head too), f16 KV cache at context {ctx}, HIP graph per step")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +176,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decoder tok/s leg")
     ap.add_argument("--per-linear", action="store_true",
                     help="one launch per linear instead of one per shared-input group")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -255,6 +291,12 @@ def main() -> int:
     except Exception as ex:  # reported, not hidden
         extra["prefill_gemm_error"] = repr(ex)
     extra["gemv_gbs_per_shape"] = shapes
+    if not args.no_decode:
+        try:
+            log("decode step")
+            extra["decode_tok_s"] = decode_tok_s(torch)
+        except Exception as ex:  # reported, not hidden
+            extra["decode_error"] = repr(ex)
     extra["graph"] = graph is not None
 
     cpu = None

@@ -1,0 +1,57 @@
+/* exl3_decoder.h -- the non-EXL3 operations of a Qwen3-8B-shaped decode step,
+ * exported by libexl3_mi355x.so for the decode tok/s harness.
+ *
+ * These are not part of the reference's quant-plugin table: they stand in for
+ * the caller of that table (the reference's model plugin, whose ops run on
+ * MLX: turboexl3_qwen38/src/direct/linear.zig:65-85 for RMSNorm and SiLU,
+ * attn.zig:133-141 and attn_core.zig for q/k norm, RoPE, the KV append and
+ * attention; paths relative to /root/reference/plugins/).  Device pointers,
+ * f16 as uint16_t bits, streams as hipStream_t; every entry returns 0 or a
+ * HIP error code and launches nothing when its shape checks fail.
+ */
+#ifndef EXL3_DECODER_H
+#define EXL3_DECODER_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Head dimension the attention kernels are built for (Qwen3-8B: 128). */
+#define EXL3D_HEAD_DIM 128
+
+/* h[b][:] = f32(table[ids[b]][:]); table f16 [vocab][H], h f32 [B][H]. */
+int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *h, hipStream_t s);
+
+/* h += add (f16 [B][H], may be NULL); out = f16(h * rsqrt(mean(h^2) + eps) * w). */
+int exl3d_add_rmsnorm(float *h, const uint16_t *add, const uint16_t *w, uint16_t *out, int B,
+                      int H, float eps, hipStream_t s);
+
+/* q [B][nq*D], k, v [B][nkv*D] (projections, f16); per head RMSNorm with qn / kn
+ * (D), rotate-half RoPE at position pos[b] (angle pos * theta^(-2i/D)); q to
+ * qout [B][nq*D]; k, v into kcache / vcache [B][nkv][Tmax][D] at row pos[b]. */
+int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *qn,
+                       const uint16_t *kn, const int32_t *pos, int B, int nq, int nkv, float eps,
+                       float theta, uint16_t *qout, uint16_t *kcache, uint16_t *vcache, int Tmax,
+                       hipStream_t s);
+
+/* Scratch bytes exl3d_attn_decode needs for these sizes. */
+size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax);
+
+/* Decode attention, grouped-query (nq = 4 nkv): out [B][nq*D] f16 =
+ * softmax(q k^T * scale) v over keys 0 .. pos[b] of row b's cache. */
+int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
+                      const int32_t *pos, int B, int nq, int nkv, int Tmax, float scale,
+                      uint16_t *out, float *scratch, size_t scratch_bytes, hipStream_t s);
+
+/* out = f16(silu(g) * u), n elements. */
+int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_DECODER_H */

@@ -36,6 +36,7 @@ HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-par
 SOURCES = [
     ("exl3_kernels.hip", "exl3_kernels", DEVICE_FLAGS),
     *[("exl3_rate.hip", f"exl3_rate_k{k}", DEVICE_FLAGS + [f"-DEXL3_INST_K={k}"]) for k in range(9)],
+    ("decoder_ops.hip", "decoder_ops", DEVICE_FLAGS),
     ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
     ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
 ]

@@ -1,0 +1,202 @@
+"""The Qwen3-8B-shaped decode step around the EXL3 linears.
+
+The harness ops (include/exl3_decoder.h) are floating-point kernels, so each
+is checked against a float32 PyTorch restatement of the same op (on the CPU,
+so no library product is involved), with the tolerance written at each check;
+the whole step is checked against a float32 restatement whose linears are the
+library's EXL3 matmuls (those are pinned to the oracle in test_gpu_parity.py),
+so the comparison isolates norm, RoPE, KV append, attention and SwiGLU."""
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+
+from plugins_amd import exl3 as X
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_decoder_header_symbols_are_exported():
+    from plugins_amd import qwen3 as Q
+    text = open(os.path.join(ROOT, "include", "exl3_decoder.h")).read()
+    declared = set(re.findall(r"\b(exl3d_[a-z_0-9]+)\s*\(", text))
+    L = X.lib()
+    for name in sorted(declared):
+        assert hasattr(L, name), name
+    assert declared == set(Q._DEC_SIGS), declared ^ set(Q._DEC_SIGS)
+
+
+# ------------------------------------------------------------- GPU parity
+
+torch = pytest.importorskip("torch")
+gpu = pytest.mark.gpu
+
+
+def rel(a, b):
+    a = a.double()
+    b = b.double()
+    return float((a - b).norm() / b.norm())
+
+
+def ref_rmsnorm(h, w, eps):
+    return (h * torch.rsqrt((h * h).mean(-1, keepdim=True) + eps) * w.float()).half()
+
+
+def ref_qk_norm_rope(x, w, pos, eps, theta):
+    """x [B, heads, 128] f16 -> f16: RMSNorm (rounded to f16), rotate-half RoPE."""
+    n = ref_rmsnorm(x.float(), w, eps).float()
+    i = torch.arange(64, dtype=torch.float32)
+    inv = theta ** (-2.0 * i / 128.0)
+    ang = pos.float()[:, None, None] * inv
+    c, s = torch.cos(ang), torch.sin(ang)
+    x1, x2 = n[..., :64], n[..., 64:]
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], -1).half()
+
+
+def ref_attention(q, kc, vc, pos):
+    """q [B, nq*128] f16, caches [B, nkv, T, 128] -> [B, nq*128] f16 (float32)."""
+    B = q.shape[0]
+    nkv = kc.shape[1]
+    nq = q.shape[1] // 128
+    out = torch.empty(B, nq * 128, dtype=torch.float16)
+    for b in range(B):
+        L = int(pos[b]) + 1
+        K = kc[b, :, :L].float().repeat_interleave(nq // nkv, 0)
+        V = vc[b, :, :L].float().repeat_interleave(nq // nkv, 0)
+        Q = q[b].view(nq, 1, 128).float()
+        p = torch.softmax((Q @ K.transpose(1, 2).contiguous()) / math.sqrt(128), -1)
+        out[b] = (p @ V).view(-1).half()
+    return out
+
+
+@gpu
+def test_embed_and_add_rmsnorm():
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(1)
+    B, H, V = 5, 1024, 300
+    table = torch.randn(V, H, generator=g).half()
+    ids = torch.tensor([3, 0, 299, 17, 3], dtype=torch.int32)
+    h = torch.empty(B, H, device="cuda")
+    Q.embed(ids.cuda(), table.cuda(), h)
+    assert torch.equal(h.cpu(), table[ids.long()].float())  # exact: f16 -> f32
+    add = torch.randn(B, H, generator=g).half()
+    w = (1 + 0.1 * torch.randn(H, generator=g)).half()
+    out = torch.empty(B, H, dtype=torch.float16, device="cuda")
+    Q.add_rmsnorm(h, add.cuda(), w.cuda(), out, 1e-6)
+    href = table[ids.long()].float() + add.float()
+    assert torch.allclose(h.cpu(), href, rtol=0, atol=0)  # one f32 add per element
+    want = ref_rmsnorm(href, w, 1e-6)
+    # f16 output: within one f16 rounding of the float32 reference
+    assert rel(out.cpu(), want) < 2e-3, rel(out.cpu(), want)
+
+
+@gpu
+def test_qk_norm_rope_and_kv_append():
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(2)
+    B, nq, nkv, T = 3, 8, 2, 64
+    q = torch.randn(B, nq * 128, generator=g).half()
+    k = torch.randn(B, nkv * 128, generator=g).half()
+    v = torch.randn(B, nkv * 128, generator=g).half()
+    qn = (1 + 0.1 * torch.randn(128, generator=g)).half()
+    kn = (1 + 0.1 * torch.randn(128, generator=g)).half()
+    pos = torch.tensor([0, 17, 63], dtype=torch.int32)
+    kc = torch.zeros(B, nkv, T, 128, dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    qo = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
+    Q.qk_norm_rope(q.cuda(), k.cuda(), v.cuda(), qn.cuda(), kn.cuda(), pos.cuda(), qo, kc, vc, 1e-6,
+                   1e6)
+    wq = ref_qk_norm_rope(q.view(B, nq, 128), qn, pos, 1e-6, 1e6).view(B, -1)
+    wk = ref_qk_norm_rope(k.view(B, nkv, 128), kn, pos, 1e-6, 1e6)
+    # f16 outputs of a float32 computation (sincos / powf in f32): 2e-3 relative
+    assert rel(qo.cpu(), wq) < 2e-3, rel(qo.cpu(), wq)
+    kcc, vcc = kc.cpu(), vc.cpu()
+    for b in range(B):
+        p = int(pos[b])
+        assert rel(kcc[b, :, p], wk[b]) < 2e-3
+        assert torch.equal(vcc[b, :, p], v[b].view(nkv, 128))  # copied
+        others = torch.ones(T, dtype=torch.bool)
+        others[p] = False
+        assert not kcc[b, :, others].any() and not vcc[b, :, others].any()  # only row pos written
+
+
+@gpu
+@pytest.mark.parametrize("B,T,lens", [(1, 40, [39]), (3, 2100, [2048, 5, 700]), (16, 300, None)])
+def test_attention_decode(B, T, lens):
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(3 + B)
+    nq, nkv = 32, 8
+    q = torch.randn(B, nq * 128, generator=g).half()
+    kc = torch.randn(B, nkv, T, 128, generator=g).half()
+    vc = torch.randn(B, nkv, T, 128, generator=g).half()
+    pos = torch.tensor(lens if lens else [int(x) for x in torch.randint(0, T, (B,), generator=g)],
+                       dtype=torch.int32)
+    out = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
+    scratch = torch.empty(Q.attn_scratch_bytes(B, nq, nkv, T) // 4 + 1, device="cuda")
+    Q.attn_decode(q.cuda(), kc.cuda(), vc.cuda(), pos.cuda(), out, scratch)
+    want = ref_attention(q, kc, vc, pos)
+    # f32 online softmax in another summation order, f16 output: 2e-3 relative
+    assert rel(out.cpu(), want) < 2e-3, rel(out.cpu(), want)
+
+
+@gpu
+def test_silu_mul():
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(7, 1000, generator=g).half()
+    b = torch.randn(7, 1000, generator=g).half()
+    out = torch.empty(7, 1000, dtype=torch.float16, device="cuda")
+    Q.silu_mul(a.cuda(), b.cuda(), out)
+    want = (torch.nn.functional.silu(a.float()) * b.float()).half()
+    assert rel(out.cpu(), want) < 2e-3
+
+
+@gpu
+@pytest.mark.parametrize("batch", [1, 4])
+def test_decode_step_against_float32_restatement(batch):
+    from plugins_amd import qwen3 as Q
+    cfg = Q.Qwen3Config(layers=2, hidden=1024, heads=8, kv_heads=2, inter=2048, vocab=1024)
+    ctx = 300
+    m = Q.Qwen3Decoder(cfg, batch, ctx, seed=5)
+    m.ids.copy_(torch.randint(0, cfg.vocab, (batch,), dtype=torch.int32))
+    m.pos.copy_(torch.tensor([ctx - 7 * b for b in range(batch)], dtype=torch.int32))
+    kc0 = [L["kc"].clone() for L in m.layers]
+    vc0 = [L["vc"].clone() for L in m.layers]
+    logits = m.step().cpu()
+    torch.cuda.synchronize()
+
+    # float32 restatement; the linears are the library's EXL3 matmuls
+    def lin(L, x):
+        return L(x.cuda()).cpu()
+
+    pos, ids = m.pos.cpu(), m.ids.cpu().long()
+    h = m.embed_table.cpu()[ids].float()
+    add = None
+    for li, L in enumerate(m.layers):
+        if add is not None:
+            h = h + add.float()
+        xn = ref_rmsnorm(h, L["in_norm"].cpu(), cfg.eps)
+        q, k, v = lin(L["q"], xn), lin(L["k"], xn), lin(L["v"], xn)
+        qr = ref_qk_norm_rope(q.view(batch, cfg.heads, 128), L["q_norm"].cpu(), pos, cfg.eps,
+                              cfg.theta).view(batch, -1)
+        kr = ref_qk_norm_rope(k.view(batch, cfg.kv_heads, 128), L["k_norm"].cpu(), pos, cfg.eps,
+                              cfg.theta)
+        kc, vc = kc0[li].cpu(), vc0[li].cpu()
+        for b in range(batch):
+            kc[b, :, int(pos[b])] = kr[b]
+            vc[b, :, int(pos[b])] = v[b].view(cfg.kv_heads, 128)
+        att = ref_attention(qr, kc, vc, pos)
+        o = lin(L["o"], att)
+        h = h + o.float()
+        xn = ref_rmsnorm(h, L["post_norm"].cpu(), cfg.eps)
+        gg, uu = lin(L["gate"], xn), lin(L["up"], xn)
+        hm = (torch.nn.functional.silu(gg.float()) * uu.float()).half()
+        add = lin(L["down"], hm)
+    h = h + add.float()
+    want = lin(m.lm_head, ref_rmsnorm(h, m.final_norm.cpu(), cfg.eps))
+    # f16 rounding differences at each op propagate through two layers:
+    # 1e-2 relative Frobenius on the logits
+    assert rel(logits, want) < 1e-2, rel(logits, want)
+    assert torch.isfinite(logits).all()
