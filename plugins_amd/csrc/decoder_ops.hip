@@ -38,31 +38,68 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t *__restrict__ 
 }
 
 // h += add (f16, optional); out = f16(h * rsqrt(mean(h^2) + eps) * w).
-// One workgroup of 256 threads per row.
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ h,
-                                                          const uint16_t *__restrict__ add,
-                                                          const uint16_t *__restrict__ w,
-                                                          uint16_t *__restrict__ out, int H,
-                                                          float eps) {
-  __shared__ float part[4];
+// One workgroup of 512 threads per row; each thread loads its 8-element
+// pieces (two float4 of h, 16 bytes of add and of w) before any arithmetic,
+// so a row costs one memory round trip and one reduction.
+constexpr int RN_THREADS = 512;
+constexpr int RN_PER = 2;  // 8-element pieces per thread: rows up to 8192
+
+__global__ __launch_bounds__(RN_THREADS) void add_rmsnorm_kernel(float *__restrict__ h,
+                                                                 const uint16_t *__restrict__ add,
+                                                                 const uint16_t *__restrict__ w,
+                                                                 uint16_t *__restrict__ out, int H,
+                                                                 float eps) {
+  __shared__ float part[RN_THREADS / 64];
   float *hr = h + (size_t)blockIdx.x * H;
   const uint16_t *ar = add ? add + (size_t)blockIdx.x * H : nullptr;
+  float v[RN_PER][8];
+  uint4 wr[RN_PER];
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    float v = hr[i];
-    if (ar) {
-      v += h2f(ar[i]);
-      hr[i] = v;
+#pragma unroll
+  for (int j = 0; j < RN_PER; ++j) {
+    const int i = (threadIdx.x + j * RN_THREADS) * 8;
+    if (i < H) {
+      const float4 h0 = *reinterpret_cast<const float4 *>(hr + i);
+      const float4 h1 = *reinterpret_cast<const float4 *>(hr + i + 4);
+      v[j][0] = h0.x, v[j][1] = h0.y, v[j][2] = h0.z, v[j][3] = h0.w;
+      v[j][4] = h1.x, v[j][5] = h1.y, v[j][6] = h1.z, v[j][7] = h1.w;
+      wr[j] = *reinterpret_cast<const uint4 *>(w + i);
+      if (ar) {
+        const uint4 a4 = *reinterpret_cast<const uint4 *>(ar + i);
+        const uint32_t aw[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[j][2 * e] += h2f((uint16_t)(aw[e] & 0xFFFFu));
+          v[j][2 * e + 1] += h2f((uint16_t)(aw[e] >> 16));
+        }
+        *reinterpret_cast<float4 *>(hr + i) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+        *reinterpret_cast<float4 *>(hr + i + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
     }
-    ss += v * v;
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
-  const float tot = part[0] + part[1] + part[2] + part[3];
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RN_THREADS / 64; ++i) tot += part[i];
   const float r = rsqrtf(tot / (float)H + eps);
   uint16_t *orow = out + (size_t)blockIdx.x * H;
-  for (int i = threadIdx.x; i < H; i += 256) orow[i] = f2h(hr[i] * r * h2f(w[i]));
+#pragma unroll
+  for (int j = 0; j < RN_PER; ++j) {
+    const int i = (threadIdx.x + j * RN_THREADS) * 8;
+    if (i < H) {
+      const uint32_t ww[4] = {wr[j].x, wr[j].y, wr[j].z, wr[j].w};
+      uint32_t o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o4[e] = (uint32_t)f2h(v[j][2 * e] * r * h2f((uint16_t)(ww[e] & 0xFFFFu))) |
+                ((uint32_t)f2h(v[j][2 * e + 1] * r * h2f((uint16_t)(ww[e] >> 16))) << 16);
+      *reinterpret_cast<uint4 *>(orow + i) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    }
+  }
 }
 
 // One wave per (head, row): lane holds dims lane and lane + D/2 (the
@@ -206,25 +243,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
 }
 
-// out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.
-__global__ __launch_bounds__(EXL3D_HEAD_DIM) void attn_combine_kernel(
+// out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.  One
+// workgroup per (row, kv head): the splits' m and l go through LDS (loaded in
+// parallel), then thread (head, d) sums its o over the splits, the loads
+// unrolled so that several are in flight.
+constexpr int AC_MAXS = 256;  // splits the combine takes
+
+__global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
     const float *__restrict__ part, int nq, int nkv, int nsplit, uint16_t *__restrict__ out) {
   constexpr int D = EXL3D_HEAD_DIM;
-  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int kvh = hq / AT_G, h = hq % AT_G;
-  const float *base = part + (((size_t)b * nkv + kvh) * nsplit * AT_G + h) * (D + 2);
+  __shared__ float wsh[AT_G][AC_MAXS];
+  __shared__ float lsum[AT_G];
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int h = threadIdx.x / D, d = threadIdx.x % D;
+  const float *base = part + ((size_t)b * nkv + kvh) * nsplit * AT_G * (D + 2);
   const size_t sstride = (size_t)AT_G * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[s * sstride + D]);
-  float Ls = 0.0f, acc = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float ms = base[s * sstride + D];
-    if (ms == -INFINITY) continue;
-    const float f = __expf(ms - M);
-    Ls += base[s * sstride + D + 1] * f;
-    acc += base[s * sstride + d] * f;
+  for (int i = threadIdx.x; i < AT_G * nsplit; i += AT_G * D) {
+    const int hh = i % AT_G, s = i / AT_G;
+    wsh[hh][s] = base[s * sstride + hh * (D + 2) + D];
   }
-  out[((size_t)b * nq + hq) * D + d] = f2h(acc / Ls);
+  __syncthreads();
+  if (d == 0) {
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, wsh[h][s]);
+    float Ls = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = wsh[h][s];
+      const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
+      Ls += base[s * sstride + h * (D + 2) + D + 1] * f;
+      wsh[h][s] = f;
+    }
+    lsum[h] = Ls;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int s = 0; s < nsplit; ++s) acc += base[s * sstride + h * (D + 2) + d] * wsh[h][s];
+  out[((size_t)b * nq + kvh * AT_G + h) * D + d] = f2h(acc / lsum[h]);
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ g,
@@ -237,9 +292,12 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 }
 
 int attn_split(int Tmax, int B, int nkv, int *TS) {
-  // keys per split: a multiple of 16, with ~512+ workgroups overall
-  int ts = 16;
-  while (ts < 1024 && (long)((Tmax + ts - 1) / ts) * B * nkv > 1024) ts *= 2;
+  // keys per split: a power of two >= 64 (four iterations of the
+  // workgroup's 16 keys), about 256-512 workgroups overall, at most
+  // AC_MAXS splits
+  int ts = 64;
+  while (((long)((Tmax + ts - 1) / ts) * B * nkv > 512 || (Tmax + ts - 1) / ts > AC_MAXS))
+    ts *= 2;
   *TS = ts;
   return (Tmax + ts - 1) / ts;
 }
@@ -257,8 +315,8 @@ int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *
 
 int exl3d_add_rmsnorm(float *h, const uint16_t *add, const uint16_t *w, uint16_t *out, int B,
                       int H, float eps, hipStream_t s) {
-  if (B <= 0 || H <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(B), dim3(256), 0, s, h, add, w, out, H, eps);
+  if (B <= 0 || H <= 0 || H % 8 != 0 || H > RN_THREADS * RN_PER * 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(B), dim3(RN_THREADS), 0, s, h, add, w, out, H, eps);
   return hipGetLastError();
 }
 
@@ -288,8 +346,8 @@ int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t 
   const int ns = attn_split(Tmax, B, nkv, &ts);
   hipLaunchKernelGGL(attn_decode_kernel, dim3(ns, nkv, B), dim3(256), 0, s, q, kcache, vcache,
                      pos, nq, nkv, Tmax, ts, scale, scratch);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(nq, B), dim3(EXL3D_HEAD_DIM), 0, s, scratch, nq,
-                     nkv, ns, out);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s, scratch,
+                     nq, nkv, ns, out);
   return hipGetLastError();
 }
 
