@@ -181,32 +181,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
   }
   const size_t kvbase = ((size_t)b * nkv + kvh) * Tmax;
-  for (int t = t0 + 4 * wave + g; t < t1; t += 16) {
-    const uint4 kr = *reinterpret_cast<const uint4 *>(kcache + (kvbase + t) * D + 8 * li);
-    const uint4 vr = *reinterpret_cast<const uint4 *>(vcache + (kvbase + t) * D + 8 * li);
-    const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
-    const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
-    float kf[8], vf[8];
+  auto ld = [&](const uint16_t *c, int t) {
+    return *reinterpret_cast<const uint4 *>(c + (kvbase + t) * D + 8 * li);
+  };
+  int t = t0 + 4 * wave + g;
+  if (t0 < t1) {
+    // the next key's rows are loaded before this one is processed (clamped
+    // to the split's last key: in bounds, unused past the end)
+    uint4 kr = ld(kcache, min(t, t1 - 1)), vr = ld(vcache, min(t, t1 - 1));
+    for (; t < t1; t += 16) {
+      const int tn = min(t + 16, t1 - 1);
+      const uint4 krn = ld(kcache, tn), vrn = ld(vcache, tn);
+      const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
+      const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+      float kf[8], vf[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
-      kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
-      vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
-      vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
-    }
+      for (int e = 0; e < 4; ++e) {
+        kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
+        kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+        vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
+        vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+      }
 #pragma unroll
-    for (int h = 0; h < AT_G; ++h) {
-      float sc = 0.0f;
+      for (int h = 0; h < AT_G; ++h) {
+        float sc = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sc += qr[h][e] * kf[e];
+        for (int e = 0; e < 8; ++e) sc += qr[h][e] * kf[e];
 #pragma unroll
-      for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // over the 16 lanes
-      const float mn = fmaxf(m[h], sc);
-      const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
-      l[h] = l[h] * c + pr;
+        for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // over the 16 lanes
+        const float mn = fmaxf(m[h], sc);
+        const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
+        l[h] = l[h] * c + pr;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * c + pr * vf[e];
-      m[h] = mn;
+        for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * c + pr * vf[e];
+        m[h] = mn;
+      }
+      kr = krn;
+      vr = vrn;
     }
   }
   // merge the 16 states (4 waves x 4 key groups) per head
@@ -293,10 +304,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 
 int attn_split(int Tmax, int B, int nkv, int *TS) {
   // keys per split: a power of two >= 64 (four iterations of the
-  // workgroup's 16 keys), about 256-512 workgroups overall, at most
-  // AC_MAXS splits
+  // workgroup's 16 keys), at most ~2048 workgroups overall (each is bound
+  // by its own memory round trips, so many in flight), at most AC_MAXS
+  // splits
   int ts = 64;
-  while (((long)((Tmax + ts - 1) / ts) * B * nkv > 512 || (Tmax + ts - 1) / ts > AC_MAXS))
+  while (((long)((Tmax + ts - 1) / ts) * B * nkv > 2048 || (Tmax + ts - 1) / ts > AC_MAXS))
     ts *= 2;
   *TS = ts;
   return (Tmax + ts - 1) / ts;

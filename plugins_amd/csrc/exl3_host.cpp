@@ -498,7 +498,7 @@ static hipError_t gemv_scratch(StreamScratch *ss, const int *outs, int count, in
   int total = 0;
   for (int i = 0; i < count; ++i) total += outs[i];
   int ksplit, tps;
-  exl3::gemv_multi_plan(in, total, generic, &ksplit, &tps);
+  exl3::gemv_multi_plan(in, total, generic, rows, &ksplit, &tps);
   hipError_t e = grow(&ss->partial, &ss->partial_bytes, (size_t)ksplit * rows * total * 4, s, 0xFF);
   if (e != hipSuccess) return e;
   size_t po = 0;

@@ -279,6 +279,119 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
   }
 }
 
+// Prepare of many rows (more items than one batch): all of a workgroup's
+// rows in one pass of loads.  A 128-block is held by 16 consecutive lanes, 8
+// consecutive elements each: the butterfly's stages on index bits 0-2 are
+// in-register, bits 3-6 exchange across the 16 lanes; every element sees the
+// same f32 operations in the same order as in had128_pair, so a row's
+// prepared values (and its 64-element sums, the same pairwise tree) do not
+// depend on which path prepared it.  Group G = tid / 16 + 32 p of pass p
+// takes block G of the workgroup (row G / nb, block G % nb); groups past the
+// last block redo the last block (the same values to the same place).
+constexpr int PREP_GROUPS = GEMV_THREADS / 16;
+constexpr int PREP_PASSES = GEMV_ROWS * (GEMV_TPS_MAX / 8) / PREP_GROUPS;
+
+struct RowsRegs {
+  u4_t x[PREP_PASSES][2];  // 8 elements: one 16-byte piece (f16/bf16) or two (f32)
+  u4_t su[PREP_PASSES];
+};
+
+__device__ __forceinline__ void gemv_rows_load_x(const void *x, int xdt, int prepared,
+                                                 const RowMap &rm, int nblk, int nb, int tk0,
+                                                 RowsRegs &r) {
+  const int esz = (!prepared && xdt == OUT_F32) ? 4 : 2;
+  const int li = threadIdx.x & 15;
+#pragma unroll
+  for (int p = 0; p < PREP_PASSES; ++p) {
+    const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
+    const int row = G / nb, blk = G - row * nb;
+    const int k = tk0 * 16 + blk * 128 + 8 * li;
+    const char *pa = (const char *)x + ((size_t)rm.in_off(row) + k) * esz;
+    r.x[p][0] = *reinterpret_cast<const u4_t *>(pa);
+    r.x[p][1] = *reinterpret_cast<const u4_t *>(pa + (esz - 2) * 8);
+  }
+}
+
+__device__ __forceinline__ void gemv_rows_load_su(const void *x, int prepared, const uint16_t *suh,
+                                                  int nblk, int nb, int tk0, RowsRegs &r) {
+  const uint16_t *sup = prepared ? (const uint16_t *)x : suh;
+  const int li = threadIdx.x & 15;
+#pragma unroll
+  for (int p = 0; p < PREP_PASSES; ++p) {
+    const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
+    const int blk = G % nb;
+    r.su[p] = *(const __attribute__((address_space(1))) u4_t *)(sup + tk0 * 16 + blk * 128 + 8 * li);
+  }
+}
+
+__device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk, int nb,
+                                                uint16_t *xs, int kr, const RowsRegs &r,
+                                                float *hsum) {
+  const int li = threadIdx.x & 15, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int p = 0; p < PREP_PASSES; ++p) {
+    const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
+    const int row = G / nb, blk = G - row * nb;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a, b;
+      prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
+      const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
+      const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
+      if (!prepared && xdt == OUT_F32) {
+        a = fa;
+        b = fb;
+      }
+      const uint32_t su = r.su[p][e];
+      v[2 * e] = h2f(f2h(a)) * h2f((uint16_t)(su & 0xFFFFu));
+      v[2 * e + 1] = h2f(f2h(b)) * h2f((uint16_t)(su >> 16));
+    }
+    // stages on bits 0, 1, 2 (in-register), then 3-6 (lanes xor 1, 2, 4, 8)
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (e & m) continue;
+        const float lo = v[e], hi = v[e + m];
+        v[e] = lo + hi;
+        v[e + m] = lo - hi;
+      }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      const bool lower = (li & m) == 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pv = __shfl_xor(v[e], m, 64);
+        v[e] = lower ? v[e] + pv : pv - v[e];
+      }
+    }
+    uint32_t y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t rot =
+          (uint32_t)f2h(v[2 * e] * HAD_SCALE) | ((uint32_t)f2h(v[2 * e + 1] * HAD_SCALE) << 16);
+      y[e] = prepared ? r.x[p][0][e] : rot;
+    }
+    const u4_t yv = {y[0], y[1], y[2], y[3]};
+    *reinterpret_cast<u4_t *>(xs + row * kr + blk * 128 + 8 * li) = yv;
+    if (hsum != nullptr) {
+      // the 64-element sum as the pairwise tree had128_pair's layout forms:
+      // in-lane pairs, then pairs of pairs, ..., then across lanes
+      float s2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        s2[e] = h2f((uint16_t)(y[e] & 0xFFFFu)) + h2f((uint16_t)(y[e] >> 16));
+      float s = (s2[0] + s2[1]) + (s2[2] + s2[3]);
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) s = s + __shfl_xor(s, m, 64);
+      if ((li & 7) == 0) hsum[row * nb * 2 + blk * 2 + (li >> 3)] = s;
+    }
+  }
+  (void)lane;
+}
+
 __device__ __forceinline__ h8_t frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   const u4_t v = {a, b, c, d};
   return bits<h8_t>(v);
@@ -443,8 +556,14 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   const uint32_t *wp = twe + ((size_t)(kb + g) * out_tiles + tn) * nw + c * K;
   const size_t wstep = (size_t)4 * out_tiles * nw;  // dwords per step
   const int nb = ntk >> 3, nitems = nrows * nb;
+  // ONEB: one item (row, 128-block) per wave and batch; else every row's
+  // items in one pass (gemv_rows_*)
   PrepRegs pr;
-  gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
+  RowsRegs rr;
+  if constexpr (ONEB)
+    gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
+  else
+    gemv_rows_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, rr);
   if constexpr (K > 0) {
 #pragma unroll
     for (int i = 0; i < K; ++i) bw[0][i] = wp[i];
@@ -456,7 +575,10 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   const uint16_t *suh0 = W.suh;
   asm volatile("" : "+s"(suh0)::"memory");
   const uint16_t *suh = suh0 + (size_t)expert * in;
-  gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
+  if constexpr (ONEB)
+    gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
+  else
+    gemv_rows_load_su(x, geo.prepared, suh, nitems, nb, tk0, rr);
   if constexpr (K > 0) {
 #pragma unroll
     for (int b = 1; b < NBUF; ++b) {
@@ -469,16 +591,11 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // load without a branch around it)
   const uint16_t *svp = W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : suh;
   const uint32_t sv = ld_global_u32(svp + 2 * lane);
-  gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
-                  FOLD ? hsum : nullptr);
-  if constexpr (!ONEB) {
-    for (int base = PREP_ITEMS; base < nitems; base += PREP_ITEMS) {
-      gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, base, wave, lane, pr);
-      gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, base, wave, lane, pr);
-      gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, base, wave, lane, xs, kr, pr,
-                      FOLD ? hsum : nullptr);
-    }
-  }
+  if constexpr (ONEB)
+    gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
+                    FOLD ? hsum : nullptr);
+  else
+    gemv_rows_store(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr);
   lds_barrier();
 
   const int arow = min(lane & 15, nrows - 1);

@@ -46,8 +46,8 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 
 // The GEMV split: whole 128-input blocks per split (ksplit splits of tps
 // k-tile rows) for a GEMV over `groups` weights of (in, out).
-void gemv_plan(int in, int out, int groups, int *ksplit, int *tps);
-int gemv_ksplit(int in, int out, int groups);
+void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps);
+int gemv_ksplit(int in, int out, int groups, int rows);
 // Largest row count the GEMV path serves (the MFMA M); wider calls take the GEMM.
 constexpr int GEMV_ROWS_MAX = 16;
 
@@ -76,7 +76,7 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
                        int out, hipStream_t s);
 // The split of one GEMV launch over weights of total output width
 // total_out: a linear of width out needs ksplit * rows * out partial floats.
-void gemv_multi_plan(int in, int total_out, bool generic, int *ksplit, int *tps);
+void gemv_multi_plan(int in, int total_out, bool generic, int rows, int *ksplit, int *tps);
 
 // ------------------------------------------------------------------- MoE
 

@@ -199,25 +199,28 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
 // GEMV_TPS_MAX k-tile rows (32 for the generic rate) and GEMV_KSPLIT_MAX
-// splits, ~512 workgroups over `groups` column groups.
-void gemv_plan(int in, int out, int groups, int *ksplit, int *tps) {
+// splits, ~512 workgroups over `groups` column groups; ~256 for more than 4
+// rows, whose split-K partial sums (rows x 128 floats per workgroup) would
+// otherwise add half the weight bytes again at 16 rows.
+void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
-  int ks = std::min(nb, std::max(1, (512 + cgs - 1) / cgs));
+  const int target = rows > 4 ? 256 : 512;
+  int ks = std::min(nb, std::max(1, (target + cgs - 1) / cgs));
   int bps = std::min(GEMV_TPS_MAX / 8, (nb + ks - 1) / ks);  // blocks per split
   bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
   *tps = 8 * bps;
   *ksplit = (nb + bps - 1) / bps;
 }
 
-int gemv_ksplit(int in, int out, int groups) {
+int gemv_ksplit(int in, int out, int groups, int rows) {
   int ks, tps;
-  gemv_plan(in, out, groups, &ks, &tps);
+  gemv_plan(in, out, groups, rows, &ks, &tps);
   return ks;
 }
 
-void gemv_multi_plan(int in, int total_out, bool generic, int *ksplit, int *tps) {
-  gemv_plan(in, total_out, 1, ksplit, tps);
+void gemv_multi_plan(int in, int total_out, bool generic, int rows, int *ksplit, int *tps) {
+  gemv_plan(in, total_out, 1, rows, ksplit, tps);
   if (generic && *tps > 32) {
     *tps = 32;
     *ksplit = (in / 16 + 31) / 32;
@@ -256,7 +259,7 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   }
   if ((int64_t)rows * std::max(in, maxout) >= (int64_t)1 << 31) return hipErrorInvalidValue;
   int ksplit, tps;
-  gemv_multi_plan(in, 128 * totcg, generic, &ksplit, &tps);
+  gemv_multi_plan(in, 128 * totcg, generic, rows, &ksplit, &tps);
   if (ksplit > GEMV_KSPLIT_MAX || totcg > 65535) return hipErrorInvalidValue;
   if (in / 16 > 65535) return hipErrorInvalidValue;
   GemvArgs a{};
@@ -493,8 +496,8 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   L.slots = slots;
   L.max_items = std::min(a.experts, slots) + (slots + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
   const int groups = std::max(1, std::min(a.experts, slots));
-  gemv_plan(a.hidden, a.inter, 2 * groups, &L.ks_gu, &L.tps_gu);
-  gemv_plan(a.inter, a.hidden, groups, &L.ks_d, &L.tps_d);
+  gemv_plan(a.hidden, a.inter, 2 * groups, 1, &L.ks_gu, &L.tps_gu);
+  gemv_plan(a.inter, a.hidden, groups, 1, &L.ks_d, &L.tps_d);
   if (generic_gu && L.tps_gu > 32) {
     L.tps_gu = 32;
     L.ks_gu = (a.hidden / 16 + 31) / 32;
