@@ -102,8 +102,9 @@ def cpu_baseline(seconds: float):
                       f"packed), {el:.1f} s, oracle/exl3_oracle.c exl3o_project"}
 
 
-def gemm_tflops(torch, X, iters: int = 10):
+def gemm_tflops(torch, iters: int = 10):
     """Prefill GEMM M=2048 at K=4 on the gate/up shape (4096 -> 12288)."""
+    from plugins_amd import exl3 as X
     rows, i, o = 2048, 4096, 12288
     g = torch.Generator(device="cuda")
     g.manual_seed(11)
@@ -177,6 +178,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the decoder tok/s leg")
+    ap.add_argument("--only", choices=["gemv", "gemm", "decode"], default=None,
+                    help="run one leg (gemv: the decode GEMV pass and its roofline leg only)")
     ap.add_argument("--per-linear", action="store_true",
                     help="one launch per linear instead of one per shared-input group")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -190,6 +193,13 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_mib": args.copy_mib, "copies": 5}))
+        return 0
+    if args.only in ("gemm", "decode"):
+        # one leg alone (for counter runs of its kernels); prints that leg's numbers
+        import torch
+        torch.cuda.set_device(0)
+        res = gemm_tflops(torch) if args.only == "gemm" else decode_tok_s(torch)
+        print(json.dumps({"only": args.only, **res}), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the EXL3 path has no multi-GPU leg); "
@@ -286,12 +296,13 @@ def main() -> int:
               for k, v in per_shape.items()}
 
     extra = {}
-    try:
-        extra.update(gemm_tflops(torch, X))
-    except Exception as ex:  # reported, not hidden
-        extra["prefill_gemm_error"] = repr(ex)
+    if args.only != "gemv":
+        try:
+            extra.update(gemm_tflops(torch))
+        except Exception as ex:  # reported, not hidden
+            extra["prefill_gemm_error"] = repr(ex)
     extra["gemv_gbs_per_shape"] = shapes
-    if not args.no_decode:
+    if not args.no_decode and args.only != "gemv":
         try:
             log("decode step")
             extra["decode_tok_s"] = decode_tok_s(torch)
@@ -300,7 +311,7 @@ def main() -> int:
     extra["graph"] = graph is not None
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.only != "gemv":
         log("cpu baseline")
         cpu = cpu_baseline(args.cpu_seconds)
 
@@ -326,7 +337,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (profiles/gemv_k4_qwen3_8b_decode.md)",
                      "algorithmic_bytes_per_launch": round(kbytes / len(pairs)),
-                     "kernel": "exl3::gemv_kernel<4,0,false> (mul1, K=4, window 16)", "launches": len(pairs),
+                     "kernel": "exl3::gemv_kernel<4,0,false,true> (mul1, K=4, window 16, one prepare batch)", "launches": len(pairs),
                      "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
         "cpu_baseline": cpu,
         "extra": extra,
