@@ -25,12 +25,16 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
-// Agent-scope (all XCDs) loads and stores for the split-K hand-off.
+// Agent-scope (all XCDs) loads and stores for the split-K hand-off, through
+// the global address space (a flat access is also counted as an LDS
+// operation, so a wait for LDS would wait for it too).
+typedef __attribute__((address_space(1))) uint32_t gu32_t;
+typedef __attribute__((address_space(1))) float gf32_t;
 __device__ __forceinline__ void st_agent(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((gf32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float ld_agent(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((gf32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // s_waitcnt vmcnt(0): this wave's outstanding vector-memory operations,
 // stores included on gfx9-family parts, have completed.
@@ -553,7 +557,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // steps in flight per wave: as many as a few registers allow
   constexpr int NBUF = K <= 0 ? 1 : 3;
   uint32_t bw[NBUF][KB];
-  const uint32_t *wp = twe + ((size_t)(kb + g) * out_tiles + tn) * nw + c * K;
+  const gu32_t *wp = (const gu32_t *)(twe + ((size_t)(kb + g) * out_tiles + tn) * nw + c * K);
   const size_t wstep = (size_t)4 * out_tiles * nw;  // dwords per step
   const int nb = ntk >> 3, nitems = nrows * nb;
   // ONEB: one item (row, 128-block) per wave and batch; else every row's
@@ -582,7 +586,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   if constexpr (K > 0) {
 #pragma unroll
     for (int b = 1; b < NBUF; ++b) {
-      const uint32_t *pb = wp + (size_t)min(b, iters - 1) * wstep;
+      const gu32_t *pb = wp + (size_t)min(b, iters - 1) * wstep;
 #pragma unroll
       for (int i = 0; i < K; ++i) bw[b][i] = pb[i];
     }
@@ -629,7 +633,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
         if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
         if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
       });
-      const uint32_t *pn = wp + (size_t)min(it + NBUF, iters - 1) * wstep;
+      const gu32_t *pn = wp + (size_t)min(it + NBUF, iters - 1) * wstep;
 #pragma unroll
       for (int i = 0; i < K; ++i) b[i] = pn[i];
     };
