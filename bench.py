@@ -16,10 +16,12 @@ HIP graph and replayed.
 
 `value` = packed-weight bytes per step * steps / timed seconds (GB/s).
 `roofline` = the dominant kernel (the K=4 decode GEMV, which is the whole
-matmul: prepare, GEMV and finish in one launch) measured with HIP event pairs
-around each launch, over every linear of the model:
-algorithmic bytes (in*out*K/8 per launch) / average launch duration, against
-the 8 TB/s HBM peak.  `cpu_baseline` = the CPU oracle's projection
+matmul: prepare, GEMV and finish in one launch): algorithmic bytes per launch
+(in*out*K/8 summed over the launch's linears) / average launch duration, the
+duration from HIP events around the timed region's graph replays (the
+launches run back to back) divided by the launches, against the 8 TB/s HBM
+peak; the rocprof kernel trace of the same command agrees
+(profiles/gemv_k4_qwen3_8b_decode.md).  `cpu_baseline` = the CPU oracle's projection
 (prepare + decode + f32 dot + finish, the reference's CPU path restated in
 C, oracle/exl3_oracle.c) on the host cores over a bounded sample of the same
 linears.  `extra` carries the prefill GEMM (M=2048, K=4) TFLOP/s.
@@ -256,20 +258,27 @@ def main() -> int:
         run = graph.replay
     log("timing", args.steps, "steps")
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record()
     for _ in range(args.steps):
         run()
+    ev1.record()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     ms_per_step = el * 1e3 / args.steps
     value = step_bytes * args.steps / el / 1e9
+    # GPU time of the timed region (HIP events on the stream the graph is
+    # launched on): the launches run back to back, so a launch's average
+    # duration is the region's time over the launches it holds
+    gpu_ms_per_step = ev0.elapsed_time(ev1) / args.steps
 
-    # roofline leg: the matmul of each linear is one kernel launch (prepare,
-    # decode GEMV and finish fused); HIP event pairs around each launch, every
-    # linear of the model once per pass, 3 passes.  A sleep kernel first lets
-    # the host queue every launch ahead of the GPU, so the pairs time the
-    # kernels and not the host's submission.
-    log("roofline leg")
+    # per-shape diagnostic: the matmul of each linear is one kernel launch
+    # (prepare, decode GEMV and finish fused); HIP event pairs around each
+    # launch, every linear of the model once per pass, 3 passes (the pairs
+    # add their own ~2 us per launch; the roofline uses the timed region).  A
+    # sleep kernel first lets the host queue every launch ahead of the GPU.
+    log("per-shape leg")
     step()  # the library sizes its scratch for this stream on first use
     torch.cuda.synchronize()
     pairs = []
@@ -283,9 +292,9 @@ def main() -> int:
             name = "+".join(lins[j][0] for j in g)
             pairs.append((name, sum(packed_bytes(lins[j][1], lins[j][2]) for j in g), a, b))
     torch.cuda.synchronize()
-    kbytes = sum(p[1] for p in pairs)
-    kms = sum(a.elapsed_time(b) for _, _, a, b in pairs)
-    achieved = kbytes / (kms * 1e-3) / 1e9
+    launches = len(groups)
+    avg_launch_ms = gpu_ms_per_step / launches
+    achieved = step_bytes / launches / (avg_launch_ms * 1e-3) / 1e9
     per_shape = {}
     for name, nb, a, b in pairs:
         d = per_shape.setdefault(name, [0, 0.0, 0])
@@ -336,9 +345,11 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (profiles/gemv_k4_qwen3_8b_decode.md)",
-                     "algorithmic_bytes_per_launch": round(kbytes / len(pairs)),
-                     "kernel": "exl3::gemv_kernel<4,0,false,true> (mul1, K=4, window 16, one prepare batch)", "launches": len(pairs),
-                     "avg_launch_us": round(kms * 1e3 / len(pairs), 3)},
+                     "algorithmic_bytes_per_launch": round(step_bytes / launches),
+                     "kernel": "exl3::gemv_kernel<4,0,false,true> (mul1, K=4, window 16, one prepare batch)",
+                     "launches": launches * args.steps,
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 3),
+                     "timing": "HIP events around the timed region's graph replays / launches"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

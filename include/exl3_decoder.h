@@ -38,14 +38,29 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
                        float theta, uint16_t *qout, uint16_t *kcache, uint16_t *vcache, int Tmax,
                        hipStream_t s);
 
-/* Scratch bytes exl3d_attn_decode needs for these sizes. */
+/* Scratch bytes exl3d_attn_decode(_rope) needs for these sizes: split slots
+ * and one arrival ticket per (row, kv head).  Zero the scratch once before
+ * its first use; every call leaves the tickets zero again.  Calls that share
+ * a scratch must be ordered on one stream. */
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax);
 
 /* Decode attention, grouped-query (nq = 4 nkv): out [B][nq*D] f16 =
- * softmax(q k^T * scale) v over keys 0 .. pos[b] of row b's cache. */
+ * softmax(q k^T * scale) v over keys 0 .. pos[b] of row b's cache, split
+ * over the keys (for small grids one launch, the last split of each (row,
+ * kv head) combining the splits; else a second launch combines them). */
 int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                       const int32_t *pos, int B, int nq, int nkv, int Tmax, float scale,
                       uint16_t *out, float *scratch, size_t scratch_bytes, hipStream_t s);
+
+/* exl3d_qk_norm_rope followed by exl3d_attn_decode, in one launch: q, k, v
+ * are the raw projections; q's heads are normalized and rotated inside the
+ * attention, k (normalized, rotated) and v are appended at row pos[b] of the
+ * caches before the attention reads them. */
+int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           const uint16_t *qn, const uint16_t *kn, const int32_t *pos, int B,
+                           int nq, int nkv, float eps, float theta, uint16_t *kcache,
+                           uint16_t *vcache, int Tmax, float scale, uint16_t *out, float *scratch,
+                           size_t scratch_bytes, hipStream_t s);
 
 /* out = f16(silu(g) * u), n elements. */
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s);

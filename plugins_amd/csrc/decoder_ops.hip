@@ -140,38 +140,142 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   dst[lane + HALF] = f2h(y1);
 }
 
+// Agent-scope (all XCDs) accesses for the split hand-off, through the global
+// address space.
+typedef __attribute__((address_space(1))) float gf32_t;
+typedef __attribute__((address_space(1))) uint32_t gu32_t;
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store((gf32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load((gf32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The q/k norm + RoPE of one head's dims 8 li .. 8 li + 7 held by the 16
+// lanes of a key group (lane li): RMSNorm with weight nw (sum of squares over
+// the 16 lanes), f16, then rotate-half RoPE with the pair partner in lane
+// li ^ 8 (dims d and d + 64), f16.  sn / cs: the lane's 8 angles.
+__device__ __forceinline__ void norm_rope8(float (&x)[8], const uint4 nw, const float (&sn)[8],
+                                           const float (&cs)[8], int li, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  const float r = rsqrtf(ss / (float)EXL3D_HEAD_DIM + eps);
+  const uint32_t w4[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float wv = h2f((uint16_t)(e & 1 ? w4[e >> 1] >> 16 : w4[e >> 1] & 0xFFFFu));
+    x[e] = h2f(f2h(x[e] * r * wv));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pr = __shfl_xor(x[e], 8, 64);
+    x[e] = li < 8 ? x[e] * cs[e] - pr * sn[e] : x[e] * cs[e] + pr * sn[e];
+    x[e] = h2f(f2h(x[e]));
+  }
+}
+
+__device__ __forceinline__ void unpack8(const uint4 raw, float (&x)[8]) {
+  const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = h2f((uint16_t)(w4[e] & 0xFFFFu));
+    x[2 * e + 1] = h2f((uint16_t)(w4[e] >> 16));
+  }
+}
+__device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+  uint32_t w4[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w4[e] = (uint32_t)f2h(x[2 * e]) | ((uint32_t)f2h(x[2 * e + 1]) << 16);
+  return make_uint4(w4[0], w4[1], w4[2], w4[3]);
+}
+
+// The raw projections and norm weights of the q/k norm + RoPE that the
+// attention kernel applies itself (ROPE).
+struct RopeArgs {
+  const uint16_t *k, *v;    // [B][nkv * D]
+  const uint16_t *qn, *kn;  // [D]
+  float eps, theta;
+};
+
 // Split-T decode attention, grouped-query: a workgroup (4 waves) takes one
 // (row b, kv head) and keys [s TS, min((s + 1) TS, L)), L = pos[b] + 1, for
 // the G = nq / nkv query heads that share the kv head.  Lane l of a wave:
 // key group l / 16 (four keys per wave per iteration), dims 8 (l % 16) ..
 // +7.  Online softmax per (key group, head) in f32; the 16 partial states of
-// the workgroup merge in LDS and go out as (m, l, o[D]) per head.
+// the workgroup merge in LDS into (m, l, o[D]) per head, stored in the
+// split's slot.  TICKET: the split that arrives last at the (row, kv head)'s
+// ticket (all other slots are then stored) combines the slots in split
+// order: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16, and
+// resets the ticket; else attn_combine_kernel does, as its own launch.
+// ROPE: q arrives raw; every workgroup applies the q norm and RoPE to its
+// heads, and the workgroup of the split holding key pos[b] also normalizes,
+// rotates and appends that key (and copies the value) into the caches first.
 constexpr int AT_G = 4;  // query heads per kv head (Qwen3-8B: 32 / 8)
+constexpr int AC_MAXS = 256;  // splits
+constexpr int AT_KD = 4;  // key rows in flight per key group
 
+template <bool ROPE, bool TICKET>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kcache,
-    const uint16_t *__restrict__ vcache, const int32_t *__restrict__ pos, int nq, int nkv,
-    int Tmax, int TS, float scale, float *__restrict__ part) {
+    const uint16_t *__restrict__ q, uint16_t *__restrict__ kcache, uint16_t *__restrict__ vcache,
+    const int32_t *__restrict__ pos, int nq, int nkv, int Tmax, int TS, float scale, RopeArgs ra,
+    float *__restrict__ part, uint32_t *__restrict__ tickets, uint16_t *__restrict__ out) {
   constexpr int D = EXL3D_HEAD_DIM;
   __shared__ float sm[16][AT_G][D + 2];
+  __shared__ float wsh[AT_G][AC_MAXS];
+  __shared__ float lsum[AT_G];
+  __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int L = pos[b] + 1;
+  const int p = pos[b];
+  const int L = p + 1;
   const int t0 = s * TS, t1 = min(t0 + TS, L);
   const int nsplit = gridDim.x;
   float qr[AT_G][8];
 #pragma unroll
-  for (int h = 0; h < AT_G; ++h) {
-    const uint4 raw =
-        *reinterpret_cast<const uint4 *>(q + ((size_t)b * nq + kvh * AT_G + h) * D + 8 * li);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+  for (int h = 0; h < AT_G; ++h)
+    unpack8(*reinterpret_cast<const uint4 *>(q + ((size_t)b * nq + kvh * AT_G + h) * D + 8 * li),
+            qr[h]);
+  const size_t kvbase = ((size_t)b * nkv + kvh) * Tmax;
+  if constexpr (ROPE) {
+    // angle of dim d: pos * theta^(-2 (d mod 64) / D), the 64 angles once
+    // per workgroup (the argument reaches thousands of radians, where a sine
+    // costs a long reduction)
+    __shared__ float sc_sn[D / 2], sc_cs[D / 2];
+    if (threadIdx.x < D / 2) {
+      const float inv = powf(ra.theta, -2.0f * (float)threadIdx.x / (float)D);
+      sincosf((float)p * inv, &sc_sn[threadIdx.x], &sc_cs[threadIdx.x]);
+    }
+    __syncthreads();
+    float sn[8], cs[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qr[h][2 * e] = h2f((uint16_t)(w4[e] & 0xFFFFu)) * scale;
-      qr[h][2 * e + 1] = h2f((uint16_t)(w4[e] >> 16)) * scale;
+    for (int e = 0; e < 8; ++e) {
+      const int i = (8 * li + e) & (D / 2 - 1);
+      sn[e] = sc_sn[i];
+      cs[e] = sc_cs[i];
+    }
+    const uint4 qn = *reinterpret_cast<const uint4 *>(ra.qn + 8 * li);
+#pragma unroll
+    for (int h = 0; h < AT_G; ++h) norm_rope8(qr[h], qn, sn, cs, li, ra.eps);
+    if (s == p / TS) {
+      float kx[8];
+      unpack8(*reinterpret_cast<const uint4 *>(ra.k + ((size_t)b * nkv + kvh) * D + 8 * li), kx);
+      const uint4 vr = *reinterpret_cast<const uint4 *>(ra.v + ((size_t)b * nkv + kvh) * D + 8 * li);
+      norm_rope8(kx, *reinterpret_cast<const uint4 *>(ra.kn + 8 * li), sn, cs, li, ra.eps);
+      if (wave == 0 && g == 0) {
+        *reinterpret_cast<uint4 *>(kcache + (kvbase + p) * D + 8 * li) = pack8(kx);
+        *reinterpret_cast<uint4 *>(vcache + (kvbase + p) * D + 8 * li) = vr;
+      }
+      __syncthreads();  // the key loop below reads row p
     }
   }
+#pragma unroll
+  for (int h = 0; h < AT_G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qr[h][e] *= scale;
   float m[AT_G], l[AT_G], o[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h) {
@@ -180,44 +284,47 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
   }
-  const size_t kvbase = ((size_t)b * nkv + kvh) * Tmax;
   auto ld = [&](const uint16_t *c, int t) {
     return *reinterpret_cast<const uint4 *>(c + (kvbase + t) * D + 8 * li);
   };
-  int t = t0 + 4 * wave + g;
+  // The key group's keys t, t + 16, ...: AT_KD of them in flight (a split of
+  // 64 keys is loaded at once), each reloaded AT_KD keys ahead once used;
+  // keys past the split's end reload its last key (in bounds, unused).
+  const int tg = t0 + 4 * wave + g;
   if (t0 < t1) {
-    // the next key's rows are loaded before this one is processed (clamped
-    // to the split's last key: in bounds, unused past the end)
-    uint4 kr = ld(kcache, min(t, t1 - 1)), vr = ld(vcache, min(t, t1 - 1));
-    for (; t < t1; t += 16) {
-      const int tn = min(t + 16, t1 - 1);
-      const uint4 krn = ld(kcache, tn), vrn = ld(vcache, tn);
-      const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
-      const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
-      float kf[8], vf[8];
+    uint4 kr[AT_KD], vr[AT_KD];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
-        kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
-        vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
-        vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+    for (int j = 0; j < AT_KD; ++j) {
+      kr[j] = ld(kcache, min(tg + 16 * j, t1 - 1));
+      vr[j] = ld(vcache, min(tg + 16 * j, t1 - 1));
+    }
+    for (int tb = tg; tb < t1; tb += 16 * AT_KD) {
+#pragma unroll
+      for (int j = 0; j < AT_KD; ++j) {
+        const int t = tb + 16 * j;
+        if (t < t1) {
+          float kf[8], vf[8];
+          unpack8(kr[j], kf);
+          unpack8(vr[j], vf);
+          const int tn = min(t + 16 * AT_KD, t1 - 1);
+          kr[j] = ld(kcache, tn);
+          vr[j] = ld(vcache, tn);
+#pragma unroll
+          for (int h = 0; h < AT_G; ++h) {
+            float sc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sc += qr[h][e] * kf[e];
+#pragma unroll
+            for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // 16 lanes
+            const float mn = fmaxf(m[h], sc);
+            const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
+            l[h] = l[h] * c + pr;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * c + pr * vf[e];
+            m[h] = mn;
+          }
+        }
       }
-#pragma unroll
-      for (int h = 0; h < AT_G; ++h) {
-        float sc = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sc += qr[h][e] * kf[e];
-#pragma unroll
-        for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // over the 16 lanes
-        const float mn = fmaxf(m[h], sc);
-        const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
-        l[h] = l[h] * c + pr;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * c + pr * vf[e];
-        m[h] = mn;
-      }
-      kr = krn;
-      vr = vrn;
     }
   }
   // merge the 16 states (4 waves x 4 key groups) per head
@@ -245,21 +352,90 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       a1 += sm[i][h][d + 1] * f;
     }
   }
-  float *dst = part + ((((size_t)b * nkv + kvh) * nsplit + s) * AT_G + h) * (D + 2);
-  dst[d] = a0;
-  dst[d + 1] = a1;
-  if (d == 0) {
-    dst[D] = M;
-    dst[D + 1] = Ls;
+  const size_t sstride = (size_t)AT_G * (D + 2);
+  float *slots = part + ((size_t)b * nkv + kvh) * nsplit * sstride;
+  float *dst = slots + s * sstride + h * (D + 2);
+  if constexpr (!TICKET) {  // attn_combine_kernel follows
+    dst[d] = a0;
+    dst[d + 1] = a1;
+    if (d == 0) {
+      dst[D] = M;
+      dst[D + 1] = Ls;
+    }
+    return;
   }
+  st_agent(dst + d, a0);
+  st_agent(dst + d + 1, a1);
+  if (d == 0) {
+    st_agent(dst + D, M);
+    st_agent(dst + D + 1, Ls);
+  }
+  // every wave's slot stores have completed before the ticket is taken
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t *tk = tickets + (size_t)b * nkv + kvh;
+    const uint32_t n = __hip_atomic_fetch_add((gu32_t *)tk, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    s_last = n == (uint32_t)nsplit - 1u;
+    if (s_last) __hip_atomic_store((gu32_t *)tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // combine the splits: their m and l through LDS (loaded in parallel,
+  // agent scope: other workgroups stored them), then thread (head, d pair)
+  // sums its o over the splits, the loads of 16 splits in flight at a time
+  float(*lsh)[AC_MAXS] = reinterpret_cast<float(*)[AC_MAXS]>(&sm[0][0][0]);
+  for (int i = threadIdx.x; i < AT_G * nsplit; i += blockDim.x) {
+    const int hh = i % AT_G, ss = i / AT_G;
+    const float *ml = slots + ss * sstride + hh * (D + 2) + D;
+    const float mv = ld_agent(ml), lv = ld_agent(ml + 1);
+    wsh[hh][ss] = mv;
+    lsh[hh][ss] = lv;
+  }
+  __syncthreads();
+  if (threadIdx.x < AT_G) {
+    const int hh = threadIdx.x;
+    float MM = -INFINITY;
+    for (int ss = 0; ss < nsplit; ++ss) MM = fmaxf(MM, wsh[hh][ss]);
+    float LL = 0.0f;
+    for (int ss = 0; ss < nsplit; ++ss) {
+      const float ms = wsh[hh][ss];
+      const float f = ms == -INFINITY ? 0.0f : __expf(ms - MM);
+      LL += lsh[hh][ss] * f;
+      wsh[hh][ss] = f;
+    }
+    lsum[hh] = LL;
+  }
+  __syncthreads();
+  float c0 = 0.0f, c1 = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += 16) {
+    float v0[16], v1[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float *o_s = slots + min(s0 + j, nsplit - 1) * sstride + h * (D + 2);
+      v0[j] = ld_agent(o_s + d);
+      v1[j] = ld_agent(o_s + d + 1);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (s0 + j < nsplit) {
+        c0 += v0[j] * wsh[h][s0 + j];
+        c1 += v1[j] * wsh[h][s0 + j];
+      }
+    }
+  }
+  uint16_t *op = out + ((size_t)b * nq + kvh * AT_G + h) * D + d;
+  *reinterpret_cast<uint32_t *>(op) =
+      (uint32_t)f2h(c0 / lsum[h]) | ((uint32_t)f2h(c1 / lsum[h]) << 16);
 }
 
+// The split combine as its own launch (large grids, where holding every
+// attention workgroup through the ticket hand-off costs more than a launch):
 // out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.  One
 // workgroup per (row, kv head): the splits' m and l go through LDS (loaded in
 // parallel), then thread (head, d) sums its o over the splits, the loads
 // unrolled so that several are in flight.
-constexpr int AC_MAXS = 256;  // splits the combine takes
-
 __global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
     const float *__restrict__ part, int nq, int nkv, int nsplit, uint16_t *__restrict__ out) {
   constexpr int D = EXL3D_HEAD_DIM;
@@ -293,6 +469,7 @@ __global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
   out[((size_t)b * nq + kvh * AT_G + h) * D + d] = f2h(acc / lsum[h]);
 }
 
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ g,
                                                        const uint16_t *__restrict__ u,
                                                        uint16_t *__restrict__ out, size_t n) {
@@ -312,6 +489,40 @@ int attn_split(int Tmax, int B, int nkv, int *TS) {
     ts *= 2;
   *TS = ts;
   return (Tmax + ts - 1) / ts;
+}
+
+constexpr long ATTN_TICKET_MAX_WG = 512;
+
+size_t attn_slot_floats(int B, int nkv, int ns) {
+  return (size_t)B * nkv * ns * AT_G * (EXL3D_HEAD_DIM + 2);
+}
+
+int attn_launch(bool rope, const uint16_t *q, const RopeArgs &ra, uint16_t *kcache,
+                uint16_t *vcache, const int32_t *pos, int B, int nq, int nkv, int Tmax, float scale,
+                uint16_t *out, float *scratch, size_t scratch_bytes, hipStream_t s) {
+  if (B <= 0 || nkv <= 0 || nq != AT_G * nkv || B > 65535 || nkv > 65535 || Tmax <= 0)
+    return hipErrorInvalidValue;
+  if (scratch_bytes < exl3d_attn_scratch_bytes(B, nq, nkv, Tmax)) return hipErrorInvalidValue;
+  int ts;
+  const int ns = attn_split(Tmax, B, nkv, &ts);
+  uint32_t *tickets = reinterpret_cast<uint32_t *>(scratch + attn_slot_floats(B, nkv, ns));
+  // small grids (decode at batch 1) combine in the last split's workgroup;
+  // large ones (every workgroup would be held through the hand-off) in a
+  // second launch
+  const bool ticket = (long)ns * nkv * B <= ATTN_TICKET_MAX_WG;
+  const dim3 grid(ns, nkv, B);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, q, kcache, vcache, pos, nq, nkv, Tmax, ts,
+                       scale, ra, scratch, tickets, out);
+  };
+  if (rope)
+    ticket ? go(attn_decode_kernel<true, true>) : go(attn_decode_kernel<true, false>);
+  else
+    ticket ? go(attn_decode_kernel<false, true>) : go(attn_decode_kernel<false, false>);
+  if (!ticket)
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s,
+                       scratch, nq, nkv, ns, out);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -345,22 +556,26 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax) {
   int ts;
   const int ns = attn_split(Tmax, B, nkv, &ts);
-  return (size_t)B * nkv * ns * AT_G * (EXL3D_HEAD_DIM + 2) * sizeof(float);
+  return attn_slot_floats(B, nkv, ns) * sizeof(float) + (size_t)B * nkv * sizeof(uint32_t);
 }
 
 int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                       const int32_t *pos, int B, int nq, int nkv, int Tmax, float scale,
                       uint16_t *out, float *scratch, size_t scratch_bytes, hipStream_t s) {
-  if (B <= 0 || nkv <= 0 || nq != AT_G * nkv || B > 65535 || nkv > 65535)
-    return hipErrorInvalidValue;
-  if (scratch_bytes < exl3d_attn_scratch_bytes(B, nq, nkv, Tmax)) return hipErrorInvalidValue;
-  int ts;
-  const int ns = attn_split(Tmax, B, nkv, &ts);
-  hipLaunchKernelGGL(attn_decode_kernel, dim3(ns, nkv, B), dim3(256), 0, s, q, kcache, vcache,
-                     pos, nq, nkv, Tmax, ts, scale, scratch);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s, scratch,
-                     nq, nkv, ns, out);
-  return hipGetLastError();
+  // the caches are only read without ROPE
+  return attn_launch(false, q, RopeArgs{}, const_cast<uint16_t *>(kcache),
+                     const_cast<uint16_t *>(vcache), pos, B, nq, nkv, Tmax, scale, out, scratch,
+                     scratch_bytes, s);
+}
+
+int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           const uint16_t *qn, const uint16_t *kn, const int32_t *pos, int B,
+                           int nq, int nkv, float eps, float theta, uint16_t *kcache,
+                           uint16_t *vcache, int Tmax, float scale, uint16_t *out, float *scratch,
+                           size_t scratch_bytes, hipStream_t s) {
+  const RopeArgs ra{k, v, qn, kn, eps, theta};
+  return attn_launch(true, q, ra, kcache, vcache, pos, B, nq, nkv, Tmax, scale, out, scratch,
+                     scratch_bytes, s);
 }
 
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s) {

@@ -57,6 +57,9 @@ _DEC_SIGS = {
     "exl3d_attn_scratch_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "exl3d_attn_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                   c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "exl3d_attn_decode_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_int, c_int, c_int, c_float, c_float, c_void_p, c_void_p,
+                                       c_int, c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
     "exl3d_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 _dec = None
@@ -116,6 +119,17 @@ def attn_decode(q, kcache, vcache, pos, out, scratch, stream=None):
                                     1.0 / math.sqrt(HEAD_DIM), _p(out), _p(scratch),
                                     scratch.numel() * scratch.element_size(),
                                     X.stream_handle(stream)), "attn_decode")
+
+
+def attn_decode_rope(q, k, v, qn, kn, pos, kcache, vcache, out, scratch, eps, theta, stream=None):
+    """q/k norm + RoPE + KV append + attention in one launch (raw q, k, v)."""
+    B = q.shape[0]
+    nq, nkv, tmax = q.shape[1] // HEAD_DIM, kcache.shape[1], kcache.shape[2]
+    _ck(dec_lib().exl3d_attn_decode_rope(_p(q), _p(k), _p(v), _p(qn), _p(kn), _p(pos), B, nq, nkv,
+                                         eps, theta, _p(kcache), _p(vcache), tmax,
+                                         1.0 / math.sqrt(HEAD_DIM), _p(out), _p(scratch),
+                                         scratch.numel() * scratch.element_size(),
+                                         X.stream_handle(stream)), "attn_decode_rope")
 
 
 def silu_mul(g, u, out, stream=None):
@@ -182,7 +196,6 @@ class Qwen3Decoder:
         self.q = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
         self.k = torch.empty(B, cfg.kv_dim, dtype=f16, device=dev)
         self.v = torch.empty(B, cfg.kv_dim, dtype=f16, device=dev)
-        self.qr = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
         self.att = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
         self.o = torch.empty(B, H, dtype=f16, device=dev)
         self.g = torch.empty(B, cfg.inter, dtype=f16, device=dev)
@@ -191,7 +204,8 @@ class Qwen3Decoder:
         self.d = torch.empty(B, H, dtype=f16, device=dev)
         self.logits = torch.empty(B, cfg.vocab, dtype=f16, device=dev)
         nbytes = attn_scratch_bytes(B, cfg.heads, cfg.kv_heads, self.tmax)
-        self.scratch = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=dev)
+        # zeroed once: the attention leaves its arrival tickets zero
+        self.scratch = torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=dev)
         self.ids = torch.zeros(B, dtype=torch.int32, device=dev)
         self.pos = torch.full((B,), ctx, dtype=torch.int32, device=dev)
 
@@ -217,9 +231,8 @@ class Qwen3Decoder:
             add_rmsnorm(self.h, add, L["in_norm"], self.xn, c.eps, stream)
             X.matmul_shared([L["q"].weight, L["k"].weight, L["v"].weight], self.xn,
                             outs=[self.q, self.k, self.v], stream=stream)
-            qk_norm_rope(self.q, self.k, self.v, L["q_norm"], L["k_norm"], self.pos, self.qr, L["kc"],
-                         L["vc"], c.eps, c.theta, stream)
-            attn_decode(self.qr, L["kc"], L["vc"], self.pos, self.att, self.scratch, stream)
+            attn_decode_rope(self.q, self.k, self.v, L["q_norm"], L["k_norm"], self.pos, L["kc"],
+                             L["vc"], self.att, self.scratch, c.eps, c.theta, stream)
             L["o"](self.att, out=self.o, stream=stream)
             add_rmsnorm(self.h, self.o, L["post_norm"], self.xn, c.eps, stream)
             X.matmul_shared([L["gate"].weight, L["up"].weight], self.xn, outs=[self.g, self.u],

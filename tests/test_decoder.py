@@ -134,10 +134,55 @@ def test_attention_decode(B, T, lens):
     pos = torch.tensor(lens if lens else [int(x) for x in torch.randint(0, T, (B,), generator=g)],
                        dtype=torch.int32)
     out = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
-    scratch = torch.empty(Q.attn_scratch_bytes(B, nq, nkv, T) // 4 + 1, device="cuda")
-    Q.attn_decode(q.cuda(), kc.cuda(), vc.cuda(), pos.cuda(), out, scratch)
+    scratch = torch.zeros(Q.attn_scratch_bytes(B, nq, nkv, T) // 4 + 1, device="cuda")
     want = ref_attention(q, kc, vc, pos)
-    # f32 online softmax in another summation order, f16 output: 2e-3 relative
+    for _ in range(2):  # the second call reuses the scratch (its tickets were left zero)
+        out.fill_(float("nan"))
+        Q.attn_decode(q.cuda(), kc.cuda(), vc.cuda(), pos.cuda(), out, scratch)
+        # f32 online softmax in another summation order, f16 output: 2e-3 relative
+        assert rel(out.cpu(), want) < 2e-3, rel(out.cpu(), want)
+
+
+@gpu
+@pytest.mark.parametrize("B,T,lens", [(1, 80, [79]), (3, 2100, [2048, 5, 700]), (16, 300, None)])
+def test_attention_decode_with_rope_and_append(B, T, lens):
+    # q/k norm + RoPE + KV append + attention in one launch, against the
+    # float32 restatement of the two steps
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(30 + B)
+    nq, nkv = 32, 8
+    q = torch.randn(B, nq * 128, generator=g).half()
+    k = torch.randn(B, nkv * 128, generator=g).half()
+    v = torch.randn(B, nkv * 128, generator=g).half()
+    qn = (1 + 0.1 * torch.randn(128, generator=g)).half()
+    kn = (1 + 0.1 * torch.randn(128, generator=g)).half()
+    kc = torch.randn(B, nkv, T, 128, generator=g).half()
+    vc = torch.randn(B, nkv, T, 128, generator=g).half()
+    pos = torch.tensor(lens if lens else [int(x) for x in torch.randint(0, T, (B,), generator=g)],
+                       dtype=torch.int32)
+    kcd, vcd = kc.cuda(), vc.cuda()
+    out = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
+    scratch = torch.zeros(Q.attn_scratch_bytes(B, nq, nkv, T) // 4 + 1, device="cuda")
+    Q.attn_decode_rope(q.cuda(), k.cuda(), v.cuda(), qn.cuda(), kn.cuda(), pos.cuda(), kcd, vcd, out,
+                       scratch, 1e-6, 1e6)
+    wq = ref_qk_norm_rope(q.view(B, nq, 128), qn, pos, 1e-6, 1e6).view(B, -1)
+    wk = ref_qk_norm_rope(k.view(B, nkv, 128), kn, pos, 1e-6, 1e6)
+    kw, vw = kc.clone(), vc.clone()
+    for b in range(B):
+        kw[b, :, int(pos[b])] = wk[b]
+        vw[b, :, int(pos[b])] = v[b].view(nkv, 128)
+    kcc, vcc = kcd.cpu(), vcd.cpu()
+    # the appended key: f16 outputs of a float32 computation, 2e-3 relative;
+    # the value is copied; every other row is untouched
+    for b in range(B):
+        p = int(pos[b])
+        assert rel(kcc[b, :, p], wk[b]) < 2e-3
+        assert torch.equal(vcc[b, :, p], v[b].view(nkv, 128))
+        others = torch.ones(T, dtype=torch.bool)
+        others[p] = False
+        assert torch.equal(kcc[b, :, others], kc[b, :, others])
+        assert torch.equal(vcc[b, :, others], vc[b, :, others])
+    want = ref_attention(wq, kw, vw, pos)
     assert rel(out.cpu(), want) < 2e-3, rel(out.cpu(), want)
 
 
