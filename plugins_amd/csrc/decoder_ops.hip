@@ -216,6 +216,8 @@ struct RopeArgs {
 constexpr int AT_G = 4;  // query heads per kv head (Qwen3-8B: 32 / 8)
 constexpr int AC_MAXS = 256;  // splits
 constexpr int AT_KD = 4;  // key rows in flight per key group
+constexpr int AT_CB = 48;  // splits whose o pairs the combine loads at once
+static_assert(AT_G == 256 / 64, "the combine gives each head one wave of the workgroup");
 
 template <bool ROPE, bool TICKET>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
@@ -240,6 +242,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     unpack8(*reinterpret_cast<const uint4 *>(q + ((size_t)b * nq + kvh * AT_G + h) * D + 8 * li),
             qr[h]);
   const size_t kvbase = ((size_t)b * nkv + kvh) * Tmax;
+  auto ld = [&](const uint16_t *c, int t) {
+    return *reinterpret_cast<const uint4 *>(c + (kvbase + t) * D + 8 * li);
+  };
+  // The key group's keys t, t + 16, ...: AT_KD of them in flight (a split of
+  // 64 keys is loaded at once), each reloaded AT_KD keys ahead once used;
+  // keys past the split's end reload its last key (in bounds, unused).  The
+  // first ones go out at once, bounded by the cache's rows rather than by
+  // pos[b] (so they need not wait for it; rows past the split's end are
+  // loaded and not used), before the q/k prologue.
+  const int tg = t0 + 4 * wave + g;
+  uint4 kr[AT_KD], vr[AT_KD];
+#pragma unroll
+  for (int j = 0; j < AT_KD; ++j) {
+    kr[j] = ld(kcache, min(tg + 16 * j, Tmax - 1));
+    vr[j] = ld(vcache, min(tg + 16 * j, Tmax - 1));
+  }
   if constexpr (ROPE) {
     // angle of dim d: pos * theta^(-2 (d mod 64) / D), the 64 angles once
     // per workgroup (the argument reaches thousands of radians, where a sine
@@ -263,13 +281,24 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     if (s == p / TS) {
       float kx[8];
       unpack8(*reinterpret_cast<const uint4 *>(ra.k + ((size_t)b * nkv + kvh) * D + 8 * li), kx);
-      const uint4 vr = *reinterpret_cast<const uint4 *>(ra.v + ((size_t)b * nkv + kvh) * D + 8 * li);
+      const uint4 vnew =
+          *reinterpret_cast<const uint4 *>(ra.v + ((size_t)b * nkv + kvh) * D + 8 * li);
       norm_rope8(kx, *reinterpret_cast<const uint4 *>(ra.kn + 8 * li), sn, cs, li, ra.eps);
+      const uint4 knew = pack8(kx);
       if (wave == 0 && g == 0) {
-        *reinterpret_cast<uint4 *>(kcache + (kvbase + p) * D + 8 * li) = pack8(kx);
-        *reinterpret_cast<uint4 *>(vcache + (kvbase + p) * D + 8 * li) = vr;
+        *reinterpret_cast<uint4 *>(kcache + (kvbase + p) * D + 8 * li) = knew;
+        *reinterpret_cast<uint4 *>(vcache + (kvbase + p) * D + 8 * li) = vnew;
       }
-      __syncthreads();  // the key loop below reads row p
+      // row p in the ring was loaded before it was written: take it from
+      // registers; later reloads read it from the cache (after the barrier)
+#pragma unroll
+      for (int j = 0; j < AT_KD; ++j) {
+        if (tg + 16 * j == p) {
+          kr[j] = knew;
+          vr[j] = vnew;
+        }
+      }
+      __syncthreads();
     }
   }
 #pragma unroll
@@ -284,20 +313,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
   }
-  auto ld = [&](const uint16_t *c, int t) {
-    return *reinterpret_cast<const uint4 *>(c + (kvbase + t) * D + 8 * li);
-  };
-  // The key group's keys t, t + 16, ...: AT_KD of them in flight (a split of
-  // 64 keys is loaded at once), each reloaded AT_KD keys ahead once used;
-  // keys past the split's end reload its last key (in bounds, unused).
-  const int tg = t0 + 4 * wave + g;
   if (t0 < t1) {
-    uint4 kr[AT_KD], vr[AT_KD];
-#pragma unroll
-    for (int j = 0; j < AT_KD; ++j) {
-      kr[j] = ld(kcache, min(tg + 16 * j, t1 - 1));
-      vr[j] = ld(vcache, min(tg + 16 * j, t1 - 1));
-    }
     for (int tb = tg; tb < t1; tb += 16 * AT_KD) {
 #pragma unroll
       for (int j = 0; j < AT_KD; ++j) {
@@ -311,16 +327,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
           vr[j] = ld(vcache, tn);
 #pragma unroll
           for (int h = 0; h < AT_G; ++h) {
+            // fused multiply-adds (this op's own arithmetic, not the
+            // reference's rounding points)
             float sc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sc += qr[h][e] * kf[e];
+            for (int e = 0; e < 8; ++e) sc = fmaf(qr[h][e], kf[e], sc);
 #pragma unroll
             for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // 16 lanes
             const float mn = fmaxf(m[h], sc);
             const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
-            l[h] = l[h] * c + pr;
+            l[h] = fmaf(l[h], c, pr);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * c + pr * vf[e];
+            for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr, vf[e], o[h][e] * c);
             m[h] = mn;
           }
         }
@@ -382,10 +400,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
   __syncthreads();
   if (!s_last) return;
-  // combine the splits: their m and l through LDS (loaded in parallel,
-  // agent scope: other workgroups stored them), then thread (head, d pair)
-  // sums its o over the splits, the loads of 16 splits in flight at a time
+  // combine the splits (slots stored by other workgroups: agent-scope
+  // loads).  One round of loads: every thread's o pairs of the first
+  // AT_CB splits and the (m, l) pairs; then wave hh computes head hh's
+  // weights f_s = e^(m_s - M) and sum l_s f_s (lanes over the splits), and
+  // thread (head, d pair) sums o_s f_s in split order.
   float(*lsh)[AC_MAXS] = reinterpret_cast<float(*)[AC_MAXS]>(&sm[0][0][0]);
+  typedef __attribute__((address_space(1))) uint64_t gu64_t;
+  auto ld_pair = [&](int ss) {
+    const float *o_s = slots + ss * sstride + h * (D + 2) + d;
+    return __hip_atomic_load((gu64_t *)o_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  uint64_t ov[AT_CB];
+#pragma unroll
+  for (int j = 0; j < AT_CB; ++j) ov[j] = ld_pair(min(j, nsplit - 1));
   for (int i = threadIdx.x; i < AT_G * nsplit; i += blockDim.x) {
     const int hh = i % AT_G, ss = i / AT_G;
     const float *ml = slots + ss * sstride + hh * (D + 2) + D;
@@ -394,34 +422,35 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     lsh[hh][ss] = lv;
   }
   __syncthreads();
-  if (threadIdx.x < AT_G) {
-    const int hh = threadIdx.x;
+  {
+    const int hh = wave;  // AT_G == waves per workgroup
     float MM = -INFINITY;
-    for (int ss = 0; ss < nsplit; ++ss) MM = fmaxf(MM, wsh[hh][ss]);
+    for (int ss = lane; ss < nsplit; ss += 64) MM = fmaxf(MM, wsh[hh][ss]);
+#pragma unroll
+    for (int mk = 32; mk >= 1; mk >>= 1) MM = fmaxf(MM, __shfl_xor(MM, mk, 64));
     float LL = 0.0f;
-    for (int ss = 0; ss < nsplit; ++ss) {
+    for (int ss = lane; ss < nsplit; ss += 64) {
       const float ms = wsh[hh][ss];
       const float f = ms == -INFINITY ? 0.0f : __expf(ms - MM);
       LL += lsh[hh][ss] * f;
       wsh[hh][ss] = f;
     }
-    lsum[hh] = LL;
+    LL = wave_sum(LL);
+    if (lane == 0) lsum[hh] = LL;
   }
   __syncthreads();
   float c0 = 0.0f, c1 = 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += 16) {
-    float v0[16], v1[16];
+  for (int s0 = 0; s0 < nsplit; s0 += AT_CB) {
+    if (s0 > 0) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float *o_s = slots + min(s0 + j, nsplit - 1) * sstride + h * (D + 2);
-      v0[j] = ld_agent(o_s + d);
-      v1[j] = ld_agent(o_s + d + 1);
+      for (int j = 0; j < AT_CB; ++j) ov[j] = ld_pair(min(s0 + j, nsplit - 1));
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < AT_CB; ++j) {
       if (s0 + j < nsplit) {
-        c0 += v0[j] * wsh[h][s0 + j];
-        c1 += v1[j] * wsh[h][s0 + j];
+        const float f = wsh[h][s0 + j];
+        c0 += __builtin_bit_cast(float, (uint32_t)ov[j]) * f;
+        c1 += __builtin_bit_cast(float, (uint32_t)(ov[j] >> 32)) * f;
       }
     }
   }
