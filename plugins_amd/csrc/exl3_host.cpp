@@ -695,6 +695,37 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   if (pg->f.n != pu->f.n) return kRate;
   exl3_verdict v = output_for(out, x, hidden, rows);
   if (v.code != EXL3_OK) return v;
+  if (inds.data == nullptr && rows <= exl3::GEMV_ROWS_MAX && pg->f.codebook == pu->f.codebook &&
+      pg->f.window == pu->f.window) {
+    // Dense MLP at decode sizes: gate and up in one GEMV launch (f16), then
+    // the down GEMV with the SwiGLU applied as it prepares its rows (the MoE
+    // path's mid step, bit for bit): two launches (above 4 rows the SwiGLU
+    // runs once on its own first).
+    StreamScratch *ss = scratch_for(pg->device, s);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    const size_t nel = (size_t)rows * pg->out;
+    hipError_t e = grow(&ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s, -1);
+    if (e != hipSuccess) return hip_failed(e);
+    uint16_t *gu = (uint16_t *)ss->moe;
+    const exl3_weight *ws2[2] = {gate, up};
+    const WeightPriv *pv2[2] = {pg, pu};
+    void *ys[2] = {gu, gu + nel};
+    e = run_linears(ws2, pv2, 2, x.data, xdt, false, ys, exl3::ACT_F16, nullptr, rows, ss, s);
+    if (e != hipSuccess) return hip_failed(e);
+    const int outs[1] = {(int)hidden};
+    exl3::Scratch sc;
+    e = gemv_scratch(ss, outs, 1, (int)pd->in, (int)rows, !pd->f.integer_rate(), &sc, s);
+    if (e != hipSuccess) return hip_failed(e);
+    const exl3::GemvLinear l{(const uint16_t *)down->w.data, (const uint16_t *)down->scales.data,
+                             (const uint16_t *)down->biases.data, out->data, nullptr, (int)hidden};
+    e = exl3::launch_gemv_swiglu(l, pd->f, gu, gu + nel, gu + 2 * nel, (float)opts->limit, xdt,
+                                 (int)rows, (int)pd->in, sc, s);
+    if (e != hipSuccess) {
+      if (e == hipErrorInvalidValue) return kShape;
+      return hip_failed(e);
+    }
+    return ok();
+  }
   a.y = out->data;
   a.ydt = xdt;
   exl3::MoeBank bg{(const uint16_t *)gate->w.data, (const uint16_t *)gate->scales.data,

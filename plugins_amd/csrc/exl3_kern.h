@@ -115,8 +115,30 @@ struct GemvCfg {
   int ydt;
   int ksplit;
   uint32_t mask;
-  int nw;  // trellis dwords per tile (n / 2)
+  int nw;               // trellis dwords per tile (n / 2)
+  const uint16_t *x2;   // SwiGLU prologue: up (f16, the layout of x = gate)
+  float limit;          // ... and its clamp (0: none)
 };
+
+// The SwiGLU of one element pair of gate (g) and up (u), f16 bits: the MoE
+// mid step's arithmetic (turboexl3_ds41/src/exl3/kernels/exl3/
+// q3_exl3_prep_gu_epi.metal:47-56 for the clamp): h = f16(silu(g) * u),
+// silu(g) = g / (1 + e^-g) in f32, with gate clamped to <= limit and up to
+// [-limit, limit] when limit > 0.
+__device__ __forceinline__ float swiglu1(uint16_t gb, uint16_t ub, float limit) {
+  float gv = h2f(gb), uv = h2f(ub);
+  if (limit > 0.0f) {
+    gv = gv < limit ? gv : limit;
+    uv = uv > -limit ? uv : -limit;
+    uv = uv < limit ? uv : limit;
+  }
+  return h2f(f2h(f32_value(gv / (1.0f + expf(-gv))) * uv));
+}
+__device__ __forceinline__ void swiglu_unpack(uint32_t g2, uint32_t u2, float limit, float &a,
+                                              float &b) {
+  a = swiglu1((uint16_t)(g2 & 0xFFFFu), (uint16_t)(u2 & 0xFFFFu), limit);
+  b = swiglu1((uint16_t)(g2 >> 16), (uint16_t)(u2 >> 16), limit);
+}
 
 struct GemvArgs {
   GemvCfg c;
@@ -234,6 +256,20 @@ __device__ __forceinline__ void gemv_prep_load_su(const void *x, int prepared, c
   }
 }
 
+// SwiGLU prologue: the up pair of every item into x1 (gate is x, loaded by
+// gemv_prep_load_x as f16).
+__device__ __forceinline__ void gemv_prep_load_up(const uint16_t *x2, const RowMap &rm,
+                                                  int nitems, int nb, int tk0, int base, int wave,
+                                                  int lane, PrepRegs &r) {
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
+    const int row = it / nb, blk = it - row * nb;
+    const int k = tk0 * 16 + blk * 128 + 2 * lane;
+    r.x1[j] = ld_global_u32(x2 + (size_t)rm.in_off(row) + k);
+  }
+}
+
 // Element i of a 128-block sits in lane i/2, register i%2: the butterfly's
 // stage on index bit 0 is in-register, bits 1..6 exchange across lanes; each
 // stage is (lo + hi, lo - hi), in bit order, as the reference's kernels
@@ -255,9 +291,10 @@ __device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
 // Stores the prepared pairs; with hsum (row stride nb * 2) also the sum of
 // each 64 prepared elements (lanes 0-31 and 32-63 of an item), added in a
 // fixed butterfly order.
+template <bool SWI = false>
 __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitems, int nb,
                                                 int base, int wave, int lane, uint16_t *xs, int kr,
-                                                const PrepRegs &r, float *hsum) {
+                                                const PrepRegs &r, float *hsum, float limit = 0.0f) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
@@ -267,7 +304,10 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
     // (expert_exl3.zig:490-501); prepared rows are taken as they are (the
     // rotation is formed regardless and not used: no branch)
     float x0, x1;
-    prep_unpack(r.x0[j], r.x1[j], xdt, x0, x1);
+    if constexpr (SWI)
+      swiglu_unpack(r.x0[j], r.x1[j], limit, x0, x1);  // x0: gate pair, x1: up pair
+    else
+      prep_unpack(r.x0[j], r.x1[j], xdt, x0, x1);
     float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
     float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
     had128_pair(v0, v1, lane);
@@ -328,9 +368,23 @@ __device__ __forceinline__ void gemv_rows_load_su(const void *x, int prepared, c
   }
 }
 
+// SwiGLU prologue (rows form): the up pieces into x[p][1].
+__device__ __forceinline__ void gemv_rows_load_up(const uint16_t *x2, const RowMap &rm, int nblk,
+                                                  int nb, int tk0, RowsRegs &r) {
+  const int li = threadIdx.x & 15;
+#pragma unroll
+  for (int p = 0; p < PREP_PASSES; ++p) {
+    const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
+    const int row = G / nb, blk = G - row * nb;
+    r.x[p][1] = *(const __attribute__((address_space(1))) u4_t *)(x2 + (size_t)rm.in_off(row) +
+                                                                  tk0 * 16 + blk * 128 + 8 * li);
+  }
+}
+
+template <bool SWI = false>
 __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk, int nb,
                                                 uint16_t *xs, int kr, const RowsRegs &r,
-                                                float *hsum) {
+                                                float *hsum, float limit = 0.0f) {
   const int li = threadIdx.x & 15, lane = threadIdx.x & 63;
 #pragma unroll
   for (int p = 0; p < PREP_PASSES; ++p) {
@@ -340,12 +394,16 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float a, b;
-      prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
-      const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
-      const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
-      if (!prepared && xdt == OUT_F32) {
-        a = fa;
-        b = fb;
+      if constexpr (SWI) {
+        swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
+      } else {
+        prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
+        const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
+        const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
+        if (!prepared && xdt == OUT_F32) {
+          a = fa;
+          b = fb;
+        }
       }
       const uint32_t su = r.su[p][e];
       v[2 * e] = h2f(f2h(a)) * h2f((uint16_t)(su & 0xFFFFu));
@@ -516,7 +574,7 @@ __device__ __forceinline__ void gemv_finish(float *zf, int ydt, void *y, uint16_
 // words `twe` (that expert's) and out_tiles output tiles, nrows <= 16 rows
 // (row map rm), column group cg, split ks.  ONEB: the rows' items fit one
 // prepare batch (nrows * tps / 8 <= PREP_ITEMS).
-template <int K, int CB, bool MASKED, bool ONEB>
+template <int K, int CB, bool MASKED, bool ONEB, bool SWI = false>
 __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, const void *x,
                                         const GemvGeo &geo, const GemvCfg &a,
                                         const GemvWeight &W, int expert, int nrows,
@@ -583,6 +641,15 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
   else
     gemv_rows_load_su(x, geo.prepared, suh, nitems, nb, tk0, rr);
+  if constexpr (SWI) {
+    // SwiGLU prologue: x is gate; up from the argument segment, like suh
+    const uint16_t *up = a.x2;
+    asm volatile("" : "+s"(up)::"memory");
+    if constexpr (ONEB)
+      gemv_prep_load_up(up, rm, nitems, nb, tk0, 0, wave, lane, pr);
+    else
+      gemv_rows_load_up(up, rm, nitems, nb, tk0, rr);
+  }
   if constexpr (K > 0) {
 #pragma unroll
     for (int b = 1; b < NBUF; ++b) {
@@ -596,10 +663,11 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   const uint16_t *svp = W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : suh;
   const uint32_t sv = ld_global_u32(svp + 2 * lane);
   if constexpr (ONEB)
-    gemv_prep_store(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
-                    FOLD ? hsum : nullptr);
+    gemv_prep_store<SWI>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
+                         FOLD ? hsum : nullptr, a.limit);
   else
-    gemv_rows_store(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr);
+    gemv_rows_store<SWI>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr,
+                         a.limit);
   lds_barrier();
 
   const int arow = min(lane & 15, nrows - 1);
@@ -717,7 +785,7 @@ __device__ __forceinline__ WeightSpan gemv_weight_of(int gx, int cg1, int cg2, i
 
 // Dense GEMV over up to four weights: the trellis pointers, the activations
 // and the geometry are the first kernel arguments (preloaded SGPRs).
-template <int K, int CB, bool MASKED, bool ONEB>
+template <int K, int CB, bool MASKED, bool ONEB, bool SWI>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
     const uint32_t *tw0, const uint32_t *tw1, const uint32_t *tw2, const uint32_t *tw3,
     const void *x, uint32_t g0, uint32_t g1, uint32_t g2, GemvArgs a) {
@@ -727,7 +795,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
   const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
   const int out_tiles = 8 * (ws.c1 - ws.c0);
   const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
-  gemv_wg<K, CB, MASKED, ONEB>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
+  gemv_wg<K, CB, MASKED, ONEB, SWI>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
                                blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
 }
 
@@ -1153,11 +1221,16 @@ void gemv_go(const Format &f, bool oneb, dim3 grid, size_t lds, hipStream_t s,
              const uint32_t *const *tw, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
              const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
+  // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up)
   auto go = [&](auto CBC, auto MC, auto OC) {
     constexpr int CB = decltype(CBC)::value;
     constexpr bool M = decltype(MC)::value, O = decltype(OC)::value;
-    hipLaunchKernelGGL((gemv_kernel<K, CB, M, O>), grid, blk, lds, s, tw[0], tw[1], tw[2], tw[3], x,
-                       g0, g1, g2, a);
+    if (a.c.x2 != nullptr)
+      hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, true>), grid, blk, lds, s, tw[0], tw[1], tw[2],
+                         tw[3], x, g0, g1, g2, a);
+    else
+      hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, false>), grid, blk, lds, s, tw[0], tw[1], tw[2],
+                         tw[3], x, g0, g1, g2, a);
   };
   using T = std::true_type;
   using F = std::false_type;

@@ -70,6 +70,15 @@ struct GemvLinear {
 hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
                              hipStream_t s);
+// The down projection of a dense SwiGLU MLP: y = (silu(g) * u) @ W^T, the
+// SwiGLU with the MoE mid step's arithmetic (clamped by limit > 0); g, u f16
+// [rows, in].  Up to SWIGLU_PROLOGUE_ROWS rows the GEMV applies it as it
+// prepares its rows (one launch); more rows go through h (f16 [rows, in],
+// caller's scratch) first.
+constexpr int SWIGLU_PROLOGUE_ROWS = 4;
+hipError_t launch_gemv_swiglu(const GemvLinear &l, const Format &f, const uint16_t *g,
+                              const uint16_t *u, uint16_t *h, float limit, int ydt, int rows,
+                              int in, Scratch &sc, hipStream_t s);
 // GEMM (any rows): the same contract through LDS-staged decode and MFMA.
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,

@@ -243,9 +243,9 @@ static void rate_dispatch(int kk, F &&launch) {
   }
 }
 
-hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
+static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
-                             hipStream_t s) {
+                             const uint16_t *x2, float limit, hipStream_t s) {
   if (count < 1 || count > GEMV_MAXW || rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
   if (in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
   if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
@@ -287,6 +287,8 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   a.c.ksplit = ksplit;
   a.c.mask = f.mask();
   a.c.nw = f.n / 2;
+  a.c.x2 = x2;
+  a.c.limit = limit;
   GemvGeo geo{};
   geo.cg1 = cgs[1];
   geo.cg2 = cgs[2];
@@ -306,6 +308,40 @@ hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     gemv_go<decltype(KC)::value>(f, oneb, grid, lds, s, tw, x, g0, g1, g2, a);
   });
   return hipGetLastError();
+}
+
+hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
+                             int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
+                             hipStream_t s) {
+  return gemv_multi(ls, count, f, x, xdt, prepared, ydt, rows, in, sc, nullptr, 0.0f, s);
+}
+
+namespace {
+// h = f16(silu(g) * u) elementwise (the prologue's arithmetic, swiglu1).
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ g,
+                                                     const uint16_t *__restrict__ u,
+                                                     uint16_t *__restrict__ h, size_t n,
+                                                     float limit) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    h[i] = f2h(swiglu1(g[i], u[i], limit));
+}
+}  // namespace
+
+hipError_t launch_gemv_swiglu(const GemvLinear &l, const Format &f, const uint16_t *g,
+                              const uint16_t *u, uint16_t *h, float limit, int ydt, int rows,
+                              int in, Scratch &sc, hipStream_t s) {
+  if (g == nullptr || u == nullptr || !(limit >= 0.0f)) return hipErrorInvalidValue;
+  if (rows <= SWIGLU_PROLOGUE_ROWS)
+    return gemv_multi(&l, 1, f, g, OUT_F16, false, ydt, rows, in, &sc, u, limit, s);
+  // more rows: every column group would redo the rows' SwiGLU, so it runs
+  // once here
+  if (h == nullptr) return hipErrorInvalidValue;
+  const size_t n = (size_t)rows * in;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, u, h, n, limit);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return gemv_multi(&l, 1, f, h, OUT_F16, false, ydt, rows, in, &sc, nullptr, 0.0f, s);
 }
 
 hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,

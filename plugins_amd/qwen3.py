@@ -10,8 +10,8 @@ model.zig; paths relative to /root/reference/plugins/), its linears through the
 quant table this library exports.
 
 Every operation runs in libexl3_mi355x.so: the linears through the EXL3 entries
-(q, k, v and gate, up as shared-input launches), the rest through the
-exl3d_* harness entries (include/exl3_decoder.h).  PyTorch only allocates the
+(q, k, v as one shared-input launch; the MLP through the dense swiglu entry),
+the rest through the exl3d_* harness entries (include/exl3_decoder.h).  PyTorch only allocates the
 buffers and supplies the stream.
 """
 from __future__ import annotations
@@ -198,9 +198,6 @@ class Qwen3Decoder:
         self.v = torch.empty(B, cfg.kv_dim, dtype=f16, device=dev)
         self.att = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
         self.o = torch.empty(B, H, dtype=f16, device=dev)
-        self.g = torch.empty(B, cfg.inter, dtype=f16, device=dev)
-        self.u = torch.empty(B, cfg.inter, dtype=f16, device=dev)
-        self.hm = torch.empty(B, cfg.inter, dtype=f16, device=dev)
         self.d = torch.empty(B, H, dtype=f16, device=dev)
         self.logits = torch.empty(B, cfg.vocab, dtype=f16, device=dev)
         nbytes = attn_scratch_bytes(B, cfg.heads, cfg.kv_heads, self.tmax)
@@ -235,10 +232,10 @@ class Qwen3Decoder:
                              L["vc"], self.att, self.scratch, c.eps, c.theta, stream)
             L["o"](self.att, out=self.o, stream=stream)
             add_rmsnorm(self.h, self.o, L["post_norm"], self.xn, c.eps, stream)
-            X.matmul_shared([L["gate"].weight, L["up"].weight], self.xn, outs=[self.g, self.u],
-                            stream=stream)
-            silu_mul(self.g, self.u, self.hm, stream)
-            L["down"](self.hm, out=self.d, stream=stream)
+            # the dense SwiGLU MLP entry (QuantTable.swiglu without routes):
+            # gate+up in one launch, down with the SwiGLU in its prepare
+            X.swiglu(L["gate"].weight, L["up"].weight, L["down"].weight, self.xn, out=self.d,
+                     stream=stream)
             add = self.d
         add_rmsnorm(self.h, add, self.final_norm, self.xn, c.eps, stream)
         self.lm_head(self.xn, out=self.logits, stream=stream)

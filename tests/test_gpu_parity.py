@@ -309,6 +309,46 @@ def test_swiglu_routed_against_oracle(rows, limit):
     assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
 
 
+@pytest.mark.parametrize("rows,limit,n,dtype", [(1, 0, 64, "f16"), (3, 7, 48, "f16"),
+                                                (16, 0, 64, "f16"), (2, 0, 64, "bf16"),
+                                                (5, 3, 32, "f32"), (24, 0, 64, "f16")])
+def test_swiglu_dense_decode_sizes(rows, limit, n, dtype):
+    # the dense MLP (inds empty): up to 16 rows take gate+up in one GEMV and
+    # the down GEMV with the SwiGLU in its prepare; 24 rows take the routed
+    # path's kernels; both against the oracle's composition (clamp included)
+    rng = np.random.default_rng(700 + rows + limit)
+    hidden, inter = 512, 1024
+    tg, sg, vg = S.linear(rng, hidden, inter, n)
+    tu, su, vu = S.linear(rng, hidden, inter, n)
+    td, sd, vd = S.linear(rng, inter, hidden, n)
+    G = X.Linear(dev_u16(tg), dev_f16(sg), dev_f16(vg))
+    U = X.Linear(dev_u16(tu), dev_f16(su), dev_f16(vu))
+    D = X.Linear(dev_u16(td), dev_f16(sd), dev_f16(vd))
+    x = S.activations(rng, rows, hidden)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    xd = torch.from_numpy(x.astype(np.float32)).to(DEV).to(tdt)
+    y = X.swiglu(G.weight, U.weight, D.weight, xd, limit=limit)
+    assert y.dtype == tdt and y.shape == (rows, hidden)
+    want = O.moe_swiglu(xd.float().cpu().numpy(), (tg[None], sg[None], vg[None]),
+                        (tu[None], su[None], vu[None]), (td[None], sd[None], vd[None]),
+                        np.zeros((rows, 1), np.int32), np.ones((rows, 1), np.float32), hidden,
+                        inter, n, limit=float(limit))
+    got = y.float().cpu().numpy()
+    if dtype == "bf16":
+        # f16 result then bf16: three chained linears' f16 roundings (in
+        # another summation order) move elements by a few f16 ulps, which can
+        # cross bf16 rounding boundaries, so each element is within two bf16
+        # ulps plus 4e-3 of the rms of the oracle's value in bf16, and the
+        # whole within 4e-3 (the bf16 output's own rounding is 2^-9 relative)
+        wb = torch.from_numpy(want).to(tdt).float().numpy()
+        ulp = np.spacing(np.abs(wb)).astype(np.float64) * 2.0**16
+        slack = 4e-3 * np.sqrt(np.mean(wb.astype(np.float64) ** 2))
+        assert (np.abs(got - wb) - 2 * ulp - slack).max() <= 0
+        assert S.rel_fro(got, want) < 4e-3
+    else:
+        assert S.rel_fro(got, want) < 1e-3
+
+
 def test_swiglu_dense_shared_expert():
     rng = np.random.default_rng(31)
     hidden, inter, n = 256, 256, 64
