@@ -16,6 +16,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "exl3_mi355x.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -23,8 +25,11 @@ extern "C" {
 /* Head dimension the attention kernels are built for (Qwen3-8B: 128). */
 #define EXL3D_HEAD_DIM 128
 
-/* h[b][:] = f32(table[ids[b]][:]); table f16 [vocab][H], h f32 [B][H]. */
-int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *h, hipStream_t s);
+/* h[b][:] = f32(table[ids[b]][:]); table f16 [vocab][H], h f32 [B][H]; with
+ * ssq (H a multiple of 128) also ssq[b][g] = sum of h^2 over columns 128 g ..
+ * 128 g + 127 (the input of exl3d_linears' RMSNorm). */
+int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *h, float *ssq,
+                hipStream_t s);
 
 /* h += add (f16 [B][H], may be NULL); out = f16(h * rsqrt(mean(h^2) + eps) * w). */
 int exl3d_add_rmsnorm(float *h, const uint16_t *add, const uint16_t *w, uint16_t *out, int B,
@@ -61,6 +66,23 @@ int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t 
                            int nq, int nkv, float eps, float theta, uint16_t *kcache,
                            uint16_t *vcache, int Tmax, float scale, uint16_t *out, float *scratch,
                            size_t scratch_bytes, hipStream_t s);
+
+/* The decode step's EXL3 linears with their neighbours fused in, B <= 16
+ * rows: outs[i] = x @ W_i^T (f16) for the count weights (as
+ * exl3_matmul_shared), where x is
+ *  - with norm_w: the RMSNorm of the f32 residual h = x [B][in],
+ *    f16(h * rsqrt(sum_g nssq[b][g] / in + eps) * norm_w), nssq [B][in/128]
+ *    its sums of squares per 128 columns (in <= 8192; rows that fit one
+ *    prepare batch, e.g. B = 1 at in = 4096);
+ *  - with up (f16 [B][in]): f16(silu(x) * up), x the gate (f16);
+ *  - else x itself (f16);
+ * and, with res (count 1): res [B][out] += f32(y) instead of storing
+ * outs[0] (outs may be NULL), and res_ssq [B][out/128] = the new res's sums
+ * of squares per 128 columns.  Returns 0, a HIP error, or -1 when the
+ * weights or shapes are refused. */
+int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
+                  const uint16_t *norm_w, const float *nssq, float eps, const uint16_t *up,
+                  float *res, float *res_ssq, uint16_t *const *outs, hipStream_t s);
 
 /* out = f16(silu(g) * u), n elements. */
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s);

@@ -37,6 +37,27 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t *__restrict__ 
     h[(size_t)b * H + i] = h2f(table[row * H + i]);
 }
 
+// h[b] = f32(table[ids[b]]) with the row's sums of squares per 128 columns
+// (the RMSNorm prologue's input): one wave per (row, 128 columns), lane l
+// columns 2 l, 2 l + 1, the pair's squares summed over the lanes pairwise.
+__global__ __launch_bounds__(64) void embed_ssq_kernel(const int32_t *__restrict__ ids,
+                                                       const uint16_t *__restrict__ table, int H,
+                                                       float *__restrict__ h,
+                                                       float *__restrict__ ssq) {
+  const int blk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const size_t row = (size_t)ids[b];
+  const int i = blk * 128 + 2 * lane;
+  const uint32_t t2 = *reinterpret_cast<const uint32_t *>(table + row * H + i);
+  float2 v;
+  v.x = h2f((uint16_t)(t2 & 0xFFFFu));
+  v.y = h2f((uint16_t)(t2 >> 16));
+  *reinterpret_cast<float2 *>(h + (size_t)b * H + i) = v;
+  float ss = v.x * v.x + v.y * v.y;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+  if (lane == 0) ssq[(size_t)b * (H / 128) + blk] = ss;
+}
+
 // h += add (f16, optional); out = f16(h * rsqrt(mean(h^2) + eps) * w).
 // One workgroup of 512 threads per row; each thread loads its 8-element
 // pieces (two float4 of h, 16 bytes of add and of w) before any arithmetic,
@@ -558,10 +579,15 @@ int attn_launch(bool rope, const uint16_t *q, const RopeArgs &ra, uint16_t *kcac
 
 extern "C" {
 
-int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *h,
+int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *h, float *ssq,
                 hipStream_t s) {
   if (B <= 0 || H <= 0 || B > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256, B), dim3(256), 0, s, ids, table, H, h);
+  if (ssq != nullptr) {
+    if (H % 128 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_ssq_kernel, dim3(H / 128, B), dim3(64), 0, s, ids, table, H, h, ssq);
+  } else {
+    hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256, B), dim3(256), 0, s, ids, table, H, h);
+  }
   return hipGetLastError();
 }
 

@@ -19,6 +19,7 @@
 #include <utility>
 #include <vector>
 
+#include "../../include/exl3_decoder.h"
 #include "../../include/exl3_mi355x.h"
 #include "exl3_json.h"
 #include "exl3_kernels.h"
@@ -862,3 +863,76 @@ static const exl3_quant_table kTable = {
 const exl3_quant_table *exl3_quant_table_get(void) { return &kTable; }
 
 }  // extern "C"
+
+// ------------------------------------------------ decode-step fused linears
+
+int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
+                  const uint16_t *norm_w, const float *nssq, float eps, const uint16_t *up,
+                  float *res, float *res_ssq, uint16_t *const *outs, hipStream_t s) {
+  if (!ws || !x || count < 1 || count > 4 || B < 1 || B > exl3::GEMV_ROWS_MAX) return -1;
+  if ((norm_w != nullptr) != (nssq != nullptr) || (norm_w && up)) return -1;
+  if (res && (count != 1 || !res_ssq)) return -1;
+  const WeightPriv *pvs[4];
+  for (int i = 0; i < count; ++i) {
+    pvs[i] = priv_of(ws[i]);
+    if (!pvs[i] || pvs[i]->experts != 0) return -1;
+    if (pvs[i]->in != pvs[0]->in || pvs[i]->f.n != pvs[0]->f.n ||
+        pvs[i]->f.codebook != pvs[0]->f.codebook || pvs[i]->f.window != pvs[0]->f.window ||
+        pvs[i]->device != pvs[0]->device)
+      return -1;
+    if (!res && (!outs || !outs[i])) return -1;
+  }
+  if (hipSetDevice(pvs[0]->device) != hipSuccess) return hipErrorInvalidDevice;
+  const int in = (int)pvs[0]->in;
+  StreamScratch *ss = scratch_for(pvs[0]->device, s);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  int wouts[4];
+  exl3::GemvLinear ls[4];
+  for (int i = 0; i < count; ++i) {
+    wouts[i] = (int)pvs[i]->out;
+    ls[i].trellis = (const uint16_t *)ws[i]->w.data;
+    ls[i].suh = (const uint16_t *)ws[i]->scales.data;
+    ls[i].svh = (const uint16_t *)ws[i]->biases.data;
+    ls[i].y = outs ? outs[i] : nullptr;
+    ls[i].zout = nullptr;
+    ls[i].out = wouts[i];
+  }
+  exl3::Scratch sc[4];
+  hipError_t e = gemv_scratch(ss, wouts, count, in, B, !pvs[0]->f.integer_rate(), sc, s);
+  if (e != hipSuccess) return e;
+  exl3::GemvFuse fz;
+  fz.up = up;
+  fz.nssq = nssq;
+  fz.norm_w = norm_w;
+  fz.eps = eps;
+  fz.res = res;
+  fz.res_ssq = res_ssq;
+  int xdt = norm_w ? exl3::ACT_F32 : exl3::ACT_F16;
+  int total = 0;
+  for (int i = 0; i < count; ++i) total += wouts[i];
+  const bool pre_norm = norm_w && (!exl3::gemv_one_batch(in, total, !pvs[0]->f.integer_rate(), B) ||
+                                   in / 128 > exl3::NORM_MAXBLK);
+  const bool pre_swiglu = up && B > exl3::SWIGLU_PROLOGUE_ROWS;
+  if (pre_norm || pre_swiglu) {
+    // rows the prologue does not take: the RMSNorm (of h as it stands) or
+    // the SwiGLU first, into scratch, then a plain GEMV
+    e = grow(&ss->xp, &ss->xp_bytes, (size_t)B * in * sizeof(uint16_t), s, -1);
+    if (e != hipSuccess) return e;
+    uint16_t *xs = (uint16_t *)ss->xp;
+    if (pre_norm) {
+      const int r = exl3d_add_rmsnorm((float *)x, nullptr, norm_w, xs, B, in, eps, s);
+      if (r != 0) return r;
+      fz.nssq = nullptr;
+      fz.norm_w = nullptr;
+    } else {
+      e = exl3::launch_swiglu((const uint16_t *)x, up, xs, (size_t)B * in, 0.0f, s);
+      if (e != hipSuccess) return e;
+      fz.up = nullptr;
+    }
+    x = xs;
+    xdt = exl3::ACT_F16;
+  }
+  e = exl3::launch_gemv_fused(ls, count, pvs[0]->f, x, xdt, exl3::ACT_F16, B, in, sc, fz, s);
+  if (e == hipErrorInvalidValue) return -1;
+  return e;
+}

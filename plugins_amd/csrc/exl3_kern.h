@@ -118,7 +118,22 @@ struct GemvCfg {
   int nw;               // trellis dwords per tile (n / 2)
   const uint16_t *x2;   // SwiGLU prologue: up (f16, the layout of x = gate)
   float limit;          // ... and its clamp (0: none)
+  // RMSNorm prologue: x is the f32 residual h [rows][in]; nssq [rows][in /
+  // 128] its sums of squares per 128 columns; x = f16(h * r * nw), r =
+  // rsqrt(sum / in + eps)
+  const float *nssq;
+  const uint16_t *nw_norm;
+  float eps;
+  // residual finish (res set): res[row][col] += f32(y) instead of storing y,
+  // and res_ssq[row][group] = the group's sum of squares of the new res
+  float *res;
+  float *res_ssq;
 };
+
+// Prologue forms of the GEMV prepare (compile time: they decide which loads
+// a workgroup issues at its start).
+constexpr int PRO_PLAIN = 0, PRO_SWIGLU = 1, PRO_RMSNORM = 2;
+
 
 // The SwiGLU of one element pair of gate (g) and up (u), f16 bits: the MoE
 // mid step's arithmetic (turboexl3_ds41/src/exl3/kernels/exl3/
@@ -203,7 +218,35 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 // for f32), su the two suh values.
 struct PrepRegs {
   uint32_t x0[PREP_BATCH], x1[PREP_BATCH], su[PREP_BATCH];
+  uint32_t nw[PREP_BATCH];  // RMSNorm: weights of the pair
+  float nt[PREP_BATCH];     // ... and the row's partial sums of squares
 };
+
+// RMSNorm prologue: the item's norm-weight pair and the lane's share of its
+// row's partial sums (nssq[row][lane], 0 past the row's groups).
+__device__ __forceinline__ void gemv_prep_load_norm(const GemvCfg &a, const RowMap &rm,
+                                                    int nitems, int nb, int tk0, int in, int base,
+                                                    int wave, int lane, PrepRegs &r) {
+  const uint16_t *nwp = a.nw_norm;
+  const float *ssq = a.nssq;
+  asm volatile("" : "+s"(nwp), "+s"(ssq)::"memory");
+  const int ng = in >> 7;
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
+    const int row = it / nb, blk = it - row * nb;
+    const int k = tk0 * 16 + blk * 128 + 2 * lane;
+    r.nw[j] = *(const __attribute__((address_space(1))) uint32_t *)(nwp + k);
+    const float t = *(const __attribute__((address_space(1))) float *)(ssq + (size_t)row * ng +
+                                                                          min(lane, ng - 1));
+    r.nt[j] = lane < ng ? t : 0.0f;
+  }
+}
+__device__ __forceinline__ float norm_scale(float part, int in, float eps) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+  return rsqrtf(part / (float)in + eps);
+}
 
 // Branch-free: all three readings are formed and one is selected, so no
 // control flow joins while the weight loads are in flight.
@@ -291,10 +334,11 @@ __device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
 // Stores the prepared pairs; with hsum (row stride nb * 2) also the sum of
 // each 64 prepared elements (lanes 0-31 and 32-63 of an item), added in a
 // fixed butterfly order.
-template <bool SWI = false>
+template <int PRO = PRO_PLAIN>
 __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitems, int nb,
                                                 int base, int wave, int lane, uint16_t *xs, int kr,
-                                                const PrepRegs &r, float *hsum, float limit = 0.0f) {
+                                                const PrepRegs &r, float *hsum, float limit = 0.0f,
+                                                int in = 0, float eps = 0.0f) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
@@ -304,10 +348,16 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
     // (expert_exl3.zig:490-501); prepared rows are taken as they are (the
     // rotation is formed regardless and not used: no branch)
     float x0, x1;
-    if constexpr (SWI)
+    if constexpr (PRO == PRO_SWIGLU) {
       swiglu_unpack(r.x0[j], r.x1[j], limit, x0, x1);  // x0: gate pair, x1: up pair
-    else
+    } else if constexpr (PRO == PRO_RMSNORM) {
+      // the residual pair (f32) normalized: f16(h * r * w)
+      const float rs = norm_scale(r.nt[j], in, eps);
+      x0 = h2f(f2h(bits<float>(r.x0[j]) * rs * h2f((uint16_t)(r.nw[j] & 0xFFFFu))));
+      x1 = h2f(f2h(bits<float>(r.x1[j]) * rs * h2f((uint16_t)(r.nw[j] >> 16))));
+    } else {
       prep_unpack(r.x0[j], r.x1[j], xdt, x0, x1);
+    }
     float v0 = h2f(f2h(x0)) * h2f((uint16_t)(r.su[j] & 0xFFFFu));
     float v1 = h2f(f2h(x1)) * h2f((uint16_t)(r.su[j] >> 16));
     had128_pair(v0, v1, lane);
@@ -381,7 +431,7 @@ __device__ __forceinline__ void gemv_rows_load_up(const uint16_t *x2, const RowM
   }
 }
 
-template <bool SWI = false>
+template <int PRO = PRO_PLAIN>
 __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk, int nb,
                                                 uint16_t *xs, int kr, const RowsRegs &r,
                                                 float *hsum, float limit = 0.0f) {
@@ -394,7 +444,7 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float a, b;
-      if constexpr (SWI) {
+      if constexpr (PRO == PRO_SWIGLU) {
         swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
       } else {
         prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
@@ -570,11 +620,43 @@ __device__ __forceinline__ void gemv_finish(float *zf, int ydt, void *y, uint16_
   }
 }
 
+// The finish into a residual: y as gemv_finish forms it (f16), then
+// res += f32(y) over the group's 128 columns of each row (the old values in
+// resv, loaded at the start: rows wave and wave + 8), and the group's
+// sum of squares of the new res (a fixed pairwise order) into
+// res_ssq[row][cg], for the RMSNorm prologue of the next GEMV.
+__device__ __forceinline__ void gemv_finish_res(float *zf, float *res, float *res_ssq, size_t out,
+                                                int nrows, const RowMap &rm, uint32_t sv, int cg,
+                                                const float2 (&resv)[2]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float sv0 = h2f((uint16_t)(sv & 0xFFFFu)), sv1 = h2f((uint16_t)(sv >> 16));
+  const int ng = (int)(out >> 7);
+#pragma unroll
+  for (int r2 = 0; r2 < 2; ++r2) {
+    const int b = wave + r2 * (GEMV_THREADS / 64);
+    if (b >= nrows) break;
+    float v0 = zf[b * 128 + 2 * lane], v1 = zf[b * 128 + 2 * lane + 1];
+    had128_pair(v0, v1, lane);
+    const float s0 = v0 * HAD_SCALE, s1 = v1 * HAD_SCALE;
+    const float y0 = h2f(f2h(s0 * sv0)), y1 = h2f(f2h(s1 * sv1));
+    float *hp = res + (size_t)rm.out_off(b) + cg * 128 + 2 * lane;
+    const float2 h = resv[r2];  // loaded at the workgroup's start
+    float2 hn;
+    hn.x = h.x + y0;
+    hn.y = h.y + y1;
+    *reinterpret_cast<float2 *>(hp) = hn;
+    float ss = hn.x * hn.x + hn.y * hn.y;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    if (lane == 0) res_ssq[(size_t)rm.prow(b) * ng + cg] = ss;
+  }
+}
+
 // One workgroup of the GEMV: expert `expert` of the weight with trellis
 // words `twe` (that expert's) and out_tiles output tiles, nrows <= 16 rows
 // (row map rm), column group cg, split ks.  ONEB: the rows' items fit one
 // prepare batch (nrows * tps / 8 <= PREP_ITEMS).
-template <int K, int CB, bool MASKED, bool ONEB, bool SWI = false>
+template <int K, int CB, bool MASKED, bool ONEB, int PRO = PRO_PLAIN>
 __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, const void *x,
                                         const GemvGeo &geo, const GemvCfg &a,
                                         const GemvWeight &W, int expert, int nrows,
@@ -641,7 +723,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
   else
     gemv_rows_load_su(x, geo.prepared, suh, nitems, nb, tk0, rr);
-  if constexpr (SWI) {
+  if constexpr (PRO == PRO_SWIGLU) {
     // SwiGLU prologue: x is gate; up from the argument segment, like suh
     const uint16_t *up = a.x2;
     asm volatile("" : "+s"(up)::"memory");
@@ -649,6 +731,10 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
       gemv_prep_load_up(up, rm, nitems, nb, tk0, 0, wave, lane, pr);
     else
       gemv_rows_load_up(up, rm, nitems, nb, tk0, rr);
+  }
+  if constexpr (PRO == PRO_RMSNORM) {
+    static_assert(ONEB, "the RMSNorm prologue is for rows that fit one prepare batch");
+    gemv_prep_load_norm(a, rm, nitems, nb, tk0, in, 0, wave, lane, pr);
   }
   if constexpr (K > 0) {
 #pragma unroll
@@ -662,11 +748,28 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // load without a branch around it)
   const uint16_t *svp = W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : suh;
   const uint32_t sv = ld_global_u32(svp + 2 * lane);
+  // residual finish: the column group's residual pairs of the rows this wave
+  // finishes (rows wave, wave + 8), loaded now so the finish does not wait
+  // on them (without a residual, 8 bytes of the group's 128 svh values: a
+  // load in bounds and without a branch)
+  static_assert(GEMV_ROWS <= 2 * (GEMV_THREADS / 64), "two finish rows per wave");
+  typedef float f2v_t __attribute__((ext_vector_type(2)));
+  float2 resv[2];
+#pragma unroll
+  for (int r2 = 0; r2 < 2; ++r2) {
+    const int b = min(wave + r2 * (GEMV_THREADS / 64), nrows - 1);
+    const float *rp = a.res != nullptr
+                          ? a.res + (size_t)rm.out_off(b) + cg * 128 + 2 * lane
+                          : reinterpret_cast<const float *>(svp + 4 * (lane >> 1));
+    const f2v_t v = *(const __attribute__((address_space(1))) f2v_t *)rp;
+    resv[r2].x = v.x;
+    resv[r2].y = v.y;
+  }
   if constexpr (ONEB)
-    gemv_prep_store<SWI>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
-                         FOLD ? hsum : nullptr, a.limit);
+    gemv_prep_store<PRO>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
+                         FOLD ? hsum : nullptr, a.limit, in, a.eps);
   else
-    gemv_rows_store<SWI>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr,
+    gemv_rows_store<PRO>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr,
                          a.limit);
   lds_barrier();
 
@@ -768,7 +871,10 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   lds_barrier();
   if (!gemv_splitk_last(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) return;
-  gemv_finish(zf, a.ydt, W.y, W.zout, nrows, rm, sv, cg * 128);
+  if (a.res != nullptr)
+    gemv_finish_res(zf, a.res, a.res_ssq, out, nrows, rm, sv, cg, resv);
+  else
+    gemv_finish(zf, a.ydt, W.y, W.zout, nrows, rm, sv, cg * 128);
 }
 
 // The weight of grid column group `gx` (weights' groups side by side) and
@@ -785,7 +891,7 @@ __device__ __forceinline__ WeightSpan gemv_weight_of(int gx, int cg1, int cg2, i
 
 // Dense GEMV over up to four weights: the trellis pointers, the activations
 // and the geometry are the first kernel arguments (preloaded SGPRs).
-template <int K, int CB, bool MASKED, bool ONEB, bool SWI>
+template <int K, int CB, bool MASKED, bool ONEB, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
     const uint32_t *tw0, const uint32_t *tw1, const uint32_t *tw2, const uint32_t *tw3,
     const void *x, uint32_t g0, uint32_t g1, uint32_t g2, GemvArgs a) {
@@ -795,7 +901,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
   const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
   const int out_tiles = 8 * (ws.c1 - ws.c0);
   const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
-  gemv_wg<K, CB, MASKED, ONEB, SWI>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
+  gemv_wg<K, CB, MASKED, ONEB, PRO>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
                                blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
 }
 
@@ -1221,16 +1327,25 @@ void gemv_go(const Format &f, bool oneb, dim3 grid, size_t lds, hipStream_t s,
              const uint32_t *const *tw, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
              const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
-  // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up)
+  // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up); a.c.nssq set: the
+  // RMSNorm prologue (x is the f32 residual; rows in one prepare batch)
   auto go = [&](auto CBC, auto MC, auto OC) {
     constexpr int CB = decltype(CBC)::value;
     constexpr bool M = decltype(MC)::value, O = decltype(OC)::value;
-    if (a.c.x2 != nullptr)
-      hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, true>), grid, blk, lds, s, tw[0], tw[1], tw[2],
-                         tw[3], x, g0, g1, g2, a);
-    else
-      hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, false>), grid, blk, lds, s, tw[0], tw[1], tw[2],
-                         tw[3], x, g0, g1, g2, a);
+    if (a.c.x2 != nullptr) {
+      hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_SWIGLU>), grid, blk, lds, s, tw[0], tw[1],
+                         tw[2], tw[3], x, g0, g1, g2, a);
+      return;
+    }
+    if constexpr (O) {
+      if (a.c.nssq != nullptr) {
+        hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_RMSNORM>), grid, blk, lds, s, tw[0],
+                           tw[1], tw[2], tw[3], x, g0, g1, g2, a);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_PLAIN>), grid, blk, lds, s, tw[0], tw[1],
+                       tw[2], tw[3], x, g0, g1, g2, a);
   };
   using T = std::true_type;
   using F = std::false_type;

@@ -70,6 +70,33 @@ struct GemvLinear {
 hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
                              hipStream_t s);
+// The decode step's fusions around a GEMV launch (all off when zero):
+//  * up: SwiGLU prologue, x = f16(silu(x) * up) (x and up f16);
+//  * nssq: RMSNorm prologue, x is the f32 residual h [rows][in], nssq its
+//    sums of squares per 128 columns [rows][in / 128] (<= 64 of them), x =
+//    f16(h * rsqrt(sum / in + eps) * norm_w); rows in one prepare batch;
+//  * res (one linear): res [rows][out] += f32(y) instead of storing y, and
+//    res_ssq [rows][out / 128] = the new res's sums of squares per group.
+struct GemvFuse {
+  const uint16_t *up = nullptr;
+  float limit = 0.0f;
+  const float *nssq = nullptr;
+  const uint16_t *norm_w = nullptr;
+  float eps = 0.0f;
+  float *res = nullptr;
+  float *res_ssq = nullptr;
+};
+hipError_t launch_gemv_fused(const GemvLinear *ls, int count, const Format &f, const void *x,
+                             int xdt, int ydt, int rows, int in, Scratch *sc, const GemvFuse &fz,
+                             hipStream_t s);
+// Largest in / 128 the RMSNorm prologue takes (one partial sum per lane).
+constexpr int NORM_MAXBLK = 64;
+// Whether a GEMV launch's rows fit one prepare batch (what the RMSNorm
+// prologue needs).
+bool gemv_one_batch(int in, int total_out, bool generic, int rows);
+// h = f16(silu(g) * u) elementwise, the SwiGLU prologue's arithmetic.
+hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, uint16_t *h, size_t n, float limit,
+                         hipStream_t s);
 // The down projection of a dense SwiGLU MLP: y = (silu(g) * u) @ W^T, the
 // SwiGLU with the MoE mid step's arithmetic (clamped by limit > 0); g, u f16
 // [rows, in].  Up to SWIGLU_PROLOGUE_ROWS rows the GEMV applies it as it

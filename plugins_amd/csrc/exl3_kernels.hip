@@ -245,7 +245,7 @@ static void rate_dispatch(int kk, F &&launch) {
 
 static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
-                             const uint16_t *x2, float limit, hipStream_t s) {
+                             const GemvFuse &fz, hipStream_t s) {
   if (count < 1 || count > GEMV_MAXW || rows < 1 || rows > GEMV_ROWS_MAX) return hipErrorInvalidValue;
   if (in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
   if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
@@ -253,7 +253,7 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   int maxout = 0, totcg = 0;
   for (int i = 0; i < count; ++i) {
     if (ls[i].out <= 0 || ls[i].out % 128 != 0) return hipErrorInvalidValue;
-    if (ls[i].y == nullptr && ls[i].zout == nullptr) return hipErrorInvalidValue;
+    if (ls[i].y == nullptr && ls[i].zout == nullptr && fz.res == nullptr) return hipErrorInvalidValue;
     maxout = std::max(maxout, ls[i].out);
     totcg += ls[i].out / 128;
   }
@@ -287,8 +287,13 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   a.c.ksplit = ksplit;
   a.c.mask = f.mask();
   a.c.nw = f.n / 2;
-  a.c.x2 = x2;
-  a.c.limit = limit;
+  a.c.x2 = fz.up;
+  a.c.limit = fz.limit;
+  a.c.nssq = fz.nssq;
+  a.c.nw_norm = fz.norm_w;
+  a.c.eps = fz.eps;
+  a.c.res = fz.res;
+  a.c.res_ssq = fz.res_ssq;
   GemvGeo geo{};
   geo.cg1 = cgs[1];
   geo.cg2 = cgs[2];
@@ -304,6 +309,10 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   const size_t lds = gemv_lds_bytes(rows, tps, generic);
   const dim3 grid(totcg, ksplit);
   const bool oneb = rows * (tps / 8) <= PREP_ITEMS;
+  if (fz.nssq != nullptr &&
+      (!oneb || xdt != OUT_F32 || prepared || fz.norm_w == nullptr || in / 128 > NORM_MAXBLK))
+    return hipErrorInvalidValue;
+  if (fz.res != nullptr && (count != 1 || fz.res_ssq == nullptr)) return hipErrorInvalidValue;
   rate_dispatch(generic ? 0 : f.n / 16, [&](auto KC) {
     gemv_go<decltype(KC)::value>(f, oneb, grid, lds, s, tw, x, g0, g1, g2, a);
   });
@@ -313,7 +322,14 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
 hipError_t launch_gemv_multi(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, bool prepared, int ydt, int rows, int in, Scratch *sc,
                              hipStream_t s) {
-  return gemv_multi(ls, count, f, x, xdt, prepared, ydt, rows, in, sc, nullptr, 0.0f, s);
+  return gemv_multi(ls, count, f, x, xdt, prepared, ydt, rows, in, sc, GemvFuse{}, s);
+}
+
+hipError_t launch_gemv_fused(const GemvLinear *ls, int count, const Format &f, const void *x,
+                             int xdt, int ydt, int rows, int in, Scratch *sc, const GemvFuse &fz,
+                             hipStream_t s) {
+  if (fz.up != nullptr && (xdt != OUT_F16 || fz.nssq != nullptr)) return hipErrorInvalidValue;
+  return gemv_multi(ls, count, f, x, xdt, false, ydt, rows, in, sc, fz, s);
 }
 
 namespace {
@@ -331,17 +347,32 @@ hipError_t launch_gemv_swiglu(const GemvLinear &l, const Format &f, const uint16
                               const uint16_t *u, uint16_t *h, float limit, int ydt, int rows,
                               int in, Scratch &sc, hipStream_t s) {
   if (g == nullptr || u == nullptr || !(limit >= 0.0f)) return hipErrorInvalidValue;
-  if (rows <= SWIGLU_PROLOGUE_ROWS)
-    return gemv_multi(&l, 1, f, g, OUT_F16, false, ydt, rows, in, &sc, u, limit, s);
+  if (rows <= SWIGLU_PROLOGUE_ROWS) {
+    GemvFuse fz{};
+    fz.up = u;
+    fz.limit = limit;
+    return gemv_multi(&l, 1, f, g, OUT_F16, false, ydt, rows, in, &sc, fz, s);
+  }
   // more rows: every column group would redo the rows' SwiGLU, so it runs
   // once here
   if (h == nullptr) return hipErrorInvalidValue;
-  const size_t n = (size_t)rows * in;
+  hipError_t e = launch_swiglu(g, u, h, (size_t)rows * in, limit, s);
+  if (e != hipSuccess) return e;
+  return gemv_multi(&l, 1, f, h, OUT_F16, false, ydt, rows, in, &sc, GemvFuse{}, s);
+}
+
+hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, uint16_t *h, size_t n, float limit,
+                         hipStream_t s) {
+  if (n == 0 || !(limit >= 0.0f)) return hipErrorInvalidValue;
   const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, u, h, n, limit);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return gemv_multi(&l, 1, f, h, OUT_F16, false, ydt, rows, in, &sc, nullptr, 0.0f, s);
+  return hipGetLastError();
+}
+
+bool gemv_one_batch(int in, int total_out, bool generic, int rows) {
+  int ks, tps;
+  gemv_multi_plan(in, total_out, generic, rows, &ks, &tps);
+  return rows * (tps / 8) <= PREP_ITEMS;
 }
 
 hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, int xdt,

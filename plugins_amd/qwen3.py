@@ -9,9 +9,10 @@ checkpoints here).  The reference's model plugin runs the same step on MLX
 model.zig; paths relative to /root/reference/plugins/), its linears through the
 quant table this library exports.
 
-Every operation runs in libexl3_mi355x.so: the linears through the EXL3 entries
-(q, k, v as one shared-input launch; the MLP through the dense swiglu entry),
-the rest through the exl3d_* harness entries (include/exl3_decoder.h).  PyTorch only allocates the
+Every operation runs in libexl3_mi355x.so: the linears through exl3d_linears
+(the EXL3 GEMV with the step's norms, SwiGLU and residual adds fused into its
+prepare and finish), embedding and attention through the other exl3d_*
+harness entries (include/exl3_decoder.h).  PyTorch only allocates the
 buffers and supplies the stream.
 """
 from __future__ import annotations
@@ -48,7 +49,9 @@ class Qwen3Config:
 
 
 _DEC_SIGS = {
-    "exl3d_embed": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "exl3d_embed": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "exl3d_linears": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_float, c_void_p,
+                              c_void_p, c_void_p, c_void_p, c_void_p]),
     "exl3d_add_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_float,
                                   c_void_p]),
     "exl3d_qk_norm_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
@@ -89,9 +92,27 @@ def _p(t) -> int:
 
 # ------------------------------------------------------------------ ops
 
-def embed(ids, table, h, stream=None):
+def embed(ids, table, h, ssq=None, stream=None):
     B, H = h.shape
-    _ck(dec_lib().exl3d_embed(_p(ids), B, _p(table), H, _p(h), X.stream_handle(stream)), "embed")
+    _ck(dec_lib().exl3d_embed(_p(ids), B, _p(table), H, _p(h), _p(ssq) if ssq is not None else None,
+                              X.stream_handle(stream)), "embed")
+
+
+def linears(ws, x, outs=None, norm_w=None, nssq=None, eps=0.0, up=None, res=None, res_ssq=None,
+            stream=None):
+    """exl3d_linears: the EXL3 linears ws on x with the decode step's fusions
+    (RMSNorm of an f32 residual x, SwiGLU with up, residual finish into res)."""
+    n = len(ws)
+    wp = (ctypes.POINTER(X.Weight) * n)(*[ctypes.pointer(w) for w in ws])
+    op = (c_void_p * n)(*[_p(t) for t in outs]) if outs is not None else None
+    opt = lambda t: _p(t) if t is not None else None  # noqa: E731
+    rc = dec_lib().exl3d_linears(ctypes.cast(wp, c_void_p), n, _p(x), x.shape[0], opt(norm_w),
+                                 opt(nssq), eps, opt(up), opt(res), opt(res_ssq),
+                                 ctypes.cast(op, c_void_p) if op is not None else None,
+                                 X.stream_handle(stream))
+    if rc == -1:
+        raise RuntimeError("linears: weights or shapes refused")
+    _ck(rc, "linears")
 
 
 def add_rmsnorm(h, add, w, out, eps, stream=None):
@@ -192,13 +213,13 @@ class Qwen3Decoder:
         B = batch
         f16 = torch.float16
         self.h = torch.empty(B, H, dtype=torch.float32, device=dev)
-        self.xn = torch.empty(B, H, dtype=f16, device=dev)
+        self.ssq = torch.empty(B, H // 128, dtype=torch.float32, device=dev)
+        self.g = torch.empty(B, cfg.inter, dtype=f16, device=dev)
+        self.u = torch.empty(B, cfg.inter, dtype=f16, device=dev)
         self.q = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
         self.k = torch.empty(B, cfg.kv_dim, dtype=f16, device=dev)
         self.v = torch.empty(B, cfg.kv_dim, dtype=f16, device=dev)
         self.att = torch.empty(B, cfg.q_dim, dtype=f16, device=dev)
-        self.o = torch.empty(B, H, dtype=f16, device=dev)
-        self.d = torch.empty(B, H, dtype=f16, device=dev)
         self.logits = torch.empty(B, cfg.vocab, dtype=f16, device=dev)
         nbytes = attn_scratch_bytes(B, cfg.heads, cfg.kv_heads, self.tmax)
         # zeroed once: the attention leaves its arrival tickets zero
@@ -220,23 +241,27 @@ class Qwen3Decoder:
 
     def step(self, stream=None):
         """One decode step: logits [B, vocab] for tokens self.ids at positions
-        self.pos (the caches take their k, v at row pos)."""
+        self.pos (the caches take their k, v at row pos).
+
+        Five launches a layer: q+k+v with the input RMSNorm of the residual h
+        in their prepare; attention with q/k norm, RoPE and the KV append;
+        o, whose finish adds into h (and leaves h's sums of squares per 128
+        columns for the next norm); gate+up with the post-attention RMSNorm
+        in their prepare; down with the SwiGLU in its prepare and its finish
+        adding into h."""
         c = self.cfg
-        embed(self.ids, self.embed_table, self.h, stream)
-        add = None
+        embed(self.ids, self.embed_table, self.h, self.ssq, stream)
         for L in self.layers:
-            add_rmsnorm(self.h, add, L["in_norm"], self.xn, c.eps, stream)
-            X.matmul_shared([L["q"].weight, L["k"].weight, L["v"].weight], self.xn,
-                            outs=[self.q, self.k, self.v], stream=stream)
+            linears([L["q"].weight, L["k"].weight, L["v"].weight], self.h,
+                    outs=[self.q, self.k, self.v], norm_w=L["in_norm"], nssq=self.ssq, eps=c.eps,
+                    stream=stream)
             attn_decode_rope(self.q, self.k, self.v, L["q_norm"], L["k_norm"], self.pos, L["kc"],
                              L["vc"], self.att, self.scratch, c.eps, c.theta, stream)
-            L["o"](self.att, out=self.o, stream=stream)
-            add_rmsnorm(self.h, self.o, L["post_norm"], self.xn, c.eps, stream)
-            # the dense SwiGLU MLP entry (QuantTable.swiglu without routes):
-            # gate+up in one launch, down with the SwiGLU in its prepare
-            X.swiglu(L["gate"].weight, L["up"].weight, L["down"].weight, self.xn, out=self.d,
-                     stream=stream)
-            add = self.d
-        add_rmsnorm(self.h, add, self.final_norm, self.xn, c.eps, stream)
-        self.lm_head(self.xn, out=self.logits, stream=stream)
+            linears([L["o"].weight], self.att, res=self.h, res_ssq=self.ssq, stream=stream)
+            linears([L["gate"].weight, L["up"].weight], self.h, outs=[self.g, self.u],
+                    norm_w=L["post_norm"], nssq=self.ssq, eps=c.eps, stream=stream)
+            linears([L["down"].weight], self.g, up=self.u, res=self.h, res_ssq=self.ssq,
+                    stream=stream)
+        linears([self.lm_head.weight], self.h, outs=[self.logits], norm_w=self.final_norm,
+                nssq=self.ssq, eps=c.eps, stream=stream)
         return self.logits

@@ -186,6 +186,53 @@ def test_attention_decode_with_rope_and_append(B, T, lens):
     assert rel(out.cpu(), want) < 2e-3, rel(out.cpu(), want)
 
 
+def _ssq(h):
+    """Sums of squares per 128 columns of an f32 [B, H] residual."""
+    return (h.double() ** 2).view(h.shape[0], -1, 128).sum(-1).float()
+
+
+@gpu
+@pytest.mark.parametrize("B", [1, 16])
+def test_linears_fusions(B):
+    # exl3d_linears against the separate ops: RMSNorm prologue (B = 1: in
+    # the GEMV's prepare; B = 16: normalized first), residual finish (bit
+    # for bit against exl3_matmul, whose launch it is), SwiGLU prologue
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(40 + B)
+    H, I = 512, 1024
+    lq = Q.random_linear(torch, H, H, 4, torch.Generator(device="cuda").manual_seed(1))
+    lk = Q.random_linear(torch, H, 256, 4, torch.Generator(device="cuda").manual_seed(2))
+    lo = Q.random_linear(torch, H, H, 4, torch.Generator(device="cuda").manual_seed(3))
+    ld = Q.random_linear(torch, I, H, 4, torch.Generator(device="cuda").manual_seed(4))
+    h = torch.randn(B, H, generator=g)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).half()
+    hd, ssq = h.cuda(), _ssq(h).cuda()
+    # RMSNorm prologue
+    yq = torch.empty(B, H, dtype=torch.float16, device="cuda")
+    yk = torch.empty(B, 256, dtype=torch.float16, device="cuda")
+    Q.linears([lq.weight, lk.weight], hd, outs=[yq, yk], norm_w=w.cuda(), nssq=ssq, eps=1e-6)
+    xn = ref_rmsnorm(h, w, 1e-6)
+    wq, wk = lq(xn.cuda()).cpu(), lk(xn.cuda()).cpu()
+    # the norm's sum in another order moves some f16 inputs by an ulp
+    assert rel(yq.cpu(), wq) < 1e-3 and rel(yk.cpu(), wk) < 1e-3
+    # residual finish: h += y, and the new sums of squares
+    x = torch.randn(B, H, generator=g).half()
+    res = hd.clone()
+    rssq = torch.empty(B, H // 128, device="cuda")
+    Q.linears([lo.weight], x.cuda(), res=res, res_ssq=rssq)
+    y = lo(x.cuda()).cpu()
+    assert torch.equal(res.cpu(), h + y.float())  # one f32 add of the same y
+    assert torch.allclose(rssq.cpu(), _ssq(res.cpu()), rtol=1e-5, atol=0)
+    # SwiGLU prologue (B = 16: the SwiGLU first, elementwise)
+    gt = torch.randn(B, I, generator=g).half()
+    up = torch.randn(B, I, generator=g).half()
+    yd = torch.empty(B, H, dtype=torch.float16, device="cuda")
+    Q.linears([ld.weight], gt.cuda(), outs=[yd], up=up.cuda())
+    hm = (torch.nn.functional.silu(gt.float()) * up.float()).half()
+    # the SwiGLU in f32 with expf against torch's: an f16 ulp here and there
+    assert rel(yd.cpu(), ld(hm.cuda()).cpu()) < 1e-3
+
+
 @gpu
 def test_silu_mul():
     from plugins_amd import qwen3 as Q
