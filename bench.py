@@ -346,7 +346,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (profiles/gemv_k4_qwen3_8b_decode.md)",
                      "algorithmic_bytes_per_launch": round(step_bytes / launches),
-                     "kernel": "exl3::gemv_kernel<4,0,false,true> (mul1, K=4, window 16, one prepare batch)",
+                     "kernel": "exl3::gemv_kernel<4,0,false,true,0> (mul1, K=4, window 16, one prepare batch, plain input)",
                      "launches": launches * args.steps,
                      "avg_launch_us": round(avg_launch_ms * 1e3, 3),
                      "timing": "HIP events around the timed region's graph replays / launches"},
