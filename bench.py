@@ -53,11 +53,11 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_model(torch, X, layers: int, seed: int):
+def build_model(torch, X, layers: int, seed: int, k_bits: int = K_BITS):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     lins = []
-    n = 16 * K_BITS
+    n = 16 * k_bits
     for _ in range(layers):
         for name, i, o in SHAPES:
             t = torch.randint(-32768, 32768, (i // 16, o // 16, n), dtype=torch.int32, device="cuda",
@@ -135,6 +135,141 @@ def gemm_tflops(torch, iters: int = 10):
                                               "includes": "prepare + LDS-decode MFMA GEMM + finish"}}
 
 
+def _graph_ms(torch, fn, reps: int) -> float:
+    """Captures fn (after two eager calls on the capture stream) into a HIP
+    graph and returns the average replay time in ms (HIP events)."""
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        fn()
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap, capture_error_mode="thread_local"):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def gemv_sweep(torch, X, ks=(2, 3, 4, 5, 6, 8), batches=(1, 2, 4, 8), layers=4, reps=10):
+    """the decode GEMV over the Qwen3-8B-shaped linears at
+    each rate K and batch (4 layers, launches grouped as a decoder issues
+    them, HIP graph): packed GB/s."""
+    out = {}
+    for k in ks:
+        lins = build_model(torch, X, layers, seed=100 + k, k_bits=k)
+        nbytes = sum(i * o * k // 8 for _, i, o, _ in lins)
+        per = len(SHAPES)
+        groups = []
+        for l0 in range(0, len(lins), per):
+            groups += [[l0, l0 + 1, l0 + 2], [l0 + 3], [l0 + 4, l0 + 5], [l0 + 6]]
+        res = {}
+        for B in batches:
+            xs = {i: torch.randn(B, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
+            ys = [torch.empty(B, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+
+            def step():
+                for g in groups:
+                    i = lins[g[0]][1]
+                    X.matmul_shared([lins[j][3].weight for j in g], xs[i], outs=[ys[j] for j in g])
+            ms = _graph_ms(torch, step, reps)
+            res[f"batch{B}"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                "us_per_launch": round(ms * 1e3 / len(groups), 2)}
+        out[f"K{k}"] = res
+        del lins
+        torch.cuda.empty_cache()
+    return {"gemv_sweep": {"layers": layers, "packed_bytes": "in*out*K/8", **out}}
+
+
+def gemm_sweep(torch, X, ms=(128, 512, 2048, 4096), iters=8):
+    """the prefill GEMM at K=4 on each Qwen3-8B layer shape
+    and M (prepare + GEMM + finish; 3 weight copies rotated): TFLOP/s."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+    shapes = [("q/o", 4096, 4096), ("k/v", 4096, 1024), ("gate/up", 4096, 12288),
+              ("down", 12288, 4096)]
+    out = {}
+    for name, i, o in shapes:
+        lins = []
+        for _ in range(3):
+            t = torch.randint(-32768, 32768, (i // 16, o // 16, 64), dtype=torch.int32,
+                              device="cuda", generator=g).to(torch.int16)
+            lins.append(X.Linear(t, torch.ones(i, dtype=torch.float16, device="cuda"),
+                                 torch.full((o,), 0.02, dtype=torch.float16, device="cuda")))
+        res = {}
+        for M in ms:
+            x = torch.randn(M, i, device="cuda", generator=g).to(torch.float16)
+            y = torch.empty(M, o, dtype=torch.float16, device="cuda")
+            for lin in lins:
+                lin(x, out=y)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for it in range(iters):
+                lins[it % 3](x, out=y)
+            b.record()
+            torch.cuda.synchronize()
+            t_ms = a.elapsed_time(b) / iters
+            res[f"M{M}"] = {"tflops": round(2.0 * M * i * o / (t_ms * 1e-3) / 1e12, 1),
+                            "us": round(t_ms * 1e3, 1)}
+        out[name] = res
+    return {"gemm_sweep_k4": out}
+
+
+def moe_bench(torch, X, batches=(1, 16, 64), reps=10):
+    """a DeepSeek-V3-style routed MoE layer at K=3 (hidden
+    7168, expert intermediate 2048, 256 routed experts top-8 from the softmax
+    of N(0,1) logits, renormalized, plus one shared expert): the routed
+    swiglu and the shared expert's dense swiglu per batch, HIP graph;
+    packed bytes = (distinct routed experts + 1) * 3 * 7168 * 2048 * 3/8."""
+    E, H, I, K, topk = 256, 7168, 2048, 3, 8
+    n = 16 * K
+    g = torch.Generator(device="cuda")
+    g.manual_seed(13)
+
+    def bank(e, i, o):
+        t = torch.randint(-32768, 32768, (e, i // 16, o // 16, n), dtype=torch.int32, device="cuda",
+                          generator=g).to(torch.int16)
+        suh = (torch.randint(0, 2, (e, i), device="cuda", generator=g) * 2 - 1).to(torch.float16)
+        svh = ((torch.randint(0, 2, (e, o), device="cuda", generator=g) * 2 - 1) *
+               (torch.rand(e, o, device="cuda", generator=g) + 0.5) * 0.02).to(torch.float16)
+        return t, suh, svh
+
+    gb, ub, db = bank(E, H, I), bank(E, H, I), bank(E, I, H)
+    G, U, D = X.wrap(*gb), X.wrap(*ub), X.wrap(*db)
+    sg, su, sd = (X.Linear(*[a[0] for a in bank(1, H, I)]), X.Linear(*[a[0] for a in bank(1, H, I)]),
+                  X.Linear(*[a[0] for a in bank(1, I, H)]))
+    per_expert = 3 * H * I * K // 8
+    out = {}
+    for B in batches:
+        x = torch.randn(B, 1, H, device="cuda", generator=g).to(torch.float16)
+        probs = torch.softmax(torch.randn(B, E, device="cuda", generator=g), -1)
+        top = probs.topk(topk, -1)
+        scores = (top.values / top.values.sum(-1, keepdim=True)).reshape(B, 1, topk)
+        inds = top.indices.to(torch.int32).reshape(B, 1, topk)
+        distinct = int(torch.unique(inds).numel())
+        y = torch.empty_like(x)
+        ys = torch.empty_like(x)
+
+        def layer():
+            X.swiglu(G, U, D, x, inds, scores, out=y)
+            X.swiglu(sg.weight, su.weight, sd.weight, x, out=ys)
+        ms = _graph_ms(torch, layer, reps)
+        nbytes = (distinct + 1) * per_expert
+        out[f"batch{B}"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1),
+                            "distinct_experts": distinct}
+    for w in (G, U, D):
+        X.release(w)
+    return {"moe_k3_deepseek_v3_layer": out}
+
+
 def decode_tok_s(torch, batches=(1, 16), ctx=2048, steps=8):
     """a 36-layer Qwen3-8B-shaped decoder decode step (EXL3
     K=4 linears incl. lm_head, f16 attention over a random KV cache at context
@@ -180,7 +315,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the decoder tok/s leg")
-    ap.add_argument("--only", choices=["gemv", "gemm", "decode"], default=None,
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the config 1-3 legs (GEMV K x batch sweep, GEMM M sweep, MoE layer)")
+    ap.add_argument("--only", choices=["gemv", "gemm", "decode", "sweep"], default=None,
                     help="run one leg (gemv: the decode GEMV pass and its roofline leg only)")
     ap.add_argument("--per-linear", action="store_true",
                     help="one launch per linear instead of one per shared-input group")
@@ -196,11 +333,17 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_mib": args.copy_mib, "copies": 5}))
         return 0
-    if args.only in ("gemm", "decode"):
+    if args.only in ("gemm", "decode", "sweep"):
         # one leg alone (for counter runs of its kernels); prints that leg's numbers
         import torch
+        from plugins_amd import exl3 as X
         torch.cuda.set_device(0)
-        res = gemm_tflops(torch) if args.only == "gemm" else decode_tok_s(torch)
+        if args.only == "gemm":
+            res = gemm_tflops(torch)
+        elif args.only == "decode":
+            res = decode_tok_s(torch)
+        else:
+            res = {**gemv_sweep(torch, X), **gemm_sweep(torch, X), **moe_bench(torch, X)}
         print(json.dumps({"only": args.only, **res}), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -317,6 +460,13 @@ def main() -> int:
             extra["decode_tok_s"] = decode_tok_s(torch)
         except Exception as ex:  # reported, not hidden
             extra["decode_error"] = repr(ex)
+    if not args.no_sweep and args.only != "gemv":
+        for name, leg in (("gemv sweep", gemv_sweep), ("gemm sweep", gemm_sweep), ("moe", moe_bench)):
+            try:
+                log(name)
+                extra.update(leg(torch, X))
+            except Exception as ex:  # reported, not hidden
+                extra[name.replace(" ", "_") + "_error"] = repr(ex)
     extra["graph"] = graph is not None
 
     cpu = None

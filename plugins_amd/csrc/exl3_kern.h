@@ -385,18 +385,22 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
 constexpr int PREP_GROUPS = GEMV_THREADS / 16;
 constexpr int PREP_PASSES = GEMV_ROWS * (GEMV_TPS_MAX / 8) / PREP_GROUPS;
 
+// NP passes of the PREP_GROUPS groups cover nblk <= NP * PREP_GROUPS blocks
+// (a launch takes the smallest NP in 1, 2, PREP_PASSES that covers its rows).
+template <int NP>
 struct RowsRegs {
-  u4_t x[PREP_PASSES][2];  // 8 elements: one 16-byte piece (f16/bf16) or two (f32)
-  u4_t su[PREP_PASSES];
+  u4_t x[NP][2];  // 8 elements: one 16-byte piece (f16/bf16) or two (f32)
+  u4_t su[NP];
 };
 
+template <int NP>
 __device__ __forceinline__ void gemv_rows_load_x(const void *x, int xdt, int prepared,
                                                  const RowMap &rm, int nblk, int nb, int tk0,
-                                                 RowsRegs &r) {
+                                                 RowsRegs<NP> &r) {
   const int esz = (!prepared && xdt == OUT_F32) ? 4 : 2;
   const int li = threadIdx.x & 15;
 #pragma unroll
-  for (int p = 0; p < PREP_PASSES; ++p) {
+  for (int p = 0; p < NP; ++p) {
     const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
     const int row = G / nb, blk = G - row * nb;
     const int k = tk0 * 16 + blk * 128 + 8 * li;
@@ -406,12 +410,13 @@ __device__ __forceinline__ void gemv_rows_load_x(const void *x, int xdt, int pre
   }
 }
 
+template <int NP>
 __device__ __forceinline__ void gemv_rows_load_su(const void *x, int prepared, const uint16_t *suh,
-                                                  int nblk, int nb, int tk0, RowsRegs &r) {
+                                                  int nblk, int nb, int tk0, RowsRegs<NP> &r) {
   const uint16_t *sup = prepared ? (const uint16_t *)x : suh;
   const int li = threadIdx.x & 15;
 #pragma unroll
-  for (int p = 0; p < PREP_PASSES; ++p) {
+  for (int p = 0; p < NP; ++p) {
     const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
     const int blk = G % nb;
     r.su[p] = *(const __attribute__((address_space(1))) u4_t *)(sup + tk0 * 16 + blk * 128 + 8 * li);
@@ -419,11 +424,12 @@ __device__ __forceinline__ void gemv_rows_load_su(const void *x, int prepared, c
 }
 
 // SwiGLU prologue (rows form): the up pieces into x[p][1].
+template <int NP>
 __device__ __forceinline__ void gemv_rows_load_up(const uint16_t *x2, const RowMap &rm, int nblk,
-                                                  int nb, int tk0, RowsRegs &r) {
+                                                  int nb, int tk0, RowsRegs<NP> &r) {
   const int li = threadIdx.x & 15;
 #pragma unroll
-  for (int p = 0; p < PREP_PASSES; ++p) {
+  for (int p = 0; p < NP; ++p) {
     const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
     const int row = G / nb, blk = G - row * nb;
     r.x[p][1] = *(const __attribute__((address_space(1))) u4_t *)(x2 + (size_t)rm.in_off(row) +
@@ -431,13 +437,13 @@ __device__ __forceinline__ void gemv_rows_load_up(const uint16_t *x2, const RowM
   }
 }
 
-template <int PRO = PRO_PLAIN>
+template <int PRO, int NP>
 __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk, int nb,
-                                                uint16_t *xs, int kr, const RowsRegs &r,
+                                                uint16_t *xs, int kr, const RowsRegs<NP> &r,
                                                 float *hsum, float limit = 0.0f) {
   const int li = threadIdx.x & 15, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int p = 0; p < PREP_PASSES; ++p) {
+  for (int p = 0; p < NP; ++p) {
     const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
     const int row = G / nb, blk = G - row * nb;
     float v[8];
@@ -654,14 +660,19 @@ __device__ __forceinline__ void gemv_finish_res(float *zf, float *res, float *re
 
 // One workgroup of the GEMV: expert `expert` of the weight with trellis
 // words `twe` (that expert's) and out_tiles output tiles, nrows <= 16 rows
-// (row map rm), column group cg, split ks.  ONEB: the rows' items fit one
-// prepare batch (nrows * tps / 8 <= PREP_ITEMS).
-template <int K, int CB, bool MASKED, bool ONEB, int PRO = PRO_PLAIN>
+// (row map rm), column group cg, split ks.  PREP 0: the rows' items fit one
+// prepare batch (nrows * tps / 8 <= PREP_ITEMS); else the rows form in PREP
+// passes (nrows * tps / 8 <= PREP * PREP_GROUPS).
+template <int K, int CB, bool MASKED, int PREP, int PRO = PRO_PLAIN>
 __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, const void *x,
                                         const GemvGeo &geo, const GemvCfg &a,
                                         const GemvWeight &W, int expert, int nrows,
                                         const RowMap &rm, int cg, int ks, char *smem,
                                         int rows_alloc) {
+  // PREP 0: the rows' items fit one prepare batch (one item per wave);
+  // else the rows form in PREP passes
+  constexpr bool ONEB = PREP == 0;
+  constexpr int NP = ONEB ? 1 : PREP;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = wave & 3, kp = wave >> 2;
@@ -703,7 +714,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // ONEB: one item (row, 128-block) per wave and batch; else every row's
   // items in one pass (gemv_rows_*)
   PrepRegs pr;
-  RowsRegs rr;
+  RowsRegs<NP> rr;
   if constexpr (ONEB)
     gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
   else
@@ -769,8 +780,8 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     gemv_prep_store<PRO>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
                          FOLD ? hsum : nullptr, a.limit, in, a.eps);
   else
-    gemv_rows_store<PRO>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr, FOLD ? hsum : nullptr,
-                         a.limit);
+    gemv_rows_store<PRO, NP>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr,
+                             FOLD ? hsum : nullptr, a.limit);
   lds_barrier();
 
   const int arow = min(lane & 15, nrows - 1);
@@ -891,7 +902,7 @@ __device__ __forceinline__ WeightSpan gemv_weight_of(int gx, int cg1, int cg2, i
 
 // Dense GEMV over up to four weights: the trellis pointers, the activations
 // and the geometry are the first kernel arguments (preloaded SGPRs).
-template <int K, int CB, bool MASKED, bool ONEB, int PRO>
+template <int K, int CB, bool MASKED, int PREP, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
     const uint32_t *tw0, const uint32_t *tw1, const uint32_t *tw2, const uint32_t *tw3,
     const void *x, uint32_t g0, uint32_t g1, uint32_t g2, GemvArgs a) {
@@ -901,7 +912,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
   const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
   const int out_tiles = 8 * (ws.c1 - ws.c0);
   const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
-  gemv_wg<K, CB, MASKED, ONEB, PRO>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
+  gemv_wg<K, CB, MASKED, PREP, PRO>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
                                blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
 }
 
@@ -1311,7 +1322,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
   }
   lds_barrier();
   const RowMap rm{ri, 0, 0};
-  gemv_wg<K, CB, MASKED, false>(tw + (size_t)it.expert * W.expert_words, out_tiles, x, geo, a.c,
+  gemv_wg<K, CB, MASKED, PREP_PASSES>(tw + (size_t)it.expert * W.expert_words, out_tiles, x, geo, a.c,
                                 W, (int)it.expert, (int)it.count, rm, blockIdx.x - ws.c0,
                                 blockIdx.y, smem + 256, MOE_ITEM_ROWS);
 }
@@ -1323,21 +1334,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
 
 // Dense GEMV over up to four weights (tw[i] their trellis words).
 template <int K>
-void gemv_go(const Format &f, bool oneb, dim3 grid, size_t lds, hipStream_t s,
+void gemv_go(const Format &f, int prep, dim3 grid, size_t lds, hipStream_t s,
              const uint32_t *const *tw, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
              const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
   // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up); a.c.nssq set: the
   // RMSNorm prologue (x is the f32 residual; rows in one prepare batch)
-  auto go = [&](auto CBC, auto MC, auto OC) {
+  auto go2 = [&](auto CBC, auto MC, auto PC) {
     constexpr int CB = decltype(CBC)::value;
-    constexpr bool M = decltype(MC)::value, O = decltype(OC)::value;
+    constexpr bool M = decltype(MC)::value;
+    constexpr int O = decltype(PC)::value;
     if (a.c.x2 != nullptr) {
       hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_SWIGLU>), grid, blk, lds, s, tw[0], tw[1],
                          tw[2], tw[3], x, g0, g1, g2, a);
       return;
     }
-    if constexpr (O) {
+    if constexpr (O == 0) {
       if (a.c.nssq != nullptr) {
         hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_RMSNORM>), grid, blk, lds, s, tw[0],
                            tw[1], tw[2], tw[3], x, g0, g1, g2, a);
@@ -1347,22 +1359,32 @@ void gemv_go(const Format &f, bool oneb, dim3 grid, size_t lds, hipStream_t s,
     hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_PLAIN>), grid, blk, lds, s, tw[0], tw[1],
                        tw[2], tw[3], x, g0, g1, g2, a);
   };
+  // prep: 0 (one prepare batch) or the rows form's passes (1, 2, PREP_PASSES)
+  auto go = [&](auto CBC, auto MC) {
+    switch (prep) {
+      case 0: go2(CBC, MC, std::integral_constant<int, 0>{}); break;
+      case 1: go2(CBC, MC, std::integral_constant<int, 1>{}); break;
+      case 2: go2(CBC, MC, std::integral_constant<int, 2>{}); break;
+      default: go2(CBC, MC, std::integral_constant<int, PREP_PASSES>{});
+    }
+  };
   using T = std::true_type;
   using F = std::false_type;
   using MUL1 = std::integral_constant<int, CB_MUL1>;
   using MCG = std::integral_constant<int, CB_MCG>;
   const bool masked = f.window < 16;
-  if (f.codebook == CB_MCG) {
-    if (masked)
-      oneb ? go(MCG{}, T{}, T{}) : go(MCG{}, T{}, F{});
-    else
-      oneb ? go(MCG{}, F{}, T{}) : go(MCG{}, F{}, F{});
-  } else {
-    if (masked)
-      oneb ? go(MUL1{}, T{}, T{}) : go(MUL1{}, T{}, F{});
-    else
-      oneb ? go(MUL1{}, F{}, T{}) : go(MUL1{}, F{}, F{});
-  }
+  if (f.codebook == CB_MCG)
+    masked ? go(MCG{}, T{}) : go(MCG{}, F{});
+  else
+    masked ? go(MUL1{}, T{}) : go(MUL1{}, F{});
+}
+
+// The prepare form of a GEMV launch: 0 when its rows' items fit one batch,
+// else the fewest passes of the rows form that cover them.
+inline int gemv_prep_form(int rows, int tps) {
+  const int items = rows * (tps / 8);
+  if (items <= PREP_ITEMS) return 0;
+  return items <= PREP_GROUPS ? 1 : items <= 2 * PREP_GROUPS ? 2 : PREP_PASSES;
 }
 
 template <int K>
@@ -1414,7 +1436,7 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
 
 // Declarations of one rate's launcher instantiations.
 #define EXL3_GEMV_GO(KK)                                                                 \
-  void gemv_go<KK>(const Format &, bool, dim3, size_t, hipStream_t, const uint32_t *const *, \
+  void gemv_go<KK>(const Format &, int, dim3, size_t, hipStream_t, const uint32_t *const *, \
                    const void *, uint32_t, uint32_t, uint32_t, const GemvArgs &)
 #define EXL3_MOE_GEMV_GO(KK)                                                                    \
   void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, const uint32_t *,            \

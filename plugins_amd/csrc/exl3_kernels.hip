@@ -308,13 +308,14 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   gemv_geo_pack(geo, &g0, &g1, &g2);
   const size_t lds = gemv_lds_bytes(rows, tps, generic);
   const dim3 grid(totcg, ksplit);
-  const bool oneb = rows * (tps / 8) <= PREP_ITEMS;
+  const int prep = gemv_prep_form(rows, tps);
+  const bool oneb = prep == 0;
   if (fz.nssq != nullptr &&
       (!oneb || xdt != OUT_F32 || prepared || fz.norm_w == nullptr || in / 128 > NORM_MAXBLK))
     return hipErrorInvalidValue;
   if (fz.res != nullptr && (count != 1 || fz.res_ssq == nullptr)) return hipErrorInvalidValue;
   rate_dispatch(generic ? 0 : f.n / 16, [&](auto KC) {
-    gemv_go<decltype(KC)::value>(f, oneb, grid, lds, s, tw, x, g0, g1, g2, a);
+    gemv_go<decltype(KC)::value>(f, prep, grid, lds, s, tw, x, g0, g1, g2, a);
   });
   return hipGetLastError();
 }
