@@ -130,9 +130,24 @@ def gemm_tflops(torch, iters: int = 10):
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / iters
     tf = 2.0 * rows * i * o / (ms * 1e-3) / 1e12
+    # context: a dense f16 GEMM of the same shape through torch (hipBLASLt),
+    # the library's rate on unquantized weights (3 x 100 MB rotated)
+    del lins
+    ws = [torch.randn(i, o, device="cuda", generator=g).to(torch.float16) for _ in range(3)]
+    for w in ws:
+        torch.matmul(x, w, out=y)
+    torch.cuda.synchronize()
+    s.record()
+    for it in range(iters):
+        torch.matmul(x, ws[it % 3], out=y)
+    e.record()
+    torch.cuda.synchronize()
+    dms = s.elapsed_time(e) / iters
+    dtf = 2.0 * rows * i * o / (dms * 1e-3) / 1e12
     return {"prefill_gemm_m2048_gate_up_k4": {"tflops": round(tf, 2), "ms": round(ms, 4),
                                               "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
-                                              "includes": "prepare + LDS-decode MFMA GEMM + finish"}}
+                                              "includes": "prepare + LDS-decode MFMA GEMM + finish",
+                                              "dense_f16_torch_same_shape_tflops": round(dtf, 1)}}
 
 
 def _graph_ms(torch, fn, reps: int) -> float:

@@ -148,6 +148,8 @@ exl3_array make_array(void *data, int dt, std::initializer_list<int64_t> shape, 
 struct StreamScratch {
   void *xp = nullptr;
   size_t xp_bytes = 0;
+  void *kpart = nullptr;  // GEMM split-K planes
+  size_t kpart_bytes = 0;
   void *partial = nullptr;
   size_t partial_bytes = 0;
   void *moe = nullptr;
@@ -539,9 +541,15 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
         }
         xp = (const uint16_t *)ss->xp;
       }
-      hipError_t e = exl3::launch_gemm((const uint16_t *)ws[i]->w.data, pvs[i]->f, xp,
-                                       (const uint16_t *)ws[i]->biases.data, ys ? ys[i] : nullptr,
-                                       ydt, zs ? zs[i] : nullptr, (int)rows, in, (int)pvs[i]->out, s);
+      const exl3::GemmSplit sp = exl3::gemm_split((int)rows, in, (int)pvs[i]->out);
+      if (sp.splits > 1) {
+        hipError_t e = grow(&ss->kpart, &ss->kpart_bytes, sp.part_floats * 4, s, -1);
+        if (e != hipSuccess) return e;
+      }
+      hipError_t e = exl3::launch_gemm(
+          (const uint16_t *)ws[i]->w.data, pvs[i]->f, xp, (const uint16_t *)ws[i]->biases.data,
+          ys ? ys[i] : nullptr, ydt, zs ? zs[i] : nullptr, (int)rows, in, (int)pvs[i]->out,
+          (float *)ss->kpart, ss->kpart_bytes / 4, s);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;

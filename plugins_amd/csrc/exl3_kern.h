@@ -1154,7 +1154,7 @@ template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    int M, int in_tiles, int out_tiles, uint32_t mask) {
+    int M, int in_tiles, int out_tiles, uint32_t mask, float *__restrict__ kpart) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_BYTES / 2];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1202,17 +1202,41 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // split-K (small grids): split ks of S takes an even run of the stages
+  const int S = gridDim.z, ks = blockIdx.z;
+  const int P = NS / 2;
+  const int st0 = 2 * (P * ks / S), st1 = 2 * (P * (ks + 1) / S);
   if (wave < 4)
-    gemm_main<K, CB, MASKED, 0>(acc, lds, twc, wstage, src, bst, xp, aoff, ast, ard, brd, NS,
-                                mask);
+    gemm_main<K, CB, MASKED, 0>(acc, lds, twc + (size_t)st0 * wstage, wstage, src, bst,
+                                xp + st0 * GM_BK, aoff, ast, ard, brd, st1 - st0, mask);
   else
-    gemm_main<K, CB, MASKED, 1>(acc, lds, twc, wstage, src, bst, xp, aoff, ast, ard, brd, NS,
-                                mask);
+    gemm_main<K, CB, MASKED, 1>(acc, lds, twc + (size_t)st0 * wstage, wstage, src, bst,
+                                xp + st0 * GM_BK, aoff, ast, ard, brd, st1 - st0, mask);
 
   // acc[i][j] = z^T for columns 64 wc + 32 j .. and rows 64 wm + 32 i .. of
   // the tile: lane l holds row (l & 31), register r column
   // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
   const int rb = m0 + 64 * wm + (lane & 31);
+  if (S > 1) {
+    // split-K: this split's sums of rows < M go to its plane of
+    // kpart [S][M][out] (f32, row-major; four consecutive columns per
+    // store); gemm_splitk_finish_kernel adds the planes and finishes
+    float *plane = kpart + (size_t)ks * M * out;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (rb + 32 * i >= M) continue;
+      float *pr = plane + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 v = make_float4(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1],
+                                       acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
+          *reinterpret_cast<float4 *>(pr + 32 * j + 8 * q4) = v;
+        }
+    }
+    return;
+  }
   if (y == nullptr) {
     static_for<2>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -1413,25 +1437,18 @@ void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, const ui
 template <int K>
 void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
              const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
-             int out_tiles) {
+             int out_tiles, float *kpart) {
   static_assert(K > 0, "the GEMM serves integer rates");
   const dim3 blk(GM_THREADS);
   const uint32_t m = f.mask();
-  if (f.codebook == CB_MCG) {
-    if (f.window < 16)
-      hipLaunchKernelGGL((gemm_kernel<K, CB_MCG, true>), grid, blk, 0, s, tw, xp, svh, y, ydt, zout,
-                         M, in_tiles, out_tiles, m);
-    else
-      hipLaunchKernelGGL((gemm_kernel<K, CB_MCG, false>), grid, blk, 0, s, tw, xp, svh, y, ydt,
-                         zout, M, in_tiles, out_tiles, m);
-  } else {
-    if (f.window < 16)
-      hipLaunchKernelGGL((gemm_kernel<K, CB_MUL1, true>), grid, blk, 0, s, tw, xp, svh, y, ydt,
-                         zout, M, in_tiles, out_tiles, m);
-    else
-      hipLaunchKernelGGL((gemm_kernel<K, CB_MUL1, false>), grid, blk, 0, s, tw, xp, svh, y, ydt,
-                         zout, M, in_tiles, out_tiles, m);
-  }
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, blk, 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles,
+                       m, kpart);
+  };
+  if (f.codebook == CB_MCG)
+    f.window < 16 ? go(gemm_kernel<K, CB_MCG, true>) : go(gemm_kernel<K, CB_MCG, false>);
+  else
+    f.window < 16 ? go(gemm_kernel<K, CB_MUL1, true>) : go(gemm_kernel<K, CB_MUL1, false>);
 }
 
 // Declarations of one rate's launcher instantiations.
@@ -1444,7 +1461,7 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
                        const uint32_t *, const MoeItem *, const uint32_t *, const GemvArgs &)
 #define EXL3_GEMM_GO(KK)                                                                    \
   void gemm_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
-                   const uint16_t *, void *, int, uint16_t *, int, int, int)
+                   const uint16_t *, void *, int, uint16_t *, int, int, int, float *)
 
 #ifndef EXL3_INST_K
 // instantiated in the per-rate units only

@@ -107,9 +107,19 @@ hipError_t launch_gemv_swiglu(const GemvLinear &l, const Format &f, const uint16
                               const uint16_t *u, uint16_t *h, float limit, int ydt, int rows,
                               int in, Scratch &sc, hipStream_t s);
 // GEMM (any rows): the same contract through LDS-staged decode and MFMA.
+// Grids of at most 128 tiles (small rows or outputs) split k: the
+// splits store f32 planes (kpart, gemm_split's size, private to the
+// stream) and a second launch adds them and finishes.
+constexpr int GM_SPLIT_MAX = 32;
+constexpr int GM_SPLIT_TILES = 128;  // grids above this many tiles run whole
+struct GemmSplit {
+  int splits = 1, tiles = 0;
+  size_t part_floats = 0;
+};
+GemmSplit gemm_split(int rows, int in, int out);
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
-                       int out, hipStream_t s);
+                       int out, float *kpart, size_t kpart_floats, hipStream_t s);
 // The split of one GEMV launch over weights of total output width
 // total_out: a linear of width out needs ksplit * rows * out partial floats.
 void gemv_multi_plan(int in, int total_out, bool generic, int rows, int *ksplit, int *tps);

@@ -384,21 +384,79 @@ hipError_t launch_gemv(const uint16_t *trellis, const Format &f, const void *x, 
 }
 
 
+namespace {
+// The end of a split-K GEMM: z = f16(sum of the S planes of kpart, in split
+// order), then the finish (Hadamard-128 in the reference's stage order,
+// * 1/sqrt(128) * svh, as the GEMV's) or z itself.  One wave per row, lane l
+// columns 2 l, 2 l + 1 of the block's 128.
+__global__ __launch_bounds__(512) void gemm_splitk_finish_kernel(
+    const float *__restrict__ part, int S, int M, int out, const uint16_t *__restrict__ svh,
+    void *__restrict__ y, int ydt, uint16_t *__restrict__ zout) {
+  const int cg = blockIdx.x, lane = threadIdx.x & 63;
+  const int m = blockIdx.y * 8 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const size_t plane = (size_t)M * out;
+  const float *p = part + (size_t)m * out + cg * 128 + 2 * lane;
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < S; ++k) {
+    const float2 v = *reinterpret_cast<const float2 *>(p + (size_t)k * plane);
+    s0 += v.x;
+    s1 += v.y;
+  }
+  float v0 = h2f(f2h(s0)), v1 = h2f(f2h(s1));
+  const size_t o = (size_t)m * out + cg * 128 + 2 * lane;
+  if (y == nullptr) {
+    zout[o] = f2h(v0);
+    zout[o + 1] = f2h(v1);
+    return;
+  }
+  had128_pair(v0, v1, lane);
+  const float sv0 = h2f(svh[cg * 128 + 2 * lane]), sv1 = h2f(svh[cg * 128 + 2 * lane + 1]);
+  store_out2(y, o, f2h(v0 * HAD_SCALE * sv0), f2h(v1 * HAD_SCALE * sv1), ydt);
+}
+}  // namespace
+
+// Split-K of a GEMM whose tiles fill at most half the GPU: S splits (an
+// even run of stages each) so that tiles x S reaches ~256 workgroups; their
+// f32 sums take S planes of rows x out floats.  Above 128 tiles the planes'
+// traffic costs more than the idle CUs (gate+up at 512 rows: 192 tiles,
+// 547 TFLOP/s split in two against 629 whole).
+GemmSplit gemm_split(int rows, int in, int out) {
+  GemmSplit g;
+  const int mblocks = (rows + GM_BM - 1) / GM_BM;
+  const int tiles = ((out + GM_BN - 1) / GM_BN) * mblocks;
+  const int pairs = in / 16 / 4 / 2;  // stage pairs
+  int S = tiles > GM_SPLIT_TILES ? 1 : (256 + tiles - 1) / tiles;
+  S = std::max(1, std::min(S, std::min(pairs, GM_SPLIT_MAX)));
+  g.splits = S;
+  g.tiles = tiles;
+  g.part_floats = S > 1 ? (size_t)S * rows * out : 0;
+  return g;
+}
+
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
-                       int out, hipStream_t s) {
+                       int out, float *kpart, size_t kpart_floats, hipStream_t s) {
   if (rows < 1 || in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
   if (!f.integer_rate()) return hipErrorInvalidValue;
   if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
   const int mblocks = (rows + GM_BM - 1) / GM_BM;
   if (mblocks > 65535) return hipErrorInvalidValue;
-  const dim3 grid((out + GM_BN - 1) / GM_BN, mblocks);
+  const GemmSplit sp = gemm_split(rows, in, out);
+  if (sp.splits > 1 && (kpart == nullptr || kpart_floats < sp.part_floats))
+    return hipErrorInvalidValue;
+  if (sp.splits > 1 && (rows + 7) / 8 > 65535) return hipErrorInvalidValue;
+  const dim3 grid((out + GM_BN - 1) / GM_BN, mblocks, sp.splits);
   const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
   const int it = in / 16, ot = out / 16;
   rate_dispatch(f.n / 16, [&](auto KC) {
     constexpr int K = decltype(KC)::value;
-    if constexpr (K > 0) gemm_go<K>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot);
+    if constexpr (K > 0) gemm_go<K>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, kpart);
   });
+  if (sp.splits > 1)
+    hipLaunchKernelGGL(gemm_splitk_finish_kernel, dim3(out / 128, (rows + 7) / 8), dim3(512), 0, s,
+                       kpart, sp.splits, rows, out, svh, y, ydt, zout);
   return hipGetLastError();
 }
 

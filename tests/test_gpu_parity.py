@@ -256,6 +256,23 @@ def test_gemm_full_size_sampled_rows():
     assert S.rel_fro(y[pick], yo) < 1e-3
 
 
+@pytest.mark.parametrize("rows,in_f,out_f,n", [(17, 4096, 1024, 64), (128, 4096, 4096, 64),
+                                               (300, 2048, 512, 48), (513, 1024, 256, 80)])
+def test_gemm_split_k(rows, in_f, out_f, n):
+    # grids of at most 128 tiles split k; a second launch adds the splits'
+    # planes in split order, so the result is deterministic and within the bar
+    rng = np.random.default_rng(rows + in_f)
+    lin, trellis, suh, svh = make(rng, in_f, out_f, n)
+    x = S.activations(rng, rows, in_f)
+    assert X.matmul_path(lin.weight, rows) == "gemm"
+    y1 = lin(dev_f16(x))
+    y2 = lin(dev_f16(x))
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    pick = np.unique(np.array([0, 1, rows // 2, rows - 2, rows - 1]))
+    yo = S.h2f(O.project(x[pick].astype(np.float32), trellis, suh, svh, in_f, out_f, n))
+    assert S.rel_fro(y1.float().cpu().numpy()[pick], yo) < 1e-3
+
+
 # --------------------------------------------------------------- loading
 
 def test_load_tensor_from_a_source_and_refusals():
