@@ -1150,6 +1150,119 @@ __device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
   }
 }
 
+// The end of a GEMM tile, by all THREADS threads of the workgroup (mw: this
+// wave holds accumulators, wave tile (wm, wc); the others take part in the
+// barriers and the butterflies).  Split k: the f32 sums go to their plane.
+// Else z^T is stored (y null) or finished: the Hadamard-128 on the
+// accumulators, * 1/sqrt(128) * svh, the output dtype.
+template <int THREADS>
+__device__ __forceinline__ void gemm_tile_end(f16v_t (&acc)[2][2], uint16_t *lds, bool mw, int wm,
+                                              int wc, int m0, int cg, int M, size_t out, int S,
+                                              int ks, const uint16_t *__restrict__ svh,
+                                              void *__restrict__ y, int ydt,
+                                              uint16_t *__restrict__ zout,
+                                              float *__restrict__ kpart) {
+  // acc[i][j] = z^T for columns 64 wc + 32 j .. and rows 64 wm + 32 i .. of
+  // the tile: lane l holds row (l & 31), register r column
+  // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int rb = m0 + 64 * wm + (lane & 31);
+  if (S > 1) {
+    if (!mw) return;
+    // split-K: this split's sums of rows < M go to its plane of
+    // kpart [S][M][out] (f32, row-major; four consecutive columns per
+    // store); gemm_splitk_finish_kernel adds the planes and finishes
+    float *plane = kpart + (size_t)ks * M * out;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (rb + 32 * i >= M) continue;
+      float *pr = plane + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 v = make_float4(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1],
+                                       acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
+          *reinterpret_cast<float4 *>(pr + 32 * j + 8 * q4) = v;
+        }
+    }
+    return;
+  }
+  if (y == nullptr) {
+    if (!mw) return;
+    static_for<2>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (rb + 32 * i < M) {
+        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[i][j][r]);
+      }
+    });
+    return;
+  }
+  // H_32 as the second operand: element e of fragment kk pairs with column
+  // 16 kk + 8 (e / 4) + 4 (l / 32) + e % 4 of a 32-column block (the
+  // registers 8 kk + e above), output column (l & 31).
+  h8_t hb[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int nl = 16 * kk + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      hb[kk][e] = (__builtin_popcount(nl & lane & 31) & 1) ? -1.0f16 : 1.0f16;
+    }
+  // The stage buffers are free now: the H_32 outputs go through them as f32
+  // [64 rows][GM_FLD], in four passes of 64 rows (row block i of the waves
+  // with wm / 2 == g), so the butterflies across the four 32-column blocks
+  // (two waves) can pair them.
+  float *fx = reinterpret_cast<float *>(lds);
+  static_for<4>([&](auto P) {
+    constexpr int i = decltype(P)::value & 1, g = decltype(P)::value >> 1;
+    lds_barrier();  // the previous use of the buffers is done
+    if (mw && (wm >> 1) == g) {
+      // D2_j = f16(z block j) H_32: lane l holds output column (l & 31) of
+      // block 2 wc + j, register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the
+      // wave's rows 32 i ..
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        h8_t a0, a1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a0[e] = bits<_Float16>(f2h(acc[i][j][e]));
+          a1[e] = bits<_Float16>(f2h(acc[i][j][8 + e]));
+        }
+        f16v_t zero = {};
+        f16v_t d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * (wm & 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          fx[row * GM_FLD + 32 * (2 * wc + j) + (lane & 31)] = d2[r];
+        }
+      }
+    }
+    lds_barrier();
+    // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi),
+    // then * 1/sqrt(128) * svh
+    for (int e = tid; e < 64 * 32; e += THREADS) {
+      const int row = e >> 5, cl = e & 31;
+      const float *fr = fx + row * GM_FLD + cl;
+      const float t0 = fr[0] + fr[32], t1 = fr[0] - fr[32];
+      const float t2 = fr[64] + fr[96], t3 = fr[64] - fr[96];
+      const float u[4] = {t0 + t2, t1 + t3, t0 - t2, t1 - t3};
+      const int m = m0 + 64 * (2 * g + (row >> 5)) + 32 * i + (row & 31);
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          store_out(y, (size_t)m * out + cg * 128 + 32 * j + cl,
+                    f2h((u[j] * HAD_SCALE) * h2f(svh[cg * 128 + 32 * j + cl])), ydt);
+      }
+    }
+  });
+}
+
 template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
@@ -1213,102 +1326,268 @@ __global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
     gemm_main<K, CB, MASKED, 1>(acc, lds, twc + (size_t)st0 * wstage, wstage, src, bst,
                                 xp + st0 * GM_BK, aoff, ast, ard, brd, st1 - st0, mask);
 
-  // acc[i][j] = z^T for columns 64 wc + 32 j .. and rows 64 wm + 32 i .. of
-  // the tile: lane l holds row (l & 31), register r column
-  // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
-  const int rb = m0 + 64 * wm + (lane & 31);
-  if (S > 1) {
-    // split-K: this split's sums of rows < M go to its plane of
-    // kpart [S][M][out] (f32, row-major; four consecutive columns per
-    // store); gemm_splitk_finish_kernel adds the planes and finishes
-    float *plane = kpart + (size_t)ks * M * out;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (rb + 32 * i >= M) continue;
-      float *pr = plane + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 v = make_float4(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1],
-                                       acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
-          *reinterpret_cast<float4 *>(pr + 32 * j + 8 * q4) = v;
-        }
-    }
-    return;
-  }
-  if (y == nullptr) {
-    static_for<2>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      if (rb + 32 * i < M) {
-        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) zr[32 * j + 8 * (r >> 2) + (r & 3)] = f2h(acc[i][j][r]);
+  gemm_tile_end<GM_THREADS>(acc, lds, true, wm, wc, m0, cg, M, out, S, ks, svh, y, ydt, zout,
+                            kpart);
+}
+
+// ================================================ GEMM, specialised waves
+//
+// gemm_ws_kernel: gemm_kernel's tile (256 rows x 128 columns, 64-k stages),
+// arithmetic and result, with the work split by wave.  Waves 0-7 (the MFMA
+// waves, wave tile 64 x 64) issue the MFMAs and bring the activations into
+// LDS with direct global-to-LDS loads (no registers; three A buffers, the
+// loads of stage x issued during stage x - 2).  Waves 8-15 (the decode
+// waves) decode the next stage's packed words into the other B buffer: the
+// 256 chunks of a stage, half a chunk per thread (waves 8-11 rows 0-7 of
+// each chunk's columns, waves 12-15 rows 8-15).  Four waves per SIMD: the
+// decode's VALU work issues beside the other waves' MFMAs.  One barrier per stage, as in
+// gemm_kernel.
+//
+// A buffer (unpadded, 128 bytes a row): 16-byte piece q of row R sits at
+// piece place q ^ ((R / 2) % 8), so a fragment read (rows R0 .. R0 + 15 of
+// one piece, R0 % 32 == 0) touches 16 distinct 16-byte bank groups, and
+// a load instruction fills 1 KiB (8 rows) contiguously.
+constexpr int GW_THREADS = 1024;
+constexpr int GW_BBUF = GM_BTILE * 2;         // bytes of a B buffer ([128][72] halfs)
+constexpr int GW_ABUF = GM_BM * GM_BK * 2;    // bytes of an A buffer
+constexpr int GW_A0 = 2 * GW_BBUF;            // the A buffers follow the two B buffers
+constexpr int GW_LDS_BYTES = GW_A0 + 3 * GW_ABUF;  // 132 KiB
+static_assert(64 * GM_FLD * 4 <= GW_A0, "finish exchange reaches the A buffers");
+
+// 16 bytes per lane from global memory (base + voff) straight into LDS at
+// address lds + 16 * lane.  M0 carries the LDS address (the compiler uses
+// M0 for nothing in these kernels); an LDS DMA that reads M0 right after it
+// is written needs wait states between them (the compiler's hazard check
+// does not see into asm), hence the s_nop.  vmcnt counts the load until its
+// bytes are in LDS.
+__device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds),
+               "v"(voff), "s"(base)
+               : "memory");
+}
+
+// The MFMA waves' main loop.  ax[kk]: byte address of the wave's A fragment
+// kk in A buffer 0 (row block i adds 4 KiB, buffer a adds a * GW_ABUF);
+// brd: half index of its B fragment 0 in B buffer 0; voff[u]: its
+// activation pieces (rows 32 w + 8 u + l / 8); dma0: LDS address of its
+// first load in A buffer 0.
+__device__ __forceinline__ void gw_mfma_main(f16v_t (&acc)[2][2], uint16_t *lds, const char *xpb,
+                                             const uint32_t (&voff)[4], uint32_t dma0,
+                                             const uint32_t (&ax)[4], int brd, int NS) {
+  const char *L = reinterpret_cast<const char *>(lds);
+  h8_t af[2][2], bf[2][2];
+  auto dma = [&](int st, int a, int u) {
+    lds_dma16(xpb + (size_t)st * (GM_BK * 2), voff[u], dma0 + a * GW_ABUF + u * 1024);
+  };
+  auto read_af = [&](int q, int a, int kk, int i) {
+    af[q][i] = *reinterpret_cast<const h8_t *>(L + ax[kk] + a * GW_ABUF + i * 32 * 128);
+  };
+  auto read_bf = [&](int q, int b, int kk, int j) {
+    bf[q][j] = *reinterpret_cast<const h8_t *>(lds + b * GM_BTILE + brd + j * 32 * GM_LD + 8 * kk);
+  };
+  auto stage = [&](auto PH, int st) {
+    constexpr int ph = decltype(PH)::value;
+    constexpr int a = ph % 3, b = ph & 1;                  // this stage's buffers
+    constexpr int an = (ph + 1) % 3, bn = (ph + 1) & 1;    // the next stage's
+    constexpr int a2 = (ph + 2) % 3;                       // stage st + 2's A buffer
+    const int st2 = min(st + 2, NS - 1);  // past the end: a free buffer, drained below
+    static_for<16>([&](auto SL) {
+      constexpr int s = decltype(SL)::value;
+      constexpr int kk = s >> 2, i = (s >> 1) & 1, j = s & 1;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk & 1][j], af[kk & 1][i], acc[i][j],
+                                                          0, 0, 0);
+      if constexpr (kk < 2) {
+        constexpr int qn = (kk + 1) & 1;
+        if constexpr ((s & 3) < 2) read_af(qn, a, kk + 1, s & 1);
+        if constexpr ((s & 3) >= 2) read_bf(qn, b, kk + 1, s & 1);
       }
+      if constexpr (s == 8) {
+        read_af(1, a, 3, 0);
+        read_af(1, a, 3, 1);
+      }
+      if constexpr (s == 9) {
+        read_bf(1, b, 3, 0);
+        read_bf(1, b, 3, 1);
+      }
+      if constexpr (s < 4) dma(st2, a2, s);
+      // stage st + 1's activations (loaded during stage st - 1) and B
+      // (decoded during stage st) are in, this stage's buffers are read
+      if constexpr (s == 10) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if constexpr (s == 12) {
+        read_af(0, an, 0, 0);
+        read_af(0, an, 0, 1);
+      }
+      if constexpr (s == 13) {
+        read_bf(0, bn, 0, 0);
+        read_bf(0, bn, 0, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     });
-    return;
+  };
+  // prologue: stages 0 and 1 in flight, wait for stage 0 (and its B)
+  for (int u = 0; u < 4; ++u) dma(0, 0, u);
+  for (int u = 0; u < 4; ++u) dma(1, 1, u);
+  asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  read_af(0, 0, 0, 0);
+  read_af(0, 0, 0, 1);
+  read_bf(0, 0, 0, 0);
+  read_bf(0, 0, 0, 1);
+  int st = 0;
+  for (; st + 6 <= NS; st += 6) {
+    static_for<6>([&](auto PH) { stage(PH, st + decltype(PH)::value); });
   }
-  // H_32 as the second operand: element e of fragment kk pairs with column
-  // 16 kk + 8 (e / 4) + 4 (l / 32) + e % 4 of a 32-column block (the
-  // registers 8 kk + e above), output column (l & 31).
-  h8_t hb[2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int nl = 16 * kk + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-      hb[kk][e] = (__builtin_popcount(nl & lane & 31) & 1) ? -1.0f16 : 1.0f16;
+  if (st < NS) {  // NS is even: 2 or 4 stages left
+    stage(std::integral_constant<int, 0>{}, st);
+    stage(std::integral_constant<int, 1>{}, st + 1);
+    if (st + 2 < NS) {
+      stage(std::integral_constant<int, 2>{}, st + 2);
+      stage(std::integral_constant<int, 3>{}, st + 3);
     }
-  // The stage buffers are free now: the H_32 outputs go through them as f32
-  // [64 rows][GM_FLD], in four passes of 64 rows (row block i of the waves
-  // with wm / 2 == g), so the butterflies across the four 32-column blocks
-  // (two waves) can pair them.
-  float *fx = reinterpret_cast<float *>(lds);
-  static_for<4>([&](auto P) {
-    constexpr int i = decltype(P)::value & 1, g = decltype(P)::value >> 1;
-    lds_barrier();  // the previous use of the buffers is done
-    if ((wm >> 1) == g) {
-      // D2_j = f16(z block j) H_32: lane l holds output column (l & 31) of
-      // block 2 wc + j, register r row 8 (r / 4) + 4 (l / 32) + r % 4 of the
-      // wave's rows 32 i ..
+  }
+  // no load may still write this workgroup's LDS when it ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// The decode waves' main loop: the thread decodes fragments 2 HALF and
+// 2 HALF + 1 of chunk c of output tile tnl of k-tile row tkl of every stage
+// (twc: its words in stage 0), stage st + 1 during stage st, into B buffer
+// (st + 1) % 2 at bst.
+template <int K, int CB, bool MASKED, int HALF>
+__device__ __forceinline__ void gw_decode_main(uint16_t *lds, const uint32_t *twc, size_t wstage,
+                                               int src, int bst, int NS, uint32_t mask) {
+  constexpr int WL = gm_wl<K>();
+  uint32_t wn[WL][K];
+  uint32_t hist[2];
+  auto load_w = [&](auto S, int st) {
+    constexpr int q = decltype(S)::value;
+    const uint32_t *p = twc + (size_t)min(st, NS - 1) * wstage;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        h8_t a0, a1;
+    for (int j = 0; j < K; ++j) wn[q][j] = p[j];
+  };
+  auto bperm = [&](auto S, auto HS) {
+    constexpr int q = decltype(S)::value, hq = decltype(HS)::value;
+    hist[hq] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
+  };
+  // the thread's half of the chunk of word set S (history HS) into B
+  // buffer b: two fragments
+  auto decode = [&](auto S, auto HS, int b) {
+    constexpr int q = decltype(S)::value, hq = decltype(HS)::value;
+    uint32_t wd[K + 1];
+    wd[0] = hist[hq];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          a0[e] = bits<_Float16>(f2h(acc[i][j][e]));
-          a1[e] = bits<_Float16>(f2h(acc[i][j][8 + e]));
-        }
-        f16v_t zero = {};
-        f16v_t d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, hb[0], zero, 0, 0, 0);
-        d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, hb[1], d2, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 32 * (wm & 1) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          fx[row * GM_FLD + 32 * (2 * wc + j) + (lane & 31)] = d2[r];
-        }
-      }
+    for (int j = 0; j < K; ++j) wd[j + 1] = wn[q][j];
+    static_for<2>([&](auto F) {
+      constexpr int f = 2 * HALF + decltype(F)::value;
+      uint32_t v[4];
+      static_for<4>([&](auto J) {
+        v[J] = chunk_pair_cw<K, CB, MASKED, gm_pair(f, decltype(J)::value)>(wd, mask);
+      });
+      const u4_t u = {v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<u4_t *>(lds + b * GM_BTILE + bst + 8 * (f & 1) * GM_LD + 8 * (f >> 1)) = u;
+    });
+  };
+  using IC0 = std::integral_constant<int, 0>;
+  using IC1 = std::integral_constant<int, 1>;
+  auto stage = [&](auto PH, int st) {
+    constexpr int ph = decltype(PH)::value;
+    using W0 = std::integral_constant<int, ph % WL>;
+    using W1 = std::integral_constant<int, (ph + 1) % WL>;
+    using W2 = std::integral_constant<int, (ph + 2) % WL>;
+    using H1 = std::integral_constant<int, (ph + 1) & 1>;
+    using H2 = std::integral_constant<int, ph & 1>;
+    if (st + 1 < NS) decode(W1{}, H1{}, (ph + 1) & 1);
+    load_w(W0{}, st + WL);
+    bperm(W2{}, H2{});
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  static_for<WL>([&](auto W) { load_w(W, decltype(W)::value); });
+  bperm(IC0{}, IC0{});
+  decode(IC0{}, IC0{}, 0);
+  bperm(IC1{}, IC1{});
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  int st = 0;
+  for (; st + 6 <= NS; st += 6) {
+    static_for<6>([&](auto PH) { stage(PH, st + decltype(PH)::value); });
+  }
+  if (st < NS) {
+    stage(std::integral_constant<int, 0>{}, st);
+    stage(std::integral_constant<int, 1>{}, st + 1);
+    if (st + 2 < NS) {
+      stage(std::integral_constant<int, 2>{}, st + 2);
+      stage(std::integral_constant<int, 3>{}, st + 3);
     }
-    lds_barrier();
-    // butterflies on column bits 5 and 6, in that order (lo + hi, lo - hi),
-    // then * 1/sqrt(128) * svh
-    for (int e = tid; e < 64 * 32; e += GM_THREADS) {
-      const int row = e >> 5, cl = e & 31;
-      const float *fr = fx + row * GM_FLD + cl;
-      const float t0 = fr[0] + fr[32], t1 = fr[0] - fr[32];
-      const float t2 = fr[64] + fr[96], t3 = fr[64] - fr[96];
-      const float u[4] = {t0 + t2, t1 + t3, t0 - t2, t1 - t3};
-      const int m = m0 + 64 * (2 * g + (row >> 5)) + 32 * i + (row & 31);
-      if (m < M) {
+  }
+}
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
+    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
+    int M, int in_tiles, int out_tiles, uint32_t mask, float *__restrict__ kpart) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[GW_LDS_BYTES / 2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool mw = wave < 8;
+  const int wm = (wave & 7) >> 1, wc = wave & 1;
+  const int mblocks = gridDim.y;  // row block n % (row blocks) per XCD, as gemm_kernel
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int cg = lin / mblocks;
+  const int m0 = (lin % mblocks) * GM_BM;
+  const int in = in_tiles * 16;
+  const size_t out = (size_t)out_tiles * 16;
+  constexpr int NW = 8 * K;
+  const int NS = in_tiles / 4;
+  const int S = gridDim.z, ks = blockIdx.z;
+  const int P = NS / 2;
+  const int st0 = 2 * (P * ks / S), st1 = 2 * (P * (ks + 1) / S);
+
+  f16v_t acc[2][2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          store_out(y, (size_t)m * out + cg * 128 + 32 * j + cl,
-                    f2h((u[j] * HAD_SCALE) * h2f(svh[cg * 128 + 32 * j + cl])), ydt);
-      }
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if (mw) {
+    // activation loads: rows 32 w + 8 u + l / 8 of the tile, the piece
+    // (l % 8) ^ ((row / 2) % 8) of them (rows past M read row M - 1)
+    uint32_t voff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int R = 32 * wave + 8 * u + (lane >> 3);
+      const int q = (lane & 7) ^ ((R >> 1) & 7);
+      voff[u] = (uint32_t)(((size_t)min(m0 + R, M - 1) * in + 8 * q) * 2);
     }
-  });
+    const uint32_t dma0 =
+        (uint32_t)(uintptr_t)lds + GW_A0 + (uint32_t)(32 * wave) * 128;  // 4 KiB per wave
+    // fragment reads: A row 64 wm + 32 i + (l & 31), k 32 h + 8 kk (piece
+    // 4 h + kk); B column 64 wc + 32 j + (l & 31)
+    const int h = lane >> 5;
+    uint32_t ax[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      ax[kk] = GW_A0 + (64 * wm + (lane & 31)) * 128 + 16 * ((4 * h + kk) ^ ((lane >> 1) & 7));
+    const int brd = (64 * wc + (lane & 31)) * GM_LD + 32 * h;
+    gw_mfma_main(acc, lds, reinterpret_cast<const char *>(xp + (size_t)st0 * GM_BK), voff, dma0,
+                 ax, brd, st1 - st0);
+  } else {
+    // chunk c of output tile tnl of k-tile row tkl (threads dt and dt + 256
+    // take the same chunk); the 8 chunks of a tile sit in 8 consecutive lanes
+    const int dt = (tid - 512) & 255;
+    const int tkl = dt >> 6, tnl = (dt >> 3) & 7, c = dt & 7;
+    const uint32_t *twc = tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
+    const size_t wstage = (size_t)4 * out_tiles * NW;
+    const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    const int bst = (tnl * 16 + c) * GM_LD + tkl * 16;
+    twc += (size_t)st0 * wstage;
+    if (wave < 12)
+      gw_decode_main<K, CB, MASKED, 0>(lds, twc, wstage, src, bst, st1 - st0, mask);
+    else
+      gw_decode_main<K, CB, MASKED, 1>(lds, twc, wstage, src, bst, st1 - st0, mask);
+  }
+  gemm_tile_end<GW_THREADS>(acc, lds, mw, wm, wc, m0, cg, M, out, S, ks, svh, y, ydt, zout,
+                            kpart);
 }
 
 // ==================================================== grouped MoE GEMV
@@ -1434,6 +1713,11 @@ void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, const ui
   }
 }
 
+#ifndef EXL3_GEMM_WS
+#define EXL3_GEMM_WS 1
+#endif
+constexpr bool GEMM_WAVE_SPECIALISED = EXL3_GEMM_WS != 0;
+
 template <int K>
 void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
              const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
@@ -1445,6 +1729,19 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
     hipLaunchKernelGGL(kern, grid, blk, 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles,
                        m, kpart);
   };
+  // the specialised kernel addresses the activations with 32-bit offsets
+  if (GEMM_WAVE_SPECIALISED && (size_t)M * in_tiles * 32 <= 0xFFFFFFFFu) {
+    auto gow = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, zout, M,
+                         in_tiles, out_tiles, m, kpart);
+    };
+    if (f.codebook == CB_MCG)
+      f.window < 16 ? gow(gemm_ws_kernel<K, CB_MCG, true>) : gow(gemm_ws_kernel<K, CB_MCG, false>);
+    else
+      f.window < 16 ? gow(gemm_ws_kernel<K, CB_MUL1, true>)
+                    : gow(gemm_ws_kernel<K, CB_MUL1, false>);
+    return;
+  }
   if (f.codebook == CB_MCG)
     f.window < 16 ? go(gemm_kernel<K, CB_MCG, true>) : go(gemm_kernel<K, CB_MCG, false>);
   else
