@@ -12,6 +12,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/exl3_decoder.h"
 
 namespace {
@@ -198,6 +200,23 @@ __device__ __forceinline__ void norm_rope8(float (&x)[8], const uint4 nw, const 
   }
 }
 
+// Sum over the 16 lanes of a DPP row (a key group), in every lane of it:
+// quad permutations for lanes i ^ 1 and i ^ 2, then the half-row mirror
+// (i with 7 - i) and the row mirror (i with 15 - i).  VALU data movement, no
+// LDS; every lane adds the same pairs, so all 16 hold the same value.
+__device__ __forceinline__ float row16_sum(float v) {
+  auto dpp = [](float x, auto CTRL) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), decltype(CTRL)::value, 0xF,
+                                        0xF, false));
+  };
+  v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1, 0, 3, 2]
+  v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2, 3, 0, 1]
+  v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+  return v;
+}
+
 __device__ __forceinline__ void unpack8(const uint4 raw, float (&x)[8]) {
   const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -353,8 +372,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             float sc = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sc = fmaf(qr[h][e], kf[e], sc);
-#pragma unroll
-            for (int mk = 8; mk >= 1; mk >>= 1) sc += __shfl_xor(sc, mk, 64);  // 16 lanes
+            sc = row16_sum(sc);
             const float mn = fmaxf(m[h], sc);
             const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
             l[h] = fmaf(l[h], c, pr);
