@@ -308,6 +308,25 @@ exl3_verdict exl3_finish(const exl3_weight *w, exl3_array z, exl3_array y, exl3_
  * (sushi_ds41/src/sushi/exl3/expert_exl3.zig:503-532). */
 exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_stream s);
 
+/* A Source over a pack's safetensors files: the pack loader for hosts without
+ * a Source of their own.  The reference's host (mlx-serve) hands the format an
+ * MLX Source over the same files (turboexl3_ds41/plugin.zig:86-103,127-185:
+ * <base>.trellis i16 [in/16, out/16, n], <base>.suh f16 [in], <base>.svh f16
+ * [out]); this one maps each file read-only and hands out host views into the
+ * mappings, valid until exl3_safetensors_close.  Returns NULL, with *why set
+ * (a missing file, a header past its file, offsets that disagree with a
+ * tensor's shape and dtype, an unknown dtype, a name in two files), or the
+ * source to put in exl3_load_ctx.source. */
+exl3_source *exl3_safetensors_open(const char *const *paths, uint32_t count, exl3_verdict *why);
+void exl3_safetensors_close(exl3_source *src);
+
+/* A PackDir over a directory (the kit's `dir.fileBytes(name)`,
+ * turboexl3_ds41/plugin.zig:62): file_bytes(name) = the size of root/name,
+ * 0 when absent or when name leaves the directory.  NULL if root is not a
+ * directory. */
+exl3_pack_dir *exl3_pack_dir_open(const char *root);
+void exl3_pack_dir_close(exl3_pack_dir *dir);
+
 /* Library version string and the kernel variant a matmul of `rows` rows
  * takes ("gemv", "gemm"): diagnostics for tests and benchmarks. */
 const char *exl3_version(void);

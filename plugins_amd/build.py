@@ -39,6 +39,7 @@ SOURCES = [
     ("decoder_ops.hip", "decoder_ops", DEVICE_FLAGS),
     ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
     ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
+    ("exl3_pack.cpp", "exl3_pack", HOST_FLAGS),
 ]
 
 

@@ -127,6 +127,10 @@ SIGNATURES = {
     "exl3_finish": (Verdict, [POINTER(Weight), Array, Array, c_void_p]),
     "exl3_inner": (Verdict, [POINTER(Weight), Array, Array, c_void_p]),
     "exl3_version": (c_char_p, []),
+    "exl3_safetensors_open": (c_void_p, [POINTER(c_char_p), c_uint32, POINTER(Verdict)]),
+    "exl3_safetensors_close": (None, [c_void_p]),
+    "exl3_pack_dir_open": (c_void_p, [c_char_p]),
+    "exl3_pack_dir_close": (None, [c_void_p]),
     "exl3_matmul_path": (c_char_p, [POINTER(Weight), c_int64]),
 }
 
@@ -252,6 +256,55 @@ class DictSource:
         for i, s in enumerate(a.shape):
             t.shape[i] = s
         return 1
+
+
+class SafetensorsSource:
+    """A weight source over a pack's safetensors files (exl3_safetensors_open):
+    the library maps the files and hands out host views; the same interface as
+    DictSource for Loader."""
+
+    def __init__(self, paths):
+        if isinstance(paths, (str, os.PathLike)):
+            paths = [paths]
+        enc = [os.fsencode(p) for p in paths]
+        arr = (c_char_p * len(enc))(*enc)
+        self.verdict = Verdict()
+        self.handle = lib().exl3_safetensors_open(arr, len(enc), ctypes.byref(self.verdict))
+        if not self.handle:
+            raise OSError(f"exl3_safetensors_open: {self.verdict}")
+        self.struct = ctypes.cast(self.handle, POINTER(Source)).contents
+
+    def tensor(self, name: str):
+        """The host view of `name` (dtype code, shape, data address), or None."""
+        t = HostTensor()
+        if not self.struct.tensor(self.struct.self, Str.of(name), ctypes.byref(t)):
+            return None
+        return t.dtype, tuple(t.shape[i] for i in range(t.ndim)), t.data
+
+    def close(self) -> None:
+        if self.handle:
+            lib().exl3_safetensors_close(self.handle)
+            self.handle = None
+            self.struct = None
+
+
+class PackDirectory:
+    """A PackDir over a directory (exl3_pack_dir_open): file_bytes(name)."""
+
+    def __init__(self, root):
+        self.handle = lib().exl3_pack_dir_open(os.fsencode(root))
+        if not self.handle:
+            raise OSError(f"not a directory: {root}")
+        self.struct = ctypes.cast(self.handle, POINTER(PackDir)).contents
+
+    def file_bytes(self, name: str) -> int:
+        return int(self.struct.file_bytes(self.struct.self, Str.of(name)))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().exl3_pack_dir_close(self.handle)
+            self.handle = None
+            self.struct = None
 
 
 class Loader:

@@ -302,6 +302,43 @@ def test_load_tensor_from_a_source_and_refusals():
     L.close()
 
 
+def test_load_from_safetensors_pack(tmp_path):
+    # a pack on disk (written by the `safetensors` package): one linear and a
+    # bank of three experts with its router, through exl3_safetensors_open
+    st = pytest.importorskip("safetensors.numpy")
+    rng = np.random.default_rng(81)
+    trellis, suh, svh = S.linear(rng, 256, 128, 64)
+    bank = [S.linear(rng, 256, 128, 64) for _ in range(3)]
+    f1 = {"m.q.trellis": trellis.view(np.int16), "m.q.suh": suh.view(np.float16),
+          "m.q.svh": svh.view(np.float16)}
+    f2 = {"L.mlp.gate.weight": rng.standard_normal((3, 256)).astype(np.float16)}
+    for e, (t, u, v) in enumerate(bank):
+        f2[f"L.mlp.experts.{e}.gate_proj.trellis"] = t.view(np.int16)
+        f2[f"L.mlp.experts.{e}.gate_proj.suh"] = u.view(np.float16)
+        f2[f"L.mlp.experts.{e}.gate_proj.svh"] = v.view(np.float16)
+    st.save_file(f1, str(tmp_path / "model-00001.safetensors"))
+    st.save_file(f2, str(tmp_path / "model-00002.safetensors"))
+    src = X.SafetensorsSource(sorted(tmp_path.glob("*.safetensors")))
+    L = X.Loader('{"format":"exl3","codebook":"mul1"}', src)
+    assert L.opened.is_ok(), L.opened
+    v, w = L.load_tensor("m.q", 256)
+    assert v.is_ok(), v
+    x = S.activations(rng, 5, 256)
+    y = X.matmul(w, dev_f16(x)).float().cpu().numpy()
+    yo = S.h2f(O.project(x.astype(np.float32), trellis, suh, svh, 256, 128, 64))
+    assert S.rel_fro(y, yo) < 1e-3
+    vb, wb = L.load_bank("L.mlp.experts.gate_proj", 256)
+    assert vb.is_ok(), vb
+    assert wb.w.dims() == (3, 16, 8, 64)
+    for e in range(3):
+        got = host_u16(X.decode_matrix(wb, e))
+        assert np.array_equal(got, O.reconstruct_inner(bank[e][0], 256, 128, 64)), e
+    X.release(w)
+    X.release(wb)
+    L.close()
+    src.close()
+
+
 # -------------------------------------------------------------------- MoE
 
 def _bank(rng, E, in_f, out_f, n):
