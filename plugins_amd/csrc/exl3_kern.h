@@ -1625,9 +1625,23 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
   }
   lds_barrier();
   const RowMap rm{ri, 0, 0};
-  gemv_wg<K, CB, MASKED, PREP_PASSES>(tw + (size_t)it.expert * W.expert_words, out_tiles, x, geo, a.c,
-                                W, (int)it.expert, (int)it.count, rm, blockIdx.x - ws.c0,
-                                blockIdx.y, smem + 256, MOE_ITEM_ROWS);
+  // the prepare form the item's rows need (most items hold a few slots: one
+  // batch or one pass instead of the passes 16 rows take)
+  const uint32_t *twe = tw + (size_t)it.expert * W.expert_words;
+  auto run = [&](auto P) {
+    gemv_wg<K, CB, MASKED, decltype(P)::value>(twe, out_tiles, x, geo, a.c, W, (int)it.expert,
+                                               (int)it.count, rm, blockIdx.x - ws.c0, blockIdx.y,
+                                               smem + 256, MOE_ITEM_ROWS);
+  };
+  const int items_n = (int)it.count * (geo.tps / 8);
+  if (items_n <= PREP_ITEMS)
+    run(std::integral_constant<int, 0>{});
+  else if (items_n <= PREP_GROUPS)
+    run(std::integral_constant<int, 1>{});
+  else if (items_n <= 2 * PREP_GROUPS)
+    run(std::integral_constant<int, 2>{});
+  else
+    run(std::integral_constant<int, PREP_PASSES>{});
 }
 
 // ====================================================== per-rate launchers
