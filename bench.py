@@ -332,7 +332,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the decoder tok/s leg")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the config 1-3 legs (GEMV K x batch sweep, GEMM M sweep, MoE layer)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "decode", "sweep"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "decode", "sweep", "moe"], default=None,
                     help="run one leg (gemv: the decode GEMV pass and its roofline leg only)")
     ap.add_argument("--per-linear", action="store_true",
                     help="one launch per linear instead of one per shared-input group")
@@ -348,7 +348,7 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_mib": args.copy_mib, "copies": 5}))
         return 0
-    if args.only in ("gemm", "decode", "sweep"):
+    if args.only in ("gemm", "decode", "sweep", "moe"):
         # one leg alone (for counter runs of its kernels); prints that leg's numbers
         import torch
         from plugins_amd import exl3 as X
@@ -357,6 +357,8 @@ def main() -> int:
             res = gemm_tflops(torch)
         elif args.only == "decode":
             res = decode_tok_s(torch)
+        elif args.only == "moe":
+            res = moe_bench(torch, X)
         else:
             res = {**gemv_sweep(torch, X), **gemm_sweep(torch, X), **moe_bench(torch, X)}
         print(json.dumps({"only": args.only, **res}), flush=True)
