@@ -174,18 +174,27 @@ struct GemvGeo {
     g.cg3 = (int)(g1 & 0xFFFFu);
     g.cgend = (int)(g1 >> 16);
     g.in_tiles = (int)(g2 & 0xFFFFu);
-    g.tps = (int)((g2 >> 16) & 0x7Fu);
+    g.tps = 8 * (int)((g2 >> 16) & 0x7Fu);  // stored in blocks of 8 tiles
     g.rows = (int)((g2 >> 23) & 0x1Fu);
     g.xdt = (int)((g2 >> 28) & 3u);
     g.prepared = (int)((g2 >> 30) & 1u);
     return g;
   }
 };
-inline void gemv_geo_pack(const GemvGeo &g, uint32_t *g0, uint32_t *g1, uint32_t *g2) {
+// Fields: cg1, cg2, cg3, cgend, in_tiles 16 bits each; tps / 8 in 7 bits
+// (tps a multiple of 8, at most 1016); rows 5, xdt 2, prepared 1.  False
+// when a value does not fit its field (the launchers refuse the launch).
+inline bool gemv_geo_pack(const GemvGeo &g, uint32_t *g0, uint32_t *g1, uint32_t *g2) {
+  if (g.cg1 < 0 || g.cg1 > 0xFFFF || g.cg2 < 0 || g.cg2 > 0xFFFF || g.cg3 < 0 ||
+      g.cg3 > 0xFFFF || g.cgend < 0 || g.cgend > 0xFFFF || g.in_tiles < 0 ||
+      g.in_tiles > 0xFFFF || g.tps <= 0 || g.tps % 8 != 0 || g.tps / 8 > 0x7F || g.rows < 0 ||
+      g.rows > 0x1F || g.xdt < 0 || g.xdt > 3)
+    return false;
   *g0 = (uint32_t)g.cg1 | ((uint32_t)g.cg2 << 16);
   *g1 = (uint32_t)g.cg3 | ((uint32_t)g.cgend << 16);
-  *g2 = (uint32_t)g.in_tiles | ((uint32_t)g.tps << 16) | ((uint32_t)g.rows << 23) |
-        ((uint32_t)g.xdt << 28) | ((uint32_t)g.prepared << 30);
+  *g2 = (uint32_t)g.in_tiles | ((uint32_t)(g.tps / 8) << 16) | ((uint32_t)g.rows << 23) |
+        ((uint32_t)g.xdt << 28) | ((uint32_t)(g.prepared & 1) << 30);
+  return true;
 }
 
 // Row b of a workgroup: its activations, output and partial-sum row.  A
@@ -1597,7 +1606,14 @@ struct MoeItem {
   uint32_t expert, start, count, pad;
 };
 
-constexpr int MOE_ITEM_ROWS = GEMV_ROWS;
+// Work items of up to 8 slots over splits of up to 128 k-tiles: an item's
+// rows fill at most the rows form's passes (8 rows x 16 blocks), and a
+// workgroup streams twice the weights of a dense split for its fixed costs
+// (row gathering, prepare, split-K hand-off).
+constexpr int MOE_ITEM_ROWS = 8;
+constexpr int MOE_TPS_MAX = 128;
+static_assert(MOE_ITEM_ROWS * (MOE_TPS_MAX / 8) <= PREP_PASSES * PREP_GROUPS,
+              "a work item's prepare exceeds the rows form");
 
 // Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
 // launch's weights (gate and up side by side, or down).  Raw inputs are rows

@@ -46,7 +46,8 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 
 // The GEMV split: whole 128-input blocks per split (ksplit splits of tps
 // k-tile rows) for a GEMV over `groups` weights of (in, out).
-void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps);
+// tps_max: the most k-tiles a split takes (dense GEMV 64, MoE items 128).
+void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int tps_max);
 int gemv_ksplit(int in, int out, int groups, int rows);
 // Largest row count the GEMV path serves (the MFMA M); wider calls take the GEMM.
 constexpr int GEMV_ROWS_MAX = 16;

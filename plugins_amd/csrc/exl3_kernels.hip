@@ -202,12 +202,12 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 // splits, ~512 workgroups over `groups` column groups; ~256 for more than 4
 // rows, whose split-K partial sums (rows x 128 floats per workgroup) would
 // otherwise add half the weight bytes again at 16 rows.
-void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps) {
+void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int tps_max) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
   const int target = rows > 4 ? 256 : 512;
   int ks = std::min(nb, std::max(1, (target + cgs - 1) / cgs));
-  int bps = std::min(GEMV_TPS_MAX / 8, (nb + ks - 1) / ks);  // blocks per split
+  int bps = std::min(tps_max / 8, (nb + ks - 1) / ks);  // blocks per split
   bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
   *tps = 8 * bps;
   *ksplit = (nb + bps - 1) / bps;
@@ -215,12 +215,12 @@ void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps) {
 
 int gemv_ksplit(int in, int out, int groups, int rows) {
   int ks, tps;
-  gemv_plan(in, out, groups, rows, &ks, &tps);
+  gemv_plan(in, out, groups, rows, &ks, &tps, GEMV_TPS_MAX);
   return ks;
 }
 
 void gemv_multi_plan(int in, int total_out, bool generic, int rows, int *ksplit, int *tps) {
-  gemv_plan(in, total_out, 1, rows, ksplit, tps);
+  gemv_plan(in, total_out, 1, rows, ksplit, tps, GEMV_TPS_MAX);
   if (generic && *tps > 32) {
     *tps = 32;
     *ksplit = (in / 16 + 31) / 32;
@@ -305,7 +305,7 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   geo.in_tiles = in / 16;
   geo.tps = tps;
   uint32_t g0, g1, g2;
-  gemv_geo_pack(geo, &g0, &g1, &g2);
+  if (!gemv_geo_pack(geo, &g0, &g1, &g2)) return hipErrorInvalidValue;
   const size_t lds = gemv_lds_bytes(rows, tps, generic);
   const dim3 grid(totcg, ksplit);
   const int prep = gemv_prep_form(rows, tps);
@@ -622,8 +622,8 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   L.slots = slots;
   L.max_items = std::min(a.experts, slots) + (slots + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
   const int groups = std::max(1, std::min(a.experts, slots));
-  gemv_plan(a.hidden, a.inter, 2 * groups, 1, &L.ks_gu, &L.tps_gu);
-  gemv_plan(a.inter, a.hidden, groups, 1, &L.ks_d, &L.tps_d);
+  gemv_plan(a.hidden, a.inter, 2 * groups, 1, &L.ks_gu, &L.tps_gu, MOE_TPS_MAX);
+  gemv_plan(a.inter, a.hidden, groups, 1, &L.ks_d, &L.tps_d, MOE_TPS_MAX);
   if (generic_gu && L.tps_gu > 32) {
     L.tps_gu = 32;
     L.ks_gu = (a.hidden / 16 + 31) / 32;
@@ -662,9 +662,8 @@ struct MoeGemv {
   GemvArgs a;
 };
 
-void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const MoeGemv &m,
-                     const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
-                     int topk) {
+// The launch's packed geometry; false when a field does not fit.
+bool moe_geo(const MoeGemv &m, dim3 grid, uint32_t *g0, uint32_t *g1, uint32_t *g2) {
   GemvGeo geo{};
   geo.cg1 = m.nweights > 1 ? m.out / 128 : 0;
   geo.cgend = (int)grid.x;
@@ -673,8 +672,14 @@ void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, cons
   geo.prepared = m.prepared ? 1 : 0;
   geo.in_tiles = m.in / 16;
   geo.tps = m.tps;
+  return gemv_geo_pack(geo, g0, g1, g2);
+}
+
+void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, const MoeGemv &m,
+                     const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
+                     int topk) {
   uint32_t g0, g1, g2;
-  gemv_geo_pack(geo, &g0, &g1, &g2);
+  if (!moe_geo(m, grid, &g0, &g1, &g2)) return;  // checked before the first launch
   rate_dispatch(f.integer_rate() ? f.n / 16 : 0, [&](auto KC) {
     moe_gemv_go<decltype(KC)::value>(f, grid, lds, s, m.tw[0], m.tw[1], m.x, g0, g1, g2, topk,
                                      sorted, items, n_items, m.a);
@@ -747,27 +752,30 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   uint16_t *xd = (uint16_t *)(base + L.xd), *d = (uint16_t *)(base + L.d);
   float *pgu = partial, *pd = partial + (size_t)2 * L.ks_gu * L.slots * a.inter;
 
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
-                     a.experts, sorted, items, n_items);
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
   mgu.nweights = 2;
+  MoeGemv md = moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d, L.tps_d);
+  md.nweights = 1;
+  const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, L.max_items);
+  const dim3 grid_d(a.hidden / 128, L.ks_d, L.max_items);
+  uint32_t gg[3];
+  if (!moe_geo(mgu, grid_gu, &gg[0], &gg[1], &gg[2]) || !moe_geo(md, grid_d, &gg[0], &gg[1], &gg[2]))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
+                     a.experts, sorted, items, n_items);
   mgu.tw[0] = reinterpret_cast<const uint32_t *>(gate.trellis);
   mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
   mgu.a.w[0] = moe_weight(gate, g, pgu);
   mgu.a.w[1] = moe_weight(up, u, pgu + gu_part);
-  moe_gemv_launch(gate.f, dim3(2 * (a.inter / 128), L.ks_gu, L.max_items),
-                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu, sorted, items,
-                  n_items, a.topk);
+  moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu,
+                  sorted, items, n_items, a.topk);
   hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
                      a.experts, down.suh, xd, a.inter, a.limit);
-  MoeGemv md = moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d, L.tps_d);
-  md.nweights = 1;
   md.tw[0] = md.tw[1] = reinterpret_cast<const uint32_t *>(down.trellis);
   md.a.w[0] = moe_weight(down, d, pd);
-  moe_gemv_launch(down.f, dim3(a.hidden / 128, L.ks_d, L.max_items),
-                  gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted, items, n_items,
-                  a.topk);
+  moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted,
+                  items, n_items, a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();

@@ -363,6 +363,24 @@ def test_swiglu_routed_against_oracle(rows, limit):
     assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
 
 
+def test_swiglu_routed_long_splits():
+    # enough experts and columns that the planner gives the gate+up launch
+    # 128-tile splits (the most a work item takes: 16 blocks of its rows),
+    # items of up to 8 slots; against the oracle's composition
+    rng = np.random.default_rng(77)
+    E, hidden, inter, topk, n, rows = 40, 2048, 1024, 8, 48, 8
+    g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
+    u_np, u, u_keep = _bank(rng, E, hidden, inter, n)
+    d_np, d, d_keep = _bank(rng, E, inter, hidden, n)
+    x = rng.standard_normal((rows, hidden)).astype(np.float16)
+    inds, scores = O.route_topk(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    y = X.swiglu(g, u, d, dev_f16(x).reshape(rows, 1, hidden),
+                 torch.from_numpy(inds).to(DEV).reshape(rows, 1, topk),
+                 torch.from_numpy(scores).to(DEV).reshape(rows, 1, topk))
+    want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n)
+    assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
+
+
 @pytest.mark.parametrize("rows,limit,n,dtype", [(1, 0, 64, "f16"), (3, 7, 48, "f16"),
                                                 (16, 0, 64, "f16"), (2, 0, 64, "bf16"),
                                                 (5, 3, 32, "f32"), (24, 0, 64, "f16")])
