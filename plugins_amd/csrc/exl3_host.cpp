@@ -735,6 +735,33 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
     }
     return ok();
   }
+  if (inds.data == nullptr && pg->f.integer_rate() && pu->f.integer_rate() &&
+      pd->f.integer_rate()) {
+    // Dense MLP of more rows (prefill, a shared expert at large batches):
+    // gate and up through the GEMM (f16), the SwiGLU once (the MoE path's mid
+    // step, bit for bit), the down projection through the GEMM.
+    StreamScratch *ss = scratch_for(pg->device, s);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    const size_t nel = (size_t)rows * pg->out;
+    hipError_t e = grow(&ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s, -1);
+    if (e != hipSuccess) return hip_failed(e);
+    uint16_t *gu = (uint16_t *)ss->moe;
+    const exl3_weight *ws2[2] = {gate, up};
+    const WeightPriv *pv2[2] = {pg, pu};
+    void *ys[2] = {gu, gu + nel};
+    e = run_linears(ws2, pv2, 2, x.data, xdt, false, ys, exl3::ACT_F16, nullptr, rows, ss, s);
+    if (e == hipSuccess) e = exl3::launch_swiglu(gu, gu + nel, gu + 2 * nel, nel, (float)opts->limit, s);
+    const exl3_weight *wd[1] = {down};
+    const WeightPriv *pvd[1] = {pd};
+    void *yd[1] = {out->data};
+    if (e == hipSuccess)
+      e = run_linears(wd, pvd, 1, gu + 2 * nel, exl3::ACT_F16, false, yd, xdt, nullptr, rows, ss, s);
+    if (e != hipSuccess) {
+      if (e == hipErrorInvalidValue) return kShape;
+      return hip_failed(e);
+    }
+    return ok();
+  }
   a.y = out->data;
   a.ydt = xdt;
   exl3::MoeBank bg{(const uint16_t *)gate->w.data, (const uint16_t *)gate->scales.data,

@@ -383,11 +383,13 @@ def test_swiglu_routed_long_splits():
 
 @pytest.mark.parametrize("rows,limit,n,dtype", [(1, 0, 64, "f16"), (3, 7, 48, "f16"),
                                                 (16, 0, 64, "f16"), (2, 0, 64, "bf16"),
-                                                (5, 3, 32, "f32"), (24, 0, 64, "f16")])
+                                                (5, 3, 32, "f32"), (24, 0, 64, "f16"),
+                                                (300, 5, 48, "f16"), (64, 0, 64, "bf16")])
 def test_swiglu_dense_decode_sizes(rows, limit, n, dtype):
     # the dense MLP (inds empty): up to 16 rows take gate+up in one GEMV and
-    # the down GEMV with the SwiGLU in its prepare; 24 rows take the routed
-    # path's kernels; both against the oracle's composition (clamp included)
+    # the down GEMV with the SwiGLU in its prepare; more rows take the GEMM
+    # for the three linears and the SwiGLU between; both against the
+    # oracle's composition (clamp included)
     rng = np.random.default_rng(700 + rows + limit)
     hidden, inter = 512, 1024
     tg, sg, vg = S.linear(rng, hidden, inter, n)
