@@ -1170,7 +1170,10 @@ __device__ __forceinline__ void gemm_tile_end(f16v_t (&acc)[2][2], uint16_t *lds
                                               int ks, const uint16_t *__restrict__ svh,
                                               void *__restrict__ y, int ydt,
                                               uint16_t *__restrict__ zout,
-                                              float *__restrict__ kpart) {
+                                              float *__restrict__ kpart,
+                                              const uint32_t *__restrict__ rowmap = nullptr) {
+  // output row of tile row m (< M): m, or rowmap[m] (a routed item's slots)
+  auto orow = [&](int m) -> size_t { return rowmap ? (size_t)rowmap[m] : (size_t)m; };
   // acc[i][j] = z^T for columns 64 wc + 32 j .. and rows 64 wm + 32 i .. of
   // the tile: lane l holds row (l & 31), register r column
   // 8 (r / 4) + 4 (l / 32) + r % 4 (the 32 x 32 MFMA result layout).
@@ -1202,7 +1205,7 @@ __device__ __forceinline__ void gemm_tile_end(f16v_t (&acc)[2][2], uint16_t *lds
     static_for<2>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if (rb + 32 * i < M) {
-        uint16_t *zr = zout + (size_t)(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
+        uint16_t *zr = zout + orow(rb + 32 * i) * out + cg * 128 + 64 * wc + 4 * (lane >> 5);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1265,7 +1268,7 @@ __device__ __forceinline__ void gemm_tile_end(f16v_t (&acc)[2][2], uint16_t *lds
       if (m < M) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          store_out(y, (size_t)m * out + cg * 128 + 32 * j + cl,
+          store_out(y, orow(m) * out + cg * 128 + 32 * j + cl,
                     f2h((u[j] * HAD_SCALE) * h2f(svh[cg * 128 + 32 * j + cl])), ydt);
       }
     }
@@ -1660,6 +1663,99 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     run(std::integral_constant<int, PREP_PASSES>{});
 }
 
+// Grouped GEMM over routed work items (prefill-sized expert batches): the
+// specialised-wave GEMM with workgroup (column group cg, item) taking item
+// `blockIdx.y` = (expert e, up to 256 slots sorted[start ..]): activation
+// rows gathered by slot (x holds one prepared row per slot), expert e's
+// trellis words and svh, outputs scattered to the slots' rows.  No split k.
+struct GemmGroup {
+  const uint32_t *sorted;
+  const MoeItem *items;
+  const uint32_t *n_items;
+  size_t expert_words;  // trellis dwords per expert
+};
+
+template <int K, int CB, bool MASKED>
+__global__ __launch_bounds__(GW_THREADS, 1) void gemm_grouped_kernel(
+    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
+    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, int in_tiles, int out_tiles,
+    uint32_t mask, GemmGroup gg) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[GW_LDS_BYTES / 2];
+  __shared__ uint32_t rows[GM_BM];
+  if (blockIdx.y >= *gg.n_items) return;  // the whole workgroup, before any barrier
+  const MoeItem item = gg.items[blockIdx.y];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool mw = wave < 8;
+  const int wm = (wave & 7) >> 1, wc = wave & 1;
+  const int cg = blockIdx.x;
+  const int M = (int)item.count;  // 1 .. GM_BM
+  const int in = in_tiles * 16;
+  const size_t out = (size_t)out_tiles * 16;
+  constexpr int NW = 8 * K;
+  const int NS = in_tiles / 4;
+  if (tid < GM_BM) rows[tid] = gg.sorted[item.start + min(tid, M - 1)];
+  lds_barrier();
+
+  f16v_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const uint32_t *twe = tw + (size_t)item.expert * gg.expert_words;
+  if (mw) {
+    uint32_t voff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int R = 32 * wave + 8 * u + (lane >> 3);
+      const int q = (lane & 7) ^ ((R >> 1) & 7);
+      voff[u] = (uint32_t)(((size_t)rows[R] * in + 8 * q) * 2);
+    }
+    const uint32_t dma0 = (uint32_t)(uintptr_t)lds + GW_A0 + (uint32_t)(32 * wave) * 128;
+    const int h = lane >> 5;
+    uint32_t ax[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      ax[kk] = GW_A0 + (64 * wm + (lane & 31)) * 128 + 16 * ((4 * h + kk) ^ ((lane >> 1) & 7));
+    const int brd = (64 * wc + (lane & 31)) * GM_LD + 32 * h;
+    gw_mfma_main(acc, lds, reinterpret_cast<const char *>(xp), voff, dma0, ax, brd, NS);
+  } else {
+    const int dt = (tid - 512) & 255;
+    const int tkl = dt >> 6, tnl = (dt >> 3) & 7, c = dt & 7;
+    const uint32_t *twc = twe + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
+    const size_t wstage = (size_t)4 * out_tiles * NW;
+    const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    const int bst = (tnl * 16 + c) * GM_LD + tkl * 16;
+    if (wave < 12)
+      gw_decode_main<K, CB, MASKED, 0>(lds, twc, wstage, src, bst, NS, mask);
+    else
+      gw_decode_main<K, CB, MASKED, 1>(lds, twc, wstage, src, bst, NS, mask);
+  }
+  gemm_tile_end<GW_THREADS>(acc, lds, mw, wm, wc, 0, cg, M, out, 1, 0,
+                            svh + (size_t)item.expert * out, y, ydt, nullptr, nullptr, rows);
+}
+
+template <int K>
+void gemm_grouped_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw,
+                     const uint16_t *xp, const uint16_t *svh, void *y, int ydt, int in_tiles,
+                     int out_tiles, const GemmGroup &gg) {
+  static_assert(K > 0, "the GEMM serves integer rates");
+  const uint32_t m = f.mask();
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, in_tiles,
+                       out_tiles, m, gg);
+  };
+  if (f.codebook == CB_MCG)
+    f.window < 16 ? go(gemm_grouped_kernel<K, CB_MCG, true>)
+                  : go(gemm_grouped_kernel<K, CB_MCG, false>);
+  else
+    f.window < 16 ? go(gemm_grouped_kernel<K, CB_MUL1, true>)
+                  : go(gemm_grouped_kernel<K, CB_MUL1, false>);
+}
+
 // ====================================================== per-rate launchers
 //
 // K = 1..8: an integer rate (n = 16K) with compile-time windows; K = 0: any
@@ -1786,6 +1882,9 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
   void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, const uint32_t *,            \
                        const uint32_t *, const void *, uint32_t, uint32_t, uint32_t, int,       \
                        const uint32_t *, const MoeItem *, const uint32_t *, const GemvArgs &)
+#define EXL3_GEMM_GROUPED_GO(KK)                                                             \
+  void gemm_grouped_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
+                           const uint16_t *, void *, int, int, int, const GemmGroup &)
 #define EXL3_GEMM_GO(KK)                                                                    \
   void gemm_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
                    const uint16_t *, void *, int, uint16_t *, int, int, int, float *)
@@ -1806,13 +1905,21 @@ EXL3_EXTERN_RATE(7)
 EXL3_EXTERN_RATE(8)
 #undef EXL3_EXTERN_RATE
 extern template EXL3_GEMM_GO(1);
+extern template EXL3_GEMM_GROUPED_GO(1);
 extern template EXL3_GEMM_GO(2);
+extern template EXL3_GEMM_GROUPED_GO(2);
 extern template EXL3_GEMM_GO(3);
+extern template EXL3_GEMM_GROUPED_GO(3);
 extern template EXL3_GEMM_GO(4);
+extern template EXL3_GEMM_GROUPED_GO(4);
 extern template EXL3_GEMM_GO(5);
+extern template EXL3_GEMM_GROUPED_GO(5);
 extern template EXL3_GEMM_GO(6);
+extern template EXL3_GEMM_GROUPED_GO(6);
 extern template EXL3_GEMM_GO(7);
+extern template EXL3_GEMM_GROUPED_GO(7);
 extern template EXL3_GEMM_GO(8);
+extern template EXL3_GEMM_GROUPED_GO(8);
 #endif
 
 }  // namespace exl3

@@ -511,7 +511,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *t
 
 __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(
     const uint32_t *__restrict__ inds, int slots, int experts, uint32_t *__restrict__ sorted,
-    MoeItem *__restrict__ items, uint32_t *__restrict__ n_items) {
+    MoeItem *__restrict__ items, uint32_t *__restrict__ n_items, uint32_t item_rows) {
   __shared__ uint32_t cnt[MOE_ROUTE_THREADS], cur[MOE_ROUTE_THREADS], tmp[MOE_ROUTE_THREADS / 64];
   __shared__ uint32_t total;
   const int t = threadIdx.x;
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(
   __syncthreads();
   const uint32_t c = t < experts ? cnt[t] : 0u;
   const uint32_t off = block_exclusive_scan(c, tmp, &total);
-  const uint32_t nit = (c + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
+  const uint32_t nit = (c + item_rows - 1) / item_rows;
   const uint32_t ioff = block_exclusive_scan(nit, tmp, &total);
   cur[t] = off;
   __syncthreads();
@@ -535,12 +535,44 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(
   for (uint32_t r = 0; r < nit; ++r) {
     MoeItem it;
     it.expert = (uint32_t)t;
-    it.start = off + r * MOE_ITEM_ROWS;
-    it.count = min((uint32_t)MOE_ITEM_ROWS, c - r * MOE_ITEM_ROWS);
+    it.start = off + r * item_rows;
+    it.count = min(item_rows, c - r * item_rows);
     it.pad = 0;
     items[ioff + r] = it;
   }
   if (t == 0) *n_items = total;
+}
+
+// The grouped GEMM's gate and up inputs: slot s's row x[s / topk] prepared
+// with expert e = inds[s]'s suh of each (as prepare_kernel: f16(x) * suh,
+// Hadamard-128, * 1/sqrt(128), f16), one wave per 128-block.
+__global__ __launch_bounds__(256) void moe_prep_kernel(const void *__restrict__ x, int xdt,
+                                                       const uint32_t *__restrict__ inds,
+                                                       int experts, int topk,
+                                                       const uint16_t *__restrict__ suh_g,
+                                                       const uint16_t *__restrict__ suh_u,
+                                                       uint16_t *__restrict__ xg,
+                                                       uint16_t *__restrict__ xu, int in,
+                                                       int nblk) {
+  const int lane = threadIdx.x & 63;
+  const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= nblk) return;  // whole waves
+  const size_t slot = blockIdx.y;
+  const uint32_t e = inds[slot];
+  if (e >= (uint32_t)experts) return;
+  const int k = blk * 128 + 2 * lane;
+  const size_t xrow = (slot / (size_t)topk) * in;
+  const float x0 = h2f(f2h(load_act(x, xrow + k, xdt))), x1 = h2f(f2h(load_act(x, xrow + k + 1, xdt)));
+  const uint16_t *const su[2] = {suh_g + (size_t)e * in, suh_u + (size_t)e * in};
+  uint16_t *const dst[2] = {xg, xu};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const uint32_t sv = *reinterpret_cast<const uint32_t *>(su[w] + k);
+    float v0 = x0 * h2f((uint16_t)(sv & 0xFFFFu)), v1 = x1 * h2f((uint16_t)(sv >> 16));
+    had128_pair(v0, v1, lane);
+    *reinterpret_cast<uint32_t *>(dst[w] + slot * in + k) =
+        (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+  }
 }
 
 // h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e].
@@ -609,10 +641,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
 namespace {
 
 struct MoeLayout {
-  size_t sorted, items, n_items, g, u, xd, d, total;
+  size_t sorted, items, n_items, g, u, xd, d, xg, xu, total;
   size_t partial_floats;  // slots in the separate slot buffer: gate, up, down
   int slots, max_items, ks_gu, ks_d, tps_gu, tps_d;
+  bool gemm;  // prefill-sized expert batches: grouped GEMMs over 256-slot items
 };
+
+// Grouped GEMMs when the slots average at least this many per expert (and
+// every rate is an integer rate).  Switched off: a run at the DeepSeek-V3
+// prefill shape (7168 -> 2048, 256 experts, 1024+ tokens) faulted the GPU and
+// its cause is not found; the routed GEMV items serve every batch until it is.
+constexpr bool MOE_GROUPED_GEMM = false;
+constexpr int MOE_GEMM_SLOTS_PER_EXPERT = 32;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -620,7 +660,10 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   MoeLayout L{};
   const int slots = a.rows * a.topk;
   L.slots = slots;
-  L.max_items = std::min(a.experts, slots) + (slots + MOE_ITEM_ROWS - 1) / MOE_ITEM_ROWS;
+  L.gemm = MOE_GROUPED_GEMM && !generic_gu && !generic_d && a.inds != nullptr &&
+           (long)slots >= (long)MOE_GEMM_SLOTS_PER_EXPERT * a.experts;
+  const int item_rows = L.gemm ? GM_BM : MOE_ITEM_ROWS;
+  L.max_items = std::min(a.experts, slots) + (slots + item_rows - 1) / item_rows;
   const int groups = std::max(1, std::min(a.experts, slots));
   gemv_plan(a.hidden, a.inter, 2 * groups, 1, &L.ks_gu, &L.tps_gu, MOE_TPS_MAX);
   gemv_plan(a.inter, a.hidden, groups, 1, &L.ks_d, &L.tps_d, MOE_TPS_MAX);
@@ -645,8 +688,13 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   L.u = take((size_t)slots * a.inter * 2);
   L.xd = take((size_t)slots * a.inter * 2);
   L.d = take((size_t)slots * a.hidden * 2);
+  if (L.gemm) {
+    L.xg = take((size_t)slots * a.hidden * 2);
+    L.xu = take((size_t)slots * a.hidden * 2);
+  }
   L.total = o;
-  L.partial_floats = (size_t)2 * L.ks_gu * slots * a.inter + (size_t)L.ks_d * slots * a.hidden;
+  L.partial_floats = L.gemm ? 1
+                            : (size_t)2 * L.ks_gu * slots * a.inter + (size_t)L.ks_d * slots * a.hidden;
   return L;
 }
 
@@ -752,6 +800,34 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   uint16_t *xd = (uint16_t *)(base + L.xd), *d = (uint16_t *)(base + L.d);
   float *pgu = partial, *pd = partial + (size_t)2 * L.ks_gu * L.slots * a.inter;
 
+  if (L.gemm) {
+    // prefill-sized expert batches: per-slot prepared rows, grouped GEMMs
+    // gate and up, the mid step, grouped GEMM down, the weighted sum
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
+                       a.experts, sorted, items, n_items, (uint32_t)GM_BM);
+    uint16_t *xg = (uint16_t *)(base + L.xg), *xu = (uint16_t *)(base + L.xu);
+    const int nblk = a.hidden / 128;
+    hipLaunchKernelGGL(moe_prep_kernel, dim3((nblk + 3) / 4, L.slots), dim3(256), 0, s, a.x,
+                       a.xdt, a.inds, a.experts, a.topk, gate.suh, up.suh, xg, xu, a.hidden, nblk);
+    auto grouped = [&](const MoeBank &b, const uint16_t *xp, uint16_t *yo) {
+      GemmGroup gg{sorted, items, n_items, (size_t)(b.in / 16) * (b.out / 16) * (b.f.n / 2)};
+      const dim3 grid(b.out / 128, L.max_items);
+      const uint32_t *tw = reinterpret_cast<const uint32_t *>(b.trellis);
+      rate_dispatch(b.f.n / 16, [&](auto KC) {
+        constexpr int K = decltype(KC)::value;
+        if constexpr (K > 0)
+          gemm_grouped_go<K>(b.f, grid, s, tw, xp, b.svh, yo, OUT_F16, b.in / 16, b.out / 16, gg);
+      });
+    };
+    grouped(gate, xg, g);
+    grouped(up, xu, u);
+    hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
+                       a.experts, down.suh, xd, a.inter, a.limit);
+    grouped(down, xd, d);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s,
+                       d, a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
+    return hipGetLastError();
+  }
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
   mgu.nweights = 2;
@@ -763,7 +839,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   if (!moe_geo(mgu, grid_gu, &gg[0], &gg[1], &gg[2]) || !moe_geo(md, grid_d, &gg[0], &gg[1], &gg[2]))
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
-                     a.experts, sorted, items, n_items);
+                     a.experts, sorted, items, n_items, (uint32_t)MOE_ITEM_ROWS);
   mgu.tw[0] = reinterpret_cast<const uint32_t *>(gate.trellis);
   mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
   mgu.a.w[0] = moe_weight(gate, g, pgu);

@@ -14,6 +14,7 @@ template EXL3_GEMV_GO(EXL3_INST_K);
 template EXL3_MOE_GEMV_GO(EXL3_INST_K);
 #if EXL3_INST_K > 0
 template EXL3_GEMM_GO(EXL3_INST_K);
+template EXL3_GEMM_GROUPED_GO(EXL3_INST_K);
 #endif
 
 }  // namespace exl3

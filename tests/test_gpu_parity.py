@@ -363,6 +363,26 @@ def test_swiglu_routed_against_oracle(rows, limit):
     assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
 
 
+@pytest.mark.parametrize("E,topk,rows,limit", [(4, 2, 128, 0), (2, 1, 600, 0), (3, 2, 200, 7)])
+def test_swiglu_routed_prefill_sizes(E, topk, rows, limit):
+    # prefill-sized expert batches (32+ slots per expert on average, an
+    # expert past 256 slots): the routed GEMV items (the grouped-GEMM form
+    # for these batches is switched off), against the oracle's composition
+    rng = np.random.default_rng(E * 1000 + rows + limit)
+    hidden, inter, n = 512, 256, 48
+    g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
+    u_np, u, u_keep = _bank(rng, E, hidden, inter, n)
+    d_np, d, d_keep = _bank(rng, E, inter, hidden, n)
+    x = (rng.standard_normal((rows, hidden)) * (20.0 if limit else 1.0)).astype(np.float16)
+    inds, scores = O.route_topk(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    y = X.swiglu(g, u, d, dev_f16(x).reshape(rows, 1, hidden),
+                 torch.from_numpy(inds).to(DEV).reshape(rows, 1, topk),
+                 torch.from_numpy(scores).to(DEV).reshape(rows, 1, topk), limit=limit)
+    want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n,
+                        limit=float(limit))
+    assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
+
+
 def test_swiglu_routed_long_splits():
     # enough experts and columns that the planner gives the gate+up launch
     # 128-tile splits (the most a work item takes: 16 blocks of its rows),
