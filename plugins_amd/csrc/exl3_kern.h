@@ -1373,6 +1373,9 @@ static_assert(64 * GM_FLD * 4 <= GW_A0, "finish exchange reaches the A buffers")
 // does not see into asm), hence the s_nop.  vmcnt counts the load until its
 // bytes are in LDS.
 __device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint32_t lds) {
+  // M0 is not named as clobbered: the AMDGPU backend reserves it and ignores
+  // (with a warning) such a clobber; no other instruction in the kernels that
+  // call this reads M0 (their gfx950 code sets it only here).
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds),
                "v"(voff), "s"(base)
                : "memory");
