@@ -78,11 +78,83 @@ __global__ __launch_bounds__(64) void finish_kernel(const uint16_t *__restrict__
   finish_row_wave(z + off, svh + blockIdx.x * 128, y, ydt, off, threadIdx.x);
 }
 
+// prepare_kernel's rotation with 8 elements per lane and 16-byte accesses:
+// a 128-block is 16 lanes, element 8 j + i in lane j's register i.  The
+// butterflies on element bits 0-2 run in registers, bits 3-6 across the 16
+// lanes, in had128_pair's stage order and with its sums (lo + hi, lo - hi),
+// so the results are identical.  Block gb of the flattened [rows][in / 128]
+// starts at element 128 gb.  x, suh and xp must be 16-byte aligned.
+__global__ __launch_bounds__(256) void prepare8_kernel(const void *__restrict__ x, int xdt,
+                                                       const uint16_t *__restrict__ suh,
+                                                       uint16_t *__restrict__ xp, int nblk,
+                                                       uint32_t nblocks) {
+  const int j = threadIdx.x & 15;
+  const uint32_t gb0 = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const bool valid = gb0 < nblocks;  // a 16-lane group is valid or not as a whole
+  const uint32_t gb = valid ? gb0 : nblocks - 1;
+  const size_t off = (size_t)gb * 128 + 8 * j;
+  const int k = (int)(gb % (uint32_t)nblk) * 128 + 8 * j;
+  float v[8];
+  if (xdt == OUT_F32) {
+    const float4 a = *reinterpret_cast<const float4 *>((const float *)x + off);
+    const float4 b = *reinterpret_cast<const float4 *>((const float *)x + off + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4 *>((const uint16_t *)x + off);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = (uint16_t)(ws[i] & 0xFFFFu), hi = (uint16_t)(ws[i] >> 16);
+      v[2 * i] = xdt == OUT_F16 ? h2f(lo) : bf2f(lo);
+      v[2 * i + 1] = xdt == OUT_F16 ? h2f(hi) : bf2f(hi);
+    }
+  }
+  const uint4 su = *reinterpret_cast<const uint4 *>(suh + k);
+  const uint32_t ss[4] = {su.x, su.y, su.z, su.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f(f2h(v[2 * i])) * h2f((uint16_t)(ss[i] & 0xFFFFu));
+    v[2 * i + 1] = h2f(f2h(v[2 * i + 1])) * h2f((uint16_t)(ss[i] >> 16));
+  }
+#pragma unroll
+  for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if ((i & b) == 0) {
+        const float lo = v[i], hi = v[i + b];
+        v[i] = lo + hi;
+        v[i + b] = lo - hi;
+      }
+#pragma unroll
+  for (int bit = 1; bit <= 8; bit <<= 1) {
+    const bool lower = (j & bit) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = __shfl_xor(v[i], bit, 64);
+      v[i] = lower ? v[i] + p : p - v[i];
+    }
+  }
+  if (valid) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f2h(v[2 * i] * HAD_SCALE) | ((uint32_t)f2h(v[2 * i + 1] * HAD_SCALE) << 16);
+    *reinterpret_cast<uint4 *>(xp + off) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t *xp, int rows,
                           int in, hipStream_t s) {
   if (rows <= 0 || in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
   if (rows > 65535) return hipErrorInvalidValue;
   const int nblk = in / 128;
+  const size_t nblocks = (size_t)rows * nblk;
+  const bool aligned = (((uintptr_t)x | (uintptr_t)suh | (uintptr_t)xp) & 15) == 0;
+  if (aligned && nblocks * 16 < ((size_t)1 << 31)) {
+    hipLaunchKernelGGL(prepare8_kernel, dim3((unsigned)((nblocks + 15) / 16)), dim3(256), 0, s, x,
+                       xdt, suh, xp, nblk, (uint32_t)nblocks);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(prepare_kernel, dim3((nblk + 3) / 4, rows), dim3(256), 0, s, x, xdt, suh, xp,
                      in, nblk);
   return hipGetLastError();

@@ -104,13 +104,21 @@ def test_decode_matrix_reference_frac_tiles(n):
 # ------------------------------------------------------- prepare / finish
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
-def test_prepare_bit_exact(dtype):
+@pytest.mark.parametrize("rows,shift", [(5, 0), (37, 0), (37, 1)])
+def test_prepare_bit_exact(dtype, rows, shift):
+    """37 rows of 4 blocks: the last group of 16 blocks is partly past the end;
+    shift 1 starts x one element into its buffer (not 16-byte aligned), which
+    takes the one-pair-per-lane kernel instead of the 16-byte one."""
     rng = np.random.default_rng(3)
     lin, _, suh, _ = make(rng, 512, 128, 64)
-    x32 = (rng.standard_normal((5, 512)) * 3).astype(np.float32)
+    x32 = (rng.standard_normal((rows, 512)) * 3).astype(np.float32)
     tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dtype]
     x = torch.from_numpy(x32).to(tdt)
-    xp = host_u16(X.prepare(lin.weight, x.to(DEV)))
+    buf = torch.zeros(rows * 512 + shift, dtype=tdt, device=DEV)
+    xd = buf[shift:].view(rows, 512)
+    xd.copy_(x.to(DEV))
+    assert (xd.data_ptr() % 16 == 0) == (shift == 0)
+    xp = host_u16(X.prepare(lin.weight, xd))
     want = O.prepare(x.float().numpy(), suh)
     np.testing.assert_array_equal(xp, want)
 
