@@ -872,6 +872,26 @@ const char *exl3_matmul_path(const exl3_weight *w, int64_t rows) {
   return pv->f.integer_rate() ? "gemm" : "gemv";
 }
 
+const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
+                             const exl3_weight *down, int64_t rows, int32_t topk) {
+  const WeightPriv *pg = priv_of(gate), *pu = priv_of(up), *pd = priv_of(down);
+  if (!pg || !pu || !pd || rows <= 0) return "none";
+  if (topk <= 0) {
+    if (rows <= exl3::GEMV_ROWS_MAX && pg->f.codebook == pu->f.codebook &&
+        pg->f.window == pu->f.window)
+      return "dense-gemv";
+    if (pg->f.integer_rate() && pu->f.integer_rate() && pd->f.integer_rate()) return "dense-gemm";
+    return "dense-items";
+  }
+  exl3::MoeArgs a{};
+  a.rows = (int)rows;
+  a.topk = (int)topk;
+  a.experts = (int)std::max<int64_t>(pg->experts, 1);
+  a.inds = reinterpret_cast<const uint32_t *>(&a);  // routed: any non-null
+  return exl3::moe_uses_gemm(a, !pg->f.integer_rate(), !pd->f.integer_rate()) ? "routed-gemm"
+                                                                              : "routed-gemv";
+}
+
 static exl3_verdict register_kernels(const void *host) {
   (void)host;
   return ok();

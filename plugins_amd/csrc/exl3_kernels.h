@@ -151,6 +151,10 @@ struct MoeArgs {
   void *y;
   int ydt;
 };
+// Whether a routed call takes the grouped GEMM (prefill-sized expert
+// batches: at least 32 slots per expert on average, integer rates) rather
+// than the grouped GEMV's items of up to 8 slots.
+bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic);
 // Staging bytes for a call, and (in *partial_floats) the partial-sum slots
 // it needs (a Scratch slot buffer: empty between calls, left empty).
 size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,

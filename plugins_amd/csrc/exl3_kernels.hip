@@ -720,20 +720,26 @@ struct MoeLayout {
 };
 
 // Grouped GEMMs when the slots average at least this many per expert (and
-// every rate is an integer rate).  Switched off: a run at the DeepSeek-V3
-// prefill shape (7168 -> 2048, 256 experts, 1024+ tokens) faulted the GPU and
-// its cause is not found; the routed GEMV items serve every batch until it is.
-constexpr bool MOE_GROUPED_GEMM = false;
+// every rate is an integer rate); below, the routed GEMV items.
 constexpr int MOE_GEMM_SLOTS_PER_EXPERT = 32;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic) {
+  const long slots = (long)a.rows * a.topk;
+  return !gu_generic && !d_generic && a.inds != nullptr &&
+         slots >= (long)MOE_GEMM_SLOTS_PER_EXPERT * a.experts;
+}
+
+namespace {
 
 MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   MoeLayout L{};
   const int slots = a.rows * a.topk;
   L.slots = slots;
-  L.gemm = MOE_GROUPED_GEMM && !generic_gu && !generic_d && a.inds != nullptr &&
-           (long)slots >= (long)MOE_GEMM_SLOTS_PER_EXPERT * a.experts;
+  L.gemm = moe_uses_gemm(a, generic_gu, generic_d);
   const int item_rows = L.gemm ? GM_BM : MOE_ITEM_ROWS;
   L.max_items = std::min(a.experts, slots) + (slots + item_rows - 1) / item_rows;
   const int groups = std::max(1, std::min(a.experts, slots));

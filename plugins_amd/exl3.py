@@ -132,6 +132,7 @@ SIGNATURES = {
     "exl3_pack_dir_open": (c_void_p, [c_char_p]),
     "exl3_pack_dir_close": (None, [c_void_p]),
     "exl3_matmul_path": (c_char_p, [POINTER(Weight), c_int64]),
+    "exl3_swiglu_path": (c_char_p, [POINTER(Weight), POINTER(Weight), POINTER(Weight), c_int64, c_int32]),
 }
 
 _lib = None
@@ -343,12 +344,18 @@ def release(w: Weight) -> None:
 
 
 def wrap(trellis, suh, svh, codebook: str = "mul1", window: int = 16, device: int = 0) -> Weight:
-    """A Weight over device tensors the caller keeps alive (borrowed)."""
+    """A Weight over device tensors (the library borrows their memory).  The
+    returned Weight holds references to the three tensors, so the memory it
+    points at stays allocated for as long as the Weight object lives, even
+    when the caller passed temporaries (a freed block could otherwise be
+    handed to the next allocation, or returned to the driver by
+    torch.cuda.empty_cache(), which torch.cuda.graph() calls on entry)."""
     w = Weight()
     block = json.dumps({"format": "exl3", "codebook": codebook, "window": window})
     tdt = DT_U16 if str(trellis.dtype) in ("torch.int16", "torch.uint16") else dtype_of(trellis)
     check(lib().exl3_weight_wrap(array(trellis, tdt), array(suh), array(svh), Str.of(block), device,
                                  ctypes.byref(w)), "weight_wrap")
+    w._keep = (trellis, suh, svh)
     return w
 
 
@@ -431,6 +438,12 @@ def inner(w: Weight, xp, stream=None):
 
 def matmul_path(w: Weight, rows: int) -> str:
     return lib().exl3_matmul_path(ctypes.byref(w), rows).decode()
+
+
+def swiglu_path(gate: Weight, up: Weight, down: Weight, rows: int, topk: int = 0) -> str:
+    """The kernel path a swiglu call takes (topk 0: dense, no routes)."""
+    return lib().exl3_swiglu_path(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), rows,
+                                  topk).decode()
 
 
 class Linear:

@@ -44,6 +44,28 @@ def public_weight(w_inner_f16_bits, suh, svh) -> np.ndarray:
     return h2f(suh).astype(np.float64)[:, None] * Wr * h2f(svh).astype(np.float64)[None, :]
 
 
+def public_matmul(x, w_inner_f16_bits, suh, svh) -> np.ndarray:
+    """x @ W_public in float64 with W_public = diag(suh) H W_inner H diag(svh)
+    applied factor by factor (the same product as public_weight, without
+    forming the dense matrix): ((x * suh) H) W_inner H * svh, H the
+    orthonormal 128-point Hadamard per block (symmetric)."""
+    H = hadamard(128) / np.sqrt(128.0)
+    x64 = np.asarray(x, np.float64) * h2f(suh).astype(np.float64)
+    rows, in_f = x64.shape
+    xh = (x64.reshape(rows, in_f // 128, 128) @ H).reshape(rows, in_f)
+    z = xh @ h2f(w_inner_f16_bits).astype(np.float64)
+    out_f = z.shape[1]
+    zh = (z.reshape(rows, out_f // 128, 128) @ H).reshape(rows, out_f)
+    return zh * h2f(svh).astype(np.float64)
+
+
+def row_rel(a, b) -> np.ndarray:
+    """Relative Frobenius error of each row of a against b."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.linalg.norm(a - b, axis=-1) / np.maximum(np.linalg.norm(b, axis=-1), 1e-30)
+
+
 def rel_fro(a, b) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
