@@ -327,6 +327,34 @@ void exl3_safetensors_close(exl3_source *src);
 exl3_pack_dir *exl3_pack_dir_open(const char *root);
 void exl3_pack_dir_close(exl3_pack_dir *dir);
 
+/* Frees the library's scratch for (device, stream): prepared rows, split-K
+ * slots and counters, MoE staging, and every smaller buffer a growing call
+ * replaced.  The library keeps scratch per (device, stream) and, when a call
+ * needs more, makes a larger buffer and keeps the old one (a HIP graph
+ * captured earlier on the stream may still read it), so growth never
+ * invalidates a captured graph; call this once no graph captured on the
+ * stream will be replayed again (e.g. before destroying the stream).  The
+ * next call on the stream makes its scratch anew.  Refused while the stream
+ * is being captured.  No counterpart in the reference (MLX owns its
+ * temporaries there). */
+exl3_verdict exl3_scratch_release(int32_t device, exl3_stream s);
+
+/* Status of the split-K hand-offs of (device, stream)'s calls since the last
+ * check.  A GEMV or routed-MoE launch that splits k has the workgroup of the
+ * last split wait for the other splits' partial sums; the wait is bounded,
+ * and one that gives up (a partial sum that never arrived) leaves NaN in its
+ * outputs and sets a status word instead of blocking.  This synchronizes the
+ * stream, returns FAILED (with the reason) if any wait gave up, and then
+ * resets the slots so later calls are sound; ok otherwise.  No counterpart
+ * in the reference (MLX's kernels do not hand off across workgroups). */
+exl3_verdict exl3_stream_status(int32_t device, exl3_stream s);
+
+/* Diagnostic: the split-K wait's bound in polls for launches issued from now
+ * on (a negative value restores the default, about 2^20 polls).  Lowering it
+ * to 0 makes waits give up whenever a partial sum has not landed yet, which
+ * tests of exl3_stream_status use; every kernel still exits normally. */
+void exl3_set_splitk_poll_bound(int32_t polls);
+
 /* Library version string and the kernel variant a matmul of `rows` rows
  * takes ("gemv", "gemm"): diagnostics for tests and benchmarks. */
 const char *exl3_version(void);

@@ -141,42 +141,79 @@ exl3_array make_array(void *data, int dt, std::initializer_list<int64_t> shape, 
 
 // -------------------------------------------------------------- scratch
 
-// Device scratch per (device, stream): prepared rows, split-K partial-sum
-// slots (GEMV and MoE alike), MoE staging.  Grown on demand (after draining
-// the stream); the slots are set to all-ones bytes (the kernels' empty mark)
-// when allocated, and each use leaves them so.
+// Device scratch per (device, stream): prepared rows, GEMM split-K planes,
+// the GEMV/MoE slot buffer (a header with the split-K status word, then the
+// partial-sum slots, all-ones bytes when made and left so by every call), MoE
+// staging.  Calls on one
+// stream take its lock; calls on different streams or devices run
+// independently.  A buffer that must grow is replaced by a larger one (at
+// least twice the size) and the old one is kept, not freed, until
+// exl3_scratch_release: a HIP graph captured earlier on the stream may still
+// point at it.  Growing while the stream is being captured is refused (the
+// allocation and its fill cannot be captured): run the call once outside the
+// capture first.
 struct StreamScratch {
+  std::mutex mu;
   void *xp = nullptr;
   size_t xp_bytes = 0;
-  void *kpart = nullptr;  // GEMM split-K planes
+  void *kpart = nullptr;
   size_t kpart_bytes = 0;
-  void *partial = nullptr;
-  size_t partial_bytes = 0;
+  void *slots = nullptr;
+  size_t slot_bytes = 0;
   void *moe = nullptr;
   size_t moe_bytes = 0;
+  std::vector<void *> retired;  // superseded buffers, freed by exl3_scratch_release
+  // superseded slot buffers (each with its own status word and slots)
+  std::vector<std::pair<void *, size_t>> retired_slots;
 };
 
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, StreamScratch> g_scratch;
 
-// fill: the byte every new allocation is set to, or -1 for none.
-hipError_t grow(void **p, size_t *have, size_t need, hipStream_t s, int fill) {
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+hipError_t grow(StreamScratch *ss, void **p, size_t *have, size_t need, hipStream_t s) {
   if (*have >= need && *p != nullptr) return hipSuccess;
-  if (*p != nullptr) {
-    hipError_t e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return e;
-    (void)hipFree(*p);
-    *p = nullptr;
-    *have = 0;
-  }
-  size_t bytes = std::max<size_t>(need, 256);
-  hipError_t e = hipMalloc(p, bytes);
+  if (capturing(s)) return hipErrorStreamCaptureUnsupported;
+  const size_t bytes = std::max<size_t>({need, 2 * *have, 256});
+  void *fresh = nullptr;
+  hipError_t e = hipMalloc(&fresh, bytes);
   if (e != hipSuccess) return e;
-  if (fill >= 0) {
-    e = hipMemsetAsync(*p, fill, bytes, s);
-    if (e != hipSuccess) return e;
-  }
+  if (*p != nullptr) ss->retired.push_back(*p);
+  *p = fresh;
   *have = bytes;
+  return hipSuccess;
+}
+
+// The stream's slot buffer with room for `pf` partial-sum floats, as one
+// exl3::Scratch: a header with the status word (zero when made), then the
+// slots (the empty mark, all-ones bytes, when made).
+hipError_t slots_for(StreamScratch *ss, size_t pf, hipStream_t s, exl3::Scratch *out) {
+  const size_t have = ss->slots ? (ss->slot_bytes - exl3::SLOT_HEADER_BYTES) / 4 : 0;
+  if (ss->slots == nullptr || pf > have) {
+    if (capturing(s)) return hipErrorStreamCaptureUnsupported;
+    const size_t p2 = std::max<size_t>({pf, 2 * have, 64});
+    const size_t bytes = exl3::SLOT_HEADER_BYTES + p2 * 4;
+    void *fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, bytes);
+    if (e != hipSuccess) return e;
+    e = hipMemsetAsync(fresh, 0, exl3::SLOT_HEADER_BYTES, s);
+    if (e == hipSuccess)
+      e = hipMemsetAsync((char *)fresh + exl3::SLOT_HEADER_BYTES, 0xFF, p2 * 4, s);
+    if (e != hipSuccess) {
+      (void)hipFree(fresh);
+      return e;
+    }
+    if (ss->slots != nullptr) ss->retired_slots.push_back({ss->slots, ss->slot_bytes});
+    ss->slots = fresh;
+    ss->slot_bytes = bytes;
+  }
+  out->status = (uint32_t *)ss->slots;
+  out->partial = (float *)((char *)ss->slots + exl3::SLOT_HEADER_BYTES);
+  out->partial_floats = (ss->slot_bytes - exl3::SLOT_HEADER_BYTES) / 4;
   return hipSuccess;
 }
 
@@ -186,7 +223,11 @@ StreamScratch *scratch_for(int device, hipStream_t s) {
 }
 
 exl3_verdict hip_failed(hipError_t e) {
-  (void)e;
+  if (e == hipErrorStreamCaptureUnsupported)
+    return refuse(EXL3_FAILED,
+                  "turboexl3_mi355x: scratch must grow while the stream is being captured; run the "
+                  "call once outside the capture first");
+  if (e == hipErrorOutOfMemory) return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
   return refuse(EXL3_FAILED, "turboexl3_mi355x: a HIP call failed");
 }
 
@@ -494,22 +535,39 @@ static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t las
   return ok();
 }
 
-// Scratch of one GEMV launch over `count` linears of widths outs[] for
-// `rows` rows: partial-sum slots, split per linear.
-static hipError_t gemv_scratch(StreamScratch *ss, const int *outs, int count, int in, int rows,
-                               bool generic, exl3::Scratch *sc, hipStream_t s) {
+// The partial-sum floats one GEMV launch over linears of widths outs[] needs.
+static size_t gemv_slot_need(const int *outs, int count, int in, int rows, bool generic) {
   int total = 0;
   for (int i = 0; i < count; ++i) total += outs[i];
   int ksplit, tps;
   exl3::gemv_multi_plan(in, total, generic, rows, &ksplit, &tps);
-  hipError_t e = grow(&ss->partial, &ss->partial_bytes, (size_t)ksplit * rows * total * 4, s, 0xFF);
-  if (e != hipSuccess) return e;
+  return (size_t)ksplit * rows * total;
+}
+
+// The scratch of one GEMV launch over `count` linears, carved from a slot
+// buffer with room for gemv_slot_need: its status word, and partial sums
+// split per linear.
+static void gemv_carve(const exl3::Scratch &slots, const int *outs, int count, int in, int rows,
+                       bool generic, exl3::Scratch *sc) {
+  int total = 0;
+  for (int i = 0; i < count; ++i) total += outs[i];
+  int ksplit, tps;
+  exl3::gemv_multi_plan(in, total, generic, rows, &ksplit, &tps);
   size_t po = 0;
   for (int i = 0; i < count; ++i) {
-    sc[i].partial = (float *)ss->partial + po;
+    sc[i].partial = slots.partial + po;
     sc[i].partial_floats = (size_t)ksplit * rows * outs[i];
+    sc[i].status = slots.status;
     po += sc[i].partial_floats;
   }
+}
+
+static hipError_t gemv_scratch(StreamScratch *ss, const int *outs, int count, int in, int rows,
+                               bool generic, exl3::Scratch *sc, hipStream_t s) {
+  exl3::Scratch slots;
+  hipError_t e = slots_for(ss, gemv_slot_need(outs, count, in, rows, generic), s, &slots);
+  if (e != hipSuccess) return e;
+  gemv_carve(slots, outs, count, in, rows, generic, sc);
   return hipSuccess;
 }
 
@@ -530,7 +588,7 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
     for (int i = 0; i < count; ++i) {
       const uint16_t *xp = (const uint16_t *)x;
       if (!prepared) {
-        hipError_t e = grow(&ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s, -1);
+        hipError_t e = grow(ss, &ss->xp, &ss->xp_bytes, (size_t)rows * in * 2, s);
         if (e != hipSuccess) return e;
         for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
           const int r = (int)std::min<int64_t>(65535, rows - r0);
@@ -543,7 +601,7 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
       }
       const exl3::GemmSplit sp = exl3::gemm_split((int)rows, in, (int)pvs[i]->out);
       if (sp.splits > 1) {
-        hipError_t e = grow(&ss->kpart, &ss->kpart_bytes, sp.part_floats * 4, s, -1);
+        hipError_t e = grow(ss, &ss->kpart, &ss->kpart_bytes, sp.part_floats * 4, s);
         if (e != hipSuccess) return e;
       }
       hipError_t e = exl3::launch_gemm(
@@ -601,7 +659,7 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   exl3_verdict v = output_for(out, x, pv->out, rows);
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
-  std::lock_guard<std::mutex> g(g_scratch_mu);
+  std::lock_guard<std::mutex> g(ss->mu);
   hipError_t e = run_linear(w, pv, x.data, xdt, false, out->data, xdt, nullptr, rows, ss, s);
   if (e != hipSuccess) return hip_failed(e);
   return ok();
@@ -635,7 +693,7 @@ exl3_verdict exl3_matmul_shared(const exl3_weight *const *ws, uint32_t count, ex
     ys[i] = outs[i].data;
   }
   StreamScratch *ss = scratch_for(pvs[0]->device, s);
-  std::lock_guard<std::mutex> g(g_scratch_mu);
+  std::lock_guard<std::mutex> g(ss->mu);
   hipError_t e = run_linears(ws, pvs, (int)count, x.data, xdt, false, ys, xdt, nullptr, rows, ss, s);
   if (e != hipSuccess) return hip_failed(e);
   return ok();
@@ -711,9 +769,9 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
     // path's mid step, bit for bit): two launches (above 4 rows the SwiGLU
     // runs once on its own first).
     StreamScratch *ss = scratch_for(pg->device, s);
-    std::lock_guard<std::mutex> g(g_scratch_mu);
+    std::lock_guard<std::mutex> g(ss->mu);
     const size_t nel = (size_t)rows * pg->out;
-    hipError_t e = grow(&ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s, -1);
+    hipError_t e = grow(ss, &ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s);
     if (e != hipSuccess) return hip_failed(e);
     uint16_t *gu = (uint16_t *)ss->moe;
     const exl3_weight *ws2[2] = {gate, up};
@@ -741,9 +799,9 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
     // gate and up through the GEMM (f16), the SwiGLU once (the MoE path's mid
     // step, bit for bit), the down projection through the GEMM.
     StreamScratch *ss = scratch_for(pg->device, s);
-    std::lock_guard<std::mutex> g(g_scratch_mu);
+    std::lock_guard<std::mutex> g(ss->mu);
     const size_t nel = (size_t)rows * pg->out;
-    hipError_t e = grow(&ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s, -1);
+    hipError_t e = grow(ss, &ss->moe, &ss->moe_bytes, nel * 3 * sizeof(uint16_t), s);
     if (e != hipSuccess) return hip_failed(e);
     uint16_t *gu = (uint16_t *)ss->moe;
     const exl3_weight *ws2[2] = {gate, up};
@@ -771,16 +829,16 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   exl3::MoeBank bd{(const uint16_t *)down->w.data, (const uint16_t *)down->scales.data,
                    (const uint16_t *)down->biases.data, pd->f, (int)pd->in, (int)pd->out};
   StreamScratch *ss = scratch_for(pg->device, s);
-  std::lock_guard<std::mutex> g(g_scratch_mu);
-  size_t nslots = 0;
+  std::lock_guard<std::mutex> g(ss->mu);
+  size_t pf = 0;
   const size_t need =
-      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &nslots);
-  hipError_t e = grow(&ss->moe, &ss->moe_bytes, need, s, -1);
+      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &pf);
+  hipError_t e = grow(ss, &ss->moe, &ss->moe_bytes, need, s);
   if (e != hipSuccess) return hip_failed(e);
-  e = grow(&ss->partial, &ss->partial_bytes, nslots * 4, s, 0xFF);
+  exl3::Scratch slots;
+  e = slots_for(ss, pf, s, &slots);
   if (e != hipSuccess) return hip_failed(e);
-  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, (float *)ss->partial,
-                       ss->partial_bytes / 4, s);
+  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, slots, s);
   if (e != hipSuccess) {
     if (e == hipErrorInvalidValue) return kShape;
     return hip_failed(e);
@@ -857,13 +915,80 @@ exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   StreamScratch *ss = scratch_for(pv->device, s);
-  std::lock_guard<std::mutex> g(g_scratch_mu);
+  std::lock_guard<std::mutex> g(ss->mu);
   hipError_t e = run_linear(w, pv, xp.data, exl3::ACT_F16, true, nullptr, 0, (uint16_t *)z.data,
                             rows, ss, s);
   return e == hipSuccess ? ok() : hip_failed(e);
 }
 
-const char *exl3_version(void) { return "exl3_mi355x 0.1.0 (gfx950)"; }
+exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
+  hipStream_t s = (hipStream_t)stream;
+  StreamScratch *ss = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    auto it = g_scratch.find({device, s});
+    if (it == g_scratch.end()) return ok();
+    ss = &it->second;
+  }
+  std::lock_guard<std::mutex> g(ss->mu);
+  if (hipSetDevice(device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  if (capturing(s))
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: scratch released while its stream is being captured");
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_failed(e);
+  for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
+  ss->xp_bytes = ss->kpart_bytes = ss->slot_bytes = ss->moe_bytes = 0;
+  for (void *p : ss->retired) (void)hipFree(p);
+  ss->retired.clear();
+  for (auto &b : ss->retired_slots) (void)hipFree(b.first);
+  ss->retired_slots.clear();
+  return ok();
+}
+
+void exl3_set_splitk_poll_bound(int32_t polls) { exl3::set_splitk_poll_max(polls); }
+
+exl3_verdict exl3_stream_status(int32_t device, exl3_stream stream) {
+  hipStream_t s = (hipStream_t)stream;
+  StreamScratch *ss = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    auto it = g_scratch.find({device, s});
+    if (it == g_scratch.end()) return ok();
+    ss = &it->second;
+  }
+  std::lock_guard<std::mutex> g(ss->mu);
+  if (hipSetDevice(device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  if (capturing(s))
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: status read while its stream is being captured");
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_failed(e);
+  std::vector<std::pair<void *, size_t>> bufs = ss->retired_slots;
+  if (ss->slots) bufs.push_back({ss->slots, ss->slot_bytes});
+  bool failed = false;
+  for (auto &b : bufs) {
+    uint32_t st = 0;
+    e = hipMemcpy(&st, b.first, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_failed(e);
+    if (st == 0) continue;
+    failed = true;
+    // the stream is idle, so every late store has landed: empty the slots
+    e = hipMemset((char *)b.first + exl3::SLOT_HEADER_BYTES, 0xFF,
+                  b.second - exl3::SLOT_HEADER_BYTES);
+    if (e == hipSuccess) e = hipMemset(b.first, 0, 4);
+    if (e != hipSuccess) return hip_failed(e);
+  }
+  if (failed)
+    return refuse(EXL3_FAILED,
+                  "turboexl3_mi355x: a split-K partial sum did not arrive within the wait's bound; "
+                  "outputs of this stream's calls since the last check may hold NaN (the slots "
+                  "are reset)");
+  return ok();
+}
+
+const char *exl3_version(void) { return "exl3_mi355x 0.2.0 (gfx950)"; }
 
 const char *exl3_matmul_path(const exl3_weight *w, int64_t rows) {
   const WeightPriv *pv = priv_of(w);
@@ -940,7 +1065,7 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
   if (hipSetDevice(pvs[0]->device) != hipSuccess) return hipErrorInvalidDevice;
   const int in = (int)pvs[0]->in;
   StreamScratch *ss = scratch_for(pvs[0]->device, s);
-  std::lock_guard<std::mutex> g(g_scratch_mu);
+  std::lock_guard<std::mutex> g(ss->mu);
   int wouts[4];
   exl3::GemvLinear ls[4];
   for (int i = 0; i < count; ++i) {
@@ -971,7 +1096,7 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
   if (pre_norm || pre_swiglu) {
     // rows the prologue does not take: the RMSNorm (of h as it stands) or
     // the SwiGLU first, into scratch, then a plain GEMV
-    e = grow(&ss->xp, &ss->xp_bytes, (size_t)B * in * sizeof(uint16_t), s, -1);
+    e = grow(ss, &ss->xp, &ss->xp_bytes, (size_t)B * in * sizeof(uint16_t), s);
     if (e != hipSuccess) return e;
     uint16_t *xs = (uint16_t *)ss->xp;
     if (pre_norm) {

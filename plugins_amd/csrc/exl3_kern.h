@@ -112,6 +112,9 @@ struct GemvWeight {
 
 struct GemvCfg {
   size_t ptotal;  // rows of the partial-sum slots
+  // the word a split-K wait that gives up sets, and the wait's bound
+  uint32_t *status;
+  int poll_max;
   int ydt;
   int ksplit;
   uint32_t mask;
@@ -542,9 +545,11 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 // back.  It never waits on a workgroup that has not started: the last split
 // has the highest workgroup index of its column group, and workgroups are
 // dispatched in index order, so every slot it waits for belongs to a
-// workgroup already running, whose stores land within a memory round trip
-// (PARTIAL_POLL_MAX bounds the wait regardless: a slot still empty then
-// makes the sum NaN).  Slots are agent-scope atomics, coherent across the
+// workgroup already running, whose stores land within a memory round trip.
+// PARTIAL_POLL_MAX bounds the wait regardless: a slot still empty then makes
+// the sum NaN, is left as it is (its store may still land), and sets the
+// status word, which the host reads (and after which it refills the slots:
+// exl3_stream_status).  Slots are agent-scope atomics, coherent across the
 // XCDs' L2s, so no fence is needed.  (A device fence would write back and
 // invalidate the L2 in every workgroup.)
 constexpr uint32_t PARTIAL_EMPTY = 0xFFFFFFFFu;
@@ -570,6 +575,7 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
     return false;
   }
   const float empty = bits<float>(PARTIAL_EMPTY);
+  bool gave_up = false;
   for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
     float *p = partial + (size_t)rm.prow(b) * out + col0 + col;
@@ -583,16 +589,20 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
       for (int j = 0; j < 16; ++j) {
         if (k0 + j >= ks) break;
         float *slot = p + (size_t)(k0 + j) * stride;
-        for (int n = 0; bits<uint32_t>(v[j]) == PARTIAL_EMPTY && n < PARTIAL_POLL_MAX; ++n) {
+        for (int n = 0; bits<uint32_t>(v[j]) == PARTIAL_EMPTY && n < a.poll_max; ++n) {
           __builtin_amdgcn_s_sleep(2);
           v[j] = ld_agent(slot);
         }
-        st_agent(slot, empty);
+        if (bits<uint32_t>(v[j]) == PARTIAL_EMPTY)
+          gave_up = true;
+        else
+          st_agent(slot, empty);
         s = s + v[j];
       }
     }
     zf[e] = h2f(f2h(s + zf[e]));
   }
+  if (gave_up) atomicOr(a.status, 1u);
   lds_barrier();
   return true;
 }

@@ -22,14 +22,22 @@ struct Format {
   bool integer_rate() const { return n % 16 == 0 && n >= 16 && n <= 128; }
 };
 
-// Device scratch a matmul uses: split-K partial-sum slots, each holding the
-// empty mark (all-ones bytes) between calls: every call leaves the slots it
-// used empty again, so one slot buffer serves any sequence of calls on one
-// stream whatever their shapes.
+// Device scratch a GEMV or routed-MoE call uses for its split-K hand-off:
+// partial-sum slots, each holding the empty mark (all-ones bytes) between
+// calls -- every call leaves the slots it used empty again, so one slot
+// buffer serves any sequence of calls on one stream whatever their shapes --
+// and a status word (zero) that a split-K wait which gives up sets.
 struct Scratch {
   float *partial = nullptr;
   size_t partial_floats = 0;
+  uint32_t *status = nullptr;
 };
+// A slot buffer is a 256-byte header holding the status word, then the slots.
+constexpr size_t SLOT_HEADER_BYTES = 256;
+// The split-K wait's bound in polls (PARTIAL_POLL_MAX unless lowered by
+// set_splitk_poll_max; a negative value restores it).
+int splitk_poll_max();
+void set_splitk_poll_max(int polls);
 
 // Output / activation element types understood by the kernels.
 enum ActType { ACT_F16 = 0, ACT_BF16 = 1, ACT_F32 = 2 };
@@ -156,11 +164,11 @@ struct MoeArgs {
 // than the grouped GEMV's items of up to 8 slots.
 bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic);
 // Staging bytes for a call, and (in *partial_floats) the partial-sum slots
-// it needs (a Scratch slot buffer: empty between calls, left empty).
+// of its Scratch.
 size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
                          size_t *partial_floats);
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
-                      const MoeBank &down, void *scratch, size_t scratch_bytes, float *partial,
-                      size_t partial_floats, hipStream_t s);
+                      const MoeBank &down, void *scratch, size_t scratch_bytes,
+                      const Scratch &slots, hipStream_t s);
 
 }  // namespace exl3

@@ -21,6 +21,8 @@
 // multiply-adds are written out where they are meant.
 // The rate-templated kernels live in exl3_kern.h; their launchers are
 // instantiated once per rate in exl3_rate.hip.
+#include <atomic>
+
 #include "exl3_kern.h"
 
 namespace exl3 {
@@ -274,6 +276,13 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
 // splits, ~512 workgroups over `groups` column groups; ~256 for more than 4
 // rows, whose split-K partial sums (rows x 128 floats per workgroup) would
 // otherwise add half the weight bytes again at 16 rows.
+static std::atomic<int> g_poll_bound{-1};
+int splitk_poll_max() {
+  const int v = g_poll_bound.load(std::memory_order_relaxed);
+  return v >= 0 ? v : PARTIAL_POLL_MAX;
+}
+void set_splitk_poll_max(int polls) { g_poll_bound.store(polls, std::memory_order_relaxed); }
+
 void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int tps_max) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
@@ -354,6 +363,9 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     }
     w.partial = sc[i].partial;
   }
+  if (ksplit > 1 && sc[0].status == nullptr) return hipErrorInvalidValue;
+  a.c.status = sc[0].status;
+  a.c.poll_max = splitk_poll_max();
   a.c.ydt = ydt;
   a.c.ptotal = (size_t)rows;
   a.c.ksplit = ksplit;
@@ -855,8 +867,8 @@ size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
 }
 
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
-                      const MoeBank &down, void *scratch, size_t scratch_bytes, float *partial,
-                      size_t partial_floats, hipStream_t s) {
+                      const MoeBank &down, void *scratch, size_t scratch_bytes,
+                      const Scratch &slots, hipStream_t s) {
   if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
@@ -867,9 +879,11 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     return hipErrorInvalidValue;
   const bool gu_generic = !gate.f.integer_rate(), d_generic = !down.f.integer_rate();
   const MoeLayout L = moe_layout(a, gu_generic, d_generic);
-  if (scratch_bytes < L.total || partial_floats < L.partial_floats || L.slots > 65535 ||
+  if (scratch_bytes < L.total || slots.status == nullptr || slots.partial == nullptr ||
+      slots.partial_floats < L.partial_floats || L.slots > 65535 ||
       L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
     return hipErrorInvalidValue;
+  float *partial = slots.partial;
   char *base = (char *)scratch;
   uint32_t *sorted = (uint32_t *)(base + L.sorted);
   MoeItem *items = (MoeItem *)(base + L.items);
@@ -911,6 +925,8 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   mgu.nweights = 2;
   MoeGemv md = moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d, L.tps_d);
   md.nweights = 1;
+  mgu.a.c.status = md.a.c.status = slots.status;
+  mgu.a.c.poll_max = md.a.c.poll_max = splitk_poll_max();
   const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, L.max_items);
   const dim3 grid_d(a.hidden / 128, L.ks_d, L.max_items);
   uint32_t gg[3];

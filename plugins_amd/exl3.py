@@ -133,6 +133,9 @@ SIGNATURES = {
     "exl3_pack_dir_close": (None, [c_void_p]),
     "exl3_matmul_path": (c_char_p, [POINTER(Weight), c_int64]),
     "exl3_swiglu_path": (c_char_p, [POINTER(Weight), POINTER(Weight), POINTER(Weight), c_int64, c_int32]),
+    "exl3_scratch_release": (Verdict, [c_int32, c_void_p]),
+    "exl3_stream_status": (Verdict, [c_int32, c_void_p]),
+    "exl3_set_splitk_poll_bound": (None, [c_int32]),
 }
 
 _lib = None
@@ -466,3 +469,15 @@ class Linear:
                 release(self.weight)
         except Exception:
             pass
+
+
+def scratch_release(device: int = 0, stream=None) -> None:
+    """Frees the library's scratch for (device, stream) (exl3_scratch_release):
+    call once no graph captured on the stream will be replayed again."""
+    check(lib().exl3_scratch_release(device, stream_handle(stream)), "scratch_release")
+
+
+def stream_status(device: int = 0, stream=None) -> Verdict:
+    """exl3_stream_status: synchronizes the stream and reports (FAILED) whether a
+    split-K wait gave up since the last check; resets the slots if so."""
+    return lib().exl3_stream_status(device, stream_handle(stream))

@@ -496,3 +496,86 @@ def test_matmul_shared_refuses_mixed_rates():
     b, *_ = make(rng, 256, 128, 64)
     with pytest.raises(X.Exl3Error, match="differ"):
         X.matmul_shared([a.weight, b.weight], dev_f16(S.activations(rng, 1, 256)))
+
+
+# ------------------------------------------------------------ scratch lifetime
+
+def test_scratch_growth_keeps_captured_graphs_valid():
+    """A graph captured on a stream keeps working after a larger eager call
+    on the same stream grows the library's scratch (the old buffers are kept,
+    not freed); growing while capturing is refused by name; releasing the
+    stream's scratch afterwards leaves later calls working."""
+    rng = np.random.default_rng(900)
+    small, *_ = make(rng, 512, 256, 64)
+    big, *_ = make(rng, 4096, 4096, 64)
+    xs = dev_f16(S.activations(rng, 1, 512))
+    xb = dev_f16(S.activations(rng, 16, 4096))
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    ys = torch.empty(1, 256, dtype=torch.float16, device=DEV)
+    with torch.cuda.stream(cap):
+        small(xs, out=ys, stream=cap)
+        want = ys.clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap, capture_error_mode="thread_local"):
+        small(xs, out=ys, stream=cap)
+    # a larger call on the capture stream: its scratch grows past the graph's
+    with torch.cuda.stream(cap):
+        yb = big(xb, stream=cap)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ys.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys, want)
+    # growing inside a capture is refused before anything is recorded
+    s2 = torch.cuda.Stream()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(X.Exl3Error, match="captured"):
+        with torch.cuda.graph(g2, stream=s2, capture_error_mode="thread_local"):
+            big(xb, stream=s2)
+    del g
+    X.scratch_release(0, cap)
+    with torch.cuda.stream(cap):
+        again = big(xb, stream=cap)
+    torch.cuda.synchronize()
+    assert torch.equal(again, yb)
+
+
+def test_splitk_give_up_is_reported_and_recovered():
+    """A split-K wait that gives up (forced from the host: a bound of 0 polls,
+    so the last split stops at the first slot that has not landed) leaves NaN
+    in its output and sets the stream's status; exl3_stream_status reports it
+    and resets the slots, after which calls at the default bound are exact
+    again.  Every kernel exits normally throughout."""
+    rng = np.random.default_rng(901)
+    lin, *_ = make(rng, 4096, 4096, 64)  # 16 splits at batch 1
+    x = dev_f16(S.activations(rng, 1, 4096))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        want = lin(x, stream=s)
+    torch.cuda.synchronize()
+    assert X.stream_status(0, s).is_ok()
+    gave_up = None
+    try:
+        X.lib().exl3_set_splitk_poll_bound(0)
+        for _ in range(40):
+            with torch.cuda.stream(s):
+                y = lin(x, stream=s)
+            v = X.stream_status(0, s)
+            if not v.is_ok():
+                gave_up = (v, y)
+                break
+    finally:
+        X.lib().exl3_set_splitk_poll_bound(-1)
+    if gave_up is None:
+        pytest.skip("no split-K wait gave up at a bound of 0 polls in 40 calls")
+    v, y = gave_up
+    assert v.code == X.FAILED and "did not arrive" in v.reason
+    assert torch.isnan(y.float()).any()
+    for _ in range(3):
+        with torch.cuda.stream(s):
+            again = lin(x, stream=s)
+        assert X.stream_status(0, s).is_ok()
+        assert torch.equal(again, want)
