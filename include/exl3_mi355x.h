@@ -219,6 +219,23 @@ void exl3_release(exl3_weight *w);
  * caller's buffer, which must have x's dtype and the result's shape. */
 exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3_array *out);
 
+/* exl3_matmul without any allocation: no counterpart in the reference; for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Same kernels and the
+ * same results as exl3_matmul, bit for bit.  `out` must be the caller's
+ * buffer (x's dtype, the result's shape).  Scratch comes from one array per
+ * GPU, 64 MiB, held by the library from its load onto that GPU until the
+ * process ends: 8 MiB of split-K slots (GEMV, up to 16 rows) and 56 MiB of
+ * staging (the GEMM's prepared rows, rows * in * 2 bytes, and its split-K
+ * planes); a call needing more is refused with EXL3_TOO_LARGE before any
+ * launch (exl3_matmul serves it).  The first call on a GPU sets the array up
+ * (its address, the slots' empty mark) and must run outside graph capture;
+ * later calls may be captured.  Calls share their GPU's array: calls that
+ * overlap in time on one GPU (on different streams) race on it, so the
+ * caller orders them. */
+exl3_verdict exl3_matmul_noalloc(const exl3_weight *w, exl3_array x, exl3_stream s,
+                                 exl3_array out);
+
 /* Up to four linears that read the same rows, in one launch: outs[i] =
  * x @ W_i^T, each in x's dtype (turboexl3's linearShared,
  * sushi_ds41/src/sushi/exl3/linear.zig:34-60: q/k/v, gate/up).  The weights

@@ -37,6 +37,7 @@ SOURCES = [
     ("exl3_kernels.hip", "exl3_kernels", DEVICE_FLAGS),
     *[("exl3_rate.hip", f"exl3_rate_k{k}", DEVICE_FLAGS + [f"-DEXL3_INST_K={k}"]) for k in range(9)],
     ("decoder_ops.hip", "decoder_ops", DEVICE_FLAGS),
+    ("exl3_noalloc.hip", "exl3_noalloc", DEVICE_FLAGS),
     ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
     ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
     ("exl3_pack.cpp", "exl3_pack", HOST_FLAGS),

@@ -165,6 +165,9 @@ struct StreamScratch {
   std::vector<void *> retired;  // superseded buffers, freed by exl3_scratch_release
   // superseded slot buffers (each with its own status word and slots)
   std::vector<std::pair<void *, size_t>> retired_slots;
+  // fixed: the buffers above are given (exl3_matmul_noalloc's array) and are
+  // never replaced; a call that needs more is refused, not grown
+  bool fixed = false;
 };
 
 std::mutex g_scratch_mu;
@@ -177,6 +180,7 @@ bool capturing(hipStream_t s) {
 
 hipError_t grow(StreamScratch *ss, void **p, size_t *have, size_t need, hipStream_t s) {
   if (*have >= need && *p != nullptr) return hipSuccess;
+  if (ss->fixed) return hipErrorOutOfMemory;
   if (capturing(s)) return hipErrorStreamCaptureUnsupported;
   const size_t bytes = std::max<size_t>({need, 2 * *have, 256});
   void *fresh = nullptr;
@@ -194,6 +198,7 @@ hipError_t grow(StreamScratch *ss, void **p, size_t *have, size_t need, hipStrea
 hipError_t slots_for(StreamScratch *ss, size_t pf, hipStream_t s, exl3::Scratch *out) {
   const size_t have = ss->slots ? (ss->slot_bytes - exl3::SLOT_HEADER_BYTES) / 4 : 0;
   if (ss->slots == nullptr || pf > have) {
+    if (ss->fixed) return hipErrorOutOfMemory;
     if (capturing(s)) return hipErrorStreamCaptureUnsupported;
     const size_t p2 = std::max<size_t>({pf, 2 * have, 64});
     const size_t bytes = exl3::SLOT_HEADER_BYTES + p2 * 4;
@@ -661,6 +666,73 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
   hipError_t e = run_linear(w, pv, x.data, xdt, false, out->data, xdt, nullptr, rows, ss, s);
+  if (e != hipSuccess) return hip_failed(e);
+  return ok();
+}
+
+// exl3_matmul's kernels over exl3_matmul_noalloc's per-device array: the
+// call's needs are checked against the array's regions first, and the
+// fixed scratch refuses (never allocates) if a launch asked for more.
+static std::mutex g_noalloc_mu;
+
+exl3_verdict exl3_matmul_noalloc(const exl3_weight *w, exl3_array x, exl3_stream stream,
+                                 exl3_array out) {
+  const WeightPriv *pv = priv_of(w);
+  if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  if (x.ndim < 1 || x.ndim > EXL3_MAX_DIMS || !x.data || x.shape[x.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(x) / pv->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  if (out.data == nullptr)
+    return refuse(EXL3_FAILED,
+                  "turboexl3_mi355x: the no-alloc matmul writes into the caller's output (out.data "
+                  "is NULL)");
+  if (out.dtype != x.dtype || out.ndim < 1 || out.shape[out.ndim - 1] != pv->out ||
+      numel(out) != rows * pv->out)
+    return kShape;
+  // what run_linears will ask of the scratch
+  const bool gemm = rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate();
+  size_t slot_floats = 0, xp_bytes = 0, kpart_bytes = 0;
+  if (gemm) {
+    xp_bytes = ((size_t)rows * pv->in * 2 + 255) & ~(size_t)255;
+    const exl3::GemmSplit sp = exl3::gemm_split((int)rows, (int)pv->in, (int)pv->out);
+    if (sp.splits > 1) kpart_bytes = sp.part_floats * 4;
+  } else {
+    const int outs[1] = {(int)pv->out};
+    slot_floats = gemv_slot_need(outs, 1, (int)pv->in,
+                                 (int)std::min<int64_t>(rows, exl3::GEMV_ROWS_MAX),
+                                 !pv->f.integer_rate());
+  }
+  if (exl3::SLOT_HEADER_BYTES + slot_floats * 4 > exl3::NOALLOC_SLOT_BYTES ||
+      xp_bytes + kpart_bytes > exl3::NOALLOC_BYTES - exl3::NOALLOC_SLOT_BYTES)
+    return refuse(EXL3_TOO_LARGE,
+                  "turboexl3_mi355x: the call needs more scratch than the no-alloc matmul's 64 MiB "
+                  "per device (8 MiB of split-K slots, 56 MiB of prepared rows and split-K "
+                  "planes); exl3_matmul serves it");
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  void *base = nullptr;
+  hipError_t e = exl3::noalloc_scratch(pv->device, s, &base);
+  if (e == hipErrorStreamCaptureUnsupported)
+    return refuse(EXL3_FAILED,
+                  "turboexl3_mi355x: the no-alloc matmul's first call on a device sets up its "
+                  "array and must run outside graph capture");
+  if (e != hipSuccess) return hip_failed(e);
+  StreamScratch ss;
+  ss.fixed = true;
+  ss.slots = base;
+  ss.slot_bytes = exl3::NOALLOC_SLOT_BYTES;
+  char *staging = (char *)base + exl3::NOALLOC_SLOT_BYTES;
+  ss.xp = staging;
+  ss.xp_bytes = xp_bytes;
+  ss.kpart = staging + xp_bytes;
+  ss.kpart_bytes = exl3::NOALLOC_BYTES - exl3::NOALLOC_SLOT_BYTES - xp_bytes;
+  e = run_linear(w, pv, x.data, xdt, false, out.data, xdt, nullptr, rows, &ss, s);
+  if (e == hipErrorOutOfMemory)
+    return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: the no-alloc matmul's scratch is too small");
   if (e != hipSuccess) return hip_failed(e);
   return ok();
 }

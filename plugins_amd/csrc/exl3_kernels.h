@@ -34,6 +34,15 @@ struct Scratch {
 };
 // A slot buffer is a 256-byte header holding the status word, then the slots.
 constexpr size_t SLOT_HEADER_BYTES = 256;
+
+// exl3_matmul_noalloc's scratch (exl3_noalloc.hip): 64 MiB per device, of
+// which a slot buffer of 8 MiB (2M partial-sum floats) and 56 MiB of staging
+// for the GEMM's prepared rows and split-K planes.
+constexpr size_t NOALLOC_BYTES = (size_t)64 << 20;
+constexpr size_t NOALLOC_SLOT_BYTES = (size_t)8 << 20;
+// The array's address on `device` (current), set up on the first call per
+// device (refused with hipErrorStreamCaptureUnsupported while s is capturing).
+hipError_t noalloc_scratch(int device, hipStream_t s, void **base);
 // The split-K wait's bound in polls (PARTIAL_POLL_MAX unless lowered by
 // set_splitk_poll_max; a negative value restores it).
 int splitk_poll_max();

@@ -136,6 +136,7 @@ SIGNATURES = {
     "exl3_scratch_release": (Verdict, [c_int32, c_void_p]),
     "exl3_stream_status": (Verdict, [c_int32, c_void_p]),
     "exl3_set_splitk_poll_bound": (None, [c_int32]),
+    "exl3_matmul_noalloc": (Verdict, [POINTER(Weight), Array, c_void_p, Array]),
 }
 
 _lib = None

@@ -1,0 +1,95 @@
+"""exl3_matmul_noalloc (the allocation-free matmul) through the C ABI against
+exl3_matmul: the same kernels, so the outputs agree bit for bit, on two calls
+in a row with the second smaller, at GEMV sizes (split-K slots) and GEMM sizes
+(prepared rows and split-K planes); a call beyond the array's 64 MiB is
+refused before any launch; and captured into a HIP graph (the callers it is
+for) its replays equal the eager result."""
+import ctypes
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from plugins_amd import exl3 as X  # noqa: E402
+from tests import _synth as S  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def linear(rng, in_f, out_f, n=64):
+    t, u, v = S.linear(rng, in_f, out_f, n)
+    return X.Linear(torch.from_numpy(t.view(np.int16)).to(DEV),
+                    torch.from_numpy(u.view(np.float16)).to(DEV),
+                    torch.from_numpy(v.view(np.float16)).to(DEV))
+
+
+def noalloc(lin, x, out, stream=None):
+    return X.lib().exl3_matmul_noalloc(ctypes.byref(lin.weight), X.array(x),
+                                      X.stream_handle(stream), X.array(out))
+
+
+def both(lin, x):
+    """exl3_matmul's result and exl3_matmul_noalloc's, into separate buffers."""
+    want = torch.empty(*x.shape[:-1], lin.out_features, dtype=x.dtype, device=DEV)
+    X.check(X.lib().exl3_matmul(ctypes.byref(lin.weight), X.array(x),
+                                X.stream_handle(None), ctypes.byref(X.array(want))), "matmul")
+    got = torch.full_like(want, float("nan"))
+    X.check(noalloc(lin, x, got), "matmul_noalloc")
+    torch.cuda.synchronize()
+    return got, want
+
+
+@pytest.mark.parametrize("first,second", [
+    # GEMV (split-K slots): q/o at 8 rows, then a narrower linear at 1 row
+    ((4096, 4096, 8), (512, 256, 1)),
+    # GEMM (prepared rows; small grids also split k): 300 rows, then 17
+    ((4096, 4096, 300), (2048, 1024, 17)),
+    # GEMM then GEMV on the same array
+    ((12288, 4096, 64), (4096, 12288, 2)),
+])
+def test_noalloc_matches_matmul_twice(first, second):
+    rng = np.random.default_rng(sum(first) + sum(second))
+    for in_f, out_f, rows in (first, second):
+        lin = linear(rng, in_f, out_f)
+        x = torch.from_numpy(S.activations(rng, rows, in_f)).to(DEV)
+        got, want = both(lin, x)
+        assert not torch.isnan(got.float()).any()
+        assert torch.equal(got, want), (in_f, out_f, rows)
+    assert X.stream_status(0).is_ok()
+
+
+def test_noalloc_refuses_beyond_its_array():
+    rng = np.random.default_rng(3)
+    lin = linear(rng, 12288, 256)
+    # 4096 rows x 12288 x 2 bytes of prepared rows = 96 MiB > 56 MiB of staging
+    x = torch.zeros(4096, 12288, dtype=torch.float16, device=DEV)
+    out = torch.full((4096, 256), 7.0, dtype=torch.float16, device=DEV)
+    v = noalloc(lin, x, out)
+    assert v.code == X.TOO_LARGE and "no-alloc" in v.reason
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())  # nothing was launched
+    # no output buffer given: refused (the entry never allocates one)
+    v2 = X.lib().exl3_matmul_noalloc(ctypes.byref(lin.weight), X.array(x[:1]), None, X.Array())
+    assert v2.code == X.FAILED and "caller's output" in v2.reason
+
+
+def test_noalloc_in_a_graph():
+    rng = np.random.default_rng(5)
+    lin = linear(rng, 4096, 4096)
+    x = torch.from_numpy(S.activations(rng, 1, 4096)).to(DEV)
+    got, want = both(lin, x)  # the first call on the device ran eagerly
+    cap = torch.cuda.Stream()
+    out = torch.empty(1, 4096, dtype=torch.float16, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap, capture_error_mode="thread_local"):
+        X.check(noalloc(lin, x, out, cap), "matmul_noalloc")
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        # eager work between replays on the same array
+        g2, w2 = both(lin, x)
+        assert torch.equal(g2, w2)
