@@ -51,6 +51,41 @@ __device__ __forceinline__ T bits(F f) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)bits<_Float16>(h); }
+
+// v of lane (this lane ^ m), m in {1, 2, 4, 8, 16, 32}, without the LDS
+// crossbar (a __shfl_xor is a ds_bpermute: an LDS round trip per exchange):
+// DPP quad permutes for 1 and 2, two DPP mirrors for 4 (half-row mirror =
+// lane ^ 7, then quad lane ^ 3) and 8 (row mirror = lane ^ 15, then lane ^ 7),
+// the gfx950 permlane swaps for 16 and 32 (each returns the two halves
+// exchanged; a lane keeps the one holding its partner).  All 64 lanes must be
+// active.  m must fold to a constant (a call inside an unrolled loop).
+__device__ __forceinline__ float xor_lanes(float v, int m) {
+  const int b = bits<int>(v);
+  if (m == 1) return bits<float>(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+  if (m == 2) return bits<float>(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+  if (m == 4) {
+    const int h = __builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false);
+    return bits<float>(__builtin_amdgcn_mov_dpp(h, 0x1B, 0xF, 0xF, false));
+  }
+  if (m == 8) {
+    const int r = __builtin_amdgcn_mov_dpp(b, 0x140, 0xF, 0xF, false);
+    return bits<float>(__builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
+  }
+  const int lane = (int)(threadIdx.x & 63);
+  if (m == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+    return bits<float>((lane & 16) ? r[0] : r[1]);
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+  return bits<float>((lane & 32) ? r[0] : r[1]);
+}
+
+// One Hadamard butterfly step with the partner's value p: the lower lane of
+// the pair (sg = +1) forms v + p, the upper (sg = -1) p - v.  sg * v is exact,
+// so the fused form rounds once, exactly as the add or the subtraction does.
+__device__ __forceinline__ float butterfly(float sg, float v, float p) {
+  return __builtin_fmaf(sg, v, p);
+}
 // Materialises an f32 value in a VGPR so the operation that produced it is
 // not merged into a following conversion.  The backend otherwise turns
 // f16(a * b) into one v_fma_mixlo_f16, which rounds the exact product once;

@@ -33,8 +33,20 @@ typedef __attribute__((address_space(1))) float gf32_t;
 __device__ __forceinline__ void st_agent(float *p, float v) {
   __hip_atomic_store((gf32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_agent(const float *p) {
-  return __hip_atomic_load((gf32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// An agent-scope load (sc1, the bit an agent-scope atomic load's
+// global_load carries) through a buffer resource: the base in SGPRs, a
+// per-lane byte offset and a uniform one, so many slots of one lane cost one
+// VGPR of address between them.  Offsets stay below 2^31 (the hosts check
+// the slot planes' size).  The empty asm with a memory clobber keeps a poll
+// loop's load from being hoisted or merged: the load is re-issued on every
+// call.
+__device__ __forceinline__ float ld_agent_at(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                             uint32_t soff) {
+  asm volatile("" ::: "memory");
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 16));
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(float *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, 0x7FFFFFFF, 0x00020000);
 }
 // s_waitcnt vmcnt(0): this wave's outstanding vector-memory operations,
 // stores included on gfx9-family parts, have completed.
@@ -225,6 +237,13 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 // arithmetic are split so a workgroup issues its first items' loads with its
 // weight loads.
 
+// Batch j of a prepare holds items base + 8 j + wave (clamped to the last
+// item); a batch past the last item would only redo it (every wave's item
+// clamped), so it is skipped: the test is uniform across the workgroup.
+__device__ __forceinline__ bool prep_batch_live(int j, int base, int nitems) {
+  return j == 0 || base + j * (GEMV_THREADS / 64) < nitems;
+}
+
 // Raw bits as loaded (converted only when the rows are prepared, so the
 // loads do not wait): x holds the two elements (one dword for f16/bf16, two
 // for f32), su the two suh values.
@@ -245,6 +264,7 @@ __device__ __forceinline__ void gemv_prep_load_norm(const GemvCfg &a, const RowM
   const int ng = in >> 7;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_batch_live(j, base, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -256,7 +276,7 @@ __device__ __forceinline__ void gemv_prep_load_norm(const GemvCfg &a, const RowM
 }
 __device__ __forceinline__ float norm_scale(float part, int in, float eps) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+  for (int m = 32; m >= 1; m >>= 1) part += xor_lanes(part, m);
   return rsqrtf(part / (float)in + eps);
 }
 
@@ -283,6 +303,7 @@ __device__ __forceinline__ void gemv_prep_load_x(const void *x, int xdt, int pre
   const int esz = (!prepared && xdt == OUT_F32) ? 4 : 2;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_batch_live(j, base, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -304,6 +325,7 @@ __device__ __forceinline__ void gemv_prep_load_su(const void *x, int prepared, c
   const uint16_t *sup = prepared ? (const uint16_t *)x : suh;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_batch_live(j, base, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int blk = it % nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -318,6 +340,7 @@ __device__ __forceinline__ void gemv_prep_load_up(const uint16_t *x2, const RowM
                                                   int lane, PrepRegs &r) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_batch_live(j, base, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -335,11 +358,10 @@ __device__ __forceinline__ void had128_pair(float &v0, float &v1, int lane) {
   v1 = b;
 #pragma unroll
   for (int bit = 1; bit <= 32; bit <<= 1) {
-    const float p0 = __shfl_xor(v0, bit, 64);
-    const float p1 = __shfl_xor(v1, bit, 64);
-    const bool lower = (lane & bit) == 0;
-    v0 = lower ? v0 + p0 : p0 - v0;
-    v1 = lower ? v1 + p1 : p1 - v1;
+    const float p0 = xor_lanes(v0, bit), p1 = xor_lanes(v1, bit);
+    const float sg = (lane & bit) == 0 ? 1.0f : -1.0f;
+    v0 = butterfly(sg, v0, p0);
+    v1 = butterfly(sg, v1, p1);
   }
 }
 
@@ -353,6 +375,7 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
                                                 int in = 0, float eps = 0.0f) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_batch_live(j, base, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
@@ -379,7 +402,7 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
     if (hsum != nullptr) {
       float s = h2f((uint16_t)(y & 0xFFFFu)) + h2f((uint16_t)(y >> 16));
 #pragma unroll
-      for (int m = 1; m < 32; m <<= 1) s = s + __shfl_xor(s, m, 64);
+      for (int m = 1; m < 32; m <<= 1) s = s + xor_lanes(s, m);
       if ((lane & 31) == 0) hsum[row * nb * 2 + blk * 2 + (lane >> 5)] = s;
     }
   }
@@ -490,12 +513,9 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
     }
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) {
-      const bool lower = (li & m) == 0;
+      const float sg = (li & m) == 0 ? 1.0f : -1.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pv = __shfl_xor(v[e], m, 64);
-        v[e] = lower ? v[e] + pv : pv - v[e];
-      }
+      for (int e = 0; e < 8; ++e) v[e] = butterfly(sg, v[e], xor_lanes(v[e], m));
     }
     uint32_t y[4];
 #pragma unroll
@@ -515,7 +535,7 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
         s2[e] = h2f((uint16_t)(y[e] & 0xFFFFu)) + h2f((uint16_t)(y[e] >> 16));
       float s = (s2[0] + s2[1]) + (s2[2] + s2[3]);
 #pragma unroll
-      for (int m = 1; m < 8; m <<= 1) s = s + __shfl_xor(s, m, 64);
+      for (int m = 1; m < 8; m <<= 1) s = s + xor_lanes(s, m);
       if ((li & 7) == 0) hsum[row * nb * 2 + blk * 2 + (li >> 3)] = s;
     }
   }
@@ -541,8 +561,9 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 // split order) in zf.  Partial-sum slots hold PARTIAL_EMPTY (a NaN bit
 // pattern no arithmetic produces) between calls.  The other splits store
 // their sums and exit; the last split's workgroup reads their slots,
-// re-reading each one until its store has landed, then puts PARTIAL_EMPTY
-// back.  It never waits on a workgroup that has not started: the last split
+// re-reading all of those still empty together (one round trip per round,
+// up to 16 slots a round) until every store has landed, then puts
+// PARTIAL_EMPTY back.  It never waits on a workgroup that has not started: the last split
 // has the highest workgroup index of its column group, and workgroups are
 // dispatched in index order, so every slot it waits for belongs to a
 // workgroup already running, whose stores land within a memory round trip.
@@ -575,28 +596,40 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
     return false;
   }
   const float empty = bits<float>(PARTIAL_EMPTY);
+  const __amdgpu_buffer_rsrc_t pr = buffer_of(partial);
+  const uint32_t sstride = (uint32_t)(stride * 4);  // bytes between splits' planes
   bool gave_up = false;
   for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
     const int b = e >> 7, col = e & 127;
-    float *p = partial + (size_t)rm.prow(b) * out + col0 + col;
+    const uint32_t po = (uint32_t)(((size_t)rm.prow(b) * out + col0 + col) * 4);
     float s = 0.0f;
     for (int k0 = 0; k0 < ks; k0 += 16) {
+      const int nk = min(16, ks - k0);
       float v[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (k0 + j < ks) v[j] = ld_agent(p + (size_t)(k0 + j) * stride);
+        if (j < nk) v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
+      // every slot still empty is read again in the same round, so the wait
+      // is one round trip after the last store lands (not one per slot)
+      uint32_t pending = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (j < nk && bits<uint32_t>(v[j]) == PARTIAL_EMPTY) pending |= 1u << j;
+      for (int n = 0; pending != 0 && n < a.poll_max; ++n) {
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (pending & (1u << j)) v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if ((pending & (1u << j)) && bits<uint32_t>(v[j]) != PARTIAL_EMPTY) pending &= ~(1u << j);
+      }
+      gave_up |= pending != 0;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        if (k0 + j >= ks) break;
-        float *slot = p + (size_t)(k0 + j) * stride;
-        for (int n = 0; bits<uint32_t>(v[j]) == PARTIAL_EMPTY && n < a.poll_max; ++n) {
-          __builtin_amdgcn_s_sleep(2);
-          v[j] = ld_agent(slot);
-        }
-        if (bits<uint32_t>(v[j]) == PARTIAL_EMPTY)
-          gave_up = true;
-        else
-          st_agent(slot, empty);
+        if (j >= nk) break;
+        if (!(pending & (1u << j)))
+          st_agent(partial + (po >> 2) + (size_t)(k0 + j) * stride, empty);
         s = s + v[j];
       }
     }
@@ -672,7 +705,7 @@ __device__ __forceinline__ void gemv_finish_res(float *zf, float *res, float *re
     *reinterpret_cast<float2 *>(hp) = hn;
     float ss = hn.x * hn.x + hn.y * hn.y;
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    for (int m = 1; m < 64; m <<= 1) ss += xor_lanes(ss, m);
     if (lane == 0) res_ssq[(size_t)rm.prow(b) * ng + cg] = ss;
   }
 }
@@ -813,6 +846,13 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
 #pragma unroll
       for (int i = 0; i < K; ++i) wd[i + 1] = b[i];
       wd[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)b[K - 1]);
+      {
+        // the buffer is free once copied: its next step's load goes out
+        // before this step's decode
+        const gu32_t *pn = wp + (size_t)min(it + NBUF, iters - 1) * wstep;
+#pragma unroll
+        for (int i = 0; i < K; ++i) b[i] = pn[i];
+      }
       const h8_t alo = *reinterpret_cast<const h8_t *>(xa + it * 64);
       const h8_t ahi = *reinterpret_cast<const h8_t *>(xa + it * 64 + 8);
       // one B operand at a time (pairs f, f+4, f+8, f+12: rows 0-7 or 8-15 of
@@ -834,9 +874,6 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
         if constexpr (f == 2) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc0, 0, 0, 0);
         if constexpr (f == 3) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc1, 0, 0, 0);
       });
-      const gu32_t *pn = wp + (size_t)min(it + NBUF, iters - 1) * wstep;
-#pragma unroll
-      for (int i = 0; i < K; ++i) b[i] = pn[i];
     };
     int it = 0;
     for (; it + NBUF <= iters; it += NBUF)

@@ -61,11 +61,10 @@ __device__ __forceinline__ void finish_row_wave(const uint16_t *z, const uint16_
   float v1 = h2f(z[lane + 64]);
 #pragma unroll
   for (int bit = 1; bit <= 32; bit <<= 1) {
-    const float p0 = __shfl_xor(v0, bit, 64);
-    const float p1 = __shfl_xor(v1, bit, 64);
-    const bool lower = (lane & bit) == 0;
-    v0 = lower ? v0 + p0 : p0 - v0;
-    v1 = lower ? v1 + p1 : p1 - v1;
+    const float p0 = xor_lanes(v0, bit), p1 = xor_lanes(v1, bit);
+    const float sg = (lane & bit) == 0 ? 1.0f : -1.0f;
+    v0 = butterfly(sg, v0, p0);
+    v1 = butterfly(sg, v1, p1);
   }
   const float a = v0 + v1, b = v0 - v1;
   const float s0 = a * HAD_SCALE, s1 = b * HAD_SCALE;
@@ -129,12 +128,9 @@ __global__ __launch_bounds__(256) void prepare8_kernel(const void *__restrict__ 
       }
 #pragma unroll
   for (int bit = 1; bit <= 8; bit <<= 1) {
-    const bool lower = (j & bit) == 0;
+    const float sg = (j & bit) == 0 ? 1.0f : -1.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = __shfl_xor(v[i], bit, 64);
-      v[i] = lower ? v[i] + p : p - v[i];
-    }
+    for (int i = 0; i < 8; ++i) v[i] = butterfly(sg, v[i], xor_lanes(v[i], bit));
   }
   if (valid) {
     uint32_t o[4];
@@ -686,11 +682,10 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
   }
 #pragma unroll
   for (int bit = 1; bit <= 32; bit <<= 1) {
-    const float p0 = __shfl_xor(v[0], bit, 64);
-    const float p1 = __shfl_xor(v[1], bit, 64);
-    const bool lower = (lane & bit) == 0;
-    v[0] = lower ? v[0] + p0 : p0 - v[0];
-    v[1] = lower ? v[1] + p1 : p1 - v[1];
+    const float p0 = xor_lanes(v[0], bit), p1 = xor_lanes(v[1], bit);
+    const float sg = (lane & bit) == 0 ? 1.0f : -1.0f;
+    v[0] = butterfly(sg, v[0], p0);
+    v[1] = butterfly(sg, v[1], p1);
   }
   const float a = v[0] + v[1], b = v[0] - v[1];
   xd[slot * inter + i0] = f2h(a * HAD_SCALE);
