@@ -163,6 +163,72 @@ typedef struct exl3_swiglu_opts {
   bool verify_rows;
 } exl3_swiglu_opts;
 
+/* kit `Span(T)`: a pointer and a count (quant.zig:15), one type per element
+ * type the table's entries take. */
+typedef struct exl3_weight_span {
+  const exl3_weight *ptr;
+  size_t len;
+} exl3_weight_span;
+typedef struct exl3_array_span {
+  const exl3_array *ptr;
+  size_t len;
+} exl3_array_span;
+typedef struct exl3_u32_span {
+  const uint32_t *ptr;
+  size_t len;
+} exl3_u32_span;
+typedef struct exl3_u8_span {
+  const uint8_t *ptr;
+  size_t len;
+} exl3_u8_span;
+
+/* `LinearParts` (quant.zig:111-128): the options of the split entries
+ * (linear_split / finish / prepared / pieces / piece); each entry reads the
+ * fields its comment names.  `side` NULL: no side stream (the entry's own
+ * stream does all the work). */
+typedef struct exl3_linear_parts {
+  uint32_t size;
+  int32_t dtype;        /* EXL3_DT_* of the call's activations: the output's */
+  exl3_stream side;     /* linear_split: the stream for the work after the prepare */
+  bool inner;           /* linear_split: stop at the inner product */
+  bool prepared;        /* linear_piece: x holds rows the caller prepared */
+  exl3_array held;      /* linear_piece: what linear_pieces made */
+  exl3_u32_span rows;   /* linear_pieces: each piece's row count, in row order */
+  exl3_array_span parts; /* linear_finish: the inner products, in row order */
+} exl3_linear_parts;
+
+/* `SharedSwiglu` (quant.zig:183-197): the gated shared expert of
+ * swiglu_shared.  y = routed + sigmoid(logit) * shared(x); `logit` [rows]
+ * per row, or NULL with `gate_vec` [D] (the logit computed in the launch);
+ * `logits` [rows, E] with `k`: the routing (softmax, top-k) done in the
+ * launches, inds / scores then empty.  `sigtab` (MLX's sigmoid table) is
+ * not read: the sigmoid is computed (see exl3_swiglu_shared). */
+typedef struct exl3_shared_swiglu {
+  uint32_t size;
+  const exl3_weight *gate;
+  const exl3_weight *up;
+  const exl3_weight *down;
+  exl3_array sigtab;
+  exl3_array logit;
+  exl3_array gate_vec;
+  exl3_array logits;
+  uint32_t k;
+} exl3_shared_swiglu;
+
+/* The attention entries' options (quant.zig:129-182).  This library leaves
+ * those entries NULL (the host runs its own chain), so the types are
+ * declared only for the table's signatures. */
+typedef struct exl3_attn_in exl3_attn_in;
+typedef struct exl3_attn_in_out exl3_attn_in_out;
+typedef struct exl3_gate exl3_gate;
+typedef struct exl3_q_planes exl3_q_planes;
+typedef struct exl3_indexer exl3_indexer;
+
+/* `Weight.flags` bit of a grouped linear (turboexl3_ds41/plugin.zig:105-106):
+ * G linears `<base>.slice.<g>` stored as a G-bank; matmul takes
+ * x [..., G, in] and gives y [..., G, out], group g through linear g. */
+#define EXL3_WEIGHT_GROUPED 1u
+
 /* ---------------------------------------------------------------- entries
  * One flat symbol per QuantTable entry, each also reachable through the table
  * below.  Each replaces the reference entry cited beside it.
@@ -195,8 +261,11 @@ void exl3_close(exl3_load_ctx *ctx);
 /* QuantTable.load_tensor (quant.zig:37; turboexl3_ds41/plugin.zig:86-103):
  * `<name>.trellis` (i16/u16 [in/16, out/16, n]), `<name>.suh` (f16 [in]),
  * `<name>.svh` (f16 [out]) from ctx->source, copied to device memory on
- * ctx->stream.  in_dim != 0 must equal in.  Refusals: MissingWeight,
- * NotShaped (the reference's `not_shaped` text). */
+ * ctx->stream.  in_dim != 0 must equal in.  A pack that stores the name as
+ * `<name>.slice.<g>` linears (g = 0, 1, ..: DeepSeek-V4.1's grouped `wo_a`,
+ * turboexl3_ds41/plugin.zig:108-125) loads as a grouped linear: a G-bank
+ * with flags EXL3_WEIGHT_GROUPED.  Refusals: MissingWeight, NotShaped (the
+ * reference's `not_shaped` text). */
 exl3_verdict exl3_load_tensor(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
                               exl3_weight *out);
 
@@ -216,7 +285,10 @@ void exl3_release(exl3_weight *w);
  * xp = f16(H(f16(x)*suh)/sqrt(128)); z = f16(sum_k xp*W) (f32 accumulate);
  * y = f16(H(z)/sqrt(128)*svh) then x's dtype.  If out->data is NULL the
  * library allocates the result (owned = 1); otherwise it writes into the
- * caller's buffer, which must have x's dtype and the result's shape. */
+ * caller's buffer, which must have x's dtype and the result's shape.  A
+ * grouped linear (G linears, flags EXL3_WEIGHT_GROUPED) takes x [..., G, in]
+ * and gives [..., G, out], x[..., g, :] through linear g
+ * (turboexl3_ds41/plugin.zig:243-261, sushi_ds41/src/sushi/exl3/linear.zig:24-36). */
 exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3_array *out);
 
 /* exl3_matmul without any allocation: no counterpart in the reference; for
@@ -261,12 +333,50 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
                          exl3_array x, exl3_array inds, exl3_array scores,
                          const exl3_swiglu_opts *opts, exl3_stream s, exl3_array *out);
 
+/* QuantTable.linear_split (quant.zig:56-58): matmul with the work after x's
+ * prepare recorded on opts->side (NULL side: all on s); with opts->inner it
+ * stops before the finish and *out is the inner product z f16 [rows, out]
+ * that linear_finish takes, else y [rows, out] in x's dtype.  With a side
+ * stream, x's prepared rows live in *out's allocation behind the result, so
+ * free *out only after the side stream's work. */
+exl3_verdict exl3_linear_split(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream s, exl3_array *out);
+
+/* QuantTable.linear_finish (quant.zig:59-60): the finish of opts->parts (one
+ * inner product z f16, or a call's row pieces in row order): y [rows, out]
+ * in opts->dtype. */
+exl3_verdict exl3_linear_finish(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream s, exl3_array *out);
+
+/* QuantTable.linear_prepared (quant.zig:61-62): matmul of rows the caller
+ * prepared (xp f16 [rows, in], xp = f16(H(f16(x) * suh) / sqrt(128)) per
+ * 128-block): y [rows, out] in opts->dtype. */
+exl3_verdict exl3_linear_prepared(const exl3_weight *w, exl3_array xp,
+                                  const exl3_linear_parts *opts, exl3_stream s, exl3_array *out);
+
+/* QuantTable.linear_pieces (quant.zig:63-65): the weight in the form a call's
+ * row pieces share.  The kernels decode the packed trellis on the fly at
+ * every width, so that form is the trellis itself: *out is a borrowed view
+ * of it (owned = 0), made without a launch.  Refused when the pieces
+ * (opts->rows) would not all take the kernel path (GEMV or GEMM) of the
+ * whole call, whose sums are then ordered differently. */
+exl3_verdict exl3_linear_pieces(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream s, exl3_array *out);
+
+/* QuantTable.linear_piece (quant.zig:66-68): one piece's inner product
+ * z f16 [rows, out] against opts->held (what linear_pieces made for this
+ * weight): of x [..., in], or with opts->prepared of rows the caller
+ * prepared (f16). */
+exl3_verdict exl3_linear_piece(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream s, exl3_array *out);
+
 /* ----------------------------------------------------- the plugin table */
 
-/* kit `QuantTable` (quant.zig:24-50), the entries turboexl3_ds41 fills
- * (turboexl3_ds41/plugin.zig:28-43).  Optional entries the reference leaves
- * null for this plugin (the GDN-tail, attention and resident entries of
- * quant.zig:51-107) are not part of this table. */
+/* kit `QuantTable`, the whole layout (quant.zig:24-107): the entries
+ * turboexl3_ds41 fills (turboexl3_ds41/plugin.zig:28-43), the split
+ * entries, and NULL for the optional entries this library does not serve
+ * (the attention entries, resident / resident_pending / unrotate /
+ * linear_joined), where the host runs its own chain. */
 typedef struct exl3_quant_table {
   uint32_t size;
   uint32_t version;
@@ -288,6 +398,41 @@ typedef struct exl3_quant_table {
   exl3_verdict (*swiglu)(const exl3_weight *gate, const exl3_weight *up, const exl3_weight *down,
                          exl3_array x, exl3_array inds, exl3_array scores,
                          const exl3_swiglu_opts *opts, exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_split)(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_finish)(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_prepared)(const exl3_weight *w, exl3_array xp,
+                                  const exl3_linear_parts *opts, exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_pieces)(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_piece)(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream s, exl3_array *out);
+  exl3_verdict (*attn_in)(const exl3_weight *q, const exl3_weight *k, const exl3_weight *v,
+                          exl3_array x, const exl3_attn_in *opts, exl3_stream s,
+                          exl3_attn_in_out *out);
+  exl3_verdict (*attn_prep)(const exl3_weight *q, const exl3_weight *k, const exl3_weight *v,
+                            const exl3_weight *w4, exl3_array x, exl3_stream s, exl3_array *out);
+  exl3_verdict (*linear_prepared_idx)(const exl3_weight *w, exl3_array xp, exl3_array x,
+                                      exl3_stream s, exl3_array *out);
+  exl3_verdict (*gated_out)(const exl3_weight *o, exl3_array attn, const exl3_gate *gate,
+                            exl3_stream s, exl3_array *out);
+  exl3_verdict (*merged_gated_out)(const exl3_weight *o, exl3_array pacc, exl3_array pml,
+                                   const exl3_gate *gate, exl3_stream s, exl3_array *out);
+  exl3_verdict (*q_planes)(const exl3_weight *q, exl3_array x, const exl3_q_planes *opts,
+                           exl3_stream s, exl3_array *out);
+  exl3_verdict (*indexer)(const exl3_weight *idx, exl3_array x, const exl3_indexer *opts,
+                          exl3_stream s, exl3_array *out);
+  exl3_verdict (*swiglu_shared)(const exl3_weight *gate, const exl3_weight *up,
+                                const exl3_weight *down, exl3_array x, exl3_array inds,
+                                exl3_array scores, const exl3_shared_swiglu *opts, exl3_stream s,
+                                exl3_array *out);
+  exl3_verdict (*resident)(exl3_weight_span ws, uint64_t room, exl3_stream s, uint64_t *bytes);
+  uint64_t (*resident_pending)(void);
+  exl3_verdict (*unrotate)(exl3_weight_span ws, exl3_u8_span sizes, int32_t act, exl3_stream s,
+                           bool *took);
+  exl3_verdict (*linear_joined)(exl3_weight_span ws, exl3_array x, exl3_stream s,
+                                exl3_array *out);
 } exl3_quant_table;
 
 /* The exported table (the reference exports it as `exportName(name,

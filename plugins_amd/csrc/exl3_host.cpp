@@ -90,6 +90,7 @@ bool n_ok(int64_t n) { return n >= 16 && n <= 128 && n % 2 == 0; }
 struct WeightPriv {
   Format f;
   int64_t in = 0, out = 0, experts = 0;  // experts = 0: a single linear
+  int64_t groups = 0;  // a grouped linear: `experts` banks, x [..., groups, in]
   int device = 0;
   bool borrowed = false;
 };
@@ -162,6 +163,8 @@ struct StreamScratch {
   size_t slot_bytes = 0;
   void *moe = nullptr;
   size_t moe_bytes = 0;
+  void *grp = nullptr;  // a grouped linear's gathered rows and outputs
+  size_t grp_bytes = 0;
   std::vector<void *> retired;  // superseded buffers, freed by exl3_scratch_release
   // superseded slot buffers (each with its own status word and slots)
   std::vector<std::pair<void *, size_t>> retired_slots;
@@ -420,14 +423,25 @@ exl3_verdict exl3_load_tensor(const exl3_load_ctx *ctx, exl3_str name, uint32_t 
   if (!ctx || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
   const std::string base(name.ptr ? name.ptr : "", name.len);
   std::vector<Parts> ps(1);
-  if (!parts_of(ctx, base, &ps[0])) {
-    Parts g;
-    if (parts_of(ctx, base + ".slice.0", &g))
-      return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: grouped linears are not served");
-    return kMissing;
+  if (parts_of(ctx, base, &ps[0])) {
+    if (!shaped(ps[0], in_dim)) return kNotShaped;
+    return load_parts(ctx, ps, false, out);
   }
-  if (!shaped(ps[0], in_dim)) return kNotShaped;
-  return load_parts(ctx, ps, false, out);
+  // a grouped linear: <base>.slice.<g> for g = 0, 1, .. as one G-bank
+  // (turboexl3_ds41/plugin.zig:108-125)
+  ps.clear();
+  for (int g = 0;; ++g) {
+    Parts p;
+    if (!parts_of(ctx, base + ".slice." + std::to_string(g), &p)) break;
+    if (!shaped(p, in_dim)) return kNotShaped;
+    ps.push_back(p);
+  }
+  if (ps.empty()) return kMissing;
+  exl3_verdict v = load_parts(ctx, ps, true, out);
+  if (v.code != EXL3_OK) return v;
+  static_cast<WeightPriv *>(out->priv)->groups = (int64_t)ps.size();
+  out->flags = EXL3_WEIGHT_GROUPED;
+  return ok();
 }
 
 exl3_verdict exl3_load_bank(const exl3_load_ctx *ctx, exl3_str name, uint32_t in_dim,
@@ -649,10 +663,56 @@ static hipError_t run_linear(const exl3_weight *w, const WeightPriv *pv, const v
                      ss, s);
 }
 
+// A grouped linear (G linears stored as a G-bank): x [..., G, in] ->
+// y [..., G, out], x[..., g, :] through linear g (turboexl3_ds41/plugin.zig:
+// 252-261; sushi_ds41/src/sushi/exl3/linear.zig:24-36).  Per group: its rows
+// gathered into scratch by a strided 2-D copy, the linear's kernels (GEMV or
+// GEMM by the row count, as exl3_matmul), the result copied into y's group
+// columns.
+static exl3_verdict grouped_matmul(const exl3_weight *w, const WeightPriv *pv, exl3_array x,
+                                   hipStream_t s, exl3_array *out) {
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  const int64_t G = pv->groups, in = pv->in, outf = pv->out;
+  if (x.ndim < 2 || !x.data || x.shape[x.ndim - 1] != in || x.shape[x.ndim - 2] != G) return kShape;
+  const int64_t rows = numel(x) / (G * in);
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = output_for(out, x, outf, rows * G);
+  if (v.code != EXL3_OK) return v;
+  const size_t esz = dt_size(x.dtype);
+  const size_t xg_bytes = ((size_t)rows * in * esz + 255) & ~(size_t)255;
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> lk(ss->mu);
+  hipError_t e = grow(ss, &ss->grp, &ss->grp_bytes, xg_bytes + (size_t)rows * outf * esz, s);
+  if (e != hipSuccess) return hip_failed(e);
+  char *xg = (char *)ss->grp, *yg = xg + xg_bytes;
+  const size_t per = (size_t)(in / 16) * (outf / 16) * pv->f.n;  // trellis halfwords per linear
+  WeightPriv pg = *pv;
+  pg.experts = 0;
+  pg.groups = 0;
+  for (int64_t g = 0; g < G && e == hipSuccess; ++g) {
+    exl3_weight wg = *w;
+    wg.w.data = (uint16_t *)w->w.data + g * per;
+    wg.scales.data = (uint16_t *)w->scales.data + g * in;
+    wg.biases.data = (uint16_t *)w->biases.data + g * outf;
+    wg.flags = 0;
+    wg.priv = &pg;
+    e = hipMemcpy2DAsync(xg, in * esz, (const char *)x.data + g * in * esz, G * in * esz, in * esz,
+                         rows, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = run_linear(&wg, &pg, xg, xdt, false, yg, xdt, nullptr, rows, ss, s);
+    if (e == hipSuccess)
+      e = hipMemcpy2DAsync((char *)out->data + g * outf * esz, G * outf * esz, yg, outf * esz,
+                           outf * esz, rows, hipMemcpyDeviceToDevice, s);
+  }
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
 exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
                          exl3_array *out) {
   const WeightPriv *pv = priv_of(w);
   if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->groups != 0) return grouped_matmul(w, pv, x, (hipStream_t)stream, out);
   if (pv->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
   const int xdt = act_of(x.dtype);
   if (xdt < 0) return kDtype;
@@ -679,6 +739,8 @@ exl3_verdict exl3_matmul_noalloc(const exl3_weight *w, exl3_array x, exl3_stream
                                  exl3_array out) {
   const WeightPriv *pv = priv_of(w);
   if (!pv) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (pv->groups != 0)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: a grouped linear takes exl3_matmul");
   if (pv->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
   const int xdt = act_of(x.dtype);
   if (xdt < 0) return kDtype;
@@ -799,6 +861,8 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
       pd->in != pg->out)
     return kShape;
   if (pg->experts != pu->experts || pg->experts != pd->experts) return kShape;
+  if (pg->groups || pu->groups || pd->groups)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: a grouped linear is not an expert bank");
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pg->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   exl3::MoeArgs a{};
@@ -993,6 +1057,220 @@ exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_
   return e == hipSuccess ? ok() : hip_failed(e);
 }
 
+// ------------------------------------------------ split entries (LinearParts)
+
+// A new device array of `dt` with x's leading dims and last dimension `last`
+// (2-D [rows, last] when lead is null), `extra` bytes beyond the data.
+static exl3_verdict new_array(exl3_array *out, const exl3_array *lead, int64_t rows, int64_t last,
+                              int dt, size_t extra) {
+  const size_t bytes = ((size_t)(rows * last) * dt_size(dt) + 255) & ~(size_t)255;
+  void *p = nullptr;
+  if (hipMalloc(&p, std::max<size_t>(bytes + extra, 256)) != hipSuccess)
+    return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
+  exl3_array a{};
+  if (lead) {
+    a = *lead;
+    a.shape[a.ndim - 1] = last;
+  } else {
+    a.ndim = 2;
+    a.shape[0] = rows;
+    a.shape[1] = last;
+  }
+  a.data = p;
+  a.dtype = dt;
+  a.owned = 1;
+  a._pad = 0;
+  *out = a;
+  return ok();
+}
+
+static const WeightPriv *single_linear(const exl3_weight *w) {
+  const WeightPriv *pv = priv_of(w);
+  return pv && pv->experts == 0 && pv->groups == 0 ? pv : nullptr;
+}
+
+static bool parts_ok(const exl3_linear_parts *o) {
+  return o && o->size >= (uint32_t)sizeof(exl3_linear_parts);
+}
+
+const exl3_verdict kParts = {EXL3_FAILED,
+                             "turboexl3_mi355x: LinearParts missing or older than this library's"};
+
+exl3_verdict exl3_linear_split(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream stream, exl3_array *out) {
+  const WeightPriv *pv = single_linear(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument or not one linear");
+  if (!parts_ok(opts)) return kParts;
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  if (x.ndim < 1 || !x.data || x.shape[x.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(x) / pv->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  hipStream_t side = opts->side ? (hipStream_t)opts->side : s;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  const int odt = opts->inner ? (int)EXL3_DT_F16 : (int)x.dtype;
+  // with a side stream the prepared rows ride behind the result in its allocation
+  const size_t xp_bytes = side != s ? (size_t)rows * pv->in * 2 : 0;
+  exl3_verdict v = new_array(out, &x, rows, pv->out, odt, xp_bytes);
+  if (v.code != EXL3_OK) return v;
+  void *y = opts->inner ? nullptr : out->data;
+  uint16_t *z = opts->inner ? (uint16_t *)out->data : nullptr;
+  hipError_t e = hipSuccess;
+  if (side == s) {
+    StreamScratch *ss = scratch_for(pv->device, s);
+    std::lock_guard<std::mutex> g(ss->mu);
+    e = run_linear(w, pv, x.data, xdt, false, y, xdt, z, rows, ss, s);
+  } else {
+    const size_t ybytes = ((size_t)(rows * pv->out) * dt_size(odt) + 255) & ~(size_t)255;
+    uint16_t *xp = (uint16_t *)((char *)out->data + ybytes);
+    for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+      const int r = (int)std::min<int64_t>(65535, rows - r0);
+      e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * pv->in * dt_size(x.dtype), xdt,
+                               (const uint16_t *)w->scales.data, xp + (size_t)r0 * pv->in, r,
+                               (int)pv->in, s);
+    }
+    hipEvent_t ev = nullptr;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ev, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side, ev, 0);
+    if (ev) (void)hipEventDestroy(ev);
+    if (e == hipSuccess) {
+      StreamScratch *ss = scratch_for(pv->device, side);
+      std::lock_guard<std::mutex> g(ss->mu);
+      e = run_linear(w, pv, xp, exl3::ACT_F16, true, y, xdt, z, rows, ss, side);
+    }
+  }
+  if (e != hipSuccess) {
+    exl3_array_free(out);
+    return hip_failed(e);
+  }
+  return ok();
+}
+
+exl3_verdict exl3_linear_finish(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream stream, exl3_array *out) {
+  const WeightPriv *pv = single_linear(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument or not one linear");
+  if (!parts_ok(opts)) return kParts;
+  const int ydt = act_of(opts->dtype);
+  if (ydt < 0) return kDtype;
+  if (opts->parts.len == 0 || !opts->parts.ptr) return kShape;
+  int64_t rows = 0;
+  for (size_t i = 0; i < opts->parts.len; ++i) {
+    const exl3_array &z = opts->parts.ptr[i];
+    if (z.dtype != EXL3_DT_F16) return kDtype;
+    if (!z.data || z.ndim < 1 || z.shape[z.ndim - 1] != pv->out) return kShape;
+    rows += numel(z) / pv->out;
+  }
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = new_array(out, nullptr, rows, pv->out, opts->dtype, 0);
+  if (v.code != EXL3_OK) return v;
+  const size_t ysz = dt_size(opts->dtype);
+  hipError_t e = hipSuccess;
+  int64_t at = 0;
+  for (size_t i = 0; i < opts->parts.len && e == hipSuccess; ++i) {
+    const exl3_array &z = opts->parts.ptr[i];
+    const int64_t n = numel(z) / pv->out;
+    for (int64_t r0 = 0; r0 < n && e == hipSuccess; r0 += 65535) {
+      const int r = (int)std::min<int64_t>(65535, n - r0);
+      e = exl3::launch_finish((const uint16_t *)z.data + (size_t)r0 * pv->out,
+                              (const uint16_t *)w->biases.data,
+                              (char *)out->data + (size_t)(at + r0) * pv->out * ysz, ydt, r,
+                              (int)pv->out, s);
+    }
+    at += n;
+  }
+  if (e != hipSuccess) {
+    exl3_array_free(out);
+    return hip_failed(e);
+  }
+  return ok();
+}
+
+exl3_verdict exl3_linear_prepared(const exl3_weight *w, exl3_array xp,
+                                  const exl3_linear_parts *opts, exl3_stream stream,
+                                  exl3_array *out) {
+  const WeightPriv *pv = single_linear(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument or not one linear");
+  if (!parts_ok(opts)) return kParts;
+  const int ydt = act_of(opts->dtype);
+  if (ydt < 0 || xp.dtype != EXL3_DT_F16) return kDtype;
+  if (xp.ndim < 1 || !xp.data || xp.shape[xp.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(xp) / pv->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = new_array(out, &xp, rows, pv->out, opts->dtype, 0);
+  if (v.code != EXL3_OK) return v;
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> g(ss->mu);
+  hipError_t e = run_linear(w, pv, xp.data, exl3::ACT_F16, true, out->data, ydt, nullptr, rows, ss, s);
+  if (e != hipSuccess) {
+    exl3_array_free(out);
+    return hip_failed(e);
+  }
+  return ok();
+}
+
+// The kernel path of a call of `rows` rows (run_linears' choice).
+static bool gemm_path(const WeightPriv *pv, int64_t rows) {
+  return rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate();
+}
+
+exl3_verdict exl3_linear_pieces(const exl3_weight *w, const exl3_linear_parts *opts,
+                                exl3_stream stream, exl3_array *out) {
+  (void)stream;
+  const WeightPriv *pv = single_linear(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument or not one linear");
+  if (!parts_ok(opts)) return kParts;
+  if (act_of(opts->dtype) < 0) return kDtype;
+  if (opts->rows.len == 0 || !opts->rows.ptr) return kShape;
+  int64_t total = 0;
+  for (size_t i = 0; i < opts->rows.len; ++i) {
+    if (opts->rows.ptr[i] == 0) return kShape;
+    total += opts->rows.ptr[i];
+  }
+  const bool whole = gemm_path(pv, total);
+  for (size_t i = 0; i < opts->rows.len; ++i)
+    if (gemm_path(pv, opts->rows.ptr[i]) != whole)
+      return refuse(EXL3_UNSUPPORTED,
+                    "turboexl3_mi355x: a piece takes another kernel path (GEMV / GEMM) than the "
+                    "whole call");
+  *out = w->w;  // the packed trellis, borrowed: the pieces' kernels decode it
+  out->owned = 0;
+  return ok();
+}
+
+exl3_verdict exl3_linear_piece(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
+                               exl3_stream stream, exl3_array *out) {
+  const WeightPriv *pv = single_linear(w);
+  if (!pv || !out) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument or not one linear");
+  if (!parts_ok(opts)) return kParts;
+  if (opts->held.data != w->w.data)
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: held is not what linear_pieces made for this weight");
+  const int xdt = opts->prepared ? (int)exl3::ACT_F16 : act_of(x.dtype);
+  if (xdt < 0 || (opts->prepared && x.dtype != EXL3_DT_F16)) return kDtype;
+  if (x.ndim < 1 || !x.data || x.shape[x.ndim - 1] != pv->in) return kShape;
+  const int64_t rows = numel(x) / pv->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = new_array(out, &x, rows, pv->out, EXL3_DT_F16, 0);
+  if (v.code != EXL3_OK) return v;
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> g(ss->mu);
+  hipError_t e = run_linear(w, pv, x.data, xdt, opts->prepared, nullptr, 0, (uint16_t *)out->data,
+                            rows, ss, s);
+  if (e != hipSuccess) {
+    exl3_array_free(out);
+    return hip_failed(e);
+  }
+  return ok();
+}
+
 exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
   hipStream_t s = (hipStream_t)stream;
   StreamScratch *ss = nullptr;
@@ -1008,11 +1286,11 @@ exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
     return refuse(EXL3_FAILED, "turboexl3_mi355x: scratch released while its stream is being captured");
   hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_failed(e);
-  for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe}) {
+  for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe, &ss->grp}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
-  ss->xp_bytes = ss->kpart_bytes = ss->slot_bytes = ss->moe_bytes = 0;
+  ss->xp_bytes = ss->kpart_bytes = ss->slot_bytes = ss->moe_bytes = ss->grp_bytes = 0;
   for (void *p : ss->retired) (void)hipFree(p);
   ss->retired.clear();
   for (auto &b : ss->retired_slots) (void)hipFree(b.first);
@@ -1110,6 +1388,23 @@ static const exl3_quant_table kTable = {
     &exl3_moe,
     &register_kernels,
     &exl3_swiglu,
+    &exl3_linear_split,
+    &exl3_linear_finish,
+    &exl3_linear_prepared,
+    &exl3_linear_pieces,
+    &exl3_linear_piece,
+    nullptr,  // attn_in: the host's chain
+    nullptr,  // attn_prep
+    nullptr,  // linear_prepared_idx
+    nullptr,  // gated_out
+    nullptr,  // merged_gated_out
+    nullptr,  // q_planes
+    nullptr,  // indexer
+    nullptr,  // swiglu_shared
+    nullptr,  // resident: the GEMM decodes in LDS, kept decoded matrices do not pay
+    nullptr,  // resident_pending
+    nullptr,  // unrotate
+    nullptr,  // linear_joined
 };
 
 const exl3_quant_table *exl3_quant_table_get(void) { return &kTable; }

@@ -96,12 +96,32 @@ class SwigluOpts(Structure):
     _fields_ = [("size", c_uint32), ("limit", c_int32), ("verify_rows", c_bool)]
 
 
+class ArraySpan(Structure):
+    _fields_ = [("ptr", POINTER(Array)), ("len", c_size_t)]
+
+
+class U32Span(Structure):
+    _fields_ = [("ptr", POINTER(c_uint32)), ("len", c_size_t)]
+
+
+class LinearParts(Structure):
+    """`LinearParts` (quant.zig:111-128), the split entries' options."""
+    _fields_ = [("size", c_uint32), ("dtype", c_int32), ("side", c_void_p), ("inner", c_bool),
+                ("prepared", c_bool), ("held", Array), ("rows", U32Span), ("parts", ArraySpan)]
+
+
+# The QuantTable's entries in the reference's order (quant.zig:24-107).
+TABLE_ENTRIES = ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank",
+                 "release", "matmul", "moe", "register_kernels", "swiglu", "linear_split",
+                 "linear_finish", "linear_prepared", "linear_pieces", "linear_piece", "attn_in",
+                 "attn_prep", "linear_prepared_idx", "gated_out", "merged_gated_out", "q_planes",
+                 "indexer", "swiglu_shared", "resident", "resident_pending", "unrotate",
+                 "linear_joined")
+
+
 class QuantTable(Structure):
-    _fields_ = [("size", c_uint32), ("version", c_uint32), ("name", Str),
-                ("claims", c_void_p), ("validate", c_void_p), ("bill", c_void_p),
-                ("open", c_void_p), ("close", c_void_p), ("load_tensor", c_void_p),
-                ("load_bank", c_void_p), ("release", c_void_p), ("matmul", c_void_p),
-                ("moe", c_void_p), ("register_kernels", c_void_p), ("swiglu", c_void_p)]
+    _fields_ = [("size", c_uint32), ("version", c_uint32), ("name", Str)] + \
+        [(e, c_void_p) for e in TABLE_ENTRIES]
 
 
 # Every symbol include/exl3_mi355x.h declares, with its ctypes signature.
@@ -137,6 +157,14 @@ SIGNATURES = {
     "exl3_stream_status": (Verdict, [c_int32, c_void_p]),
     "exl3_set_splitk_poll_bound": (None, [c_int32]),
     "exl3_matmul_noalloc": (Verdict, [POINTER(Weight), Array, c_void_p, Array]),
+    "exl3_linear_split": (Verdict, [POINTER(Weight), Array, POINTER(LinearParts), c_void_p,
+                                    POINTER(Array)]),
+    "exl3_linear_finish": (Verdict, [POINTER(Weight), POINTER(LinearParts), c_void_p, POINTER(Array)]),
+    "exl3_linear_prepared": (Verdict, [POINTER(Weight), Array, POINTER(LinearParts), c_void_p,
+                                       POINTER(Array)]),
+    "exl3_linear_pieces": (Verdict, [POINTER(Weight), POINTER(LinearParts), c_void_p, POINTER(Array)]),
+    "exl3_linear_piece": (Verdict, [POINTER(Weight), Array, POINTER(LinearParts), c_void_p,
+                                    POINTER(Array)]),
 }
 
 _lib = None
@@ -438,6 +466,102 @@ def inner(w: Weight, xp, stream=None):
     z = torch.empty(*xp.shape[:-1], out_f, dtype=torch.float16, device=xp.device)
     check(lib().exl3_inner(ctypes.byref(w), array(xp), array(z), stream_handle(stream)), "inner")
     return z
+
+
+_hip = None
+
+
+def _hip_runtime():
+    """The HIP runtime the library itself links (for copying its arrays)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpyAsync.argtypes = [c_void_p, c_void_p, c_size_t, c_int32, c_void_p]
+        _hip.hipMemcpyAsync.restype = c_int32
+    return _hip
+
+
+def take(a: Array, stream=None):
+    """A torch tensor holding the contents of an array the library allocated
+    (owned = 1); the library's array is freed.  The copy is ordered on
+    `stream` (the stream the library's work was recorded on)."""
+    torch = _torch()
+    dts = {DT_F16: torch.float16, DT_BF16: torch.bfloat16, DT_F32: torch.float32}
+    t = torch.empty([a.shape[i] for i in range(a.ndim)], dtype=dts[a.dtype],
+                    device=torch.device("cuda", torch.cuda.current_device()))
+    st = stream if stream is not None else torch.cuda.current_stream()
+    rc = _hip_runtime().hipMemcpyAsync(t.data_ptr(), a.data, t.numel() * t.element_size(), 3,
+                                       st.cuda_stream)
+    st.synchronize()
+    lib().exl3_array_free(ctypes.byref(a))
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpyAsync failed ({rc})")
+    return t
+
+
+def linear_parts(dtype: int = DT_F16, side=None, inner: bool = False, prepared: bool = False,
+                 held: Array | None = None, rows=None, parts=None) -> LinearParts:
+    o = LinearParts()
+    o.size = ctypes.sizeof(LinearParts)
+    o.dtype = dtype
+    o.side = side.cuda_stream if side is not None else None
+    o.inner = inner
+    o.prepared = prepared
+    if held is not None:
+        o.held = held
+    if rows is not None:
+        buf = (c_uint32 * len(rows))(*rows)
+        o.rows = U32Span(buf, len(rows))
+        o._rows = buf
+    if parts is not None:
+        arr = (Array * len(parts))(*[array(z) for z in parts])
+        o.parts = ArraySpan(arr, len(parts))
+        o._parts = arr
+    return o
+
+
+def linear_split(w: Weight, x, inner: bool = False, side=None, stream=None):
+    """QuantTable.linear_split: y (or, inner, z f16) with the work after x's
+    prepare on `side`; returns a torch copy of the library's output."""
+    o = linear_parts(dtype_of(x), side=side, inner=inner)
+    a = Array()
+    check(lib().exl3_linear_split(ctypes.byref(w), array(x), ctypes.byref(o),
+                                  stream_handle(stream), ctypes.byref(a)), "linear_split")
+    return take(a, side if side is not None else stream)
+
+
+def linear_finish(w: Weight, zs, dtype: int = DT_F16, stream=None):
+    """QuantTable.linear_finish over inner products zs (row order)."""
+    o = linear_parts(dtype, parts=list(zs))
+    a = Array()
+    check(lib().exl3_linear_finish(ctypes.byref(w), ctypes.byref(o), stream_handle(stream),
+                                   ctypes.byref(a)), "linear_finish")
+    return take(a, stream)
+
+
+def linear_prepared(w: Weight, xp, dtype: int = DT_F16, stream=None):
+    """QuantTable.linear_prepared: y of rows already prepared (f16)."""
+    o = linear_parts(dtype)
+    a = Array()
+    check(lib().exl3_linear_prepared(ctypes.byref(w), array(xp), ctypes.byref(o),
+                                     stream_handle(stream), ctypes.byref(a)), "linear_prepared")
+    return take(a, stream)
+
+
+def linear_pieces(w: Weight, rows, dtype: int = DT_F16, stream=None) -> tuple[Verdict, Array]:
+    o = linear_parts(dtype, rows=list(rows))
+    a = Array()
+    v = lib().exl3_linear_pieces(ctypes.byref(w), ctypes.byref(o), stream_handle(stream),
+                                 ctypes.byref(a))
+    return v, a
+
+
+def linear_piece(w: Weight, x, held: Array, prepared: bool = False, stream=None):
+    o = linear_parts(DT_F16, prepared=prepared, held=held)
+    a = Array()
+    check(lib().exl3_linear_piece(ctypes.byref(w), array(x), ctypes.byref(o),
+                                  stream_handle(stream), ctypes.byref(a)), "linear_piece")
+    return take(a, stream)
 
 
 def matmul_path(w: Weight, rows: int) -> str:

@@ -28,14 +28,37 @@ def test_header_symbols_are_exported_and_bound():
 
 def test_quant_table_fields():
     t = X.quant_table()
+    # the whole layout of quant.zig:24-107: size, version, name (16 bytes),
+    # then 29 entries, each one pointer
+    assert ctypes.sizeof(X.QuantTable) == 4 + 4 + 16 + 29 * 8
     assert t.size == ctypes.sizeof(X.QuantTable)
     assert t.version == 1
     assert ctypes.string_at(t.name.ptr, t.name.len) == b"turboexl3_mi355x"
-    for f in ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank", "release",
-              "matmul", "moe", "swiglu"):
-        assert getattr(t, f), f
+    served = ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank", "release",
+              "matmul", "moe", "register_kernels", "swiglu", "linear_split", "linear_finish",
+              "linear_prepared", "linear_pieces", "linear_piece")
+    for f in X.TABLE_ENTRIES:
+        assert bool(getattr(t, f)) == (f in served), f
     # the table's pointers are the flat symbols
     assert t.matmul == ctypes.cast(X.lib().exl3_matmul, ctypes.c_void_p).value
+    assert t.linear_split == ctypes.cast(X.lib().exl3_linear_split, ctypes.c_void_p).value
+    assert t.linear_piece == ctypes.cast(X.lib().exl3_linear_piece, ctypes.c_void_p).value
+
+
+def test_table_entry_order_matches_the_reference_layout():
+    """The entries' order is the reference's (quant.zig:24-107), read from the
+    header's table declaration."""
+    text = open(os.path.join(ROOT, "include", "exl3_mi355x.h")).read()
+    body = text[text.index("typedef struct exl3_quant_table {"):text.index("} exl3_quant_table;")]
+    names = re.findall(r"\(\*([a-z_]+)\)\(", body)
+    assert tuple(names) == X.TABLE_ENTRIES
+
+
+def test_linear_parts_layout():
+    # size, dtype, side, inner, prepared, held (an Array), rows, parts
+    assert X.LinearParts.held.offset == 24
+    assert X.LinearParts.rows.offset == 24 + ctypes.sizeof(X.Array)
+    assert ctypes.sizeof(X.LinearParts) == 24 + ctypes.sizeof(X.Array) + 32
 
 
 def _ds41_block():

@@ -1,0 +1,137 @@
+"""The table's split entries (quant.zig:51-68, LinearParts :111-128) and the
+grouped linear (turboexl3_ds41/plugin.zig:105-125,243-261; sushi_ds41/src/
+sushi/exl3/linear.zig:24-36) through the C ABI, against the library's own
+matmul (bit for bit where the same kernels run) and the CPU oracle (paths
+relative to /root/reference/plugins/)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from plugins_amd import exl3 as X  # noqa: E402
+from tests import _synth as S  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def dev_u16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(DEV)
+
+
+def dev_f16(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16) if a.dtype == np.uint16
+                            else np.ascontiguousarray(a, np.float16)).to(DEV)
+
+
+def bits(t):
+    return t.cpu().contiguous().view(torch.int16).numpy()
+
+
+def _lin(seed, in_f=512, out_f=384, n=64):
+    rng = np.random.default_rng(seed)
+    t, u, v = S.linear(rng, in_f, out_f, n)
+    return rng, X.Linear(dev_u16(t), dev_f16(u), dev_f16(v)), (t, u, v)
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16, 40, 300])
+@pytest.mark.parametrize("use_side", [False, True])
+def test_linear_split_is_matmul(rows, use_side):
+    rng, lin, (t, u, v) = _lin(400 + rows)
+    x = dev_f16(S.activations(rng, rows, 512))
+    side = torch.cuda.Stream() if use_side else None
+    want = lin(x)
+    y = X.linear_split(lin.weight, x, side=side)
+    assert y.shape == want.shape and y.dtype == want.dtype
+    assert (bits(y) == bits(want)).all(), (rows, use_side)
+    # the inner product, then the finish: the same values
+    z = X.linear_split(lin.weight, x, inner=True, side=side)
+    assert (bits(z) == bits(X.inner(lin.weight, X.prepare(lin.weight, x)))).all()
+    y2 = X.linear_finish(lin.weight, [z], X.DT_F16)
+    assert (bits(y2) == bits(want)).all()
+    yo = S.h2f(O.project(x.float().cpu().numpy(), t, u, v, 512, 384, 64))
+    assert S.rel_fro(y.float().cpu().numpy(), yo) < 1e-3
+
+
+@pytest.mark.parametrize("rows", [1, 7, 40])
+@pytest.mark.parametrize("dt", [X.DT_F16, X.DT_BF16, X.DT_F32])
+def test_linear_prepared_and_finish_dtypes(rows, dt):
+    rng, lin, (t, u, v) = _lin(500 + rows)
+    x = dev_f16(S.activations(rng, rows, 512))
+    xp = X.prepare(lin.weight, x)
+    y = X.linear_prepared(lin.weight, xp, dt)
+    tdt = {X.DT_F16: torch.float16, X.DT_BF16: torch.bfloat16, X.DT_F32: torch.float32}[dt]
+    assert y.dtype == tdt and y.shape == (rows, 384)
+    # same values as the f16 matmul, in the requested dtype
+    want = lin(x).to(tdt)
+    assert torch.equal(y, want)
+
+
+def test_linear_finish_of_row_pieces():
+    rng, lin, _ = _lin(601)
+    x = dev_f16(S.activations(rng, 70, 512))
+    zs = [X.linear_split(lin.weight, x[a:b], inner=True) for a, b in ((0, 40), (40, 41), (41, 70))]
+    y = X.linear_finish(lin.weight, zs, X.DT_F16)
+    want = torch.cat([X.finish(lin.weight, z) for z in zs])
+    assert (bits(y) == bits(want)).all()
+
+
+def test_linear_pieces_and_piece():
+    rng, lin, (t, u, v) = _lin(602)
+    x = dev_f16(S.activations(rng, 64, 512))
+    v_, held = X.linear_pieces(lin.weight, [40, 24])
+    assert v_.is_ok(), v_
+    assert held.owned == 0 and held.data == lin.weight.w.data
+    zs = [X.linear_piece(lin.weight, x[:40], held), X.linear_piece(lin.weight, x[40:], held)]
+    # a piece with prepared rows gives the same inner product
+    zp = X.linear_piece(lin.weight, X.prepare(lin.weight, x[40:]), held, prepared=True)
+    assert (bits(zp) == bits(zs[1])).all()
+    y = X.linear_finish(lin.weight, zs, X.DT_F16)
+    # each piece is the matmul of its rows
+    want = torch.cat([lin(x[:40]), lin(x[40:])])
+    assert (bits(y) == bits(want)).all()
+    yo = S.h2f(O.project(x.float().cpu().numpy(), t, u, v, 512, 384, 64))
+    assert S.rel_fro(y.float().cpu().numpy(), yo) < 1e-3
+    # pieces that would take another kernel path than the whole call: refused
+    v2, _ = X.linear_pieces(lin.weight, [40, 8])
+    assert v2.code == X.UNSUPPORTED and "kernel path" in v2.reason
+    # a held array of another weight: refused
+    _, other, _ = _lin(603)
+    _, held2 = X.linear_pieces(other.weight, [20])
+    with pytest.raises(X.Exl3Error):
+        X.linear_piece(lin.weight, x[:20], held2)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 16, 40])
+def test_grouped_linear(rows):
+    rng = np.random.default_rng(700 + rows)
+    G, in_f, out_f, n = 4, 512, 256, 48
+    parts = [S.linear(rng, in_f, out_f, n) for _ in range(G)]
+    src = {}
+    for g, (t, u, v) in enumerate(parts):
+        src[f"m.wo_a.slice.{g}.trellis"] = t.view(np.int16)
+        src[f"m.wo_a.slice.{g}.suh"] = u.view(np.float16)
+        src[f"m.wo_a.slice.{g}.svh"] = v.view(np.float16)
+    L = X.Loader('{"format":"exl3","codebook":"mul1"}', X.DictSource(src))
+    assert L.opened.is_ok()
+    v, w = L.load_tensor("m.wo_a", in_f)
+    assert v.is_ok(), v
+    assert w.flags == 1 and w.w.dims() == (G, in_f // 16, out_f // 16, n)
+    x = S.activations(rng, rows * G, in_f).reshape(rows, G, in_f)
+    y = X.matmul(w, dev_f16(x.reshape(rows, G, in_f)), out=torch.empty(rows, G, out_f,
+                                                                     dtype=torch.float16, device=DEV))
+    y = y.float().cpu().numpy()
+    for g, (t, u, vv) in enumerate(parts):
+        yo = S.h2f(O.project(x[:, g, :].astype(np.float32), t, u, vv, in_f, out_f, n))
+        assert S.rel_fro(y[:, g, :], yo) < 1e-3, g
+        # group g alone through its own linear: the same values
+        lin = X.Linear(dev_u16(t), dev_f16(u), dev_f16(vv))
+        yg = lin(dev_f16(np.ascontiguousarray(x[:, g, :]))).float().cpu().numpy()
+        assert np.array_equal(y[:, g, :], yg), g
+    # a grouped linear is not an expert bank
+    xs = dev_f16(S.activations(rng, 2, in_f))
+    with pytest.raises(X.Exl3Error):
+        X.swiglu(w, w, w, xs)
+    X.release(w)
+    L.close()
