@@ -202,7 +202,7 @@ typedef struct exl3_linear_parts {
  * per row, or NULL with `gate_vec` [D] (the logit computed in the launch);
  * `logits` [rows, E] with `k`: the routing (softmax, top-k) done in the
  * launches, inds / scores then empty.  `sigtab` (MLX's sigmoid table) is
- * not read: the sigmoid is computed (see exl3_swiglu_shared). */
+ * not read: the sigmoid is computed, then rounded to x's dtype. */
 typedef struct exl3_shared_swiglu {
   uint32_t size;
   const exl3_weight *gate;
@@ -369,6 +369,23 @@ exl3_verdict exl3_linear_pieces(const exl3_weight *w, const exl3_linear_parts *o
  * prepared (f16). */
 exl3_verdict exl3_linear_piece(const exl3_weight *w, exl3_array x, const exl3_linear_parts *opts,
                                exl3_stream s, exl3_array *out);
+
+/* QuantTable.swiglu_shared (quant.zig:94-97; SharedSwiglu :183-197; the
+ * host's chain it replaces: turboexl3_qwen38/src/direct/moe.zig:113-160):
+ * y = swiglu(x; gate, up, down, routes) + sigmoid(logit) * shared(x), with
+ * shared(x) = down_s(silu(gate_s(x)) * up_s(x)) the dense SwiGLU of
+ * opts->gate / up / down (unclamped), the shared expert riding the routed
+ * GEMV launches as one more expert slot per row.  Routes: inds / scores as
+ * in exl3_swiglu, or empty with opts->logits [rows, E] and opts->k: the
+ * softmax's top k renormalized, computed in the first launch.  The logit:
+ * opts->logit [rows], or opts->gate_vec [D] (the dot with x's row, in the
+ * launch), both in x's dtype; sigmoid(logit) is rounded to x's dtype.
+ * Refused (the host runs its chain) at prefill-sized batches and when the
+ * shared expert's widths, rate or codebook differ from the banks'. */
+exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
+                                const exl3_weight *down, exl3_array x, exl3_array inds,
+                                exl3_array scores, const exl3_shared_swiglu *opts,
+                                exl3_stream s, exl3_array *out);
 
 /* ----------------------------------------------------- the plugin table */
 

@@ -99,6 +99,12 @@ WeightPriv *priv_of(const exl3_weight *w) {
   return w ? static_cast<WeightPriv *>(w->priv) : nullptr;
 }
 
+// The weight's private part when it is one linear (not a bank or a group).
+const WeightPriv *single_linear(const exl3_weight *w) {
+  const WeightPriv *pv = priv_of(w);
+  return pv && pv->experts == 0 && pv->groups == 0 ? pv : nullptr;
+}
+
 int64_t numel(const exl3_array &a) {
   int64_t n = 1;
   for (int i = 0; i < a.ndim; ++i) n *= a.shape[i];
@@ -163,8 +169,8 @@ struct StreamScratch {
   size_t slot_bytes = 0;
   void *moe = nullptr;
   size_t moe_bytes = 0;
-  void *grp = nullptr;  // a grouped linear's gathered rows and outputs
-  size_t grp_bytes = 0;
+  void *aux = nullptr;  // a grouped linear's gathered rows and outputs; swiglu_shared's routes
+  size_t aux_bytes = 0;
   std::vector<void *> retired;  // superseded buffers, freed by exl3_scratch_release
   // superseded slot buffers (each with its own status word and slots)
   std::vector<std::pair<void *, size_t>> retired_slots;
@@ -684,9 +690,9 @@ static exl3_verdict grouped_matmul(const exl3_weight *w, const WeightPriv *pv, e
   const size_t xg_bytes = ((size_t)rows * in * esz + 255) & ~(size_t)255;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> lk(ss->mu);
-  hipError_t e = grow(ss, &ss->grp, &ss->grp_bytes, xg_bytes + (size_t)rows * outf * esz, s);
+  hipError_t e = grow(ss, &ss->aux, &ss->aux_bytes, xg_bytes + (size_t)rows * outf * esz, s);
   if (e != hipSuccess) return hip_failed(e);
-  char *xg = (char *)ss->grp, *yg = xg + xg_bytes;
+  char *xg = (char *)ss->aux, *yg = xg + xg_bytes;
   const size_t per = (size_t)(in / 16) * (outf / 16) * pv->f.n;  // trellis halfwords per linear
   WeightPriv pg = *pv;
   pg.experts = 0;
@@ -982,6 +988,125 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   return ok();
 }
 
+// The routed experts and the gated shared expert in the same launches: the
+// routes gain a slot per row for the shared expert (an index past the bank's,
+// score sigmoid(logit)), which the routed GEMV launches, the mid step and the
+// weighted sum serve like any expert (quant.zig:94-97,183-197).
+exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
+                                const exl3_weight *down, exl3_array x, exl3_array inds,
+                                exl3_array scores, const exl3_shared_swiglu *opts,
+                                exl3_stream stream, exl3_array *out) {
+  const WeightPriv *pg = priv_of(gate), *pu = priv_of(up), *pd = priv_of(down);
+  if (!pg || !pu || !pd || !out || !opts) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  if (opts->size < (uint32_t)sizeof(exl3_shared_swiglu))
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: SharedSwiglu older than this library's");
+  const WeightPriv *sg = single_linear(opts->gate), *su = single_linear(opts->up),
+                   *sd = single_linear(opts->down);
+  if (!sg || !su || !sd)
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: the shared expert's linears are missing");
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0) return kDtype;
+  if (x.ndim < 1 || !x.data) return kShape;
+  const int64_t hidden = x.shape[x.ndim - 1];
+  const int64_t rows = numel(x) / std::max<int64_t>(hidden, 1);
+  if (rows <= 0) return kShape;
+  if (pg->experts == 0 || pg->experts != pu->experts || pg->experts != pd->experts ||
+      pg->groups || pu->groups || pd->groups)
+    return kShape;
+  if (pg->in != hidden || pu->in != hidden || pd->out != hidden || pg->out != pu->out ||
+      pd->in != pg->out)
+    return kShape;
+  auto same = [](const WeightPriv *a, const WeightPriv *b) {
+    return a->in == b->in && a->out == b->out && a->f.n == b->f.n &&
+           a->f.codebook == b->f.codebook && a->f.window == b->f.window && a->device == b->device;
+  };
+  if (!same(sg, pg) || !same(su, pu) || !same(sd, pd) || pg->f.n != pu->f.n ||
+      pg->f.codebook != pu->f.codebook || pg->f.window != pu->f.window)
+    return refuse(EXL3_UNSUPPORTED,
+                  "turboexl3_mi355x: the shared expert differs from the routed experts in width, "
+                  "rate or codebook (the host runs its chain)");
+  const int64_t E = pg->experts;
+  // routes: given, or from the router's logits
+  int64_t k = 0;
+  int sdt = exl3::ACT_F32;
+  const bool from_logits = opts->logits.data != nullptr;
+  if (from_logits) {
+    if (inds.data || scores.data) return kShape;
+    k = opts->k;
+    if (opts->logits.dtype != x.dtype) return kDtype;
+    if (k <= 0 || k > 31 || k > E || opts->logits.ndim < 1 ||
+        opts->logits.shape[opts->logits.ndim - 1] != E || numel(opts->logits) != rows * E)
+      return kShape;
+  } else {
+    if (!inds.data || !scores.data) return kShape;
+    if (inds.dtype != EXL3_DT_I32 && inds.dtype != EXL3_DT_U32) return kDtype;
+    sdt = act_of(scores.dtype);
+    if (sdt < 0) return kDtype;
+    k = inds.shape[inds.ndim - 1];
+    if (k <= 0 || k > 31 || numel(inds) != rows * k || numel(scores) != rows * k) return kShape;
+  }
+  // the shared gate's logit: given per row, or the dot with gate_vec
+  if (opts->logit.data) {
+    if (opts->logit.dtype != x.dtype || numel(opts->logit) != rows) return kShape;
+  } else if (opts->gate_vec.data) {
+    if (opts->gate_vec.dtype != x.dtype || numel(opts->gate_vec) != hidden) return kShape;
+  } else {
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: the shared gate needs logit or gate_vec");
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (hipSetDevice(pg->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3::MoeArgs a{};
+  a.x = x.data;
+  a.xdt = xdt;
+  a.rows = (int)rows;
+  a.hidden = (int)hidden;
+  a.inter = (int)pg->out;
+  a.limit = 0.0f;  // the table SwiGLU, unclamped (turboexl3_qwen38/src/direct/moe.zig:215-220)
+  a.experts = (int)E + 1;
+  a.topk = (int)k + 1;
+  a.sdt = exl3::ACT_F32;
+  StreamScratch *ss = scratch_for(pg->device, s);
+  std::lock_guard<std::mutex> g(ss->mu);
+  // the routes with the shared slot, k + 1 per row
+  const size_t routes = ((size_t)rows * (k + 1) * 4 + 255) & ~(size_t)255;
+  hipError_t e = grow(ss, &ss->aux, &ss->aux_bytes, 2 * routes, s);
+  if (e != hipSuccess) return hip_failed(e);
+  uint32_t *r_inds = (uint32_t *)ss->aux;
+  float *r_scores = (float *)((char *)ss->aux + routes);
+  a.inds = r_inds;
+  a.scores = r_scores;
+  if (exl3::moe_uses_gemm(a, !pg->f.integer_rate(), !pd->f.integer_rate()))
+    return refuse(EXL3_UNSUPPORTED,
+                  "turboexl3_mi355x: the shared expert rides the routed GEMV launches; at "
+                  "prefill-sized batches the host runs swiglu and its shared expert's chain");
+  exl3_verdict v = output_for(out, x, hidden, rows);
+  if (v.code != EXL3_OK) return v;
+  a.y = out->data;
+  a.ydt = xdt;
+  size_t pf = 0;
+  const size_t need =
+      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &pf);
+  e = grow(ss, &ss->moe, &ss->moe_bytes, need, s);
+  if (e != hipSuccess) return hip_failed(e);
+  e = exl3::launch_moe_shared_route(
+      (const uint32_t *)inds.data, scores.data, sdt, opts->logits.data, (int)E, (int)k,
+      opts->logit.data, opts->gate_vec.data, x.data, xdt, (int)rows, (int)hidden, r_inds,
+      r_scores, s);
+  if (e != hipSuccess) return e == hipErrorInvalidValue ? kShape : hip_failed(e);
+  exl3::Scratch slots;
+  e = slots_for(ss, pf, s, &slots);
+  if (e != hipSuccess) return hip_failed(e);
+  auto bank = [](const exl3_weight *w, const WeightPriv *p) {
+    return exl3::MoeBank{(const uint16_t *)w->w.data, (const uint16_t *)w->scales.data,
+                         (const uint16_t *)w->biases.data, p->f, (int)p->in, (int)p->out};
+  };
+  const exl3::MoeShared sh{bank(opts->gate, sg), bank(opts->up, su), bank(opts->down, sd)};
+  e = exl3::launch_moe(a, bank(gate, pg), bank(up, pu), bank(down, pd), ss->moe, ss->moe_bytes,
+                       slots, s, &sh);
+  if (e != hipSuccess) return e == hipErrorInvalidValue ? kShape : hip_failed(e);
+  return ok();
+}
+
 exl3_verdict exl3_decode_matrix(const exl3_weight *w, int32_t expert, exl3_array out,
                                 exl3_stream stream) {
   const WeightPriv *pv = priv_of(w);
@@ -1082,11 +1207,6 @@ static exl3_verdict new_array(exl3_array *out, const exl3_array *lead, int64_t r
   a._pad = 0;
   *out = a;
   return ok();
-}
-
-static const WeightPriv *single_linear(const exl3_weight *w) {
-  const WeightPriv *pv = priv_of(w);
-  return pv && pv->experts == 0 && pv->groups == 0 ? pv : nullptr;
 }
 
 static bool parts_ok(const exl3_linear_parts *o) {
@@ -1286,11 +1406,11 @@ exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
     return refuse(EXL3_FAILED, "turboexl3_mi355x: scratch released while its stream is being captured");
   hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_failed(e);
-  for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe, &ss->grp}) {
+  for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe, &ss->aux}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
-  ss->xp_bytes = ss->kpart_bytes = ss->slot_bytes = ss->moe_bytes = ss->grp_bytes = 0;
+  ss->xp_bytes = ss->kpart_bytes = ss->slot_bytes = ss->moe_bytes = ss->aux_bytes = 0;
   for (void *p : ss->retired) (void)hipFree(p);
   ss->retired.clear();
   for (auto &b : ss->retired_slots) (void)hipFree(b.first);
@@ -1400,7 +1520,7 @@ static const exl3_quant_table kTable = {
     nullptr,  // merged_gated_out
     nullptr,  // q_planes
     nullptr,  // indexer
-    nullptr,  // swiglu_shared
+    &exl3_swiglu_shared,
     nullptr,  // resident: the GEMM decodes in LDS, kept decoded matrices do not pay
     nullptr,  // resident_pending
     nullptr,  // unrotate

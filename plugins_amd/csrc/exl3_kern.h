@@ -120,6 +120,11 @@ struct GemvWeight {
   uint16_t *zout;       // the inner product z (f16) instead
   float *partial;       // [ksplit][ptotal][out] slots, empty between calls
   size_t expert_words;  // trellis dwords per expert
+  // routed launches with a shared expert: expert index GemvCfg::shared_expert
+  // reads this linear (trellis, suh, svh) instead of the bank's
+  const uint32_t *sh_tw;
+  const uint16_t *sh_suh;
+  const uint16_t *sh_svh;
 };
 
 struct GemvCfg {
@@ -143,6 +148,7 @@ struct GemvCfg {
   // and res_ssq[row][group] = the group's sum of squares of the new res
   float *res;
   float *res_ssq;
+  int shared_expert;  // routed launches: the index of the shared expert (-1: none)
 };
 
 // Prologue forms of the GEMV prepare (compile time: they decide which loads
@@ -1696,11 +1702,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
   const RowMap rm{ri, 0, 0};
   // the prepare form the item's rows need (most items hold a few slots: one
   // batch or one pass instead of the passes 16 rows take)
-  const uint32_t *twe = tw + (size_t)it.expert * W.expert_words;
+  // the shared expert (an index past the bank's) reads its own linear
+  const bool sh = (int)it.expert == a.c.shared_expert;
+  GemvWeight Wx = W;
+  if (sh) {
+    Wx.suh = W.sh_suh;
+    Wx.svh = W.sh_svh;
+  }
+  const uint32_t *twe = sh ? W.sh_tw : tw + (size_t)it.expert * W.expert_words;
   auto run = [&](auto P) {
-    gemv_wg<K, CB, MASKED, decltype(P)::value>(twe, out_tiles, x, geo, a.c, W, (int)it.expert,
-                                               (int)it.count, rm, blockIdx.x - ws.c0, blockIdx.y,
-                                               smem + 256, MOE_ITEM_ROWS);
+    gemv_wg<K, CB, MASKED, decltype(P)::value>(twe, out_tiles, x, geo, a.c, Wx,
+                                               sh ? 0 : (int)it.expert, (int)it.count, rm,
+                                               blockIdx.x - ws.c0, blockIdx.y, smem + 256,
+                                               MOE_ITEM_ROWS);
   };
   const int items_n = (int)it.count * (geo.tps / 8);
   if (items_n <= PREP_ITEMS)

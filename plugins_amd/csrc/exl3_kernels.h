@@ -176,8 +176,26 @@ bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic);
 // of its Scratch.
 size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
                          size_t *partial_floats);
+// shared (optional): a shared expert's linears (each a bank of one), served
+// inside the routed launches as expert index a.experts - 1, whose slots the
+// caller's inds / scores hold (launch_moe_shared_route makes them); the GEMV
+// path only (moe_uses_gemm false), of the banks' formats and widths.
+struct MoeShared {
+  MoeBank gate, up, down;
+};
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                       const MoeBank &down, void *scratch, size_t scratch_bytes,
-                      const Scratch &slots, hipStream_t s);
+                      const Scratch &slots, hipStream_t s, const MoeShared *shared = nullptr);
+// The routes of a swiglu with a shared expert, k + 1 slots per row into
+// inds_out / scores_out (f32): the routed experts' as given (inds, scores in
+// sdt) or, with logits [rows][E] (xdt), the softmax's top k (ties: the lower
+// index) renormalized to sum 1; then the shared expert (index E) with score
+// sigmoid(logit) rounded to xdt, the logit given per row (logit [rows], xdt)
+// or the dot of x's row with gate_vec [hidden] (xdt), rounded to xdt.
+hipError_t launch_moe_shared_route(const uint32_t *inds, const void *scores, int sdt,
+                                   const void *logits, int experts, int k, const void *logit,
+                                   const void *gate_vec, const void *x, int xdt, int rows,
+                                   int hidden, uint32_t *inds_out, float *scores_out,
+                                   hipStream_t s);
 
 }  // namespace exl3

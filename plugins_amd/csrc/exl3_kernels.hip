@@ -655,17 +655,20 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const void *__restrict__ 
   }
 }
 
-// h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e].
+// h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e]
+// (the shared expert's, sh_suh_d, for e == shared).
 __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u,
                                                      const uint32_t *__restrict__ inds, int experts,
                                                      const uint16_t *__restrict__ suh_d,
                                                      uint16_t *__restrict__ xd, int inter,
-                                                     float limit) {
+                                                     float limit, int shared,
+                                                     const uint16_t *__restrict__ sh_suh_d) {
   const int lane = threadIdx.x;
   const size_t slot = blockIdx.y;
   const uint32_t e = inds ? inds[slot] : 0u;
   if (e >= (uint32_t)experts) return;
+  const uint16_t *sud = (int)e == shared ? sh_suh_d : suh_d + (size_t)e * inter;
   const int i0 = blockIdx.x * 128 + lane;
   float v[2];
 #pragma unroll
@@ -678,7 +681,7 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
       uv = uv < limit ? uv : limit;
     }
     const float h = f32_value(gv / (1.0f + expf(-gv))) * uv;
-    v[j] = h2f(f2h(h)) * h2f(suh_d[(size_t)e * inter + i]);
+    v[j] = h2f(f2h(h)) * h2f(sud[i]);
   }
 #pragma unroll
   for (int bit = 1; bit <= 32; bit <<= 1) {
@@ -715,6 +718,110 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
     ((uint16_t *)y)[row * hidden + i] = f2bf(acc);
   else
     ((float *)y)[row * hidden + i] = acc;
+}
+
+// The routes of a swiglu with a shared expert (launch_moe_shared_route): one
+// wave per row.  Top k of a softmax: the same order as the logits' (exp is
+// monotonic), so the selection runs on the logits, k rounds of a wave argmax
+// (ties: the lower index); the kept probabilities exp(l - max) / sum are
+// renormalized to sum 1.
+constexpr int SHARED_ROUTE_PER_LANE = 16;  // experts per lane: up to 1024
+
+__device__ __forceinline__ float round_act(float v, int dt) {
+  if (dt == OUT_F16) return h2f(f2h(v));
+  if (dt == OUT_BF16) return bf2f(f2bf(v));
+  return v;
+}
+
+__global__ __launch_bounds__(64) void moe_shared_route_kernel(
+    const uint32_t *__restrict__ inds, const void *__restrict__ scores, int sdt,
+    const void *__restrict__ logits, int E, int k, const void *__restrict__ logit,
+    const void *__restrict__ gate_vec, const void *__restrict__ x, int xdt, int hidden,
+    uint32_t *__restrict__ inds_out, float *__restrict__ scores_out) {
+  const size_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int kk = k + 1;
+  if (logits != nullptr) {
+    float l[SHARED_ROUTE_PER_LANE];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < SHARED_ROUTE_PER_LANE; ++i) {
+      const int e = lane + 64 * i;
+      l[i] = e < E ? load_act(logits, row * E + e, xdt) : -INFINITY;
+      mx = fmaxf(mx, l[i]);
+    }
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SHARED_ROUTE_PER_LANE; ++i)
+      if (lane + 64 * i < E) sum += expf(l[i] - mx);
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    uint32_t taken = 0;
+    float kept = 0.0f, pk = 0.0f;
+    int ek = 0;
+    for (int j = 0; j < k; ++j) {
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int i = 0; i < SHARED_ROUTE_PER_LANE; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !(taken & (1u << i)) && (l[i] > bv || (l[i] == bv && e < bi))) {
+          bv = l[i];
+          bi = e;
+        }
+      }
+      for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(bv, m, 64);
+        const int oi = __shfl_xor(bi, m, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      const float p = expf(bv - mx) / sum;
+      kept += p;
+      if (lane == j) {
+        pk = p;
+        ek = bi;
+      }
+    }
+    if (lane < k) {
+      inds_out[row * kk + lane] = (uint32_t)ek;
+      scores_out[row * kk + lane] = pk / kept;
+    }
+  } else if (lane < k) {
+    inds_out[row * kk + lane] = inds[row * k + lane];
+    scores_out[row * kk + lane] = load_act(scores, row * k + lane, sdt);
+  }
+  float lg;
+  if (logit != nullptr) {
+    lg = load_act(logit, row, xdt);
+  } else {
+    float d = 0.0f;
+    for (int i = lane; i < hidden; i += 64)
+      d += load_act(x, row * hidden + i, xdt) * load_act(gate_vec, i, xdt);
+    for (int m = 32; m >= 1; m >>= 1) d += __shfl_xor(d, m, 64);
+    lg = round_act(d, xdt);
+  }
+  if (lane == 0) {
+    inds_out[row * kk + k] = (uint32_t)E;
+    scores_out[row * kk + k] = round_act(1.0f / (1.0f + expf(-lg)), xdt);
+  }
+}
+
+hipError_t launch_moe_shared_route(const uint32_t *inds, const void *scores, int sdt,
+                                   const void *logits, int experts, int k, const void *logit,
+                                   const void *gate_vec, const void *x, int xdt, int rows,
+                                   int hidden, uint32_t *inds_out, float *scores_out,
+                                   hipStream_t s) {
+  if (rows <= 0 || k <= 0 || k > 63 || experts <= 0 || experts > 64 * SHARED_ROUTE_PER_LANE ||
+      (logits == nullptr && (inds == nullptr || scores == nullptr)) ||
+      (logit == nullptr && (gate_vec == nullptr || x == nullptr)))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(moe_shared_route_kernel, dim3(rows), dim3(64), 0, s, inds, scores, sdt,
+                     logits, experts, k, logit, gate_vec, x, xdt, hidden, inds_out, scores_out);
+  return hipGetLastError();
 }
 
 namespace {
@@ -845,6 +952,7 @@ MoeGemv moe_gemv(const void *x, int xdt, bool prepared, size_t slots, int in, in
   m.a.c.ksplit = ksplit;
   m.a.c.mask = f.mask();
   m.a.c.nw = f.n / 2;
+  m.a.c.shared_expert = -1;
   return m;
 }
 
@@ -863,7 +971,7 @@ size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
 
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                       const MoeBank &down, void *scratch, size_t scratch_bytes,
-                      const Scratch &slots, hipStream_t s) {
+                      const Scratch &slots, hipStream_t s, const MoeShared *shared) {
   if (a.rows <= 0 || a.topk <= 0 || a.experts <= 0 || a.experts > MOE_ROUTE_THREADS)
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
@@ -874,6 +982,16 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     return hipErrorInvalidValue;
   const bool gu_generic = !gate.f.integer_rate(), d_generic = !down.f.integer_rate();
   const MoeLayout L = moe_layout(a, gu_generic, d_generic);
+  if (shared) {
+    auto same = [](const MoeBank &b, const MoeBank &r) {
+      return b.trellis && b.suh && b.svh && b.in == r.in && b.out == r.out && b.f.n == r.f.n &&
+             b.f.codebook == r.f.codebook && b.f.window == r.f.window;
+    };
+    if (L.gemm || a.inds == nullptr || !same(shared->gate, gate) || !same(shared->up, up) ||
+        !same(shared->down, down))
+      return hipErrorInvalidValue;
+  }
+  const int sh_index = shared ? a.experts - 1 : -1;
   if (scratch_bytes < L.total || slots.status == nullptr || slots.partial == nullptr ||
       slots.partial_floats < L.partial_floats || L.slots > 65535 ||
       L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
@@ -909,7 +1027,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     grouped(gate, xg, g);
     grouped(up, xu, u);
     hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
-                       a.experts, down.suh, xd, a.inter, a.limit);
+                       a.experts, down.suh, xd, a.inter, a.limit, -1, nullptr);
     grouped(down, xd, d);
     hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s,
                        d, a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
@@ -933,12 +1051,27 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
   mgu.a.w[0] = moe_weight(gate, g, pgu);
   mgu.a.w[1] = moe_weight(up, u, pgu + gu_part);
+  if (shared) {
+    mgu.a.c.shared_expert = md.a.c.shared_expert = sh_index;
+    const MoeBank *sb[2] = {&shared->gate, &shared->up};
+    for (int i = 0; i < 2; ++i) {
+      mgu.a.w[i].sh_tw = reinterpret_cast<const uint32_t *>(sb[i]->trellis);
+      mgu.a.w[i].sh_suh = sb[i]->suh;
+      mgu.a.w[i].sh_svh = sb[i]->svh;
+    }
+  }
   moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu,
                   sorted, items, n_items, a.topk);
   hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
-                     a.experts, down.suh, xd, a.inter, a.limit);
+                     a.experts, down.suh, xd, a.inter, a.limit, sh_index,
+                     shared ? shared->down.suh : nullptr);
   md.tw[0] = md.tw[1] = reinterpret_cast<const uint32_t *>(down.trellis);
   md.a.w[0] = moe_weight(down, d, pd);
+  if (shared) {
+    md.a.w[0].sh_tw = reinterpret_cast<const uint32_t *>(shared->down.trellis);
+    md.a.w[0].sh_suh = shared->down.suh;
+    md.a.w[0].sh_svh = shared->down.svh;
+  }
   moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted,
                   items, n_items, a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,

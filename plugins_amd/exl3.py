@@ -110,6 +110,13 @@ class LinearParts(Structure):
                 ("prepared", c_bool), ("held", Array), ("rows", U32Span), ("parts", ArraySpan)]
 
 
+class SharedSwiglu(Structure):
+    """`SharedSwiglu` (quant.zig:183-197): the gated shared expert's options."""
+    _fields_ = [("size", c_uint32), ("gate", POINTER(Weight)), ("up", POINTER(Weight)),
+                ("down", POINTER(Weight)), ("sigtab", Array), ("logit", Array),
+                ("gate_vec", Array), ("logits", Array), ("k", c_uint32)]
+
+
 # The QuantTable's entries in the reference's order (quant.zig:24-107).
 TABLE_ENTRIES = ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank",
                  "release", "matmul", "moe", "register_kernels", "swiglu", "linear_split",
@@ -165,6 +172,8 @@ SIGNATURES = {
     "exl3_linear_pieces": (Verdict, [POINTER(Weight), POINTER(LinearParts), c_void_p, POINTER(Array)]),
     "exl3_linear_piece": (Verdict, [POINTER(Weight), Array, POINTER(LinearParts), c_void_p,
                                     POINTER(Array)]),
+    "exl3_swiglu_shared": (Verdict, [POINTER(Weight), POINTER(Weight), POINTER(Weight), Array, Array,
+                                     Array, POINTER(SharedSwiglu), c_void_p, POINTER(Array)]),
 }
 
 _lib = None
@@ -432,6 +441,27 @@ def swiglu(gate: Weight, up: Weight, down: Weight, x, inds=None, scores=None, li
     check(lib().exl3_swiglu(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), array(x),
                             array(inds), array(scores), ctypes.byref(opts), stream_handle(stream),
                             ctypes.byref(a)), "swiglu")
+    return y
+
+
+def swiglu_shared(gate: Weight, up: Weight, down: Weight, x, shared, inds=None, scores=None,
+                  logit=None, gate_vec=None, logits=None, k: int = 0, out=None, stream=None):
+    """QuantTable.swiglu_shared: routed experts plus sigmoid(logit) * the shared
+    expert (shared = (gate, up, down) Weights), in the routed launches.  Routes
+    from inds/scores, or from the router's `logits` with `k`; the logit given
+    per row or computed from `gate_vec`."""
+    y = out if out is not None else _torch().empty_like(x)
+    o = SharedSwiglu()
+    o.size = ctypes.sizeof(SharedSwiglu)
+    o.gate, o.up, o.down = (ctypes.pointer(w) for w in shared)
+    o.logit = array(logit)
+    o.gate_vec = array(gate_vec)
+    o.logits = array(logits)
+    o.k = k
+    a = array(y)
+    check(lib().exl3_swiglu_shared(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down),
+                                   array(x), array(inds), array(scores), ctypes.byref(o),
+                                   stream_handle(stream), ctypes.byref(a)), "swiglu_shared")
     return y
 
 

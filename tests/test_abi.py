@@ -36,7 +36,7 @@ def test_quant_table_fields():
     assert ctypes.string_at(t.name.ptr, t.name.len) == b"turboexl3_mi355x"
     served = ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank", "release",
               "matmul", "moe", "register_kernels", "swiglu", "linear_split", "linear_finish",
-              "linear_prepared", "linear_pieces", "linear_piece")
+              "linear_prepared", "linear_pieces", "linear_piece", "swiglu_shared")
     for f in X.TABLE_ENTRIES:
         assert bool(getattr(t, f)) == (f in served), f
     # the table's pointers are the flat symbols

@@ -135,3 +135,76 @@ def test_grouped_linear(rows):
         X.swiglu(w, w, w, xs)
     X.release(w)
     L.close()
+
+
+# ------------------------------------------------------- swiglu_shared
+
+def _banks(rng, E, hidden, inter, n):
+    parts = [S.linear(rng, hidden, inter, n, experts=E), S.linear(rng, hidden, inter, n, experts=E),
+             S.linear(rng, inter, hidden, n, experts=E)]
+    keep = [tuple(f(a) for f, a in zip((dev_u16, dev_f16, dev_f16), p)) for p in parts]
+    return parts, [X.wrap(*k) for k in keep], keep
+
+
+def _shared_oracle(x, parts, sparts, inds, scores, lg, hidden, inter, n):
+    routed = O.moe_swiglu(x, *parts, inds, scores, hidden, inter, n)
+    one = [tuple(np.asarray(a)[None] for a in p) for p in sparts]
+    shared = O.moe_swiglu(x, *one, np.zeros((x.shape[0], 1), np.int32),
+                          np.ones((x.shape[0], 1), np.float32), hidden, inter, n)
+    sig = (1.0 / (1.0 + np.exp(-lg.astype(np.float32)))).astype(np.float16).astype(np.float32)
+    return routed + sig[:, None] * shared
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8])
+@pytest.mark.parametrize("mode", ["routes+logit", "logits+gate_vec"])
+def test_swiglu_shared_against_oracle(rows, mode):
+    rng = np.random.default_rng(800 + rows + (100 if mode[0] == "l" else 0))
+    E, hidden, inter, k, n = 8, 512, 256, 3, 64
+    parts, banks, keep = _banks(rng, E, hidden, inter, n)
+    sparts = [S.linear(rng, hidden, inter, n), S.linear(rng, hidden, inter, n),
+              S.linear(rng, inter, hidden, n)]
+    shared = [X.Linear(dev_u16(t), dev_f16(u), dev_f16(v)) for t, u, v in sparts]
+    x = S.activations(rng, rows, hidden)
+    xd = dev_f16(x)
+    if mode == "routes+logit":
+        logits = rng.standard_normal((rows, E)).astype(np.float32)
+        inds, scores = O.route_topk(logits, k)
+        lg = rng.standard_normal(rows).astype(np.float16)
+        y = X.swiglu_shared(*banks, xd, [s.weight for s in shared],
+                            inds=torch.from_numpy(inds).to(DEV),
+                            scores=torch.from_numpy(scores).to(DEV), logit=dev_f16(lg))
+    else:
+        logits = rng.standard_normal((rows, E)).astype(np.float16)
+        inds, scores = O.route_topk(logits.astype(np.float32), k)
+        gv = (rng.standard_normal(hidden) * 0.05).astype(np.float16)
+        lg = (x.astype(np.float32) @ gv.astype(np.float32)).astype(np.float16)
+        y = X.swiglu_shared(*banks, xd, [s.weight for s in shared], logits=dev_f16(logits), k=k,
+                            gate_vec=dev_f16(gv))
+    want = _shared_oracle(x, parts, sparts, inds, scores, lg, hidden, inter, n)
+    got = y.float().cpu().numpy()
+    assert S.rel_fro(got, want) < 1e-3, S.rel_fro(got, want)
+    assert (S.row_rel(got, want) < 3e-3).all()
+
+
+def test_swiglu_shared_refusals():
+    rng = np.random.default_rng(901)
+    E, hidden, inter, k, n = 8, 512, 256, 2, 64
+    parts, banks, keep = _banks(rng, E, hidden, inter, n)
+    sp = [S.linear(rng, hidden, inter, n), S.linear(rng, hidden, inter, n),
+          S.linear(rng, inter, hidden, n)]
+    shared = [X.Linear(dev_u16(t), dev_f16(u), dev_f16(v)) for t, u, v in sp]
+    # prefill-sized batches: the host's chain
+    x = dev_f16(S.activations(rng, 100, hidden))
+    logits = dev_f16(rng.standard_normal((100, E)).astype(np.float16))
+    gv = dev_f16((rng.standard_normal(hidden) * 0.05).astype(np.float16))
+    with pytest.raises(X.Exl3Error, match="chain"):
+        X.swiglu_shared(*banks, x, [s.weight for s in shared], logits=logits, k=k, gate_vec=gv)
+    # a shared expert of another width
+    wide = [S.linear(rng, hidden, 384, n), S.linear(rng, hidden, 384, n), S.linear(rng, 384, hidden, n)]
+    other = [X.Linear(dev_u16(t), dev_f16(u), dev_f16(v)) for t, u, v in wide]
+    x1 = dev_f16(S.activations(rng, 2, hidden))
+    with pytest.raises(X.Exl3Error, match="differs"):
+        X.swiglu_shared(*banks, x1, [s.weight for s in other], logits=logits[:2], k=k, gate_vec=gv)
+    # neither a logit nor gate_vec
+    with pytest.raises(X.Exl3Error):
+        X.swiglu_shared(*banks, x1, [s.weight for s in shared], logits=logits[:2], k=k)
