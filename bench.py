@@ -74,6 +74,35 @@ def packed_bytes(i: int, o: int) -> int:
     return i * o * K_BITS // 8
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_ms(torch, fn, reps: int = 20) -> float:
+    """Median over `reps` runs of fn, each bracketed by its own HIP events."""
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+# Distinct bytes a rotating working set should reach, so that each pass reads
+# HBM rather than the 256 MB Infinity Cache (MALL).
+ROTATE_BYTES = 512 << 20
+
+
 def cpu_baseline(seconds: float):
     from oracle import oracle as O
     rng = np.random.default_rng(7)
@@ -98,7 +127,7 @@ def cpu_baseline(seconds: float):
         if el >= seconds:
             break
     return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": O.threads(),
-            "kind": "port",
+            "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"{linears} batch-1 K=4 projections cycling one Qwen3-8B layer's 7 linears "
                       f"(q,k,v,o,gate,up,down; {sum(packed_bytes(i, o) for _, i, o in SHAPES) / 1e6:.1f} MB "
                       f"packed), {el:.1f} s, oracle/exl3_oracle.c exl3o_project"}
@@ -111,7 +140,8 @@ def gemm_tflops(torch, iters: int = 10):
     g = torch.Generator(device="cuda")
     g.manual_seed(11)
     lins = []
-    for _ in range(3):  # rotate 3 weights (75 MB) with a 50 MB activation block
+    copies = -(-ROTATE_BYTES // packed_bytes(i, o))  # rotate >= 512 MB of weights
+    for _ in range(copies):
         t = torch.randint(-32768, 32768, (i // 16, o // 16, 64), dtype=torch.int32, device="cuda",
                           generator=g).to(torch.int16)
         suh = torch.ones(i, dtype=torch.float16, device="cuda")
@@ -122,37 +152,39 @@ def gemm_tflops(torch, iters: int = 10):
     for lin in lins:
         lin(x, out=y)
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for it in range(iters):
-        lins[it % 3](x, out=y)
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / iters
+    turn = [0]
+
+    def one():
+        lins[turn[0] % copies](x, out=y)
+        turn[0] += 1
+    ms = _median_ms(torch, one, max(20, iters))
     tf = 2.0 * rows * i * o / (ms * 1e-3) / 1e12
     # context: a dense f16 GEMM of the same shape through torch (hipBLASLt),
-    # the library's rate on unquantized weights (3 x 100 MB rotated)
+    # the library's rate on unquantized weights (6 x 100 MB rotated)
     del lins
-    ws = [torch.randn(i, o, device="cuda", generator=g).to(torch.float16) for _ in range(3)]
+    ws = [torch.randn(i, o, device="cuda", generator=g).to(torch.float16) for _ in range(6)]
     for w in ws:
         torch.matmul(x, w, out=y)
     torch.cuda.synchronize()
-    s.record()
-    for it in range(iters):
-        torch.matmul(x, ws[it % 3], out=y)
-    e.record()
-    torch.cuda.synchronize()
-    dms = s.elapsed_time(e) / iters
+    turn[0] = 0
+
+    def dense():
+        torch.matmul(x, ws[turn[0] % len(ws)], out=y)
+        turn[0] += 1
+    dms = _median_ms(torch, dense, max(20, iters))
     dtf = 2.0 * rows * i * o / (dms * 1e-3) / 1e12
     return {"prefill_gemm_m2048_gate_up_k4": {"tflops": round(tf, 2), "ms": round(ms, 4),
+                                              "timing": f"median of 20 launches, {copies} weight copies "
+                                                        f"({copies * packed_bytes(i, o) >> 20} MiB) rotated",
                                               "frac_of_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
                                               "includes": "prepare + LDS-decode MFMA GEMM + finish",
                                               "dense_f16_torch_same_shape_tflops": round(dtf, 1)}}
 
 
-def _graph_ms(torch, fn, reps: int) -> float:
+def _graph_ms(torch, fn, reps: int = 20) -> float:
     """Captures fn (after two eager calls on the capture stream) into a HIP
-    graph and returns the average replay time in ms (HIP events)."""
+    graph and returns the median replay time in ms over max(reps, 20)
+    replays, each between its own HIP events."""
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(cap):
@@ -164,21 +196,18 @@ def _graph_ms(torch, fn, reps: int) -> float:
         fn()
     g.replay()
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
-        g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps
+    return _median_ms(torch, g.replay, max(reps, 20))
 
 
-def gemv_sweep(torch, X, ks=(2, 3, 4, 5, 6, 8), batches=(1, 2, 4, 8), layers=4, reps=10):
+def gemv_sweep(torch, X, ks=(2, 3, 4, 5, 6, 8), batches=(1, 2, 4, 8), reps=20):
     """the decode GEMV over the Qwen3-8B-shaped linears at
-    each rate K and batch (4 layers, launches grouped as a decoder issues
-    them, HIP graph): packed GB/s."""
+    each rate K and batch (as many layers as make >= 512 MB of weights at
+    that rate, launches grouped as a decoder issues them, HIP graph, median
+    of 20 replays): packed GB/s."""
     out = {}
+    per_layer = sum(i * o for _, i, o in SHAPES)
     for k in ks:
+        layers = -(-ROTATE_BYTES // (per_layer * k // 8))
         lins = build_model(torch, X, layers, seed=100 + k, k_bits=k)
         nbytes = sum(i * o * k // 8 for _, i, o, _ in lins)
         per = len(SHAPES)
@@ -197,10 +226,13 @@ def gemv_sweep(torch, X, ks=(2, 3, 4, 5, 6, 8), batches=(1, 2, 4, 8), layers=4, 
             ms = _graph_ms(torch, step, reps)
             res[f"batch{B}"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                 "us_per_launch": round(ms * 1e3 / len(groups), 2)}
+        res["layers"] = layers
+        res["distinct_mb"] = round(nbytes / 1e6, 1)
         out[f"K{k}"] = res
         del lins
         torch.cuda.empty_cache()
-    return {"gemv_sweep": {"layers": layers, "packed_bytes": "in*out*K/8", **out}}
+    return {"gemv_sweep": {"packed_bytes": "in*out*K/8", "timing": "median of 20 graph replays",
+                           **out}}
 
 
 def gemm_sweep(torch, X, ms=(128, 512, 2048, 4096), iters=8):
@@ -213,7 +245,8 @@ def gemm_sweep(torch, X, ms=(128, 512, 2048, 4096), iters=8):
     out = {}
     for name, i, o in shapes:
         lins = []
-        for _ in range(3):
+        copies = -(-ROTATE_BYTES // packed_bytes(i, o))
+        for _ in range(copies):
             t = torch.randint(-32768, 32768, (i // 16, o // 16, 64), dtype=torch.int32,
                               device="cuda", generator=g).to(torch.int16)
             lins.append(X.Linear(t, torch.ones(i, dtype=torch.float16, device="cuda"),
@@ -225,25 +258,35 @@ def gemm_sweep(torch, X, ms=(128, 512, 2048, 4096), iters=8):
             for lin in lins:
                 lin(x, out=y)
             torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            for it in range(iters):
-                lins[it % 3](x, out=y)
-            b.record()
-            torch.cuda.synchronize()
-            t_ms = a.elapsed_time(b) / iters
+            turn = [0]
+
+            def one():
+                lins[turn[0] % copies](x, out=y)
+                turn[0] += 1
+            t_ms = _median_ms(torch, one, max(20, iters))
             res[f"M{M}"] = {"tflops": round(2.0 * M * i * o / (t_ms * 1e-3) / 1e12, 1),
                             "us": round(t_ms * 1e3, 1)}
+        res["weight_copies"] = copies
         out[name] = res
-    return {"gemm_sweep_k4": out}
+        del lins
+        torch.cuda.empty_cache()
+    return {"gemm_sweep_k4": {"timing": "median of 20 launches, >= 512 MB of weights rotated", **out}}
 
 
-def moe_bench(torch, X, batches=(1, 16, 64), reps=10):
+def moe_bench(torch, X, batches=(1, 16, 64), routings=8, reps=20):
     """a DeepSeek-V3-style routed MoE layer at K=3 (hidden
     7168, expert intermediate 2048, 256 routed experts top-8 from the softmax
-    of N(0,1) logits, renormalized, plus one shared expert): the routed
-    swiglu and the shared expert's dense swiglu per batch, HIP graph;
-    packed bytes = (distinct routed experts + 1) * 3 * 7168 * 2048 * 3/8."""
+    of N(0,1) logits, renormalized, plus one shared expert).  One graph
+    replay runs the layer `routings` times, each call with its own routing,
+    so a replay reads the union of their experts (at batch 1 about 8 x 8
+    experts, ~1.1 GB, beyond the 256 MB MALL): the routed swiglu and the
+    shared expert's dense swiglu per call.  Packed bytes per replay = (the
+    union of the routed experts the replay's calls read + 1 shared) * 3 *
+    7168 * 2048 * 3/8 (distinct bytes, each counted once; `gbs_per_call_sum`
+    counts each call's own distinct experts + the shared one, the bytes the
+    calls ask for, some of which an earlier call left in L2/MALL); median of
+    20 replays.  `swiglu_shared`: the same calls with the shared expert gated
+    (sigmoid(logit)) inside the routed launches (QuantTable.swiglu_shared)."""
     E, H, I, K, topk = 256, 7168, 2048, 3, 8
     n = 16 * K
     g = torch.Generator(device="cuda")
@@ -265,24 +308,46 @@ def moe_bench(torch, X, batches=(1, 16, 64), reps=10):
     out = {}
     for B in batches:
         x = torch.randn(B, 1, H, device="cuda", generator=g).to(torch.float16)
-        probs = torch.softmax(torch.randn(B, E, device="cuda", generator=g), -1)
-        top = probs.topk(topk, -1)
-        scores = (top.values / top.values.sum(-1, keepdim=True)).reshape(B, 1, topk)
-        inds = top.indices.to(torch.int32).reshape(B, 1, topk)
-        distinct = int(torch.unique(inds).numel())
+        calls, union, per_call = [], set(), 0
+        for _ in range(routings):
+            probs = torch.softmax(torch.randn(B, E, device="cuda", generator=g), -1)
+            top = probs.topk(topk, -1)
+            scores = (top.values / top.values.sum(-1, keepdim=True)).reshape(B, 1, topk)
+            inds = top.indices.to(torch.int32).reshape(B, 1, topk)
+            distinct = torch.unique(inds).tolist()
+            union.update(distinct)
+            per_call += (len(distinct) + 1) * per_expert
+            calls.append((inds, scores))
         y = torch.empty_like(x)
         ys = torch.empty_like(x)
+        logit = torch.randn(B, device="cuda", generator=g).to(torch.float16)
 
         def layer():
-            X.swiglu(G, U, D, x, inds, scores, out=y)
-            X.swiglu(sg.weight, su.weight, sd.weight, x, out=ys)
+            for inds, scores in calls:
+                X.swiglu(G, U, D, x, inds, scores, out=y)
+                X.swiglu(sg.weight, su.weight, sd.weight, x, out=ys)
+
+        def layer_shared():
+            for inds, scores in calls:
+                X.swiglu_shared(G, U, D, x, [sg.weight, su.weight, sd.weight], inds=inds,
+                                scores=scores, logit=logit, out=y)
+        nbytes = (len(union) + 1) * per_expert
         ms = _graph_ms(torch, layer, reps)
-        nbytes = (distinct + 1) * per_expert
-        out[f"batch{B}"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1),
-                            "distinct_experts": distinct}
+        res = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us_per_call": round(ms * 1e3 / routings, 1),
+               "gbs_per_call_sum": round(per_call / (ms * 1e-3) / 1e9, 1),
+               "distinct_experts_per_replay": len(union), "distinct_mb": round(nbytes / 1e6, 1)}
+        try:
+            ms2 = _graph_ms(torch, layer_shared, reps)
+            res["swiglu_shared"] = {"gbs": round(nbytes / (ms2 * 1e-3) / 1e9, 1),
+                                    "gbs_per_call_sum": round(per_call / (ms2 * 1e-3) / 1e9, 1),
+                                    "us_per_call": round(ms2 * 1e3 / routings, 1)}
+        except Exception as ex:  # reported, not hidden (e.g. refused at prefill sizes)
+            res["swiglu_shared"] = {"refused": str(ex)}
+        out[f"batch{B}"] = res
     for w in (G, U, D):
         X.release(w)
-    return {"moe_k3_deepseek_v3_layer": out}
+    return {"moe_k3_deepseek_v3_layer": {"routings_per_replay": routings,
+                                         "timing": "median of 20 graph replays", **out}}
 
 
 def decode_tok_s(torch, batches=(1, 16), ctx=2048, steps=8):
@@ -491,13 +556,33 @@ def main() -> int:
         log("cpu baseline")
         cpu = cpu_baseline(args.cpu_seconds)
 
+    # the median of 20 single-step replays (each between its own HIP events)
+    median_launch_us = None
+    if graph is not None:
+        median_launch_us = round(_median_ms(torch, graph.replay, 20) * 1e3 / launches, 3)
+
     # HBM traffic per launch of this workload, measured by the FETCH_SIZE /
     # WRITE_SIZE counter runs of profiles/gemv_k4_qwen3_8b_decode.md (each
     # scaled by its plain-copy calibration); null when that file is absent.
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_k4_qwen3_8b_decode.json")
+    valu_ceiling = None
     if args.layers == LAYERS and not args.per_linear and os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("traffic_bytes_per_launch")
+        prof = json.load(open(tpath))
+        traffic = prof.get("traffic_bytes_per_launch")
+        # The VALU ceiling: the GB/s at which the pass's measured VALU
+        # instructions (SQ_INSTS_VALU of the counter run, decode and every
+        # fixed part included) would keep every SIMD's VALU busy: 1024 SIMDs
+        # at the held shader clock, one wave-instruction per VALU_CYCLES.
+        vi = prof.get("valu_wave_insts_per_step")
+        if vi:
+            rate = 256 * 4 * prof["shader_clock_hz"] / prof["valu_cycles_per_inst"]
+            valu_ceiling = {"gbs": round(step_bytes / (vi / rate) / 1e9, 1),
+                            "frac_of_hbm_peak": round(step_bytes / (vi / rate) / 1e9 / HBM_PEAK_GBS, 3),
+                            "valu_insts_per_weight": round(vi * 64 / (step_bytes * 8 / K_BITS), 2),
+                            "basis": "SQ_INSTS_VALU per step (profiles/gemv_k4_qwen3_8b_decode.md) at "
+                                     f"{prof['valu_cycles_per_inst']} cycles per wave-instruction, "
+                                     f"{prof['shader_clock_hz'] / 1e9:.2f} GHz, 1024 SIMDs"}
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
@@ -513,7 +598,9 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (profiles/gemv_k4_qwen3_8b_decode.md)",
                      "algorithmic_bytes_per_launch": round(step_bytes / launches),
-                     "kernel": "exl3::gemv_kernel<4,0,false,true,0> (mul1, K=4, window 16, one prepare batch, plain input)",
+                     "kernel": "exl3::gemv_kernel<4,0,false,0,0> (mul1, K=4, window 16, one prepare batch, plain input)",
+                     "median_launch_us": median_launch_us,
+                     "valu_ceiling": valu_ceiling,
                      "launches": launches * args.steps,
                      "avg_launch_us": round(avg_launch_ms * 1e3, 3),
                      "timing": "HIP events around the timed region's graph replays / launches"},

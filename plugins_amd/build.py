@@ -1,6 +1,7 @@
 """Builds libexl3_mi355x.so (HIP kernels for gfx950 + the C ABI) in-tree.
 
     python -m plugins_amd.build          # or: python plugins_amd/build.py
+    python -m plugins_amd.build --timeline   # the diagnostic GEMV-timeline build
 
 Objects go to plugins_amd/_build/, the library to plugins_amd/lib/.  hipcc
 cross-compiles gfx950 code objects without a GPU.  Device code is built with
@@ -64,23 +65,35 @@ def _compile(src: str, name: str, flags: list[str]) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
-    """Compiles every source and links the shared library; returns its path."""
+# The diagnostic build with the GEMV phase timeline compiled in
+# (EXL3_TIMELINE; plugins_amd/timeline.py reads it): a library of its own.
+TIMELINE_LIB = os.path.join(LIBDIR, "libexl3_mi355x_timeline.so")
+
+
+def build(verbose: bool = True, timeline: bool = False) -> str:
+    """Compiles every source and links the shared library; returns its path.
+    timeline: the diagnostic build (objects with a _tl suffix, TIMELINE_LIB)."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    srcs = SOURCES
+    lib_path = LIB
+    if timeline:
+        device = lambda f: any(x.startswith("--offload-arch") for x in f)  # noqa: E731
+        srcs = [(s, n + "_tl", f + ["-DEXL3_TIMELINE"] if device(f) else f) for s, n, f in SOURCES]
+        lib_path = TIMELINE_LIB
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda sf: _compile(*sf), SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda sf: _compile(*sf), srcs))
+    tmp = lib_path + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_path)
     if verbose:
-        print("built", LIB)
-    return LIB
+        print("built", lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":
-    build()
+    build(timeline="--timeline" in sys.argv[1:])

@@ -16,6 +16,29 @@
 
 namespace exl3 {
 
+// The GEMV phase timeline of a diagnostic build (EXL3_TIMELINE defined:
+// `python -m plugins_amd.build --timeline`, read by plugins_amd/timeline.py):
+// lane 0 of each wave stores the 100 MHz real-time counter at each phase of
+// its workgroup, [workgroup][wave][event], for the first 4096 workgroups of
+// a launch.  Events: 0 entry, 1 rows prepared (after the barrier), 2 loop
+// done, 3 reduced (before the split-K hand-off), 4 partial stored (the
+// other splits), 5 hand-off done and 6 finish done (the last split).  A
+// product build compiles the stores out.
+#ifdef EXL3_TIMELINE
+constexpr int TIMELINE_WGS = 4096;
+static __device__ unsigned long long g_timeline[TIMELINE_WGS * 8 * 8];
+#define EXL3_TL(k)                                                                           \
+  do {                                                                                       \
+    const size_t wg_ = (size_t)blockIdx.x + (size_t)gridDim.x * blockIdx.y;                  \
+    if ((threadIdx.x & 63) == 0 && wg_ < TIMELINE_WGS)                                       \
+      g_timeline[(wg_ * 8 + (threadIdx.x >> 6)) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define EXL3_TL(k) \
+  do {             \
+  } while (0)
+#endif
+
 template <int... Is, typename F>
 __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F &&f) {
   (f(std::integral_constant<int, Is>{}), ...);
@@ -243,11 +266,11 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int rows_alloc, int tps, boo
 // arithmetic are split so a workgroup issues its first items' loads with its
 // weight loads.
 
-// Batch j of a prepare holds items base + 8 j + wave (clamped to the last
-// item); a batch past the last item would only redo it (every wave's item
-// clamped), so it is skipped: the test is uniform across the workgroup.
-__device__ __forceinline__ bool prep_batch_live(int j, int base, int nitems) {
-  return j == 0 || base + j * (GEMV_THREADS / 64) < nitems;
+// Batch j of a wave's prepare holds item base + 8 j + wave; an item past the
+// last would only redo the last one (its index clamped), so the wave skips
+// it and every later batch (the test is uniform within the wave).
+__device__ __forceinline__ bool prep_item_live(int j, int base, int wave, int nitems) {
+  return base + wave + j * (GEMV_THREADS / 64) < nitems;
 }
 
 // Raw bits as loaded (converted only when the rows are prepared, so the
@@ -270,7 +293,7 @@ __device__ __forceinline__ void gemv_prep_load_norm(const GemvCfg &a, const RowM
   const int ng = in >> 7;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    if (!prep_batch_live(j, base, nitems)) break;
+    if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -309,7 +332,7 @@ __device__ __forceinline__ void gemv_prep_load_x(const void *x, int xdt, int pre
   const int esz = (!prepared && xdt == OUT_F32) ? 4 : 2;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    if (!prep_batch_live(j, base, nitems)) break;
+    if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -331,7 +354,7 @@ __device__ __forceinline__ void gemv_prep_load_su(const void *x, int prepared, c
   const uint16_t *sup = prepared ? (const uint16_t *)x : suh;
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    if (!prep_batch_live(j, base, nitems)) break;
+    if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int blk = it % nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -346,7 +369,7 @@ __device__ __forceinline__ void gemv_prep_load_up(const uint16_t *x2, const RowM
                                                   int lane, PrepRegs &r) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    if (!prep_batch_live(j, base, nitems)) break;
+    if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
@@ -381,7 +404,7 @@ __device__ __forceinline__ void gemv_prep_store(int xdt, int prepared, int nitem
                                                 int in = 0, float eps = 0.0f) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
-    if (!prep_batch_live(j, base, nitems)) break;
+    if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
     uint32_t *dst = reinterpret_cast<uint32_t *>(xs + row * kr + blk * 128 + 2 * lane);
@@ -731,6 +754,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // else the rows form in PREP passes
   constexpr bool ONEB = PREP == 0;
   constexpr int NP = ONEB ? 1 : PREP;
+  EXL3_TL(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = wave & 3, kp = wave >> 2;
@@ -841,6 +865,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     gemv_rows_store<PRO, NP>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr,
                              FOLD ? hsum : nullptr, a.limit);
   lds_barrier();
+  EXL3_TL(1);
 
   const int arow = min(lane & 15, nrows - 1);
   const uint16_t *xa = xs + arow * kr + (kp * part + g) * 16;
@@ -918,6 +943,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     }
   }
 
+  EXL3_TL(2);
   // C of a 16x16 MFMA: lane l holds rows 4(l/16)+i, column l%16.
   const int col = (2 * q + t) * 16 + c;
   float *zk = zp + kp * zrows * 128;
@@ -943,11 +969,17 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   float *zf = zp;
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   lds_barrier();
-  if (!gemv_splitk_last(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) return;
+  EXL3_TL(3);
+  if (!gemv_splitk_last(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) {
+    EXL3_TL(4);
+    return;
+  }
+  EXL3_TL(5);
   if (a.res != nullptr)
     gemv_finish_res(zf, a.res, a.res_ssq, out, nrows, rm, sv, cg, resv);
   else
     gemv_finish(zf, a.ydt, W.y, W.zout, nrows, rm, sv, cg * 128);
+  EXL3_TL(6);
 }
 
 // The weight of grid column group `gx` (weights' groups side by side) and
