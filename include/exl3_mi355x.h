@@ -464,7 +464,17 @@ void exl3_array_free(exl3_array *a);
 /* A weight over device arrays the caller already holds (borrowed, not freed
  * by release): the reference's `share` of source arrays
  * (turboexl3_ds41/plugin.zig:213-218) for callers whose weights are already
- * resident.  block_json supplies codebook and window (NULL/empty: mul1, 16). */
+ * resident.  block_json supplies codebook and window (NULL/empty: mul1, 16).
+ * Besides turboexl3's mul1 and mcg it takes the pack format's table
+ * codebooks (sushi_ds41/src/sushi/exl3/expert_exl3.zig:54-60,288-357):
+ * spec1 and std1 (hash-mask) and pair1 (a weight pair from one codeword),
+ * whose block names a shipped table and its digest (`codebook_table`:
+ * pair1-w16-v1, spec1-w15, spec1-w16 or std1; `codebook_digest`), resolved
+ * as codebook_tables.zig:266-279 does, refusing by name
+ * Exl3CodebookTableUnknown, ...DigestMismatch, ...LegacyConfig,
+ * ...CodebookMismatch, ...WindowMismatch, and Exl3CodebookTableRateMissing
+ * for a rate the table has no row for.  validate and open keep turboexl3's
+ * rule (mul1 or mcg). */
 exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh,
                               exl3_str block_json, int32_t device, exl3_weight *out);
 

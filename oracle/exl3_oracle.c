@@ -103,6 +103,124 @@ uint16_t exl3o_decode_mcg(uint16_t cw) {
   return exl3o_f2h(lo + hi);
 }
 
+/* ------------------------------------------------------ table codebooks */
+
+/* Rows of the pack contract's codebook tables, one per even rate n from the
+ * table's n_lo: {mult, mask} for the hash-mask codebooks (spec1, std1),
+ * {mult, rot, mask0, mask1} for pair1.  Data as sx/codebook_tables.zig:
+ * 99-203 (names, digests, ranges) and sx/expert_exl3.zig:23-46 (the pair1
+ * rows) hold them. */
+static const uint32_t PAIR1_ROWS[21][4] = {
+    {0x58F41BF3u, 3, 0x8ED78C13u, 0x8EEE8C03u},  {0x58F41BF3u, 3, 0x8ED78C13u, 0x8EEE8C03u},
+    {0x7AA2BE15u, 3, 0x8ED78C13u, 0x8ECE8C03u},  {0x7B229E11u, 3, 0x8ED78C13u, 0x8ECE8C03u},
+    {0x3B22BE15u, 3, 0x8ED78C13u, 0x8ECE8C03u},  {0x46C63E17u, 19, 0x8F9A8E6Eu, 0x8E258FFEu},
+    {0x46C63E17u, 19, 0x8F9A8E6Eu, 0x8E258FFEu}, {0x46C63E17u, 19, 0x8E6E8F9Au, 0x8E258FFEu},
+    {0x46C63E17u, 19, 0x8F9A8E6Eu, 0x8E258FFEu}, {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu},
+    {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu}, {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu},
+    {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu}, {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu},
+    {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu}, {0xF75D60FFu, 19, 0x8E6E8F9Au, 0x8E258FFEu},
+    {0x82439F67u, 19, 0x8E6E8F9Au, 0x8E258FAEu}, {0xE2C7FC0Du, 19, 0x8F408FB0u, 0x8F918F89u},
+    {0xE2C7FC0Du, 19, 0x8F408FA0u, 0x8F118FC9u}, {0xE2C7FC0Du, 19, 0x8F408FA0u, 0x8F118FC9u},
+    {0xE2C7FC0Du, 19, 0x8F408FA0u, 0x8F118FC9u},
+};
+static const uint32_t SPEC1_W15[57][2] = {
+    {0x84d1cf89u, 0x8fe08947u}, {0x84c1cf49u, 0x8fe48a47u}, {0x84d1cfe9u, 0x8fe08a47u},
+    {0x84d1cfc9u, 0x8ff08b67u}, {0x84c1cf49u, 0x8fe08b47u}, {0x84c1cf99u, 0x8fa08b66u},
+    {0x862c1d37u, 0x8ff28c50u}, {0x84641fb7u, 0x8fa08c40u}, {0x846c1fa7u, 0x8fe08c80u},
+    {0x844c1fd7u, 0x8ffe8c98u}, {0x846c1fa7u, 0x8ffe8d10u}, {0x845c1f77u, 0x8ffa8e10u},
+    {0x843c1fa7u, 0x8ffe8e40u}, {0x843c1fa7u, 0x8ffe8e40u}, {0x842c1fc7u, 0x8fff8f00u},
+    {0x843c1fb7u, 0x8ffe8f10u}, {0x84181fb5u, 0x8fe08f80u}, {0x84081f75u, 0x8ffa8f72u},
+    {0x84081f75u, 0x8fd68fd0u}, {0x84241f27u, 0x8ffc8fc0u}, {0x84081f73u, 0x8fe08f80u},
+    {0x84081f75u, 0x8fbe8ff0u}, {0x3fed4cefu, 0x8fe08fe0u}, {0x3fed4cefu, 0x8fc18ff2u},
+    {0x3fed4cefu, 0x8ff08ff0u}, {0x3fed4cefu, 0x8fe28ff0u}, {0x3fed4cefu, 0x8fe08fe0u},
+    {0x80081b7bu, 0x8ff08fc8u}, {0x80081b7bu, 0x8ff48fc0u}, {0x400036cbu, 0x8f448fffu},
+    {0x400036cbu, 0x8fe48fffu}, {0x400036cbu, 0x8f448ff9u}, {0x8000387bu, 0x8fe08ff7u},
+    {0x8000387bu, 0x8fc08feeu}, {0x80003779u, 0x8fe88ffeu}, {0x80003779u, 0x8fc88ffcu},
+    {0x80003779u, 0x8fca8ffcu}, {0x80003779u, 0x8fcc8ffeu}, {0x80003879u, 0x8ffc8fefu},
+    {0x50003851u, 0x8ff98fffu}, {0xd0003751u, 0x8ff98fffu}, {0x50003851u, 0x8ff98ff6u},
+    {0xd0003931u, 0x8ff98fffu}, {0xd0003931u, 0x8ff98ffau}, {0xd0003931u, 0x8ff48ffau},
+    {0x300031b1u, 0x8ffb8ffcu}, {0x300031b1u, 0x8ffa8ffeu}, {0x300031b1u, 0x8ffb8ffcu},
+    {0xc00031f1u, 0x8ffe8ffau}, {0x400031f1u, 0x8ffe8ffeu}, {0x400031f1u, 0x8ffe8ffeu},
+    {0x40003931u, 0x8ffc8ffcu}, {0x40003931u, 0x8ffc8ffcu}, {0x40003931u, 0x8ff88ffeu},
+    {0x40003931u, 0x8ff88ffcu}, {0x80003811u, 0x8ffc8ffcu}, {0x80003811u, 0x8ffc8ffcu},
+};
+static const uint32_t SPEC1_W16[21][2] = {
+    {0x862d1c19u, 0x8fee8c30u}, {0x862d1d37u, 0x8fee8c30u}, {0x862d1d37u, 0x8ffe8c10u},
+    {0x842f1f37u, 0x8ffc8d10u}, {0x840f1f67u, 0x8ffc8d10u}, {0x844f1f77u, 0x8ffe8d40u},
+    {0x840d1f37u, 0x8ffe8e10u}, {0x84091f33u, 0x8fe88e00u}, {0x844d1f77u, 0x8fe08e00u},
+    {0x843c1fa7u, 0x8ffe8e40u}, {0x844c1f7fu, 0x8ffc8f02u}, {0x841c1fb9u, 0x8fe88f04u},
+    {0x842c1fc7u, 0x8ffe8fd0u}, {0x83fc1fa3u, 0x8ffe8fd0u}, {0x83fc1fa3u, 0x8ffe8fc1u},
+    {0x83fc1fa3u, 0x8ffe8fd0u}, {0x83fc1fa3u, 0x8fee8fc0u}, {0x84061f77u, 0x8fd08f80u},
+    {0x84081f6fu, 0x8ffe8fc0u}, {0x84081f25u, 0x8ffe8fe0u}, {0x83f81f6fu, 0x8ff48fc0u},
+};
+/* sx/codebook_tables.zig:206: std1's one pair, at n = 24..64. */
+static const uint32_t STD1_PAIR[2] = {0x840C1F37u, 0x8FFE8FD0u};
+
+int exl3o_table_info(int table, uint32_t *n_lo, uint32_t *rows, uint32_t *fields) {
+  switch (table) {
+    case EXL3O_TAB_PAIR1_W16_V1: *n_lo = 24; *rows = 21; *fields = 4; return 1;
+    case EXL3O_TAB_SPEC1_W15: *n_lo = 16; *rows = 57; *fields = 2; return 1;
+    case EXL3O_TAB_SPEC1_W16: *n_lo = 24; *rows = 21; *fields = 2; return 1;
+    case EXL3O_TAB_STD1: *n_lo = 24; *rows = 21; *fields = 2; return 1;
+    default: return 0;
+  }
+}
+
+/* sx/codebook_tables.zig:48-52 (Table.row): row (n - n_lo) / 2 for an even n
+ * in range, else none (0).  row[] = {mult, mask} or {mult, rot, mask0, mask1}. */
+int exl3o_table_row(int table, uint32_t n, uint32_t row[4]) {
+  uint32_t n_lo, rows, fields;
+  if (!exl3o_table_info(table, &n_lo, &rows, &fields)) return 0;
+  if (n % 2u != 0u || n < n_lo || (n - n_lo) / 2u >= rows) return 0;
+  const uint32_t i = (n - n_lo) / 2u;
+  row[2] = row[3] = 0;
+  switch (table) {
+    case EXL3O_TAB_PAIR1_W16_V1: memcpy(row, PAIR1_ROWS[i], 16); break;
+    case EXL3O_TAB_SPEC1_W15: row[0] = SPEC1_W15[i][0]; row[1] = SPEC1_W15[i][1]; break;
+    case EXL3O_TAB_SPEC1_W16: row[0] = SPEC1_W16[i][0]; row[1] = SPEC1_W16[i][1]; break;
+    default: row[0] = STD1_PAIR[0]; row[1] = STD1_PAIR[1]; break;
+  }
+  return 1;
+}
+
+/* sx/expert_exl3.zig:292-295 (halfSumScaled): the f16 halves summed in f32 and
+ * rounded, then times scale in f32 and rounded. */
+static uint16_t half_sum_scaled(uint32_t halves, uint32_t scale) {
+  const uint16_t sum = exl3o_f2h(exl3o_h2f((uint16_t)(halves & 0xFFFFu)) +
+                                 exl3o_h2f((uint16_t)(halves >> 16)));
+  return exl3o_f2h(exl3o_h2f(sum) * (float)scale);
+}
+
+/* sx/expert_exl3.zig:288-290 (decodeHashMask), scale 4096 (:17). */
+uint16_t exl3o_decode_hash_mask(uint16_t cw, uint32_t mult, uint32_t mask) {
+  return half_sum_scaled(((uint32_t)cw * mult) & mask, 4096u);
+}
+
+/* sx/expert_exl3.zig:297-301 (decodePair): both weights of a pair from one
+ * codeword, w0 from p & mask0, w1 from rotl(p, rot) & mask1, p = cw * mult. */
+void exl3o_decode_pair1(uint16_t cw, const uint32_t row[4], uint16_t out[2]) {
+  const uint32_t p = (uint32_t)cw * row[0];
+  const uint32_t rot = row[1] & 31u;
+  const uint32_t r = rot == 0u ? p : (p << rot) | (p >> (32u - rot));
+  out[0] = half_sum_scaled(p & row[2], 4096u);
+  out[1] = half_sum_scaled(r & row[3], 4096u);
+}
+
+/* The decode a `codebook` argument names: the codebook in its low byte
+ * (EXL3O_CB_*), for spec1 the table + 1 in the next byte (std1 and pair1 have
+ * one table each).  Fills row for the table codebooks; aborts on a rate
+ * the table has no row for (a test's mistake). */
+static int decode_row(int codebook, uint32_t n, uint32_t row[4]) {
+  const int cb = codebook & 0xFF;
+  int table = -1;
+  if (cb == EXL3O_CB_PAIR1) table = EXL3O_TAB_PAIR1_W16_V1;
+  if (cb == EXL3O_CB_STD1) table = EXL3O_TAB_STD1;
+  if (cb == EXL3O_CB_SPEC1) table = ((codebook >> 8) & 0xFF) - 1;
+  if (table >= 0 && !exl3o_table_row(table, n, row)) abort();
+  if (cb == EXL3O_CB_SPEC1 && table < 0) abort();
+  return cb;
+}
+
 void exl3o_mul1_table(uint16_t out[65536]) {
   for (uint32_t s = 0; s < 65536u; ++s) out[s] = exl3o_decode_mul1((uint16_t)s);
 }
@@ -154,16 +272,31 @@ void exl3o_tile_perm(uint16_t out[256]) {
   }
 }
 
-/* sx/expert_exl3.zig:338-357 (scalar codebooks; window mask sx/expert_exl3.zig:124-126). */
+/* sx/expert_exl3.zig:338-357 (window mask sx/expert_exl3.zig:124-126): pair1
+ * decodes weights 2j and 2j+1 from codeword 2j+1; the others each codeword
+ * on its own, the hash-mask codebooks with their table's row for n. */
 void exl3o_decode_tile(const uint16_t *words, uint32_t n, int codebook, uint32_t window,
                        uint16_t out[256]) {
   uint16_t cws[256], perm[256];
+  uint32_t row[4] = {0, 0, 0, 0};
+  const int cb = decode_row(codebook, n, row);
   exl3o_unpack_tile(words, n, cws);
   exl3o_tile_perm(perm);
   uint16_t mask = (uint16_t)((1u << window) - 1u);
+  if (cb == EXL3O_CB_PAIR1) {
+    for (uint32_t j = 0; j < 128u; ++j) {
+      uint16_t w[2];
+      exl3o_decode_pair1(cws[2 * j + 1] & mask, row, w);
+      out[perm[2 * j]] = w[0];
+      out[perm[2 * j + 1]] = w[1];
+    }
+    return;
+  }
   for (uint32_t i = 0; i < 256u; ++i) {
     uint16_t cw = cws[i] & mask;
-    out[perm[i]] = codebook == EXL3O_CB_MCG ? exl3o_decode_mcg(cw) : exl3o_decode_mul1(cw);
+    out[perm[i]] = cb == EXL3O_CB_MCG                               ? exl3o_decode_mcg(cw)
+                   : (cb == EXL3O_CB_SPEC1 || cb == EXL3O_CB_STD1) ? exl3o_decode_hash_mask(cw, row[0], row[1])
+                                                                    : exl3o_decode_mul1(cw);
   }
 }
 

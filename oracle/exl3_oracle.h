@@ -25,7 +25,17 @@
 extern "C" {
 #endif
 
-enum { EXL3O_CB_MUL1 = 0, EXL3O_CB_MCG = 1 };
+/* Codebooks as sx/expert_exl3.zig:54-60 numbers them.  A `codebook` argument
+ * carries the codebook in its low byte and, for spec1, its table + 1 in the
+ * next byte (std1 and pair1 each have one table). */
+enum { EXL3O_CB_MUL1 = 0, EXL3O_CB_MCG = 1, EXL3O_CB_SPEC1 = 2, EXL3O_CB_PAIR1 = 3, EXL3O_CB_STD1 = 4 };
+/* The shipped codebook tables (sx/codebook_tables.zig:99-104). */
+enum {
+  EXL3O_TAB_PAIR1_W16_V1 = 0,
+  EXL3O_TAB_SPEC1_W15 = 1,
+  EXL3O_TAB_SPEC1_W16 = 2,
+  EXL3O_TAB_STD1 = 3
+};
 
 /* binary16 <-> binary32, round-to-nearest-even (sx/expert_exl3.zig:259-265). */
 float exl3o_h2f(uint16_t h);
@@ -41,6 +51,16 @@ uint32_t exl3o_bit_end(uint32_t n, uint32_t t);
 uint16_t exl3o_decode_mul1(uint16_t cw);
 uint16_t exl3o_decode_mcg(uint16_t cw);
 void exl3o_mul1_table(uint16_t out[65536]);
+/* Table codebooks: a table's first rate, row count and fields per row, and
+ * its row for rate n (0: none) (sx/codebook_tables.zig:35-52). */
+int exl3o_table_info(int table, uint32_t *n_lo, uint32_t *rows, uint32_t *fields);
+int exl3o_table_row(int table, uint32_t n, uint32_t row[4]);
+/* spec1 / std1: one weight from its codeword and the row's {mult, mask}
+ * (sx/expert_exl3.zig:288-295). */
+uint16_t exl3o_decode_hash_mask(uint16_t cw, uint32_t mult, uint32_t mask);
+/* pair1: both weights of a pair from the odd weight's codeword and the row
+ * {mult, rot, mask0, mask1} (sx/expert_exl3.zig:297-301). */
+void exl3o_decode_pair1(uint16_t cw, const uint32_t row[4], uint16_t out[2]);
 
 /* The 256 codewords of a tile, code order (sx/expert_exl3.zig:317-336). */
 void exl3o_unpack_tile(const uint16_t *words, uint32_t n, uint16_t out[256]);

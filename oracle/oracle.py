@@ -19,6 +19,21 @@ _LIB_PATH = os.path.join(_HERE, "lib", "libexl3_oracle.so")
 
 CB_MUL1 = 0
 CB_MCG = 1
+CB_SPEC1 = 2
+CB_PAIR1 = 3
+CB_STD1 = 4
+# the shipped codebook tables (sx/codebook_tables.zig:99-104)
+TAB_PAIR1_W16_V1 = 0
+TAB_SPEC1_W15 = 1
+TAB_SPEC1_W16 = 2
+TAB_STD1 = 3
+TABLE_NAMES = {TAB_PAIR1_W16_V1: "pair1-w16-v1", TAB_SPEC1_W15: "spec1-w15",
+               TAB_SPEC1_W16: "spec1-w16", TAB_STD1: "std1"}
+
+
+def spec1(table: int) -> int:
+    """The `codebook` argument of spec1 decoded with `table`."""
+    return CB_SPEC1 | ((table + 1) << 8)
 
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
@@ -50,6 +65,12 @@ def lib():
             "exl3o_decode_mul1": (ctypes.c_uint16, [ctypes.c_uint16]),
             "exl3o_decode_mcg": (ctypes.c_uint16, [ctypes.c_uint16]),
             "exl3o_mul1_table": (None, [_u16p]),
+            "exl3o_table_info": (_int, [_int, ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                                        ctypes.POINTER(_u32)]),
+            "exl3o_table_row": (_int, [_int, _u32, ctypes.POINTER(_u32)]),
+            "exl3o_decode_hash_mask": (ctypes.c_uint16, [ctypes.c_uint16, _u32, _u32]),
+            "exl3o_decode_pair1": (None, [ctypes.c_uint16, ctypes.POINTER(_u32),
+                                          ctypes.POINTER(ctypes.c_uint16)]),
             "exl3o_unpack_tile": (None, [_u16p, _u32, _u16p]),
             "exl3o_unpack_tile_bitwise": (None, [_u16p, _u32, _u16p]),
             "exl3o_tile_perm": (None, [_u16p]),
@@ -107,6 +128,33 @@ def mul1_table() -> np.ndarray:
     out = np.empty(65536, np.uint16)
     lib().exl3o_mul1_table(out)
     return out
+
+
+def table_info(table: int):
+    """(n_lo, rows, fields) of a shipped table, or None."""
+    n_lo, rows, fields = _u32(), _u32(), _u32()
+    if not lib().exl3o_table_info(table, ctypes.byref(n_lo), ctypes.byref(rows), ctypes.byref(fields)):
+        return None
+    return n_lo.value, rows.value, fields.value
+
+
+def table_row(table: int, n: int):
+    """The table's row for rate n as a 4-tuple, or None."""
+    row = (_u32 * 4)()
+    if not lib().exl3o_table_row(table, n, row):
+        return None
+    return tuple(int(v) for v in row)
+
+
+def decode_hash_mask(cw: int, mult: int, mask: int) -> int:
+    return int(lib().exl3o_decode_hash_mask(cw, mult, mask))
+
+
+def decode_pair1(cw: int, row) -> tuple:
+    r = (_u32 * 4)(*row)
+    out = (ctypes.c_uint16 * 2)()
+    lib().exl3o_decode_pair1(cw, r, out)
+    return int(out[0]), int(out[1])
 
 
 def mcg_table() -> np.ndarray:

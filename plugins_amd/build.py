@@ -41,6 +41,7 @@ SOURCES = [
     ("exl3_noalloc.hip", "exl3_noalloc", DEVICE_FLAGS),
     ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
     ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
+    ("exl3_codebooks.cpp", "exl3_codebooks", HOST_FLAGS),
     ("exl3_pack.cpp", "exl3_pack", HOST_FLAGS),
 ]
 

@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "exl3_kernels.h"
+
 namespace exl3 {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -42,7 +44,12 @@ constexpr uint16_t MUL1_BIAS = 0xC931u;
 // (expert_exl3.zig:267-273).
 constexpr uint32_t MCG_MULT = 0xCBAC1FEDu;
 
-enum Codebook { CB_MUL1 = 0, CB_MCG = 1 };
+// Kernel codebook forms: mul1, mcg, the hash-mask codebooks (spec1, std1:
+// one multiply, a mask keeping two tiny f16 halves, their sum times 4096;
+// expert_exl3.zig:288-295) and pair1 (a pair of weights from the odd
+// weight's codeword; expert_exl3.zig:297-301).
+enum Codebook { CB_MUL1 = CB_FORM_MUL1, CB_MCG = CB_FORM_MCG, CB_HASH = CB_FORM_HASH, CB_PAIR1 = CB_FORM_PAIR1 };
+
 enum OutType { OUT_F16 = 0, OUT_BF16 = 1, OUT_F32 = 2 };
 
 template <typename T, typename F>
@@ -131,29 +138,52 @@ __device__ __forceinline__ void store_out(void *p, size_t i, uint16_t y16, int d
 // v_sad_hi_u8 puts the second sum in the high half, so h = f16 pair (1024+s1,
 // 1024+s0) exactly; one packed f16 FMA then rounds once, as the reference's
 // single RNE does (kernels.zig:966-975).
+// The hash-mask codebooks' step after the masks: half sums of a = [w1 lo |
+// w0 lo] and b = [w1 hi | w0 hi] halves, then times 4096, as f16 pairs
+// (halfSumScaled, expert_exl3.zig:292-295).  One v_pk_add_f16 rounds the
+// exact sum as the reference's f32 add then f16 round does (24 >= 2 * 11 + 2
+// bits), and the power-of-two scale is exact (the masked halves are below
+// 2^-10, so nothing overflows).
+__device__ __forceinline__ uint32_t half_sums_scaled(uint32_t lo, uint32_t hi) {
+  const h2_t scale = {(_Float16)4096.0f, (_Float16)4096.0f};
+  return bits<uint32_t>((bits<h2_t>(lo) + bits<h2_t>(hi)) * scale);
+}
+
+// decode_pair on codewords already masked to the window and zero-extended
+// (c0: the even weight's, c1: the odd weight's).
 template <int CB>
-__device__ __forceinline__ uint32_t decode_pair(uint32_t v0, uint32_t v1, uint32_t mask) {
+__device__ __forceinline__ uint32_t decode_masked_pair(uint32_t c0, uint32_t c1, const CbRow &d) {
   if constexpr (CB == CB_MUL1) {
-    const uint32_t x0 = (v0 & mask) * MUL1_MULT;
-    const uint32_t x1 = (v1 & mask) * MUL1_MULT;
-    uint32_t h = __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u);
-    h = __builtin_amdgcn_sad_hi_u8(x1, 0u, h);
+    uint32_t h = __builtin_amdgcn_sad_u8(c0 * MUL1_MULT, 0u, 0x64006400u);
+    h = __builtin_amdgcn_sad_hi_u8(c1 * MUL1_MULT, 0u, h);
     const h2_t inv = {bits<_Float16>(MUL1_INV), bits<_Float16>(MUL1_INV)};
     const h2_t bias = {bits<_Float16>(MUL1_BIAS), bits<_Float16>(MUL1_BIAS)};
     return bits<uint32_t>(__builtin_elementwise_fma(bits<h2_t>(h), inv, bias));
-  } else {
-    const uint32_t p0 = 0x3B603B60u ^ (((v0 & mask) * MCG_MULT) & 0x8FFF8FFFu);
-    const uint32_t p1 = 0x3B603B60u ^ (((v1 & mask) * MCG_MULT) & 0x8FFF8FFFu);
+  } else if constexpr (CB == CB_MCG) {
+    const uint32_t p0 = 0x3B603B60u ^ ((c0 * MCG_MULT) & 0x8FFF8FFFu);
+    const uint32_t p1 = 0x3B603B60u ^ ((c1 * MCG_MULT) & 0x8FFF8FFFu);
     const uint32_t lo = __builtin_amdgcn_perm(p1, p0, 0x05040100u);  // [p1.lo | p0.lo]
     const uint32_t hi = __builtin_amdgcn_perm(p1, p0, 0x07060302u);  // [p1.hi | p0.hi]
     return bits<uint32_t>(bits<h2_t>(lo) + bits<h2_t>(hi));
+  } else if constexpr (CB == CB_HASH) {
+    const uint32_t p0 = (c0 * d.mult) & d.mask0;
+    const uint32_t p1 = (c1 * d.mult) & d.mask0;
+    return half_sums_scaled(__builtin_amdgcn_perm(p1, p0, 0x05040100u),
+                            __builtin_amdgcn_perm(p1, p0, 0x07060302u));
+  } else {
+    // pair1: w0 from p & mask0, w1 from rotl(p, rot) & mask1, p = c1 * mult
+    const uint32_t p = c1 * d.mult;
+    const uint32_t a = p & d.mask0;
+    const uint32_t b = __builtin_amdgcn_alignbit(p, p, d.rsh) & d.mask1;
+    (void)c0;
+    return half_sums_scaled(__builtin_amdgcn_perm(b, a, 0x05040100u),
+                            __builtin_amdgcn_perm(b, a, 0x07060302u));
   }
 }
 
-// One codeword's f16 bits (scalar form of decode_pair).
 template <int CB>
-__device__ __forceinline__ uint16_t decode_one(uint32_t v, uint32_t mask) {
-  return (uint16_t)(decode_pair<CB>(v, v, mask) & 0xFFFFu);
+__device__ __forceinline__ uint32_t decode_pair(uint32_t v0, uint32_t v1, const CbRow &d) {
+  return decode_masked_pair<CB>(v0 & d.mask, v1 & d.mask, d);
 }
 
 // ---------------------------------------------------- integer-rate chunks
@@ -184,8 +214,8 @@ __host__ __device__ constexpr int chunk_colhalf(int i) { return (i & 7) >= 4 ? 1
 
 // Decodes pair p (codewords 2p, 2p+1: rows r, r+1 of one column) of a chunk.
 template <int K, int CB, int P>
-__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1], uint32_t mask) {
-  return decode_pair<CB>(chunk_window<K, 2 * P>(w), chunk_window<K, 2 * P + 1>(w), mask);
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1], const CbRow &d) {
+  return decode_pair<CB>(chunk_window<K, 2 * P>(w), chunk_window<K, 2 * P + 1>(w), d);
 }
 
 // Number of a chunk's codewords whose window straddles dwords J and J+1.
@@ -230,29 +260,18 @@ __device__ __forceinline__ uint32_t chunk_cw(const uint32_t (&w)[K + 1]) {
 
 // decode_pair on zero-extended codewords; MASKED applies a window below 16.
 template <int CB, bool MASKED>
-__device__ __forceinline__ uint32_t decode_pair_cw(uint32_t c0, uint32_t c1, uint32_t mask) {
+__device__ __forceinline__ uint32_t decode_pair_cw(uint32_t c0, uint32_t c1, const CbRow &d) {
   if constexpr (MASKED) {
-    c0 &= mask;
-    c1 &= mask;
+    c0 &= d.mask;
+    c1 &= d.mask;
   }
-  if constexpr (CB == CB_MUL1) {
-    uint32_t h = __builtin_amdgcn_sad_u8(c0 * MUL1_MULT, 0u, 0x64006400u);
-    h = __builtin_amdgcn_sad_hi_u8(c1 * MUL1_MULT, 0u, h);
-    const h2_t inv = {bits<_Float16>(MUL1_INV), bits<_Float16>(MUL1_INV)};
-    const h2_t bias = {bits<_Float16>(MUL1_BIAS), bits<_Float16>(MUL1_BIAS)};
-    return bits<uint32_t>(__builtin_elementwise_fma(bits<h2_t>(h), inv, bias));
-  } else {
-    const uint32_t p0 = 0x3B603B60u ^ ((c0 * MCG_MULT) & 0x8FFF8FFFu);
-    const uint32_t p1 = 0x3B603B60u ^ ((c1 * MCG_MULT) & 0x8FFF8FFFu);
-    const uint32_t lo = __builtin_amdgcn_perm(p1, p0, 0x05040100u);
-    const uint32_t hi = __builtin_amdgcn_perm(p1, p0, 0x07060302u);
-    return bits<uint32_t>(bits<h2_t>(lo) + bits<h2_t>(hi));
-  }
+  return decode_masked_pair<CB>(c0, c1, d);
 }
 
+// (pair1 reads only the odd codeword: the even one's extraction is dead code.)
 template <int K, int CB, bool MASKED, int P>
-__device__ __forceinline__ uint32_t chunk_pair_cw(const uint32_t (&w)[K + 1], uint32_t mask) {
-  return decode_pair_cw<CB, MASKED>(chunk_cw<K, 2 * P>(w), chunk_cw<K, 2 * P + 1>(w), mask);
+__device__ __forceinline__ uint32_t chunk_pair_cw(const uint32_t (&w)[K + 1], const CbRow &d) {
+  return decode_pair_cw<CB, MASKED>(chunk_cw<K, 2 * P>(w), chunk_cw<K, 2 * P + 1>(w), d);
 }
 
 // mul1 before its affine step: the f16 pair h = (1024 + s1, 1024 + s0), exact

@@ -21,11 +21,19 @@
 
 #include "../../include/exl3_decoder.h"
 #include "../../include/exl3_mi355x.h"
+#include "exl3_codebooks.h"
 #include "exl3_json.h"
 #include "exl3_kernels.h"
 
+using exl3::CodebookTable;
 using exl3::Format;
 using exl3::Json;
+using exl3::PACK_MCG;
+using exl3::PACK_PAIR1;
+using exl3::PACK_SPEC1;
+using exl3::pack_codebook_of;
+using exl3::resolve_codebook_table;
+using exl3::codebook_row;
 
 namespace {
 
@@ -40,10 +48,13 @@ exl3_verdict refuse(int32_t code, const char *why) { return exl3_verdict{code, w
 // search used (a bank's rate comes from each tensor's packed dim).
 struct Block {
   bool exl3 = false;
-  int codebook = 0;  // 0 mul1, 1 mcg, -1 other
+  int codebook = 0;  // PackCodebook (0 mul1, 1 mcg, 2 spec1, 3 pair1, 4 std1), -1 other
   int window = 16;   // -1: not an integer in 8..16
   bool has_k = false;
   double k = 0.0;
+  // spec1, std1, pair1: the table the block names, or why it names none
+  const CodebookTable *table = nullptr;
+  const char *table_refusal = nullptr;
 };
 
 Block parse_block(const Json &b) {
@@ -52,20 +63,16 @@ Block parse_block(const Json &b) {
   const Json *qm = b.get("quant_method");
   const Json *fm = b.get("format");
   out.exl3 = (qm && qm->is_string("exl3")) || (fm && fm->is_string("exl3"));
-  if (const Json *cb = b.get("codebook")) {
-    if (cb->is_string("mul1"))
-      out.codebook = 0;
-    else if (cb->is_string("mcg"))
-      out.codebook = 1;
-    else
-      out.codebook = -1;
-  }
+  if (const Json *cb = b.get("codebook"))
+    out.codebook = cb->kind == Json::STRING ? pack_codebook_of(cb->str.c_str()) : -1;
   if (const Json *w = b.get("window")) {
     if (w->kind == Json::NUMBER && w->integral && w->num >= 8 && w->num <= 16)
       out.window = (int)w->num;
     else
       out.window = -1;
   }
+  if (out.codebook >= PACK_SPEC1 && out.window >= 0)
+    out.table_refusal = resolve_codebook_table(b, out.codebook, out.window, &out.table);
   if (const Json *k = b.get("k")) {
     out.has_k = true;
     out.k = k->kind == Json::NUMBER ? k->num : -1.0;
@@ -306,7 +313,10 @@ exl3_verdict exl3_validate(exl3_str block_json, exl3_str config_json, const exl3
   const Json b = parse(block_json);
   const Block blk = parse_block(b);
   if (!blk.exl3) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: NotExl3");
-  if (blk.codebook < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookUnsupported");
+  // turboexl3's codebooks: mul1 and mcg (the table codebooks serve through
+  // exl3_weight_wrap)
+  if (blk.codebook < 0 || blk.codebook > PACK_MCG)
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookUnsupported");
   if (blk.window < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3WindowUnsupported");
   if (blk.has_k && !rate_ok(blk.k)) return kRate;
   const Json c = parse(config_json);
@@ -329,7 +339,7 @@ uint64_t exl3_bill(exl3_str block_json, exl3_str model_dir, uint64_t stored) {
 exl3_verdict exl3_open(exl3_load_ctx *ctx) {
   if (!ctx) return refuse(EXL3_FAILED, "turboexl3_mi355x: no load context");
   const Block blk = parse_block(parse(ctx->block_json));
-  if (!blk.exl3 || blk.codebook < 0 || blk.window < 0)
+  if (!blk.exl3 || blk.codebook < 0 || blk.codebook > PACK_MCG || blk.window < 0)
     return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: not an exllamav3 mul1 or mcg block");
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
@@ -502,6 +512,7 @@ exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh
     blk = parse_block(parse(block_json));
     if (blk.codebook < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookUnsupported");
     if (blk.window < 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3WindowUnsupported");
+    if (blk.table_refusal) return refuse(EXL3_UNSUPPORTED, blk.table_refusal);
   }
   const bool bank = trellis.ndim == 4;
   if (!(trellis.ndim == 3 || bank) || !trellis.data || !suh.data || !svh.data) return kShape;
@@ -510,6 +521,9 @@ exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh
   const int o = bank ? 1 : 0;
   const int64_t it = trellis.shape[o], ot = trellis.shape[o + 1], n = trellis.shape[o + 2];
   if (!n_ok(n)) return kRate;
+  uint32_t row[4] = {0, 0, 0, 0};
+  if (blk.table && !codebook_row(*blk.table, (int)n, row))
+    return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: Exl3CodebookTableRateMissing");
   const int64_t E = bank ? trellis.shape[0] : 0;
   if (bank) {
     if (suh.ndim != 2 || svh.ndim != 2 || suh.shape[0] != E || svh.shape[0] != E) return kShape;
@@ -528,7 +542,11 @@ exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh
   w.biases.owned = 0;
   WeightPriv *pv = new WeightPriv;
   pv->f.n = (int)n;
-  pv->f.codebook = blk.codebook;
+  pv->f.codebook = blk.codebook == PACK_MCG     ? exl3::CB_FORM_MCG
+                   : blk.codebook == PACK_PAIR1 ? exl3::CB_FORM_PAIR1
+                   : blk.codebook >= PACK_SPEC1 ? exl3::CB_FORM_HASH
+                                                : exl3::CB_FORM_MUL1;
+  std::memcpy(pv->f.row, row, sizeof(row));
   pv->f.window = blk.window;
   pv->in = it * 16;
   pv->out = ot * 16;
@@ -814,8 +832,7 @@ exl3_verdict exl3_matmul_shared(const exl3_weight *const *ws, uint32_t count, ex
     if (!pvs[i]) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
     if (pvs[i]->experts != 0) return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: matmul of an expert bank");
     if (pvs[i]->in != pvs[0]->in || pvs[i]->f.n != pvs[0]->f.n ||
-        pvs[i]->f.codebook != pvs[0]->f.codebook || pvs[i]->f.window != pvs[0]->f.window ||
-        pvs[i]->device != pvs[0]->device)
+        !pvs[i]->f.same_decode(pvs[0]->f) || pvs[i]->device != pvs[0]->device)
       return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: shared linears differ in input, rate or codebook");
   }
   const int xdt = act_of(x.dtype);
@@ -904,8 +921,7 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   if (pg->f.n != pu->f.n) return kRate;
   exl3_verdict v = output_for(out, x, hidden, rows);
   if (v.code != EXL3_OK) return v;
-  if (inds.data == nullptr && rows <= exl3::GEMV_ROWS_MAX && pg->f.codebook == pu->f.codebook &&
-      pg->f.window == pu->f.window) {
+  if (inds.data == nullptr && rows <= exl3::GEMV_ROWS_MAX && pg->f.same_decode(pu->f)) {
     // Dense MLP at decode sizes: gate and up in one GEMV launch (f16), then
     // the down GEMV with the SwiGLU applied as it prepares its rows (the MoE
     // path's mid step, bit for bit): two launches (above 4 rows the SwiGLU
@@ -1018,10 +1034,10 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
     return kShape;
   auto same = [](const WeightPriv *a, const WeightPriv *b) {
     return a->in == b->in && a->out == b->out && a->f.n == b->f.n &&
-           a->f.codebook == b->f.codebook && a->f.window == b->f.window && a->device == b->device;
+           a->f.same_decode(b->f) && a->device == b->device;
   };
   if (!same(sg, pg) || !same(su, pu) || !same(sd, pd) || pg->f.n != pu->f.n ||
-      pg->f.codebook != pu->f.codebook || pg->f.window != pu->f.window)
+      !pg->f.same_decode(pu->f))
     return refuse(EXL3_UNSUPPORTED,
                   "turboexl3_mi355x: the shared expert differs from the routed experts in width, "
                   "rate or codebook (the host runs its chain)");
@@ -1472,9 +1488,7 @@ const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
   const WeightPriv *pg = priv_of(gate), *pu = priv_of(up), *pd = priv_of(down);
   if (!pg || !pu || !pd || rows <= 0) return "none";
   if (topk <= 0) {
-    if (rows <= exl3::GEMV_ROWS_MAX && pg->f.codebook == pu->f.codebook &&
-        pg->f.window == pu->f.window)
-      return "dense-gemv";
+    if (rows <= exl3::GEMV_ROWS_MAX && pg->f.same_decode(pu->f)) return "dense-gemv";
     if (pg->f.integer_rate() && pu->f.integer_rate() && pd->f.integer_rate()) return "dense-gemm";
     return "dense-items";
   }
@@ -1544,8 +1558,7 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
     pvs[i] = priv_of(ws[i]);
     if (!pvs[i] || pvs[i]->experts != 0) return -1;
     if (pvs[i]->in != pvs[0]->in || pvs[i]->f.n != pvs[0]->f.n ||
-        pvs[i]->f.codebook != pvs[0]->f.codebook || pvs[i]->f.window != pvs[0]->f.window ||
-        pvs[i]->device != pvs[0]->device)
+        !pvs[i]->f.same_decode(pvs[0]->f) || pvs[i]->device != pvs[0]->device)
       return -1;
     if (!res && (!outs || !outs[i])) return -1;
   }

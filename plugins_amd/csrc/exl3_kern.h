@@ -22,8 +22,10 @@ namespace exl3 {
 // its workgroup, [workgroup][wave][event], for the first 4096 workgroups of
 // a launch.  Events: 0 entry, 1 rows prepared (after the barrier), 2 loop
 // done, 3 reduced (before the split-K hand-off), 4 partial stored (the
-// other splits), 5 hand-off done and 6 finish done (the last split).  A
-// product build compiles the stores out.
+// other splits), 5 hand-off done and 6 finish done (the last split), 7 the
+// partial's stores acknowledged (the other splits) or the first read of the
+// slots returned (the last split).  A product build compiles the stores
+// out.
 #ifdef EXL3_TIMELINE
 constexpr int TIMELINE_WGS = 4096;
 static __device__ unsigned long long g_timeline[TIMELINE_WGS * 8 * 8];
@@ -157,7 +159,7 @@ struct GemvCfg {
   int poll_max;
   int ydt;
   int ksplit;
-  uint32_t mask;
+  CbRow dec;            // window mask and table row
   int nw;               // trellis dwords per tile (n / 2)
   const uint16_t *x2;   // SwiGLU prologue: up (f16, the layout of x = gate)
   float limit;          // ... and its clamp (0: none)
@@ -622,6 +624,10 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
       if (v != v) v = bits<float>(0x7FC00000u);  // never PARTIAL_EMPTY
       st_agent(partial + ks * stride + (size_t)rm.prow(b) * out + col0 + col, v);
     }
+#ifdef EXL3_TIMELINE
+    wait_stores();
+    EXL3_TL(7);
+#endif
     return false;
   }
   const float empty = bits<float>(PARTIAL_EMPTY);
@@ -644,6 +650,9 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (j < nk && bits<uint32_t>(v[j]) == PARTIAL_EMPTY) pending |= 1u << j;
+#ifdef EXL3_TIMELINE
+      if (e == threadIdx.x && k0 == 0) EXL3_TL(7);
+#endif
       for (int n = 0; pending != 0 && n < a.poll_max; ++n) {
         __builtin_amdgcn_s_sleep(2);
 #pragma unroll
@@ -895,9 +904,9 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
         static_for<4>([&](auto J) {
           constexpr int pq = p0 + 4 * decltype(J)::value;
           if constexpr (FOLD)
-            qv[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.mask);
+            qv[J] = chunk_pair_mul1_h<MASKED, K, pq>(wd, a.dec.mask);
           else
-            qv[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.mask);
+            qv[J] = chunk_pair_cw<K, CB, MASKED, pq>(wd, a.dec);
         });
         const h8_t bf = frag(qv[0], qv[1], qv[2], qv[3]);
         if constexpr (f == 0) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc0, 0, 0, 0);
@@ -934,7 +943,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
 #pragma unroll
       for (int pq = 0; pq < 16; ++pq) {
         const uint32_t cw = 32u * c + 2u * pq;
-        p[pq] = decode_pair<CB>(tile_window(mine, n, cw), tile_window(mine, n, cw + 1u), a.mask);
+        p[pq] = decode_pair<CB>(tile_window(mine, n, cw), tile_window(mine, n, cw + 1u), a.dec);
       }
       gemv_mfma(p, alo, ahi, acc0, acc1);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1081,7 +1090,7 @@ template <int K, int CB, bool MASKED, int HALF>
 __device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
                                           const uint32_t *twc, size_t wstage, int src, int bst,
                                           const uint16_t *xp, const int (&aoff)[4], int ast,
-                                          int ard, int brd, int NS, uint32_t mask) {
+                                          int ard, int brd, int NS, CbRow mask) {
   constexpr int WL = gm_wl<K>();
   u4_t ra[3][4];       // activation pieces of stage x in set x % 3
   uint32_t wn[WL][K];  // packed words of stage x in set x % WL
@@ -1364,7 +1373,7 @@ template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    int M, int in_tiles, int out_tiles, uint32_t mask, float *__restrict__ kpart) {
+    int M, int in_tiles, int out_tiles, CbRow mask, float *__restrict__ kpart) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_BYTES / 2];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1554,7 +1563,7 @@ __device__ __forceinline__ void gw_mfma_main(f16v_t (&acc)[2][2], uint16_t *lds,
 // (st + 1) % 2 at bst.
 template <int K, int CB, bool MASKED, int HALF>
 __device__ __forceinline__ void gw_decode_main(uint16_t *lds, const uint32_t *twc, size_t wstage,
-                                               int src, int bst, int NS, uint32_t mask) {
+                                               int src, int bst, int NS, CbRow mask) {
   constexpr int WL = gm_wl<K>();
   uint32_t wn[WL][K];
   uint32_t hist[2];
@@ -1623,7 +1632,7 @@ template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    int M, int in_tiles, int out_tiles, uint32_t mask, float *__restrict__ kpart) {
+    int M, int in_tiles, int out_tiles, CbRow mask, float *__restrict__ kpart) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GW_LDS_BYTES / 2];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1775,7 +1784,7 @@ template <int K, int CB, bool MASKED>
 __global__ __launch_bounds__(GW_THREADS, 1) void gemm_grouped_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, int in_tiles, int out_tiles,
-    uint32_t mask, GemmGroup gg) {
+    CbRow mask, GemmGroup gg) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GW_LDS_BYTES / 2];
   __shared__ uint32_t rows[GM_BM];
   if (blockIdx.y >= *gg.n_items) return;  // the whole workgroup, before any barrier
@@ -1834,22 +1843,46 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_grouped_kernel(
                             svh + (size_t)item.expert * out, y, ydt, nullptr, nullptr, rows);
 }
 
+// Calls go(codebook, masked) with both as compile-time constants for the
+// weight's codebook form and window.  pair1 exists at n = 24..64 (its table's
+// rows) and only at the full window (the table admits its own window alone),
+// so it has forms at K = 2, 3, 4 and the run-time rate (K = 0) only.
+template <int K, typename G>
+inline void cb_dispatch(const Format &f, G &&go) {
+  using T = std::true_type;
+  using F = std::false_type;
+  const bool masked = f.window < 16;
+  switch (f.codebook) {
+    case CB_MCG:
+      masked ? go(std::integral_constant<int, CB_MCG>{}, T{})
+             : go(std::integral_constant<int, CB_MCG>{}, F{});
+      break;
+    case CB_HASH:
+      masked ? go(std::integral_constant<int, CB_HASH>{}, T{})
+             : go(std::integral_constant<int, CB_HASH>{}, F{});
+      break;
+    case CB_PAIR1:
+      if constexpr (K == 0 || (K >= 2 && K <= 4)) go(std::integral_constant<int, CB_PAIR1>{}, F{});
+      break;
+    default:
+      masked ? go(std::integral_constant<int, CB_MUL1>{}, T{})
+             : go(std::integral_constant<int, CB_MUL1>{}, F{});
+  }
+}
+
 template <int K>
 void gemm_grouped_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw,
                      const uint16_t *xp, const uint16_t *svh, void *y, int ydt, int in_tiles,
                      int out_tiles, const GemmGroup &gg) {
   static_assert(K > 0, "the GEMM serves integer rates");
-  const uint32_t m = f.mask();
+  const CbRow m = f.dec();
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, in_tiles,
                        out_tiles, m, gg);
   };
-  if (f.codebook == CB_MCG)
-    f.window < 16 ? go(gemm_grouped_kernel<K, CB_MCG, true>)
-                  : go(gemm_grouped_kernel<K, CB_MCG, false>);
-  else
-    f.window < 16 ? go(gemm_grouped_kernel<K, CB_MUL1, true>)
-                  : go(gemm_grouped_kernel<K, CB_MUL1, false>);
+  cb_dispatch<K>(f, [&](auto CBC, auto MC) {
+    go(gemm_grouped_kernel<K, decltype(CBC)::value, decltype(MC)::value>);
+  });
 }
 
 // ====================================================== per-rate launchers
@@ -1893,15 +1926,7 @@ void gemv_go(const Format &f, int prep, dim3 grid, size_t lds, hipStream_t s,
       default: go2(CBC, MC, std::integral_constant<int, PREP_PASSES>{});
     }
   };
-  using T = std::true_type;
-  using F = std::false_type;
-  using MUL1 = std::integral_constant<int, CB_MUL1>;
-  using MCG = std::integral_constant<int, CB_MCG>;
-  const bool masked = f.window < 16;
-  if (f.codebook == CB_MCG)
-    masked ? go(MCG{}, T{}) : go(MCG{}, F{});
-  else
-    masked ? go(MUL1{}, T{}) : go(MUL1{}, F{});
+  cb_dispatch<K>(f, go);
 }
 
 // The prepare form of a GEMV launch: 0 when its rows' items fit one batch,
@@ -1918,21 +1943,10 @@ void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, const ui
                  int topk, const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
                  const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
-  if (f.codebook == CB_MCG) {
-    if (f.window < 16)
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, true>), grid, blk, lds, s, tw0, tw1, x, g0, g1,
-                         g2, topk, sorted, items, n_items, a);
-    else
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MCG, false>), grid, blk, lds, s, tw0, tw1, x, g0,
-                         g1, g2, topk, sorted, items, n_items, a);
-  } else {
-    if (f.window < 16)
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, true>), grid, blk, lds, s, tw0, tw1, x, g0,
-                         g1, g2, topk, sorted, items, n_items, a);
-    else
-      hipLaunchKernelGGL((moe_gemv_kernel<K, CB_MUL1, false>), grid, blk, lds, s, tw0, tw1, x, g0,
-                         g1, g2, topk, sorted, items, n_items, a);
-  }
+  cb_dispatch<K>(f, [&](auto CBC, auto MC) {
+    hipLaunchKernelGGL((moe_gemv_kernel<K, decltype(CBC)::value, decltype(MC)::value>), grid, blk,
+                       lds, s, tw0, tw1, x, g0, g1, g2, topk, sorted, items, n_items, a);
+  });
 }
 
 #ifndef EXL3_GEMM_WS
@@ -1946,7 +1960,7 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
              int out_tiles, float *kpart) {
   static_assert(K > 0, "the GEMM serves integer rates");
   const dim3 blk(GM_THREADS);
-  const uint32_t m = f.mask();
+  const CbRow m = f.dec();
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, blk, 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles,
                        m, kpart);
@@ -1957,17 +1971,14 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
       hipLaunchKernelGGL(kern, grid, dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, zout, M,
                          in_tiles, out_tiles, m, kpart);
     };
-    if (f.codebook == CB_MCG)
-      f.window < 16 ? gow(gemm_ws_kernel<K, CB_MCG, true>) : gow(gemm_ws_kernel<K, CB_MCG, false>);
-    else
-      f.window < 16 ? gow(gemm_ws_kernel<K, CB_MUL1, true>)
-                    : gow(gemm_ws_kernel<K, CB_MUL1, false>);
+    cb_dispatch<K>(f, [&](auto CBC, auto MC) {
+      gow(gemm_ws_kernel<K, decltype(CBC)::value, decltype(MC)::value>);
+    });
     return;
   }
-  if (f.codebook == CB_MCG)
-    f.window < 16 ? go(gemm_kernel<K, CB_MCG, true>) : go(gemm_kernel<K, CB_MCG, false>);
-  else
-    f.window < 16 ? go(gemm_kernel<K, CB_MUL1, true>) : go(gemm_kernel<K, CB_MUL1, false>);
+  cb_dispatch<K>(f, [&](auto CBC, auto MC) {
+    go(gemm_kernel<K, decltype(CBC)::value, decltype(MC)::value>);
+  });
 }
 
 // Declarations of one rate's launcher instantiations.

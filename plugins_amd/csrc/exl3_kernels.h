@@ -12,14 +12,44 @@
 
 namespace exl3 {
 
+// A weight's decode constants as the kernels take them: the window mask
+// and, for the table codebooks, its rate's row
+// (sushi_ds41/src/sushi/exl3/codebook_tables.zig): hash-mask {mult, mask0};
+// pair1 {mult, mask0, mask1} and rsh = 32 - rot, the v_alignbit_b32 shift
+// that rotates left by rot.
+struct CbRow {
+  uint32_t mask = 0xFFFFu;
+  uint32_t mult = 0, mask0 = 0, mask1 = 0, rsh = 0;
+};
+
 // Decode parameters of one EXL3 weight: n halfwords per 16x16 tile (even,
-// 16..128), codebook (0 mul1, 1 mcg) and window bits (8..16).
+// 16..128), kernel codebook form (0 mul1, 1 mcg, 2 hash-mask: spec1 and
+// std1, 3 pair1; the Codebook enum of exl3_device.h), window bits (8..16)
+// and the table codebooks' row for n (row: {mult, mask0, mask1, rot}).
+// The kernel codebook forms Format.codebook holds (the Codebook enum of the
+// device code, restated for host code that does not include it).
+constexpr int CB_FORM_MUL1 = 0, CB_FORM_MCG = 1, CB_FORM_HASH = 2, CB_FORM_PAIR1 = 3;
+
 struct Format {
   int n = 0;
   int codebook = 0;
   int window = 16;
+  uint32_t row[4] = {0, 0, 0, 0};
   uint32_t mask() const { return (window >= 16) ? 0xFFFFu : ((1u << window) - 1u); }
   bool integer_rate() const { return n % 16 == 0 && n >= 16 && n <= 128; }
+  CbRow dec() const {
+    CbRow d;
+    d.mask = mask();
+    d.mult = row[0];
+    d.mask0 = row[1];
+    d.mask1 = row[2];
+    d.rsh = (32u - (row[3] & 31u)) & 31u;
+    return d;
+  }
+  bool same_decode(const Format &o) const {
+    return codebook == o.codebook && window == o.window && row[0] == o.row[0] &&
+           row[1] == o.row[1] && row[2] == o.row[2] && row[3] == o.row[3];
+  }
 };
 
 // Device scratch a GEMV or routed-MoE call uses for its split-K hand-off:

@@ -173,7 +173,7 @@ hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int yd
 template <int K, int CB>
 __global__ __launch_bounds__(64) void decode_matrix_kernel(const uint32_t *__restrict__ tw,
                                                            uint16_t *__restrict__ w, int out_tiles,
-                                                           uint32_t mask) {
+                                                           CbRow d) {
   __shared__ uint32_t blk[16 * 64];  // 16 rows x 128 f16, as dwords
   const int lane = threadIdx.x;
   const int tk = blockIdx.y, cg = blockIdx.x;
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(64) void decode_matrix_kernel(const uint32_t *__res
   uint16_t *row16 = reinterpret_cast<uint16_t *>(blk);
   static_for<16>([&](auto P) {
     constexpr int p = decltype(P)::value;
-    const uint32_t v = chunk_pair<K, CB, p>(wd, mask);
+    const uint32_t v = chunk_pair<K, CB, p>(wd, d);
     constexpr int r = chunk_row(2 * p);
     const int col = tl * 16 + c + 8 * chunk_colhalf(2 * p);
     row16[r * 128 + col] = (uint16_t)(v & 0xFFFFu);
@@ -209,7 +209,7 @@ template <int CB>
 __global__ __launch_bounds__(64) void decode_matrix_generic_kernel(const uint32_t *__restrict__ tw,
                                                                    uint16_t *__restrict__ w,
                                                                    int out_tiles, int n,
-                                                                   uint32_t mask) {
+                                                                   CbRow d) {
   __shared__ uint32_t words[8 * 64];
   __shared__ uint32_t blk[16 * 64];
   const int lane = threadIdx.x;
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64) void decode_matrix_generic_kernel(const uint32_
   uint16_t *row16 = reinterpret_cast<uint16_t *>(blk);
   for (int p = 0; p < 16; ++p) {
     const uint32_t t = 32u * c + 2u * p;
-    const uint32_t v = decode_pair<CB>(tile_window(mine, n, t), tile_window(mine, n, t + 1u), mask);
+    const uint32_t v = decode_pair<CB>(tile_window(mine, n, t), tile_window(mine, n, t + 1u), d);
     const int r = chunk_row(2 * p);
     const int col = tl * 16 + c + 8 * chunk_colhalf(2 * p);
     row16[r * 128 + col] = (uint16_t)(v & 0xFFFFu);
@@ -242,7 +242,7 @@ static hipError_t decode_matrix_cb(const uint32_t *tw, const Format &f, int in, 
                                    uint16_t *w, hipStream_t s) {
   const dim3 grid(out / 128, in / 16);
   const int ot = out / 16;
-  const uint32_t m = f.mask();
+  const CbRow m = f.dec();
   switch (f.integer_rate() ? f.n / 16 : 0) {
 #define EXL3_DM(KK)                                                                             \
   case KK:                                                                                      \
@@ -263,8 +263,12 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
   if (f.n < 16 || f.n > 128 || (f.n & 1)) return hipErrorInvalidValue;
   if (in / 16 > 65535) return hipErrorInvalidValue;
   const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
-  return f.codebook == CB_MCG ? decode_matrix_cb<CB_MCG>(tw, f, in, out, w, s)
-                              : decode_matrix_cb<CB_MUL1>(tw, f, in, out, w, s);
+  switch (f.codebook) {
+    case CB_MCG: return decode_matrix_cb<CB_MCG>(tw, f, in, out, w, s);
+    case CB_HASH: return decode_matrix_cb<CB_HASH>(tw, f, in, out, w, s);
+    case CB_PAIR1: return decode_matrix_cb<CB_PAIR1>(tw, f, in, out, w, s);
+    default: return decode_matrix_cb<CB_MUL1>(tw, f, in, out, w, s);
+  }
 }
 
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
@@ -365,7 +369,7 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   a.c.ydt = ydt;
   a.c.ptotal = (size_t)rows;
   a.c.ksplit = ksplit;
-  a.c.mask = f.mask();
+  a.c.dec = f.dec();
   a.c.nw = f.n / 2;
   a.c.x2 = fz.up;
   a.c.limit = fz.limit;
@@ -950,7 +954,7 @@ MoeGemv moe_gemv(const void *x, int xdt, bool prepared, size_t slots, int in, in
   m.a.c.ydt = OUT_F16;
   m.a.c.ptotal = slots;
   m.a.c.ksplit = ksplit;
-  m.a.c.mask = f.mask();
+  m.a.c.dec = f.dec();
   m.a.c.nw = f.n / 2;
   m.a.c.shared_expert = -1;
   return m;
@@ -976,7 +980,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     return hipErrorInvalidValue;
   if (a.hidden % 128 != 0 || a.inter % 128 != 0) return hipErrorInvalidValue;
   if (a.hidden / 16 > 65535 || a.inter / 16 > 65535) return hipErrorInvalidValue;
-  if (gate.f.n != up.f.n || gate.f.codebook != up.f.codebook || gate.f.window != up.f.window ||
+  if (gate.f.n != up.f.n || !gate.f.same_decode(up.f) ||
       gate.in != a.hidden || up.in != a.hidden || down.out != a.hidden || gate.out != a.inter ||
       up.out != a.inter || down.in != a.inter)
     return hipErrorInvalidValue;
@@ -985,7 +989,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   if (shared) {
     auto same = [](const MoeBank &b, const MoeBank &r) {
       return b.trellis && b.suh && b.svh && b.in == r.in && b.out == r.out && b.f.n == r.f.n &&
-             b.f.codebook == r.f.codebook && b.f.window == r.f.window;
+             b.f.same_decode(r.f);
     };
     if (L.gemm || a.inds == nullptr || !same(shared->gate, gate) || !same(shared->up, up) ||
         !same(shared->down, down))

@@ -384,15 +384,37 @@ def release(w: Weight) -> None:
     lib().exl3_release(ctypes.byref(w))
 
 
-def wrap(trellis, suh, svh, codebook: str = "mul1", window: int = 16, device: int = 0) -> Weight:
+# The shipped codebook tables a spec1 / std1 / pair1 block names, with the
+# digests it must carry (sushi_ds41/src/sushi/exl3/codebook_tables.zig:99-104).
+TABLE_DIGESTS = {"pair1-w16-v1": "c089b4eb", "spec1-w15": "37f72431", "spec1-w16": "753ffa03",
+                 "std1": "c5dba171"}
+
+
+def quant_block(codebook: str = "mul1", window: int = 16, table: str | None = None,
+                digest: str | None = None) -> str:
+    """An EXL3 quantization block; the table codebooks name their table (std1
+    and pair1 default to their one table) and its digest (default: the
+    shipped table's)."""
+    b = {"format": "exl3", "codebook": codebook, "window": window}
+    if table is None:
+        table = {"std1": "std1", "pair1": "pair1-w16-v1"}.get(codebook)
+    if table is not None:
+        b["codebook_table"] = table
+        b["codebook_digest"] = digest if digest is not None else TABLE_DIGESTS.get(table, "")
+    return json.dumps(b)
+
+
+def wrap(trellis, suh, svh, codebook: str = "mul1", window: int = 16, device: int = 0,
+         table: str | None = None, digest: str | None = None) -> Weight:
     """A Weight over device tensors (the library borrows their memory).  The
     returned Weight holds references to the three tensors, so the memory it
     points at stays allocated for as long as the Weight object lives, even
     when the caller passed temporaries (a freed block could otherwise be
     handed to the next allocation, or returned to the driver by
-    torch.cuda.empty_cache(), which torch.cuda.graph() calls on entry)."""
+    torch.cuda.empty_cache(), which torch.cuda.graph() calls on entry).
+    spec1 / std1 / pair1 decode with the row of `table` for the weight's rate."""
     w = Weight()
-    block = json.dumps({"format": "exl3", "codebook": codebook, "window": window})
+    block = quant_block(codebook, window, table, digest)
     tdt = DT_U16 if str(trellis.dtype) in ("torch.int16", "torch.uint16") else dtype_of(trellis)
     check(lib().exl3_weight_wrap(array(trellis, tdt), array(suh), array(svh), Str.of(block), device,
                                  ctypes.byref(w)), "weight_wrap")
@@ -609,9 +631,10 @@ class Linear:
     uint16 bits), suh f16 [in], svh f16 [out].  Keeps the tensors alive for the
     borrowed Weight."""
 
-    def __init__(self, trellis, suh, svh, codebook: str = "mul1", window: int = 16):
+    def __init__(self, trellis, suh, svh, codebook: str = "mul1", window: int = 16,
+                 table: str | None = None):
         self.tensors = (trellis, suh, svh)
-        self.weight = wrap(trellis, suh, svh, codebook, window, trellis.device.index or 0)
+        self.weight = wrap(trellis, suh, svh, codebook, window, trellis.device.index or 0, table)
         self.in_features = suh.shape[-1]
         self.out_features = svh.shape[-1]
 

@@ -7,12 +7,17 @@ p90, max; microseconds from the launch's first wave) of:
 
   entry, prepared (rows prepared, after the workgroup barrier), loop done,
   loop duration, reduced (before the split-K hand-off), partial stored (the
-  other splits' exit), hand-off done and finish done (the last split's);
+  other splits' exit), stores acknowledged (theirs, after a wait the product
+  build does not make), first read returned (the last split's first read of
+  the slots), hand-off done and finish done (the last split's);
 
 and for gate+up the medians per dispatch round (workgroup id // 256: the
 first, second and third workgroup each CU holds).
 
-    python -m plugins_amd.timeline
+    python -m plugins_amd.timeline [--lib PATH]
+
+--lib: another timeline build of the library (the default is the one
+`python -m plugins_amd.build --timeline` writes).
 """
 from __future__ import annotations
 
@@ -33,10 +38,13 @@ def main() -> int:
     sys.path.insert(0, ROOT)
     from plugins_amd import build as B
     from plugins_amd import exl3 as X
-    if not os.path.exists(B.TIMELINE_LIB):
+    lib = B.TIMELINE_LIB
+    if "--lib" in sys.argv:
+        lib = sys.argv[sys.argv.index("--lib") + 1]
+    if not os.path.exists(lib):
         print("build it first: python -m plugins_amd.build --timeline", file=sys.stderr)
         return 2
-    X.LIB_PATH = B.TIMELINE_LIB
+    X.LIB_PATH = lib
     L = X.lib()
     L.exl3_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     L.exl3_timeline_clear.argtypes = []
@@ -80,6 +88,21 @@ def main() -> int:
         print(f"== {name}: {len(R)} workgroups, last event at {np.nanmax(us):.2f} us")
         for e, label in enumerate(EVENTS):
             print(f"   {label:21s}{pct(w[:, e])}")
+        last = ~np.isnan(w[:, 5])
+        print(f"   {'stores acknowledged':21s}{pct(w[~last, 7])}")
+        print(f"   {'first read returned':21s}{pct(w[last, 7])}")
+        # per column group (workgroup id = split * groups + group): the last
+        # split's first read after its own reduce, and its hand-off end after
+        # the group's last acknowledged store
+        lastwg = ~np.isnan(us[:, 0, 5])
+        gx = int(lastwg.sum())
+        if gx and len(R) % gx == 0:
+            ksplit = len(R) // gx
+            g = us.reshape(ksplit, gx, 8, 8)
+            fr = g[-1, :, :2, 7] - g[-1, :, :2, 3]
+            seen = g[-1, :, 0, 5] - np.nanmax(g[:-1, :, :, 7].reshape(ksplit - 1, gx, -1), axis=(0, 2))
+            print(f"   {'first read latency':21s}{pct(fr.ravel())}")
+            print(f"   {'done after last ack':21s}{pct(seen)}")
         print(f"   {'loop duration':21s}{pct(w[:, 2] - w[:, 1])}")
         print(f"   {'hand-off duration':21s}{pct(w[:, 5] - w[:, 3])}")
         if name == "gate+up":

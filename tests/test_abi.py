@@ -113,6 +113,81 @@ def test_validate_refuses_by_name(edit, why):
     assert v.reason == "turboexl3_mi355x: " + why
 
 
+def test_validate_keeps_turboexl3s_codebooks():
+    # turboexl3_qwen38/config.zig:91-93: mul1 or mcg; the table codebooks
+    # (spec1, std1, pair1) serve through exl3_weight_wrap only
+    for cb in ("spec1", "std1", "pair1"):
+        block = json.loads(X.quant_block(cb, table="spec1-w15" if cb == "spec1" else None))
+        v = X.validate(json.dumps(block))
+        assert v.reason == "turboexl3_mi355x: Exl3CodebookUnsupported", cb
+
+
+def _wrap_verdict(block: str, n: int = 40, fake: bool = False):
+    """exl3_weight_wrap's verdict for a block; fake: shaped arrays at a dummy
+    address (never read: the refusals come before any use)."""
+    arrays = [X.Array(), X.Array(), X.Array()]
+    if fake:
+        for a, (dt, dims) in zip(arrays, ((X.DT_U16, (8, 8, n)), (X.DT_F16, (128,)), (X.DT_F16, (128,)))):
+            a.data, a.dtype, a.ndim = 0x1000, dt, len(dims)
+            for i, d in enumerate(dims):
+                a.shape[i] = d
+    w = X.Weight()
+    return X.lib().exl3_weight_wrap(*arrays, X.Str.of(block), 0, ctypes.byref(w))
+
+
+@pytest.mark.parametrize("block,why", [
+    # sushi_ds41/src/sushi/exl3/codebook_tables.zig:351-368, through the block
+    ({"codebook": "pair1"}, "Exl3CodebookTableUnknown"),
+    ({"codebook": "pair1", "codebook_table": "pair1-w16-v9", "codebook_digest": "c089b4eb"},
+     "Exl3CodebookTableUnknown"),
+    ({"codebook": "pair1", "codebook_table": 7, "codebook_digest": "c089b4eb"}, "Exl3CodebookTableUnknown"),
+    ({"codebook": "pair1", "codebook_table": "pair1-w16-v1"}, "Exl3CodebookTableDigestMismatch"),
+    ({"codebook": "pair1", "codebook_table": "pair1-w16-v1", "codebook_digest": "deadbeef"},
+     "Exl3CodebookTableDigestMismatch"),
+    ({"codebook": "spec1", "codebook_table": "pair1-w16-v1", "codebook_digest": "c089b4eb"},
+     "Exl3CodebookTableCodebookMismatch"),
+    ({"codebook": "pair1", "window": 15, "codebook_table": "pair1-w16-v1", "codebook_digest": "c089b4eb"},
+     "Exl3CodebookTableWindowMismatch"),
+    ({"codebook": "std1", "window": 15, "codebook_table": "std1", "codebook_digest": "2ac2594d"},
+     "Exl3CodebookTableDigestMismatch"),
+    ({"codebook": "spec1", "window": 15, "codebook_table": "std1", "codebook_digest": "c5dba171"},
+     "Exl3CodebookTableCodebookMismatch"),
+    ({"codebook": "spec1", "window": 15}, "Exl3CodebookTableUnknown"),
+    ({"codebook": "spec1", "window": 15, "codebook_table": "spec1-w15", "codebook_digest": "2ac2594d"},
+     "Exl3CodebookTableLegacyConfig"),
+    ({"codebook": "3inst"}, "Exl3CodebookUnsupported"),
+])
+def test_weight_wrap_refuses_codebook_tables_by_name(block, why):
+    b = {"format": "exl3", "window": 16, **block}
+    v = _wrap_verdict(json.dumps(b))
+    assert v.code == X.UNSUPPORTED and v.reason == "turboexl3_mi355x: " + why, v
+
+
+def test_weight_wrap_admits_every_window_for_spec1_and_std1_tables():
+    # a spec1 / std1 table decodes at any window (codebook_tables.zig:354-357,
+    # 404-414): the block passes, and the null arrays are what is refused
+    for w in range(8, 17):
+        for cb, t in (("spec1", "spec1-w15"), ("spec1", "spec1-w16"), ("std1", "std1")):
+            v = _wrap_verdict(X.quant_block(cb, w, t))
+            assert v.reason == "turboexl3_mi355x: BadExl3Shape", (cb, t, w, v)
+    assert _wrap_verdict(X.quant_block("pair1", 16)).reason == "turboexl3_mi355x: BadExl3Shape"
+
+
+@pytest.mark.parametrize("cb,table,n,has_row", [
+    ("std1", "std1", 16, False), ("std1", "std1", 70, False), ("std1", "std1", 24, True),
+    ("pair1", None, 22, False), ("pair1", None, 66, False), ("pair1", None, 64, True),
+    ("spec1", "spec1-w16", 16, False), ("spec1", "spec1-w15", 16, True), ("spec1", "spec1-w15", 128, True),
+])
+def test_weight_wrap_refuses_a_rate_its_table_has_no_row_for(cb, table, n, has_row):
+    # codebook_tables.zig:48-52 and 420-429 (std1 stops at K4, spec1-w15
+    # reaches K1 and K8); a rate with a row passes to the arrays' device check
+    v = _wrap_verdict(X.quant_block(cb, 16, table), n=n, fake=True)
+    if has_row:
+        assert v.reason != "turboexl3_mi355x: Exl3CodebookTableRateMissing", v
+    else:
+        assert v.reason == "turboexl3_mi355x: Exl3CodebookTableRateMissing", v
+
+
 def test_validate_rates_every_even_halfword_count():
     for n in range(16, 129):
         v = X.validate(json.dumps({"format": "exl3", "codebook": "mcg", "k": n / 16}))

@@ -70,6 +70,117 @@ def test_mcg_closed_form_every_state():
     assert sha(got) == "95383563929baa9d1ae5de0be22490284382673620bdd85929feea7bdbef04a9"
 
 
+# ------------------------------------------------------- table codebooks
+
+TABLES = GOLD["codebook_tables"]
+TABLE_IDS = {name: t for t, name in O.TABLE_NAMES.items()}
+
+
+def table_digest(fields, ns, rows) -> str:
+    # sushi_ds41/src/sushi/exl3/codebook_tables.zig:230-247: sha256 over one
+    # line per row, "<n>,<field as 8 lowercase hex digits>,...\n", first 8 hex
+    text = "".join(f"{n}," + ",".join(f"{v:08x}" for v in r[:fields]) + "\n" for n, r in zip(ns, rows))
+    return hashlib.sha256(text.encode()).hexdigest()[:8]
+
+
+def table_rows(table):
+    n_lo, count, fields = O.table_info(table)
+    ns = [n_lo + 2 * i for i in range(count)]
+    return fields, ns, [O.table_row(table, n) for n in ns]
+
+
+def test_table_digest_function_against_the_fixed_vector():
+    v = TABLES["digest_vector"]
+    assert table_digest(v["fields"], v["ns"], v["rows"]) == v["digest"]
+
+
+@pytest.mark.parametrize("name", ["pair1-w16-v1", "spec1-w15", "spec1-w16", "std1"])
+def test_codebook_tables_match_their_pinned_digests(name):
+    # every constant of every row is under the reference's pinned digest
+    fields, ns, rows = table_rows(TABLE_IDS[name])
+    assert table_digest(fields, ns, rows) == TABLES["digests"][name]
+    for n, want in TABLES["rows"].get(name, {}).items():
+        assert O.table_row(TABLE_IDS[name], int(n))[:len(want)] == tuple(want), (name, n)
+    for n in TABLES["no_row"].get(name, []):
+        assert O.table_row(TABLE_IDS[name], n) is None, (name, n)
+    assert all(O.table_row(TABLE_IDS[name], n) is None for n in range(ns[0] + 1, ns[-1], 2))
+
+
+def test_spec1_w15_extends_its_superseded_version():
+    # codebook_tables.zig:444-448: rows n = 24..64 are the table of digest 2ac2594d
+    fields, ns, rows = table_rows(O.TAB_SPEC1_W15)
+    keep = [(n, r) for n, r in zip(ns, rows) if 24 <= n <= 64]
+    assert table_digest(fields, [n for n, _ in keep], [r for _, r in keep]) == TABLES["superseded"]["spec1-w15"][0]
+
+
+def test_table_digest_catches_a_changed_constant():
+    fields, ns, rows = table_rows(O.TAB_PAIR1_W16_V1)
+    rows = [list(r) for r in rows]
+    rows[3][0] = (rows[3][0] + 1) & 0xFFFFFFFF  # codebook_tables.zig:310-318's mutation
+    assert table_digest(fields, ns, rows) != TABLES["digests"]["pair1-w16-v1"]
+
+
+def test_hash_mask_known_answers():
+    k = GOLD["kat_hash_mask"]
+    for cw, want in k["values"].items():
+        assert O.decode_hash_mask(int(cw), k["mult"], k["mask"]) == want, cw
+
+
+def test_hash_mask_closed_form_every_state():
+    # halfSumScaled (expert_exl3.zig:288-295) evaluated in float64: the exact
+    # half sum rounded once to f16 equals the f32 sum rounded (24 >= 2 * 11 + 2
+    # bits), and * 4096 is exact
+    for table, n in ((O.TAB_STD1, 40), (O.TAB_SPEC1_W15, 16), (O.TAB_SPEC1_W15, 128)):
+        mult, mask = O.table_row(table, n)[:2]
+        cw = np.arange(65536, dtype=np.uint64)
+        p = ((cw * mult) & mask).astype(np.uint32)
+        lo = (p & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+        hi = (p >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+        want = ((lo + hi).astype(np.float16).astype(np.float64) * 4096.0).astype(np.float16).view(np.uint16)
+        got = np.array([O.decode_hash_mask(c, mult, mask) for c in range(0, 65536, 7)], np.uint16)
+        np.testing.assert_array_equal(got, want[::7])
+
+
+def test_pair1_known_answers():
+    for n, cw, w0, w1 in GOLD["kat_pair1"]:
+        assert O.decode_pair1(cw, O.table_row(O.TAB_PAIR1_W16_V1, n)) == (w0, w1), (n, cw)
+
+
+def test_pair1_kats_catch_a_rotation_the_other_way():
+    # planted on the CPU: rotr instead of rotl fails the reference's values
+    bad = 0
+    for n, cw, w0, w1 in GOLD["kat_pair1"]:
+        row = list(O.table_row(O.TAB_PAIR1_W16_V1, n))
+        row[1] = (32 - row[1]) % 32
+        bad += O.decode_pair1(cw, row) != (w0, w1)
+    assert bad > 10
+
+
+def test_table_tiles_decode_codeword_by_codeword():
+    # spec1 / std1 tiles: each codeword decoded on its own through the pinned
+    # unpack and permutation; pair1: slots 2j and 2j+1 from codeword 2j+1
+    # (expert_exl3.zig:338-357; the reference's own pair1 tile fixture,
+    # fixtures/exl3_pair1_tiles.safetensors, is not in its tree)
+    rng = np.random.default_rng(31)
+    perm = O.tile_perm()
+    for cb, table, n, window in ((O.spec1(O.TAB_SPEC1_W15), O.TAB_SPEC1_W15, 40, 15),
+                                 (O.spec1(O.TAB_SPEC1_W16), O.TAB_SPEC1_W16, 64, 16),
+                                 (O.CB_STD1, O.TAB_STD1, 24, 12),
+                                 (O.CB_PAIR1, O.TAB_PAIR1_W16_V1, 48, 16)):
+        words = rng.integers(0, 65536, n, dtype=np.uint16)
+        got = O.decode_tile(words, n, cb, window)
+        cws = O.unpack_tile(words, n, bitwise=True) & ((1 << window) - 1)
+        row = O.table_row(table, n)
+        want = np.empty(256, np.uint16)
+        if cb == O.CB_PAIR1:
+            for j in range(128):
+                want[perm[2 * j]], want[perm[2 * j + 1]] = O.decode_pair1(int(cws[2 * j + 1]), row)
+        else:
+            for i in range(256):
+                want[perm[i]] = O.decode_hash_mask(int(cws[i]), row[0], row[1])
+        np.testing.assert_array_equal(got, want)
+
+
 # ------------------------------------------------------------------- rates
 
 @pytest.mark.parametrize("n", ["40", "44", "48", "64"])
