@@ -627,7 +627,7 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
   const int in = (int)p0->in;
   const size_t xsz = prepared ? 2 : (xdt == exl3::ACT_F32 ? 4 : 2);
   const size_t ysz = ydt == exl3::ACT_F32 ? 4 : 2;
-  if (rows > exl3::GEMV_ROWS_MAX && p0->f.integer_rate()) {
+  if (rows > exl3::GEMV_ROWS_MAX && p0->f.gemm_rate()) {
     for (int i = 0; i < count; ++i) {
       const uint16_t *xp = (const uint16_t *)x;
       if (!prepared) {
@@ -779,7 +779,7 @@ exl3_verdict exl3_matmul_noalloc(const exl3_weight *w, exl3_array x, exl3_stream
       numel(out) != rows * pv->out)
     return kShape;
   // what run_linears will ask of the scratch
-  const bool gemm = rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate();
+  const bool gemm = rows > exl3::GEMV_ROWS_MAX && pv->f.gemm_rate();
   size_t slot_floats = 0, xp_bytes = 0, kpart_bytes = 0;
   if (gemm) {
     xp_bytes = ((size_t)rows * pv->in * 2 + 255) & ~(size_t)255;
@@ -951,8 +951,7 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
     }
     return ok();
   }
-  if (inds.data == nullptr && pg->f.integer_rate() && pu->f.integer_rate() &&
-      pd->f.integer_rate()) {
+  if (inds.data == nullptr && pg->f.gemm_rate() && pu->f.gemm_rate() && pd->f.gemm_rate()) {
     // Dense MLP of more rows (prefill, a shared expert at large batches):
     // gate and up through the GEMM (f16), the SwiGLU once (the MoE path's mid
     // step, bit for bit), the down projection through the GEMM.
@@ -1353,7 +1352,7 @@ exl3_verdict exl3_linear_prepared(const exl3_weight *w, exl3_array xp,
 
 // The kernel path of a call of `rows` rows (run_linears' choice).
 static bool gemm_path(const WeightPriv *pv, int64_t rows) {
-  return rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate();
+  return rows > exl3::GEMV_ROWS_MAX && pv->f.gemm_rate();
 }
 
 exl3_verdict exl3_linear_pieces(const exl3_weight *w, const exl3_linear_parts *opts,
@@ -1480,7 +1479,7 @@ const char *exl3_matmul_path(const exl3_weight *w, int64_t rows) {
   const WeightPriv *pv = priv_of(w);
   if (!pv) return "none";
   if (rows <= exl3::GEMV_ROWS_MAX) return "gemv";
-  return pv->f.integer_rate() ? "gemm" : "gemv";
+  return pv->f.gemm_rate() ? "gemm" : "gemv";
 }
 
 const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
@@ -1489,7 +1488,7 @@ const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
   if (!pg || !pu || !pd || rows <= 0) return "none";
   if (topk <= 0) {
     if (rows <= exl3::GEMV_ROWS_MAX && pg->f.same_decode(pu->f)) return "dense-gemv";
-    if (pg->f.integer_rate() && pu->f.integer_rate() && pd->f.integer_rate()) return "dense-gemm";
+    if (pg->f.gemm_rate() && pu->f.gemm_rate() && pd->f.gemm_rate()) return "dense-gemm";
     return "dense-items";
   }
   exl3::MoeArgs a{};

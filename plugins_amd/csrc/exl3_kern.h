@@ -1628,7 +1628,95 @@ __device__ __forceinline__ void gw_decode_main(uint16_t *lds, const uint32_t *tw
   }
 }
 
-template <int K, int CB, bool MASKED>
+// ------------------------------------------------ half-integer rates
+//
+// At n = 8 FR halfwords a tile (FR odd: K = FR / 2 = 1.5, 2.5, exllamav3's
+// half-integer rates; turboexl3_ds41/src/bank/frac.zig:1-21), chunk c of a
+// tile (codewords 32 c .. 32 c + 31) is stream halfwords c FR .. c FR + FR - 1
+// (bitEnd(32 c) = 2 n c: a halfword boundary, not a dword one).  A decode
+// thread loads the LW = NB + 1 dwords holding that chunk and the halfword
+// before it (the tile's last for c = 0: the ring wraps), starting at dword b;
+// one v_alignbit_b32 per dword by sh (16 when that history halfword is the
+// low half of dword b, else 0 with b one dword earlier) leaves NB dwords
+// [history | chunk], MSB first, in which codeword i's window ends at bit
+// 16 + floor((i + 1) FR / 2): compile-time positions, as chunk_cw's.
+template <int FR>
+constexpr int gf_nb() {
+  return (FR + 1) / 2;
+}
+
+template <int FR, int I>
+__device__ __forceinline__ uint32_t chunk_cw_frac(const uint32_t (&w)[gf_nb<FR>()]) {
+  constexpr int E = 16 + ((I + 1) * FR) / 2;
+  constexpr int J0 = (E - 16) >> 5, J1 = (E - 1) >> 5;
+  static_assert(J1 < gf_nb<FR>(), "window outside the chunk buffer");
+  if constexpr (J0 == J1)
+    return __builtin_amdgcn_ubfe(w[J0], 31 - ((E - 1) & 31), 16);
+  else
+    return __builtin_amdgcn_alignbit(w[J0], w[J1], 31 - ((E - 1) & 31)) & 0xFFFFu;
+}
+
+// The decode waves' main loop at a half-integer rate: gw_decode_main's
+// schedule and barriers (stage st + 1 decoded during stage st into B buffer
+// (st + 1) % 2) with each thread's chunk loaded whole (off: its LW dword
+// offsets in the tile, twt: its tile in stage 0).
+template <int FR, int CB, bool MASKED, int HALF>
+__device__ __forceinline__ void gw_decode_frac(uint16_t *lds, const uint32_t *twt, size_t wstage,
+                                               const int (&off)[gf_nb<FR>() + 1], uint32_t sh,
+                                               int bst, int NS, CbRow mask) {
+  constexpr int NB = gf_nb<FR>(), LW = NB + 1;
+  constexpr int WL = 6;
+  uint32_t wn[WL][LW];
+  auto load_w = [&](auto S, int st) {
+    constexpr int q = decltype(S)::value;
+    const uint32_t *p = twt + (size_t)min(st, NS - 1) * wstage;
+#pragma unroll
+    for (int j = 0; j < LW; ++j) wn[q][j] = p[off[j]];
+  };
+  auto decode = [&](auto S, int b) {
+    constexpr int q = decltype(S)::value;
+    uint32_t wd[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) wd[j] = __builtin_amdgcn_alignbit(wn[q][j], wn[q][j + 1], sh);
+    static_for<2>([&](auto F) {
+      constexpr int f = 2 * HALF + decltype(F)::value;
+      uint32_t v[4];
+      static_for<4>([&](auto J) {
+        constexpr int pr = gm_pair(f, decltype(J)::value);
+        v[J] = decode_pair_cw<CB, MASKED>(chunk_cw_frac<FR, 2 * pr>(wd),
+                                          chunk_cw_frac<FR, 2 * pr + 1>(wd), mask);
+      });
+      const u4_t u = {v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<u4_t *>(lds + b * GM_BTILE + bst + 8 * (f & 1) * GM_LD + 8 * (f >> 1)) = u;
+    });
+  };
+  auto stage = [&](auto PH, int st) {
+    constexpr int ph = decltype(PH)::value;
+    using W0 = std::integral_constant<int, ph % WL>;
+    using W1 = std::integral_constant<int, (ph + 1) % WL>;
+    if (st + 1 < NS) decode(W1{}, (ph + 1) & 1);
+    load_w(W0{}, st + WL);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  static_for<WL>([&](auto W) { load_w(W, decltype(W)::value); });
+  decode(std::integral_constant<int, 0>{}, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  int st = 0;
+  for (; st + 6 <= NS; st += 6) {
+    static_for<6>([&](auto PH) { stage(PH, st + decltype(PH)::value); });
+  }
+  if (st < NS) {
+    stage(std::integral_constant<int, 0>{}, st);
+    stage(std::integral_constant<int, 1>{}, st + 1);
+    if (st + 2 < NS) {
+      stage(std::integral_constant<int, 2>{}, st + 2);
+      stage(std::integral_constant<int, 3>{}, st + 3);
+    }
+  }
+}
+
+// FR = 0: an integer rate K; FR odd: the half-integer rate n = 8 FR (K unused).
+template <int K, int CB, bool MASKED, int FR = 0>
 __global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
     const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
     const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
@@ -1644,7 +1732,7 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
   const int m0 = (lin % mblocks) * GM_BM;
   const int in = in_tiles * 16;
   const size_t out = (size_t)out_tiles * 16;
-  constexpr int NW = 8 * K;
+  constexpr int NW = FR > 0 ? 4 * FR : 8 * K;
   const int NS = in_tiles / 4;
   const int S = gridDim.z, ks = blockIdx.z;
   const int P = NS / 2;
@@ -1685,15 +1773,35 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
     // take the same chunk); the 8 chunks of a tile sit in 8 consecutive lanes
     const int dt = (tid - 512) & 255;
     const int tkl = dt >> 6, tnl = (dt >> 3) & 7, c = dt & 7;
-    const uint32_t *twc = tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
     const size_t wstage = (size_t)4 * out_tiles * NW;
-    const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
     const int bst = (tnl * 16 + c) * GM_LD + tkl * 16;
-    twc += (size_t)st0 * wstage;
-    if (wave < 12)
-      gw_decode_main<K, CB, MASKED, 0>(lds, twc, wstage, src, bst, st1 - st0, mask);
-    else
-      gw_decode_main<K, CB, MASKED, 1>(lds, twc, wstage, src, bst, st1 - st0, mask);
+    if constexpr (FR > 0) {
+      // the chunk's history halfword hs (stream order: halfword s is the high
+      // half of dword s / 2 when s is even, the low half when odd)
+      constexpr int LW = gf_nb<FR>() + 1;
+      const int hs = (c * FR - 1 + 8 * FR) % (8 * FR);
+      const bool low = (hs & 1) != 0;
+      const int b0 = (hs >> 1) - (low ? 0 : 1);
+      int off[LW];
+#pragma unroll
+      for (int j = 0; j < LW; ++j) off[j] = (b0 + j) % NW;
+      const uint32_t *twt =
+          tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + (size_t)st0 * wstage;
+      if (wave < 12)
+        gw_decode_frac<FR, CB, MASKED, 0>(lds, twt, wstage, off, low ? 16u : 0u, bst, st1 - st0,
+                                          mask);
+      else
+        gw_decode_frac<FR, CB, MASKED, 1>(lds, twt, wstage, off, low ? 16u : 0u, bst, st1 - st0,
+                                          mask);
+    } else {
+      const uint32_t *twc = tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
+      const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+      twc += (size_t)st0 * wstage;
+      if (wave < 12)
+        gw_decode_main<K, CB, MASKED, 0>(lds, twc, wstage, src, bst, st1 - st0, mask);
+      else
+        gw_decode_main<K, CB, MASKED, 1>(lds, twc, wstage, src, bst, st1 - st0, mask);
+    }
   }
   gemm_tile_end<GW_THREADS>(acc, lds, mw, wm, wc, m0, cg, M, out, S, ks, svh, y, ydt, zout,
                             kpart);
@@ -1981,6 +2089,21 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
   });
 }
 
+// The prefill GEMM at a half-integer rate n = 8 FR (the specialised-wave
+// kernel; activations addressed with 32-bit offsets, checked by the caller).
+template <int FR>
+void gemm_frac_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw,
+                  const uint16_t *xp, const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M,
+                  int in_tiles, int out_tiles, float *kpart) {
+  static_assert(FR % 2 == 1, "a half-integer rate");
+  const CbRow m = f.dec();
+  cb_dispatch<0>(f, [&](auto CBC, auto MC) {
+    hipLaunchKernelGGL((gemm_ws_kernel<1, decltype(CBC)::value, decltype(MC)::value, FR>), grid,
+                       dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles,
+                       m, kpart);
+  });
+}
+
 // Declarations of one rate's launcher instantiations.
 #define EXL3_GEMV_GO(KK)                                                                 \
   void gemv_go<KK>(const Format &, int, dim3, size_t, hipStream_t, const uint32_t *const *, \
@@ -1995,6 +2118,9 @@ void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, cons
 #define EXL3_GEMM_GO(KK)                                                                    \
   void gemm_go<KK>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
                    const uint16_t *, void *, int, uint16_t *, int, int, int, float *)
+#define EXL3_GEMM_FRAC_GO(FR)                                                                    \
+  void gemm_frac_go<FR>(const Format &, dim3, hipStream_t, const uint32_t *, const uint16_t *, \
+                        const uint16_t *, void *, int, uint16_t *, int, int, int, float *)
 
 #ifndef EXL3_INST_K
 // instantiated in the per-rate units only
@@ -2027,6 +2153,8 @@ extern template EXL3_GEMM_GO(7);
 extern template EXL3_GEMM_GROUPED_GO(7);
 extern template EXL3_GEMM_GO(8);
 extern template EXL3_GEMM_GROUPED_GO(8);
+extern template EXL3_GEMM_FRAC_GO(3);
+extern template EXL3_GEMM_FRAC_GO(5);
 #endif
 
 }  // namespace exl3

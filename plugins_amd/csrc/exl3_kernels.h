@@ -37,6 +37,9 @@ struct Format {
   uint32_t row[4] = {0, 0, 0, 0};
   uint32_t mask() const { return (window >= 16) ? 0xFFFFu : ((1u << window) - 1u); }
   bool integer_rate() const { return n % 16 == 0 && n >= 16 && n <= 128; }
+  // the prefill GEMM's rates: the integer ones and the half-integer n = 24, 40
+  // (exllamav3's K 1.5 and 2.5; turboexl3_ds41/src/bank/frac.zig:42-44)
+  bool gemm_rate() const { return integer_rate() || n == 24 || n == 40; }
   CbRow dec() const {
     CbRow d;
     d.mask = mask();

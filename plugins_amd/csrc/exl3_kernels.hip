@@ -523,7 +523,10 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
                        int out, float *kpart, size_t kpart_floats, hipStream_t s) {
   if (rows < 1 || in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
-  if (!f.integer_rate()) return hipErrorInvalidValue;
+  if (!f.gemm_rate()) return hipErrorInvalidValue;
+  // the half-integer rates run the specialised-wave kernel only, whose
+  // activation offsets are 32-bit
+  if (!f.integer_rate() && (size_t)rows * (in / 16) * 32 > 0xFFFFFFFFu) return hipErrorInvalidValue;
   if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
   const int mblocks = (rows + GM_BM - 1) / GM_BM;
   if (mblocks > 65535) return hipErrorInvalidValue;
@@ -534,10 +537,15 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
   const dim3 grid((out + GM_BN - 1) / GM_BN, mblocks, sp.splits);
   const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
   const int it = in / 16, ot = out / 16;
-  rate_dispatch(f.n / 16, [&](auto KC) {
-    constexpr int K = decltype(KC)::value;
-    if constexpr (K > 0) gemm_go<K>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, kpart);
-  });
+  if (f.n == 24)
+    gemm_frac_go<3>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, kpart);
+  else if (f.n == 40)
+    gemm_frac_go<5>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, kpart);
+  else
+    rate_dispatch(f.n / 16, [&](auto KC) {
+      constexpr int K = decltype(KC)::value;
+      if constexpr (K > 0) gemm_go<K>(f, grid, s, tw, xp, svh, y, ydt, zout, rows, it, ot, kpart);
+    });
   if (sp.splits > 1)
     hipLaunchKernelGGL(gemm_splitk_finish_kernel, dim3(out / 128, (rows + 7) / 8), dim3(512), 0, s,
                        kpart, sp.splits, rows, out, svh, y, ydt, zout);
