@@ -29,11 +29,19 @@ namespace exl3 {
 #ifdef EXL3_TIMELINE
 constexpr int TIMELINE_WGS = 4096;
 static __device__ unsigned long long g_timeline[TIMELINE_WGS * 8 * 8];
+// The entry stamp also carries the XCD the workgroup runs on (HW_REG_XCC_ID)
+// in bits 56-59 (the counter's values stay far below 2^56).
+__device__ __forceinline__ unsigned long long timeline_xcc() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+  return (unsigned long long)(v & 15u) << 56;
+}
 #define EXL3_TL(k)                                                                           \
   do {                                                                                       \
     const size_t wg_ = (size_t)blockIdx.x + (size_t)gridDim.x * blockIdx.y;                  \
     if ((threadIdx.x & 63) == 0 && wg_ < TIMELINE_WGS)                                       \
-      g_timeline[(wg_ * 8 + (threadIdx.x >> 6)) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+      g_timeline[(wg_ * 8 + (threadIdx.x >> 6)) * 8 + (k)] =                                 \
+          __builtin_amdgcn_s_memrealtime() | ((k) == 0 ? timeline_xcc() : 0ull);             \
   } while (0)
 #else
 #define EXL3_TL(k) \
@@ -643,7 +651,8 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
       float v[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (j < nk) v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
+        if (j < nk)
+          v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
       // every slot still empty is read again in the same round, so the wait
       // is one round trip after the last store lands (not one per slot)
       uint32_t pending = 0;

@@ -81,7 +81,12 @@ def main() -> int:
         buf = np.zeros(WGS * 8 * 8, dtype=np.uint64)
         L.exl3_timeline_read(buf.ctypes.data, buf.nbytes)
         R = buf.reshape(WGS, 8, 8).astype(np.int64)
-        R = R[R[:, 0, 0] > 0]
+        live = R[:, 0, 0] > 0
+        # the entry stamps carry the workgroup's XCD in bits 56-59
+        xcc = (R[live, 0, 0] >> 56) & 15
+        wgid = np.nonzero(live)[0]
+        R[:, :, 0] &= (1 << 56) - 1
+        R = R[live]
         t0 = R[:, :, 0][R[:, :, 0] > 0].min()
         us = np.where(R > 0, (R - t0) * 0.01, np.nan)
         w = us.reshape(-1, 8)
@@ -102,6 +107,10 @@ def main() -> int:
             fr = g[-1, :, :2, 7] - g[-1, :, :2, 3]
             seen = g[-1, :, 0, 5] - np.nanmax(g[:-1, :, :, 7].reshape(ksplit - 1, gx, -1), axis=(0, 2))
             print(f"   {'first read latency':21s}{pct(fr.ravel())}")
+            same = np.mean([len(set(xcc[wgid % gx == c])) == 1 for c in range(gx)])
+            rr = max(np.mean(xcc == (wgid + r) % 8) for r in range(8))
+            print(f"   XCD: {len(set(xcc.tolist()))} seen; workgroups on XCD (id + r) % 8: {rr:.3f}; "
+                  f"column groups with every split on one XCD: {same:.3f}")
             print(f"   {'done after last ack':21s}{pct(seen)}")
         print(f"   {'loop duration':21s}{pct(w[:, 2] - w[:, 1])}")
         print(f"   {'hand-off duration':21s}{pct(w[:, 5] - w[:, 3])}")
