@@ -387,13 +387,44 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
                                 exl3_array scores, const exl3_shared_swiglu *opts,
                                 exl3_stream s, exl3_array *out);
 
+/* QuantTable.resident (quant.zig:96-99): memory for speed.  Admits ws'
+ * single linears: each one's decoded matrix (W_inner f16 [in, out], in * out
+ * * 2 bytes) is held from its first matmul at prefill widths (over 16 rows)
+ * on, and that matmul becomes the prepare, a dense f16 GEMM (hipBLASLt) over
+ * the held matrix and the finish; decode widths keep the EXL3 GEMV.
+ * *bytes = what ws' matrices take.  Refused EXL3_TOO_LARGE past room (0:
+ * no bound), admitting none; an empty ws drops every kept matrix. */
+exl3_verdict exl3_resident(exl3_weight_span ws, uint64_t room, exl3_stream s, uint64_t *bytes);
+
+/* QuantTable.resident_pending (quant.zig:100-101): the bytes admitted and
+ * not held yet. */
+uint64_t exl3_resident_pending(void);
+
+/* QuantTable.unrotate (quant.zig:102-104): ws in groups of sizes[g] weights
+ * that read one input; each group's matrices out of the format's basis,
+ * W_public = diag(suh) H W_inner H diag(svh) / 128 (the reference's
+ * reconstructPublic, sushi_ds41/src/sushi/exl3/expert_exl3.zig:440-488, in
+ * its operation order; f16 bit for bit), joined side by side in `act`
+ * (EXL3_DT_F16/BF16/F32) as one [in, sum of outs] matrix; each member's
+ * W_inner is freed and its prefill matmuls in `act` become one dense GEMM
+ * over its columns.  took[g]: whether group g took (members admitted by
+ * exl3_resident, one input width and device, in no other group). */
+exl3_verdict exl3_unrotate(exl3_weight_span ws, exl3_u8_span sizes, int32_t act, exl3_stream s,
+                           bool *took);
+
+/* QuantTable.linear_joined (quant.zig:105-107): x [..., in] times the joined
+ * matrix of the un-rotated group whose members are ws, in order: [..., sum
+ * of outs] in x's dtype (the group's act).  Refused when ws is not such a
+ * group and at decode widths (up to 16 rows). */
+exl3_verdict exl3_linear_joined(exl3_weight_span ws, exl3_array x, exl3_stream s,
+                                exl3_array *out);
+
 /* ----------------------------------------------------- the plugin table */
 
 /* kit `QuantTable`, the whole layout (quant.zig:24-107): the entries
  * turboexl3_ds41 fills (turboexl3_ds41/plugin.zig:28-43), the split
- * entries, and NULL for the optional entries this library does not serve
- * (the attention entries, resident / resident_pending / unrotate /
- * linear_joined), where the host runs its own chain. */
+ * entries, swiglu_shared, the resident entries, and NULL for the
+ * attention entries, where the host runs its own chain. */
 typedef struct exl3_quant_table {
   uint32_t size;
   uint32_t version;

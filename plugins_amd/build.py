@@ -42,6 +42,7 @@ SOURCES = [
     ("exl3_host.cpp", "exl3_host", HOST_FLAGS),
     ("exl3_json.cpp", "exl3_json", HOST_FLAGS),
     ("exl3_codebooks.cpp", "exl3_codebooks", HOST_FLAGS),
+    ("exl3_dense.cpp", "exl3_dense", HOST_FLAGS),
     ("exl3_pack.cpp", "exl3_pack", HOST_FLAGS),
 ]
 
@@ -86,7 +87,8 @@ def build(verbose: bool = True, timeline: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda sf: _compile(*sf), srcs))
     tmp = lib_path + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # hipBLASLt: the dense GEMMs over resident matrices (exl3_dense.cpp)
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lhipblaslt", "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)

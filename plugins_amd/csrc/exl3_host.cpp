@@ -14,7 +14,9 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
+#include <set>
 #include <string>
 #include <utility>
 #include <vector>
@@ -22,6 +24,7 @@
 #include "../../include/exl3_decoder.h"
 #include "../../include/exl3_mi355x.h"
 #include "exl3_codebooks.h"
+#include "exl3_dense.h"
 #include "exl3_json.h"
 #include "exl3_kernels.h"
 
@@ -94,12 +97,36 @@ bool n_ok(int64_t n) { return n >= 16 && n <= 128 && n % 2 == 0; }
 
 // ------------------------------------------------------------- weights
 
+// A group of un-rotated resident matrices joined side by side:
+// [in, cols] in the activation dtype `act` (mlx code), member m's columns
+// starting at its `col`.
+struct WeightPriv;
+struct Joined {
+  void *data = nullptr;
+  int act = 0;
+  int64_t in = 0, cols = 0;
+  int device = 0;
+  std::vector<WeightPriv *> members;
+};
+
+// A linear's resident state (QuantTable.resident, quant.zig:96-107):
+// admitted by exl3_resident; its decoded matrix W_inner f16 [in, out] held
+// from its first prefill call on, or, once un-rotated, its columns of a
+// joined public matrix.
+struct ResidentState {
+  bool admitted = false;
+  uint16_t *inner = nullptr;
+  std::shared_ptr<Joined> joined;
+  int64_t col = 0;
+};
+
 struct WeightPriv {
   Format f;
   int64_t in = 0, out = 0, experts = 0;  // experts = 0: a single linear
   int64_t groups = 0;  // a grouped linear: `experts` banks, x [..., groups, in]
   int device = 0;
   bool borrowed = false;
+  ResidentState res;
 };
 
 WeightPriv *priv_of(const exl3_weight *w) {
@@ -488,9 +515,112 @@ exl3_verdict exl3_load_bank(const exl3_load_ctx *ctx, exl3_str name, uint32_t in
   return load_parts(ctx, ps, true, out);
 }
 
+// ------------------------------------------------------ resident matrices
+
+// The weights exl3_resident admitted (quant.zig:96-107: `resident`,
+// `resident_pending`, `unrotate`, `linear_joined`).  Memory for speed at
+// prefill widths: a held W_inner f16 makes the matmul a prepare, a dense f16
+// GEMM (hipBLASLt) and the finish; an un-rotated group's public matrix makes
+// it one dense GEMM in the activation dtype.  Decode widths keep the EXL3
+// GEMV, which reads 2 to 8 times fewer bytes.
+static std::mutex g_res_mu;
+static std::set<WeightPriv *> g_resident;
+
+static uint64_t resident_bytes(const WeightPriv *pv) { return (uint64_t)pv->in * pv->out * 2; }
+
+// Frees what pv holds (its decoded matrix; its place in a joined group, the
+// group's matrix with its last member).  The device finishes its queued work
+// first: a kept matrix may be read by any stream.  Caller holds g_res_mu.
+static void resident_drop(WeightPriv *pv) {
+  ResidentState &r = pv->res;
+  if (r.inner || r.joined) {
+    (void)hipSetDevice(pv->device);
+    (void)hipDeviceSynchronize();
+  }
+  if (r.inner) (void)hipFree(r.inner);
+  r.inner = nullptr;
+  if (r.joined) {
+    auto &m = r.joined->members;
+    m.erase(std::remove(m.begin(), m.end(), pv), m.end());
+    if (m.empty() && r.joined->data) {
+      (void)hipFree(r.joined->data);
+      r.joined->data = nullptr;
+    }
+    r.joined.reset();
+  }
+  r.col = 0;
+  r.admitted = false;
+}
+
+// Holds pv's decoded matrix (decode_matrix into a new buffer on s).  Not
+// under graph capture (the allocation cannot be captured).
+static hipError_t resident_hold(const exl3_weight *w, WeightPriv *pv, hipStream_t s) {
+  if (pv->res.inner) return hipSuccess;
+  if (capturing(s)) return hipErrorStreamCaptureUnsupported;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, resident_bytes(pv));
+  if (e != hipSuccess) return e;
+  e = exl3::launch_decode_matrix((const uint16_t *)w->w.data, pv->f, (int)pv->in, (int)pv->out,
+                                 (uint16_t *)p, s);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return e;
+  }
+  pv->res.inner = (uint16_t *)p;
+  return hipSuccess;
+}
+
+// The matmul of an admitted weight at prefill widths through its resident
+// matrix.  *taken false: the EXL3 kernels serve the call (not admitted, or
+// an un-rotated matrix in another dtype than x's, or the first call under
+// graph capture).
+static hipError_t resident_matmul(const exl3_weight *w, WeightPriv *pv, const exl3_array &x,
+                                  int xdt, int64_t rows, void *y, StreamScratch *ss, hipStream_t s,
+                                  bool *taken) {
+  *taken = false;
+  std::lock_guard<std::mutex> g(g_res_mu);
+  ResidentState &r = pv->res;
+  if (!r.admitted) return hipSuccess;
+  if (r.joined) {
+    if (r.joined->act != x.dtype) return hipSuccess;
+    *taken = true;
+    const char *wj = (const char *)r.joined->data + (size_t)r.col * dt_size(x.dtype);
+    return exl3::dense_gemm(x.data, xdt, wj, r.joined->cols, y, xdt, rows, pv->in, pv->out, s);
+  }
+  hipError_t e = resident_hold(w, pv, s);
+  if (e == hipErrorStreamCaptureUnsupported) return hipSuccess;
+  if (e != hipSuccess) return e;
+  *taken = true;
+  const size_t xp_bytes = ((size_t)rows * pv->in * 2 + 255) & ~(size_t)255;
+  e = grow(ss, &ss->xp, &ss->xp_bytes, xp_bytes + (size_t)rows * pv->out * 2, s);
+  if (e != hipSuccess) return e;
+  uint16_t *xp = (uint16_t *)ss->xp;
+  uint16_t *z = (uint16_t *)((char *)ss->xp + xp_bytes);
+  const size_t xsz = dt_size(x.dtype);
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+    const int n = (int)std::min<int64_t>(65535, rows - r0);
+    e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * pv->in * xsz, xdt,
+                             (const uint16_t *)w->scales.data, xp + (size_t)r0 * pv->in, n,
+                             (int)pv->in, s);
+  }
+  if (e == hipSuccess)
+    e = exl3::dense_gemm(xp, exl3::DENSE_F16, r.inner, pv->out, z, exl3::DENSE_F16, rows, pv->in,
+                         pv->out, s);
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += 65535) {
+    const int n = (int)std::min<int64_t>(65535, rows - r0);
+    e = exl3::launch_finish(z + (size_t)r0 * pv->out, (const uint16_t *)w->biases.data,
+                            (char *)y + (size_t)r0 * pv->out * xsz, xdt, n, (int)pv->out, s);
+  }
+  return e;
+}
+
 void exl3_release(exl3_weight *w) {
   if (!w) return;
   WeightPriv *pv = priv_of(w);
+  if (pv) {
+    std::lock_guard<std::mutex> g(g_res_mu);
+    if (g_resident.erase(pv)) resident_drop(pv);
+  }
   if (pv && !pv->borrowed) free_weight_arrays(w);
   delete pv;
   std::memset(w, 0, sizeof(*w));
@@ -749,6 +879,13 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
+  if (rows > exl3::GEMV_ROWS_MAX && pv->res.admitted) {
+    bool taken = false;
+    hipError_t e = resident_matmul(w, const_cast<WeightPriv *>(pv), x, xdt, rows, out->data, ss,
+                                   s, &taken);
+    if (e != hipSuccess) return hip_failed(e);
+    if (taken) return ok();
+  }
   hipError_t e = run_linear(w, pv, x.data, xdt, false, out->data, xdt, nullptr, rows, ss, s);
   if (e != hipSuccess) return hip_failed(e);
   return ok();
@@ -1500,6 +1637,170 @@ const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
                                                                               : "routed-gemv";
 }
 
+// QuantTable.resident (quant.zig:98-99): admits ws' single linears, whose
+// decoded matrices (W_inner f16, in * out * 2 bytes each) are then held from
+// each one's first prefill-width matmul on; *bytes = what ws' matrices take.
+// Refused too_large past room (0: no bound), admitting none of them; an
+// empty ws drops every kept matrix.
+exl3_verdict exl3_resident(exl3_weight_span ws, uint64_t room, exl3_stream stream,
+                           uint64_t *bytes) {
+  (void)stream;
+  if (!bytes || (ws.len && !ws.ptr)) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  std::lock_guard<std::mutex> g(g_res_mu);
+  if (ws.len == 0) {
+    for (WeightPriv *pv : g_resident) resident_drop(pv);
+    g_resident.clear();
+    *bytes = 0;
+    return ok();
+  }
+  uint64_t total = 0;
+  for (size_t i = 0; i < ws.len; ++i) {
+    const WeightPriv *pv = single_linear(&ws.ptr[i]);
+    if (!pv)
+      return refuse(EXL3_UNSUPPORTED,
+                    "turboexl3_mi355x: resident matrices are kept for single linears (banks run "
+                    "through swiglu)");
+    total += resident_bytes(pv);
+  }
+  if (room != 0 && total > room)
+    return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: the decoded matrices exceed room");
+  for (size_t i = 0; i < ws.len; ++i) {
+    WeightPriv *pv = priv_of(&ws.ptr[i]);
+    pv->res.admitted = true;
+    g_resident.insert(pv);
+  }
+  *bytes = total;
+  return ok();
+}
+
+// QuantTable.resident_pending (quant.zig:100-101): the bytes admitted and
+// not held yet.
+uint64_t exl3_resident_pending(void) {
+  std::lock_guard<std::mutex> g(g_res_mu);
+  uint64_t n = 0;
+  for (const WeightPriv *pv : g_resident)
+    if (pv->res.admitted && !pv->res.inner && !pv->res.joined) n += resident_bytes(pv);
+  return n;
+}
+
+// QuantTable.unrotate (quant.zig:102-104): ws in groups of sizes[g] weights
+// that read one input; each group's resident matrices become one public
+// matrix [in, sum of outs] in `act`, members side by side in their order
+// (W_public = diag(suh) H W_inner H diag(svh) / 128, the reference's
+// reconstructPublic order), and each member's W_inner is freed.  took[g]:
+// whether group g took -- its members admitted single linears of one input
+// width and device, not yet in another group (a group already joined as
+// asked takes again).  Members not yet held are decoded first.
+exl3_verdict exl3_unrotate(exl3_weight_span ws, exl3_u8_span sizes, int32_t act,
+                           exl3_stream stream, bool *took) {
+  if ((ws.len && !ws.ptr) || (sizes.len && (!sizes.ptr || !took)))
+    return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  const int kact = act_of(act);
+  if (kact < 0) return kDtype;
+  size_t n = 0;
+  for (size_t g = 0; g < sizes.len; ++g) n += sizes.ptr[g];
+  if (n != ws.len) return kShape;
+  hipStream_t s = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lk(g_res_mu);
+  size_t off = 0;
+  for (size_t g = 0; g < sizes.len; off += sizes.ptr[g], ++g) {
+    took[g] = false;
+    const size_t m = sizes.ptr[g];
+    if (m == 0) continue;
+    std::vector<WeightPriv *> mem;
+    bool fit = true;
+    int64_t cols = 0;
+    for (size_t i = 0; i < m && fit; ++i) {
+      WeightPriv *pv = priv_of(&ws.ptr[off + i]);
+      fit = single_linear(&ws.ptr[off + i]) && pv->res.admitted && pv->in == priv_of(&ws.ptr[off])->in &&
+            pv->device == priv_of(&ws.ptr[off])->device;
+      if (fit) {
+        mem.push_back(pv);
+        cols += pv->out;
+      }
+    }
+    if (!fit) continue;
+    // already this group, in this dtype: it takes again
+    const std::shared_ptr<Joined> j0 = mem[0]->res.joined;
+    if (j0 && j0->act == act && j0->members == mem) {
+      took[g] = true;
+      continue;
+    }
+    bool free_members = true;
+    for (WeightPriv *pv : mem) free_members = free_members && !pv->res.joined;
+    if (!free_members) continue;
+    if (hipSetDevice(mem[0]->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; i < m && e == hipSuccess; ++i) e = resident_hold(&ws.ptr[off + i], mem[i], s);
+    if (e != hipSuccess) return hip_failed(e);
+    auto j = std::make_shared<Joined>();
+    j->act = act;
+    j->in = mem[0]->in;
+    j->cols = cols;
+    j->device = mem[0]->device;
+    e = hipMalloc(&j->data, (size_t)j->in * cols * dt_size(act));
+    if (e != hipSuccess) return hip_failed(e);
+    int64_t col = 0;
+    for (size_t i = 0; i < m && e == hipSuccess; ++i) {
+      const exl3_weight &w = ws.ptr[off + i];
+      e = exl3::launch_unrotate(mem[i]->res.inner, (const uint16_t *)w.scales.data,
+                                (const uint16_t *)w.biases.data, (int)j->in, (int)mem[i]->out,
+                                (char *)j->data + (size_t)col * dt_size(act), cols, kact, s);
+      col += mem[i]->out;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      (void)hipFree(j->data);
+      return hip_failed(e);
+    }
+    col = 0;
+    for (WeightPriv *pv : mem) {
+      (void)hipFree(pv->res.inner);
+      pv->res.inner = nullptr;
+      pv->res.joined = j;
+      pv->res.col = col;
+      col += pv->out;
+    }
+    j->members = mem;
+    took[g] = true;
+  }
+  return ok();
+}
+
+// QuantTable.linear_joined (quant.zig:105-107): x [..., in] times the joined
+// public matrix of the un-rotated group whose members are ws, in order:
+// [..., sum of outs] in x's dtype (the group's `act`).  Refused where the
+// members are not such a group (not un-rotated, another order, a part of
+// one) and at decode widths (up to 16 rows: the EXL3 GEMV serves them).
+exl3_verdict exl3_linear_joined(exl3_weight_span ws, exl3_array x, exl3_stream stream,
+                                exl3_array *out) {
+  if (!out || ws.len == 0 || !ws.ptr) return refuse(EXL3_FAILED, "turboexl3_mi355x: null argument");
+  std::shared_ptr<Joined> j;
+  {
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    j = priv_of(&ws.ptr[0]) ? priv_of(&ws.ptr[0])->res.joined : nullptr;
+    bool same = j && j->members.size() == ws.len;
+    for (size_t i = 0; same && i < ws.len; ++i) same = priv_of(&ws.ptr[i]) == j->members[i];
+    if (!same)
+      return refuse(EXL3_UNSUPPORTED,
+                    "turboexl3_mi355x: linear_joined takes an un-rotated group's members in order");
+  }
+  const int xdt = act_of(x.dtype);
+  if (xdt < 0 || x.dtype != j->act) return kDtype;
+  if (x.ndim < 1 || !x.data || x.shape[x.ndim - 1] != j->in) return kShape;
+  const int64_t rows = numel(x) / j->in;
+  if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
+  if (rows <= exl3::GEMV_ROWS_MAX)
+    return refuse(EXL3_UNSUPPORTED,
+                  "turboexl3_mi355x: linear_joined at decode widths (the EXL3 GEMV serves them)");
+  if (hipSetDevice(j->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  exl3_verdict v = output_for(out, x, j->cols, rows);
+  if (v.code != EXL3_OK) return v;
+  const hipError_t e = exl3::dense_gemm(x.data, xdt, j->data, j->cols, out->data, xdt, rows, j->in,
+                                        j->cols, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : hip_failed(e);
+}
+
 static exl3_verdict register_kernels(const void *host) {
   (void)host;
   return ok();
@@ -1534,10 +1835,10 @@ static const exl3_quant_table kTable = {
     nullptr,  // q_planes
     nullptr,  // indexer
     &exl3_swiglu_shared,
-    nullptr,  // resident: the GEMM decodes in LDS, kept decoded matrices do not pay
-    nullptr,  // resident_pending
-    nullptr,  // unrotate
-    nullptr,  // linear_joined
+    &exl3_resident,
+    &exl3_resident_pending,
+    &exl3_unrotate,
+    &exl3_linear_joined,
 };
 
 const exl3_quant_table *exl3_quant_table_get(void) { return &kTable; }

@@ -94,6 +94,11 @@ hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int yd
 hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in, int out,
                                 uint16_t *w, hipStream_t s);
 
+// un-rotation: W_inner f16 [in, out] -> W_public [in, out] in ydt (ACT_*),
+// rows ld elements apart, in the reference's reconstructPublic order.
+hipError_t launch_unrotate(const uint16_t *w_inner, const uint16_t *suh, const uint16_t *svh,
+                           int in, int out, void *dst, int64_t ld, int ydt, hipStream_t s);
+
 // The GEMV split: whole 128-input blocks per split (ksplit splits of tps
 // k-tile rows) for a GEMV over `groups` weights of (in, out).
 // tps_max: the most k-tiles a split takes (dense GEMV 64, MoE items 128).

@@ -271,6 +271,98 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
   }
 }
 
+// ------------------------------------------------------------ un-rotation
+
+// W_public = diag(suh) H W_inner H diag(svh) / 128 per 128 x 128 block, in
+// the reference's order (sushi_ds41/src/sushi/exl3/expert_exl3.zig:440-488,
+// `reconstructPublic`): the dense Hadamard over the input index of every
+// column (out[r] = sum_k e(r,k) * v[k], e = +-HAD_SCALE by the parity of
+// r & k, products and sums in f32 in k order), times suh per row, the dense
+// Hadamard over the output index of every row, times svh per column, then
+// one rounding to the output type (f16: the reference's value bit for bit).
+// e * v is +-(HAD_SCALE * v) exactly and acc + (-p) is acc - p, so each term
+// is the scaled value added or subtracted.  A thread keeps 8 sums: rows (or
+// columns) o0 + i, i < 8, o0 a multiple of 8, whose sign for k = k8 + j is
+// parity(o0 & k8) ^ parity(i & j) -- the second term fixed at compile time.
+constexpr int UNROT_THREADS = 256;
+constexpr int UNROT_LD = 129;  // padded LDS row (floats)
+
+__device__ __forceinline__ void unrot_eight(const float *hv, int stride, int o0, float (&acc)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int k8 = 0; k8 < 128; k8 += 8) {
+    const uint32_t flip = (uint32_t)(__builtin_popcount((unsigned)(o0 & k8)) & 1) << 31;
+    static_for<8>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const float p = bits<float>(bits<uint32_t>(hv[(k8 + j) * stride]) ^ flip);
+      static_for<8>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (__builtin_popcount(i & j) & 1)
+          acc[i] = acc[i] - p;
+        else
+          acc[i] = acc[i] + p;
+      });
+    });
+  }
+}
+
+__global__ __launch_bounds__(UNROT_THREADS) void unrotate_kernel(
+    const uint16_t *__restrict__ w, const uint16_t *__restrict__ suh,
+    const uint16_t *__restrict__ svh, void *__restrict__ dst, int out, int64_t ld, int ydt) {
+  __shared__ __attribute__((aligned(16))) float lds[2 * 128 * UNROT_LD];  // 129 KiB
+  float *A = lds;                    // HAD_SCALE * W_inner block [k][c]
+  float *B = lds + 128 * UNROT_LD;   // HAD_SCALE * (column Hadamard * suh) [r][k]
+  const int tid = threadIdx.x;
+  const int rb = blockIdx.y * 128, cb = blockIdx.x * 128;
+  for (int e = tid; e < 128 * 128; e += UNROT_THREADS) {
+    const int r = e >> 7, c = e & 127;
+    A[r * UNROT_LD + c] = f32_value(HAD_SCALE * h2f(w[(size_t)(rb + r) * out + cb + c]));
+  }
+  __syncthreads();
+  {
+    // input-index Hadamard: column c, rows o0 .. o0 + 7 at a time
+    const int c = tid & 127;
+    for (int o0 = (tid >> 7) * 8; o0 < 128; o0 += 16) {
+      float acc[8];
+      unrot_eight(A + c, UNROT_LD, o0, acc);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = f32_value(acc[i] * h2f(suh[rb + o0 + i]));
+        B[(o0 + i) * UNROT_LD + c] = f32_value(HAD_SCALE * v);
+      }
+    }
+  }
+  __syncthreads();
+  {
+    // output-index Hadamard: row r, columns o0 .. o0 + 7 at a time
+    const int r = tid & 127;
+    for (int o0 = (tid >> 7) * 8; o0 < 128; o0 += 16) {
+      float acc[8];
+      unrot_eight(B + r * UNROT_LD, 1, o0, acc);
+      const size_t base = (size_t)(rb + r) * ld + cb + o0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = f32_value(acc[i] * h2f(svh[cb + o0 + i]));
+        if (ydt == OUT_F16)
+          ((uint16_t *)dst)[base + i] = f2h(v);
+        else if (ydt == OUT_BF16)
+          ((uint16_t *)dst)[base + i] = f2bf(v);
+        else
+          ((float *)dst)[base + i] = v;
+      }
+    }
+  }
+}
+
+hipError_t launch_unrotate(const uint16_t *w_inner, const uint16_t *suh, const uint16_t *svh,
+                           int in, int out, void *dst, int64_t ld, int ydt, hipStream_t s) {
+  if (in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0 || ld < out) return hipErrorInvalidValue;
+  if (in / 128 > 65535 || ydt < OUT_F16 || ydt > OUT_F32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(unrotate_kernel, dim3(out / 128, in / 128), dim3(UNROT_THREADS), 0, s, w_inner,
+                     suh, svh, dst, out, ld, ydt);
+  return hipGetLastError();
+}
+
 // k-splits of a GEMV: whole input Hadamard blocks per split, at most
 // GEMV_TPS_MAX k-tile rows (32 for the generic rate) and GEMV_KSPLIT_MAX
 // splits, ~512 workgroups over `groups` column groups; ~256 for more than 4

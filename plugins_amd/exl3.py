@@ -104,6 +104,14 @@ class U32Span(Structure):
     _fields_ = [("ptr", POINTER(c_uint32)), ("len", c_size_t)]
 
 
+class U8Span(Structure):
+    _fields_ = [("ptr", POINTER(ctypes.c_uint8)), ("len", c_size_t)]
+
+
+class WeightSpan(Structure):
+    _fields_ = [("ptr", POINTER(Weight)), ("len", c_size_t)]
+
+
 class LinearParts(Structure):
     """`LinearParts` (quant.zig:111-128), the split entries' options."""
     _fields_ = [("size", c_uint32), ("dtype", c_int32), ("side", c_void_p), ("inner", c_bool),
@@ -174,6 +182,10 @@ SIGNATURES = {
                                     POINTER(Array)]),
     "exl3_swiglu_shared": (Verdict, [POINTER(Weight), POINTER(Weight), POINTER(Weight), Array, Array,
                                      Array, POINTER(SharedSwiglu), c_void_p, POINTER(Array)]),
+    "exl3_resident": (Verdict, [WeightSpan, c_uint64, c_void_p, POINTER(c_uint64)]),
+    "exl3_resident_pending": (c_uint64, []),
+    "exl3_unrotate": (Verdict, [WeightSpan, U8Span, c_int32, c_void_p, POINTER(c_bool)]),
+    "exl3_linear_joined": (Verdict, [WeightSpan, Array, c_void_p, POINTER(Array)]),
 }
 
 _lib = None
@@ -613,6 +625,49 @@ def linear_piece(w: Weight, x, held: Array, prepared: bool = False, stream=None)
     a = Array()
     check(lib().exl3_linear_piece(ctypes.byref(w), array(x), ctypes.byref(o),
                                   stream_handle(stream), ctypes.byref(a)), "linear_piece")
+    return take(a, stream)
+
+
+def _weight_span(ws) -> tuple[WeightSpan, object]:
+    arr = (Weight * len(ws))(*ws)
+    return WeightSpan(arr, len(ws)), arr
+
+
+def resident(ws, room: int = 0, stream=None) -> int:
+    """QuantTable.resident: admits the weights' decoded matrices (held from each
+    one's first prefill-width matmul on); returns the bytes they take.  An
+    empty list drops every kept matrix."""
+    span, keep = _weight_span(list(ws))
+    n = c_uint64(0)
+    check(lib().exl3_resident(span, room, stream_handle(stream), ctypes.byref(n)), "resident")
+    del keep
+    return n.value
+
+
+def resident_pending() -> int:
+    """QuantTable.resident_pending: bytes admitted and not held yet."""
+    return lib().exl3_resident_pending()
+
+
+def unrotate(ws, sizes, act: int = DT_F16, stream=None) -> list[bool]:
+    """QuantTable.unrotate: each group of sizes[g] weights (one input) joined
+    as one public matrix in `act`; returns took[g]."""
+    span, keep = _weight_span(list(ws))
+    sz = (ctypes.c_uint8 * len(sizes))(*sizes)
+    took = (c_bool * max(1, len(sizes)))()
+    check(lib().exl3_unrotate(span, U8Span(sz, len(sizes)), act, stream_handle(stream), took),
+          "unrotate")
+    del keep
+    return [bool(took[i]) for i in range(len(sizes))]
+
+
+def linear_joined(ws, x, stream=None):
+    """QuantTable.linear_joined: x times an un-rotated group's joined matrix."""
+    span, keep = _weight_span(list(ws))
+    a = Array()
+    check(lib().exl3_linear_joined(span, array(x), stream_handle(stream), ctypes.byref(a)),
+          "linear_joined")
+    del keep
     return take(a, stream)
 
 

@@ -36,13 +36,38 @@ def test_quant_table_fields():
     assert ctypes.string_at(t.name.ptr, t.name.len) == b"turboexl3_mi355x"
     served = ("claims", "validate", "bill", "open", "close", "load_tensor", "load_bank", "release",
               "matmul", "moe", "register_kernels", "swiglu", "linear_split", "linear_finish",
-              "linear_prepared", "linear_pieces", "linear_piece", "swiglu_shared")
+              "linear_prepared", "linear_pieces", "linear_piece", "swiglu_shared", "resident",
+              "resident_pending", "unrotate", "linear_joined")
     for f in X.TABLE_ENTRIES:
         assert bool(getattr(t, f)) == (f in served), f
     # the table's pointers are the flat symbols
     assert t.matmul == ctypes.cast(X.lib().exl3_matmul, ctypes.c_void_p).value
     assert t.linear_split == ctypes.cast(X.lib().exl3_linear_split, ctypes.c_void_p).value
     assert t.linear_piece == ctypes.cast(X.lib().exl3_linear_piece, ctypes.c_void_p).value
+    assert t.linear_joined == ctypes.cast(X.lib().exl3_linear_joined, ctypes.c_void_p).value
+
+
+def test_resident_entries_refuse_on_the_host():
+    """The resident entries' argument checks run before any device call
+    (quant.zig:96-107): an empty span drops nothing held and admits nothing,
+    a dtype that is not an activation dtype is refused by name, a span that
+    is not an un-rotated group is refused."""
+    L = X.lib()
+    n = ctypes.c_uint64(7)
+    v = L.exl3_resident(X.WeightSpan(None, 0), 0, None, ctypes.byref(n))
+    assert v.code == X.OK and n.value == 0
+    assert L.exl3_resident(X.WeightSpan(None, 0), 0, None, None).code == X.FAILED
+    assert L.exl3_resident_pending() == 0
+    took = (ctypes.c_bool * 1)()
+    v = L.exl3_unrotate(X.WeightSpan(None, 0), X.U8Span(None, 0), X.DT_I32, None, took)
+    assert v.code == X.UNSUPPORTED and "BadExl3Dtype" in v.reason
+    sizes = (ctypes.c_uint8 * 1)(2)
+    v = L.exl3_unrotate(X.WeightSpan(None, 0), X.U8Span(sizes, 1), X.DT_F16, None, took)
+    assert v.code == X.UNSUPPORTED and "BadExl3Shape" in v.reason
+    w = (X.Weight * 1)()
+    out = X.Array()
+    v = L.exl3_linear_joined(X.WeightSpan(w, 1), X.Array(), None, ctypes.byref(out))
+    assert v.code == X.UNSUPPORTED and "linear_joined" in v.reason
 
 
 def test_table_entry_order_matches_the_reference_layout():
