@@ -43,10 +43,9 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
                        float theta, uint16_t *qout, uint16_t *kcache, uint16_t *vcache, int Tmax,
                        hipStream_t s);
 
-/* Scratch bytes exl3d_attn_decode(_rope) needs for these sizes: split slots
- * and one arrival ticket per (row, kv head).  Zero the scratch once before
- * its first use; every call leaves the tickets zero again.  Calls that share
- * a scratch must be ordered on one stream. */
+/* Scratch bytes exl3d_attn_decode(_rope) needs for these sizes: the split
+ * slots (each split's softmax state), which the call's combine launch reads.
+ * Calls that share a scratch must be ordered on one stream. */
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax);
 
 /* Decode attention, grouped-query (nq = 4 nkv): out [B][nq*D] f16 =

@@ -163,16 +163,26 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   dst[lane + HALF] = f2h(y1);
 }
 
-// Agent-scope (all XCDs) accesses for the split hand-off, through the global
-// address space.
-typedef __attribute__((address_space(1))) float gf32_t;
-typedef __attribute__((address_space(1))) uint32_t gu32_t;
-__device__ __forceinline__ void st_agent(float *p, float v) {
-  __hip_atomic_store((gf32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-  return __hip_atomic_load((gf32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// The attention's phase timeline of a diagnostic build (EXL3_TIMELINE): lane
+// 0 of each wave stores the 100 MHz real-time counter at each phase,
+// [workgroup][wave][event], for the first ATL_WGS workgroups of a launch.
+// Events: 0 entry, 1 q ready (after the q/k prologue), 2 key loop done, 3
+// states merged, 4 the split's slot stored.  A product build compiles them
+// out.
+#ifdef EXL3_TIMELINE
+constexpr int ATL_WGS = 1024;
+__device__ unsigned long long g_attn_tl[ATL_WGS * 4 * 8];
+#define ATL(k)                                                                            \
+  do {                                                                                    \
+    const size_t wg_ = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z); \
+    if ((threadIdx.x & 63) == 0 && wg_ < ATL_WGS)                                         \
+      g_attn_tl[(wg_ * 4 + (threadIdx.x >> 6)) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define ATL(k) \
+  do {         \
+  } while (0)
+#endif
 
 // The q/k norm + RoPE of one head's dims 8 li .. 8 li + 7 held by the 16
 // lanes of a key group (lane li): RMSNorm with weight nw (sum of squares over
@@ -246,29 +256,24 @@ struct RopeArgs {
 // key group l / 16 (four keys per wave per iteration), dims 8 (l % 16) ..
 // +7.  Online softmax per (key group, head) in f32; the 16 partial states of
 // the workgroup merge in LDS into (m, l, o[D]) per head, stored in the
-// split's slot.  TICKET: the split that arrives last at the (row, kv head)'s
-// ticket (all other slots are then stored) combines the slots in split
-// order: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16, and
-// resets the ticket; else attn_combine_kernel does, as its own launch.
+// split's slot; attn_combine_kernel, its own launch, combines the slots.
+// (The kernel boundary is the hand-off: having the last-arriving split
+// combine behind an agent-scope ticket measured ~1 us a layer slower at
+// batch 1, its atomic and coherent loads each a round trip.)
 // ROPE: q arrives raw; every workgroup applies the q norm and RoPE to its
 // heads, and the workgroup of the split holding key pos[b] also normalizes,
 // rotates and appends that key (and copies the value) into the caches first.
 constexpr int AT_G = 4;  // query heads per kv head (Qwen3-8B: 32 / 8)
 constexpr int AC_MAXS = 256;  // splits
 constexpr int AT_KD = 4;  // key rows in flight per key group
-constexpr int AT_CB = 48;  // splits whose o pairs the combine loads at once
-static_assert(AT_G == 256 / 64, "the combine gives each head one wave of the workgroup");
 
-template <bool ROPE, bool TICKET>
+template <bool ROPE>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t *__restrict__ q, uint16_t *__restrict__ kcache, uint16_t *__restrict__ vcache,
     const int32_t *__restrict__ pos, int nq, int nkv, int Tmax, int TS, float scale, RopeArgs ra,
-    float *__restrict__ part, uint32_t *__restrict__ tickets, uint16_t *__restrict__ out) {
+    float *__restrict__ part) {
   constexpr int D = EXL3D_HEAD_DIM;
   __shared__ float sm[16][AT_G][D + 2];
-  __shared__ float wsh[AT_G][AC_MAXS];
-  __shared__ float lsum[AT_G];
-  __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -276,6 +281,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int L = p + 1;
   const int t0 = s * TS, t1 = min(t0 + TS, L);
   const int nsplit = gridDim.x;
+  ATL(0);
   float qr[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h)
@@ -299,6 +305,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     vr[j] = ld(vcache, min(tg + 16 * j, Tmax - 1));
   }
   if constexpr (ROPE) {
+    // the norm weights, and the new key and value the split holding key
+    // pos[b] appends, loaded with the keys (before any wait)
+    const uint4 qn = *reinterpret_cast<const uint4 *>(ra.qn + 8 * li);
+    const uint4 kn = *reinterpret_cast<const uint4 *>(ra.kn + 8 * li);
+    const bool appends = s == p / TS;
+    const size_t kvrow = ((size_t)b * nkv + kvh) * D + 8 * li;
+    uint4 kraw = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+    if (appends) {
+      kraw = *reinterpret_cast<const uint4 *>(ra.k + kvrow);
+      vnew = *reinterpret_cast<const uint4 *>(ra.v + kvrow);
+    }
     // angle of dim d: pos * theta^(-2 (d mod 64) / D), the 64 angles once
     // per workgroup (the argument reaches thousands of radians, where a sine
     // costs a long reduction)
@@ -315,15 +332,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       sn[e] = sc_sn[i];
       cs[e] = sc_cs[i];
     }
-    const uint4 qn = *reinterpret_cast<const uint4 *>(ra.qn + 8 * li);
 #pragma unroll
     for (int h = 0; h < AT_G; ++h) norm_rope8(qr[h], qn, sn, cs, li, ra.eps);
-    if (s == p / TS) {
+    if (appends) {
       float kx[8];
-      unpack8(*reinterpret_cast<const uint4 *>(ra.k + ((size_t)b * nkv + kvh) * D + 8 * li), kx);
-      const uint4 vnew =
-          *reinterpret_cast<const uint4 *>(ra.v + ((size_t)b * nkv + kvh) * D + 8 * li);
-      norm_rope8(kx, *reinterpret_cast<const uint4 *>(ra.kn + 8 * li), sn, cs, li, ra.eps);
+      unpack8(kraw, kx);
+      norm_rope8(kx, kn, sn, cs, li, ra.eps);
       const uint4 knew = pack8(kx);
       if (wave == 0 && g == 0) {
         *reinterpret_cast<uint4 *>(kcache + (kvbase + p) * D + 8 * li) = knew;
@@ -345,6 +359,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   for (int h = 0; h < AT_G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qr[h][e] *= scale;
+  ATL(1);
   float m[AT_G], l[AT_G], o[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h) {
@@ -354,36 +369,58 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
   }
   if (t0 < t1) {
+    // AT_KD keys of the key group at a time: their AT_KD x AT_G scores are
+    // independent (formed side by side), then one online-softmax update per
+    // head takes all of them (keys past the split's end score -inf and weigh
+    // 0; the first key of a block is always in range, so the new maximum is
+    // finite)
     for (int tb = tg; tb < t1; tb += 16 * AT_KD) {
+      float sc[AT_KD][AT_G], vf[AT_KD][8];
 #pragma unroll
       for (int j = 0; j < AT_KD; ++j) {
         const int t = tb + 16 * j;
-        if (t < t1) {
-          float kf[8], vf[8];
-          unpack8(kr[j], kf);
-          unpack8(vr[j], vf);
-          const int tn = min(t + 16 * AT_KD, t1 - 1);
-          kr[j] = ld(kcache, tn);
-          vr[j] = ld(vcache, tn);
+        float kf[8];
+        unpack8(kr[j], kf);
+        unpack8(vr[j], vf[j]);
+        const int tn = min(t + 16 * AT_KD, t1 - 1);
+        kr[j] = ld(kcache, tn);
+        vr[j] = ld(vcache, tn);
 #pragma unroll
-          for (int h = 0; h < AT_G; ++h) {
-            // fused multiply-adds (this op's own arithmetic, not the
-            // reference's rounding points)
-            float sc = 0.0f;
+        for (int h = 0; h < AT_G; ++h) {
+          // fused multiply-adds (this op's own arithmetic, not the
+          // reference's rounding points)
+          float d = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sc = fmaf(qr[h][e], kf[e], sc);
-            sc = row16_sum(sc);
-            const float mn = fmaxf(m[h], sc);
-            const float c = __expf(m[h] - mn), pr = __expf(sc - mn);
-            l[h] = fmaf(l[h], c, pr);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pr, vf[e], o[h][e] * c);
-            m[h] = mn;
-          }
+          for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], kf[e], d);
+          sc[j][h] = row16_sum(d);
+          if (t >= t1) sc[j][h] = -INFINITY;
         }
+      }
+#pragma unroll
+      for (int h = 0; h < AT_G; ++h) {
+        float mn = m[h];
+#pragma unroll
+        for (int j = 0; j < AT_KD; ++j) mn = fmaxf(mn, sc[j][h]);
+        const float c = __expf(m[h] - mn);
+        float pr[AT_KD], ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < AT_KD; ++j) {
+          pr[j] = __expf(sc[j][h] - mn);
+          ps += pr[j];
+        }
+        l[h] = fmaf(l[h], c, ps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float a = o[h][e] * c;
+#pragma unroll
+          for (int j = 0; j < AT_KD; ++j) a = fmaf(pr[j], vf[j][e], a);
+          o[h][e] = a;
+        }
+        m[h] = mn;
       }
     }
   }
+  ATL(2);
   // merge the 16 states (4 waves x 4 key groups) per head
   const int st = wave * 4 + g;
 #pragma unroll
@@ -409,98 +446,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       a1 += sm[i][h][d + 1] * f;
     }
   }
+  ATL(3);
   const size_t sstride = (size_t)AT_G * (D + 2);
   float *slots = part + ((size_t)b * nkv + kvh) * nsplit * sstride;
   float *dst = slots + s * sstride + h * (D + 2);
-  if constexpr (!TICKET) {  // attn_combine_kernel follows
-    dst[d] = a0;
-    dst[d + 1] = a1;
-    if (d == 0) {
-      dst[D] = M;
-      dst[D + 1] = Ls;
-    }
-    return;
-  }
-  st_agent(dst + d, a0);
-  st_agent(dst + d + 1, a1);
+  dst[d] = a0;
+  dst[d + 1] = a1;
   if (d == 0) {
-    st_agent(dst + D, M);
-    st_agent(dst + D + 1, Ls);
+    dst[D] = M;
+    dst[D + 1] = Ls;
   }
-  // every wave's slot stores have completed before the ticket is taken
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t *tk = tickets + (size_t)b * nkv + kvh;
-    const uint32_t n = __hip_atomic_fetch_add((gu32_t *)tk, 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    s_last = n == (uint32_t)nsplit - 1u;
-    if (s_last) __hip_atomic_store((gu32_t *)tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // combine the splits (slots stored by other workgroups: agent-scope
-  // loads).  One round of loads: every thread's o pairs of the first
-  // AT_CB splits and the (m, l) pairs; then wave hh computes head hh's
-  // weights f_s = e^(m_s - M) and sum l_s f_s (lanes over the splits), and
-  // thread (head, d pair) sums o_s f_s in split order.
-  float(*lsh)[AC_MAXS] = reinterpret_cast<float(*)[AC_MAXS]>(&sm[0][0][0]);
-  typedef __attribute__((address_space(1))) uint64_t gu64_t;
-  auto ld_pair = [&](int ss) {
-    const float *o_s = slots + ss * sstride + h * (D + 2) + d;
-    return __hip_atomic_load((gu64_t *)o_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  uint64_t ov[AT_CB];
-#pragma unroll
-  for (int j = 0; j < AT_CB; ++j) ov[j] = ld_pair(min(j, nsplit - 1));
-  for (int i = threadIdx.x; i < AT_G * nsplit; i += blockDim.x) {
-    const int hh = i % AT_G, ss = i / AT_G;
-    const float *ml = slots + ss * sstride + hh * (D + 2) + D;
-    const float mv = ld_agent(ml), lv = ld_agent(ml + 1);
-    wsh[hh][ss] = mv;
-    lsh[hh][ss] = lv;
-  }
-  __syncthreads();
-  {
-    const int hh = wave;  // AT_G == waves per workgroup
-    float MM = -INFINITY;
-    for (int ss = lane; ss < nsplit; ss += 64) MM = fmaxf(MM, wsh[hh][ss]);
-#pragma unroll
-    for (int mk = 32; mk >= 1; mk >>= 1) MM = fmaxf(MM, __shfl_xor(MM, mk, 64));
-    float LL = 0.0f;
-    for (int ss = lane; ss < nsplit; ss += 64) {
-      const float ms = wsh[hh][ss];
-      const float f = ms == -INFINITY ? 0.0f : __expf(ms - MM);
-      LL += lsh[hh][ss] * f;
-      wsh[hh][ss] = f;
-    }
-    LL = wave_sum(LL);
-    if (lane == 0) lsum[hh] = LL;
-  }
-  __syncthreads();
-  float c0 = 0.0f, c1 = 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += AT_CB) {
-    if (s0 > 0) {
-#pragma unroll
-      for (int j = 0; j < AT_CB; ++j) ov[j] = ld_pair(min(s0 + j, nsplit - 1));
-    }
-#pragma unroll
-    for (int j = 0; j < AT_CB; ++j) {
-      if (s0 + j < nsplit) {
-        const float f = wsh[h][s0 + j];
-        c0 += __builtin_bit_cast(float, (uint32_t)ov[j]) * f;
-        c1 += __builtin_bit_cast(float, (uint32_t)(ov[j] >> 32)) * f;
-      }
-    }
-  }
-  uint16_t *op = out + ((size_t)b * nq + kvh * AT_G + h) * D + d;
-  *reinterpret_cast<uint32_t *>(op) =
-      (uint32_t)f2h(c0 / lsum[h]) | ((uint32_t)f2h(c1 / lsum[h]) << 16);
+  ATL(4);
 }
 
-// The split combine as its own launch (large grids, where holding every
-// attention workgroup through the ticket hand-off costs more than a launch):
-// out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.  One
+// The split combine, its own launch: out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.  One
 // workgroup per (row, kv head): the splits' m and l go through LDS (loaded in
 // parallel), then thread (head, d) sums its o over the splits, the loads
 // unrolled so that several are in flight.
@@ -547,6 +506,20 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
   }
 }
 
+// The device's compute units (256 on MI355X), read once per device.
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int attn_split(int Tmax, int B, int nkv, int *TS) {
   // keys per split: a power of two >= 64 (four iterations of the
   // workgroup's 16 keys), at most ~2048 workgroups overall (each is bound
@@ -555,11 +528,23 @@ int attn_split(int Tmax, int B, int nkv, int *TS) {
   int ts = 64;
   while (((long)((Tmax + ts - 1) / ts) * B * nkv > 2048 || (Tmax + ts - 1) / ts > AC_MAXS))
     ts *= 2;
+  // then whole rounds of the compute units: a second workgroup on a CU gets
+  // its data after the first's, so the few workgroups past a multiple of the
+  // CU count would finish last (at batch 1, context 2048: 33 x 8 = 264
+  // workgroups ran ~4 us behind on 8 CUs); the splits grow so the grid is
+  // the round count below it times the CUs
+  const long per = (long)B * nkv;
+  const int cus = device_cus();
+  const long wgs = (long)((Tmax + ts - 1) / ts) * per;
+  const long rounds = wgs / cus;
+  if (rounds >= 1) {
+    const long ns = rounds * cus / per;
+    if (ns >= 1 && ns < (Tmax + ts - 1) / ts) ts = (int)((Tmax + ns - 1) / ns);
+  }
   *TS = ts;
   return (Tmax + ts - 1) / ts;
 }
 
-constexpr long ATTN_TICKET_MAX_WG = 512;
 
 size_t attn_slot_floats(int B, int nkv, int ns) {
   return (size_t)B * nkv * ns * AT_G * (EXL3D_HEAD_DIM + 2);
@@ -573,23 +558,17 @@ int attn_launch(bool rope, const uint16_t *q, const RopeArgs &ra, uint16_t *kcac
   if (scratch_bytes < exl3d_attn_scratch_bytes(B, nq, nkv, Tmax)) return hipErrorInvalidValue;
   int ts;
   const int ns = attn_split(Tmax, B, nkv, &ts);
-  uint32_t *tickets = reinterpret_cast<uint32_t *>(scratch + attn_slot_floats(B, nkv, ns));
-  // small grids (decode at batch 1) combine in the last split's workgroup;
-  // large ones (every workgroup would be held through the hand-off) in a
-  // second launch
-  const bool ticket = (long)ns * nkv * B <= ATTN_TICKET_MAX_WG;
   const dim3 grid(ns, nkv, B);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, q, kcache, vcache, pos, nq, nkv, Tmax, ts,
-                       scale, ra, scratch, tickets, out);
+                       scale, ra, scratch);
   };
   if (rope)
-    ticket ? go(attn_decode_kernel<true, true>) : go(attn_decode_kernel<true, false>);
+    go(attn_decode_kernel<true>);
   else
-    ticket ? go(attn_decode_kernel<false, true>) : go(attn_decode_kernel<false, false>);
-  if (!ticket)
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s,
-                       scratch, nq, nkv, ns, out);
+    go(attn_decode_kernel<false>);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s, scratch,
+                     nq, nkv, ns, out);
   return hipGetLastError();
 }
 
@@ -629,7 +608,7 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax) {
   int ts;
   const int ns = attn_split(Tmax, B, nkv, &ts);
-  return attn_slot_floats(B, nkv, ns) * sizeof(float) + (size_t)B * nkv * sizeof(uint32_t);
+  return attn_slot_floats(B, nkv, ns) * sizeof(float);
 }
 
 int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
@@ -650,6 +629,18 @@ int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t 
   return attn_launch(true, q, ra, kcache, vcache, pos, B, nq, nkv, Tmax, scale, out, scratch,
                      scratch_bytes, s);
 }
+
+#ifdef EXL3_TIMELINE
+// The attention timeline (diagnostic build only): copy out, clear.
+int exl3d_attn_timeline_read(void *dst, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_attn_tl), bytes);
+}
+int exl3d_attn_timeline_clear(void) {
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_attn_tl));
+  return e != hipSuccess ? (int)e : (int)hipMemset(p, 0, sizeof(g_attn_tl));
+}
+#endif
 
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s) {
   if (n == 0) return hipErrorInvalidValue;
