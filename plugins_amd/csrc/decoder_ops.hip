@@ -459,41 +459,52 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   ATL(4);
 }
 
-// The split combine, its own launch: out[b][head][d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), f16.  One
-// workgroup per (row, kv head): the splits' m and l go through LDS (loaded in
-// parallel), then thread (head, d) sums its o over the splits, the loads
-// unrolled so that several are in flight.
+// The split combine, its own launch: out[b][head][d] = sum_s o_s e^(m_s - M)
+// / sum_s l_s e^(m_s - M), f16.  One workgroup per (row, kv head): the
+// splits' m and l go through LDS, each thread's o values of 32 splits at a
+// time are in flight together, and every sum runs in split order.
 __global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
     const float *__restrict__ part, int nq, int nkv, int nsplit, uint16_t *__restrict__ out) {
   constexpr int D = EXL3D_HEAD_DIM;
-  __shared__ float wsh[AT_G][AC_MAXS];
-  __shared__ float lsum[AT_G];
+  constexpr int CH = 32;  // splits whose o values a thread has in flight at once
+  __shared__ float msh[AT_G][AC_MAXS], lsh[AT_G][AC_MAXS];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int h = threadIdx.x / D, d = threadIdx.x % D;
   const float *base = part + ((size_t)b * nkv + kvh) * nsplit * AT_G * (D + 2);
   const size_t sstride = (size_t)AT_G * (D + 2);
+  // one round of loads: the first CH splits' o values of this thread, and
+  // every split's (m, l) of every head (spread over the threads)
+  float ov[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) ov[j] = base[(size_t)min(j, nsplit - 1) * sstride + h * (D + 2) + d];
   for (int i = threadIdx.x; i < AT_G * nsplit; i += AT_G * D) {
     const int hh = i % AT_G, s = i / AT_G;
-    wsh[hh][s] = base[s * sstride + hh * (D + 2) + D];
+    const float *ml = base + s * sstride + hh * (D + 2) + D;
+    msh[hh][s] = ml[0];
+    lsh[hh][s] = ml[1];
   }
   __syncthreads();
-  if (d == 0) {
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, wsh[h][s]);
-    float Ls = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = wsh[h][s];
-      const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
-      Ls += base[s * sstride + h * (D + 2) + D + 1] * f;
-      wsh[h][s] = f;
+  // out = sum_s o_s f_s / sum_s l_s f_s, f_s = e^(m_s - M), in split order
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, msh[h][s]);
+  float Ls = 0.0f, acc = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += CH) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j)
+        ov[j] = base[(size_t)min(s0 + j, nsplit - 1) * sstride + h * (D + 2) + d];
     }
-    lsum[h] = Ls;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (s0 + j < nsplit) {
+        const float ms = msh[h][s0 + j];
+        const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
+        Ls += lsh[h][s0 + j] * f;
+        acc += ov[j] * f;
+      }
+    }
   }
-  __syncthreads();
-  float acc = 0.0f;
-#pragma unroll 8
-  for (int s = 0; s < nsplit; ++s) acc += base[s * sstride + h * (D + 2) + d] * wsh[h][s];
-  out[((size_t)b * nq + kvh * AT_G + h) * D + d] = f2h(acc / lsum[h]);
+  out[((size_t)b * nq + kvh * AT_G + h) * D + d] = f2h(acc / Ls);
 }
 
 
