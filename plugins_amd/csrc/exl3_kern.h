@@ -1834,8 +1834,10 @@ static_assert(MOE_ITEM_ROWS * (MOE_TPS_MAX / 8) <= PREP_PASSES * PREP_GROUPS,
 
 // Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
 // launch's weights (gate and up side by side, or down).  Raw inputs are rows
-// slot / topk of x; prepared inputs are rows slot.
-template <int K, int CB, bool MASKED>
+// slot / topk of x; prepared inputs are rows slot.  PRO_SWIGLU (down): x is
+// the slots' gate rows and a.c.x2 their up rows (topk 1: row slot), the
+// mid step's SwiGLU and rotation formed in the prepare.
+template <int K, int CB, bool MASKED, int PRO>
 __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     const uint32_t *tw0, const uint32_t *tw1, const void *x, uint32_t g0, uint32_t g1,
     uint32_t g2, int topk, const uint32_t *__restrict__ sorted,
@@ -1869,7 +1871,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
   }
   const uint32_t *twe = sh ? W.sh_tw : tw + (size_t)it.expert * W.expert_words;
   auto run = [&](auto P) {
-    gemv_wg<K, CB, MASKED, decltype(P)::value>(twe, out_tiles, x, geo, a.c, Wx,
+    gemv_wg<K, CB, MASKED, decltype(P)::value, PRO>(twe, out_tiles, x, geo, a.c, Wx,
                                                sh ? 0 : (int)it.expert, (int)it.count, rm,
                                                blockIdx.x - ws.c0, blockIdx.y, smem + 256,
                                                MOE_ITEM_ROWS);
@@ -2055,14 +2057,20 @@ inline int gemv_prep_form(int rows, int tps) {
 }
 
 template <int K>
-void moe_gemv_go(const Format &f, dim3 grid, size_t lds, hipStream_t s, const uint32_t *tw0,
-                 const uint32_t *tw1, const void *x, uint32_t g0, uint32_t g1, uint32_t g2,
-                 int topk, const uint32_t *sorted, const MoeItem *items, const uint32_t *n_items,
-                 const GemvArgs &a) {
+void moe_gemv_go(const Format &f, int pro, dim3 grid, size_t lds, hipStream_t s,
+                 const uint32_t *tw0, const uint32_t *tw1, const void *x, uint32_t g0,
+                 uint32_t g1, uint32_t g2, int topk, const uint32_t *sorted, const MoeItem *items,
+                 const uint32_t *n_items, const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
   cb_dispatch<K>(f, [&](auto CBC, auto MC) {
-    hipLaunchKernelGGL((moe_gemv_kernel<K, decltype(CBC)::value, decltype(MC)::value>), grid, blk,
-                       lds, s, tw0, tw1, x, g0, g1, g2, topk, sorted, items, n_items, a);
+    constexpr int CB = decltype(CBC)::value;
+    constexpr bool M = decltype(MC)::value;
+    if (pro == PRO_SWIGLU)
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB, M, PRO_SWIGLU>), grid, blk, lds, s, tw0, tw1, x,
+                         g0, g1, g2, topk, sorted, items, n_items, a);
+    else
+      hipLaunchKernelGGL((moe_gemv_kernel<K, CB, M, PRO_PLAIN>), grid, blk, lds, s, tw0, tw1, x,
+                         g0, g1, g2, topk, sorted, items, n_items, a);
   });
 }
 
@@ -2118,7 +2126,7 @@ void gemm_frac_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw,
   void gemv_go<KK>(const Format &, int, dim3, size_t, hipStream_t, const uint32_t *const *, \
                    const void *, uint32_t, uint32_t, uint32_t, const GemvArgs &)
 #define EXL3_MOE_GEMV_GO(KK)                                                                    \
-  void moe_gemv_go<KK>(const Format &, dim3, size_t, hipStream_t, const uint32_t *,            \
+  void moe_gemv_go<KK>(const Format &, int, dim3, size_t, hipStream_t, const uint32_t *,       \
                        const uint32_t *, const void *, uint32_t, uint32_t, uint32_t, int,       \
                        const uint32_t *, const MoeItem *, const uint32_t *, const GemvArgs &)
 #define EXL3_GEMM_GROUPED_GO(KK)                                                             \

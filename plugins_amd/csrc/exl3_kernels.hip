@@ -759,8 +759,10 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const void *__restrict__ 
   }
 }
 
-// h = silu(g) * u (clamped when limit > 0), then down's prepare with suh_d[e]
-// (the shared expert's, sh_suh_d, for e == shared).
+// The mid step: h = silu(g) * u (clamped when limit > 0), then down's
+// prepare with suh_d[e] (the shared expert's, sh_suh_d, for e == shared).
+// A down GEMV launch of few workgroups forms the same values, bit for bit,
+// in its SwiGLU prologue instead.
 __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u,
                                                      const uint32_t *__restrict__ inds, int experts,
@@ -937,6 +939,11 @@ struct MoeLayout {
   bool gemm;  // prefill-sized expert batches: grouped GEMMs over 256-slot items
 };
 
+// Down GEMV launches of at most this many workgroups take the mid step in
+// their prepare (measured on the DeepSeek-V3 shape: 1008 workgroups at
+// batch 1 gain ~3 us a call, 8064 at batch 16 lose ~11 us).
+constexpr size_t MOE_FUSED_MID_MAX_WG = 2048;
+
 // Grouped GEMMs when the slots average at least this many per expert (and
 // every rate is an integer rate); below, the routed GEMV items.
 constexpr int MOE_GEMM_SLOTS_PER_EXPERT = 32;
@@ -995,13 +1002,15 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
 }
 
 // One grouped GEMV launch over `nweights` banks (gate and up side by side,
-// or down); x holds raw rows (slot / topk) or prepared rows (slot).
+// or down); x holds raw rows (slot / topk) or prepared rows (slot); pro
+// PRO_SWIGLU: x the slots' gate rows, a.c.x2 their up rows.
 struct MoeGemv {
   const uint32_t *tw[2];
   int nweights;
   const void *x;
   int xdt;
   bool prepared;
+  int pro;
   int in, out, ksplit, tps;
   GemvArgs a;
 };
@@ -1025,8 +1034,8 @@ void moe_gemv_launch(const Format &f, dim3 grid, size_t lds, hipStream_t s, cons
   uint32_t g0, g1, g2;
   if (!moe_geo(m, grid, &g0, &g1, &g2)) return;  // checked before the first launch
   rate_dispatch(f.integer_rate() ? f.n / 16 : 0, [&](auto KC) {
-    moe_gemv_go<decltype(KC)::value>(f, grid, lds, s, m.tw[0], m.tw[1], m.x, g0, g1, g2, topk,
-                                     sorted, items, n_items, m.a);
+    moe_gemv_go<decltype(KC)::value>(f, m.pro, grid, lds, s, m.tw[0], m.tw[1], m.x, g0, g1, g2,
+                                     topk, sorted, items, n_items, m.a);
   });
 }
 
@@ -1140,12 +1149,25 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
   mgu.nweights = 2;
-  MoeGemv md = moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d, L.tps_d);
-  md.nweights = 1;
-  mgu.a.c.status = md.a.c.status = slots.status;
-  mgu.a.c.poll_max = md.a.c.poll_max = splitk_poll_max();
   const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, L.max_items);
   const dim3 grid_d(a.hidden / 128, L.ks_d, L.max_items);
+  // down: in a launch of few workgroups every workgroup forms the mid step
+  // (the SwiGLU of its slots' gate and up rows, the down rotation) for its
+  // k-slice in its prepare, which costs less than the mid launch; in larger
+  // launches the repeats across column groups cost more than the launch
+  const bool fused_mid = (size_t)grid_d.x * grid_d.y * grid_d.z <= MOE_FUSED_MID_MAX_WG;
+  MoeGemv md = fused_mid ? moe_gemv(g, OUT_F16, false, L.slots, a.inter, a.hidden, down.f, L.ks_d,
+                                    L.tps_d)
+                         : moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d,
+                                    L.tps_d);
+  md.nweights = 1;
+  if (fused_mid) {
+    md.pro = PRO_SWIGLU;
+    md.a.c.x2 = u;
+    md.a.c.limit = a.limit;
+  }
+  mgu.a.c.status = md.a.c.status = slots.status;
+  mgu.a.c.poll_max = md.a.c.poll_max = splitk_poll_max();
   uint32_t gg[3];
   if (!moe_geo(mgu, grid_gu, &gg[0], &gg[1], &gg[2]) || !moe_geo(md, grid_d, &gg[0], &gg[1], &gg[2]))
     return hipErrorInvalidValue;
@@ -1166,9 +1188,10 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   }
   moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu,
                   sorted, items, n_items, a.topk);
-  hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
-                     a.experts, down.suh, xd, a.inter, a.limit, sh_index,
-                     shared ? shared->down.suh : nullptr);
+  if (!fused_mid)
+    hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
+                       a.experts, down.suh, xd, a.inter, a.limit, sh_index,
+                       shared ? shared->down.suh : nullptr);
   md.tw[0] = md.tw[1] = reinterpret_cast<const uint32_t *>(down.trellis);
   md.a.w[0] = moe_weight(down, d, pd);
   if (shared) {
@@ -1177,7 +1200,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     md.a.w[0].sh_svh = shared->down.svh;
   }
   moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted,
-                  items, n_items, a.topk);
+                  items, n_items, fused_mid ? 1 : a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();
