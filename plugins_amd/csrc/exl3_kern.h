@@ -182,6 +182,7 @@ struct GemvCfg {
   float *res;
   float *res_ssq;
   int shared_expert;  // routed launches: the index of the shared expert (-1: none)
+  int experts;        // routed launches without an item list: expert indices below this
 };
 
 // Prologue forms of the GEMV prepare (compile time: they decide which loads
@@ -1834,7 +1835,9 @@ static_assert(MOE_ITEM_ROWS * (MOE_TPS_MAX / 8) <= PREP_PASSES * PREP_GROUPS,
 
 // Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
 // launch's weights (gate and up side by side, or down).  Raw inputs are rows
-// slot / topk of x; prepared inputs are rows slot.  PRO_SWIGLU (down): x is
+// slot / topk of x; prepared inputs are rows slot.  Without an item list
+// (items null: one row's slots) item z is slot z alone, its expert
+// sorted[z] (the routes), skipped when not below a.c.experts.  PRO_SWIGLU (down): x is
 // the slots' gate rows and a.c.x2 their up rows (topk 1: row slot), the
 // mid step's SwiGLU and rotation formed in the prepare.
 template <int K, int CB, bool MASKED, int PRO>
@@ -1844,8 +1847,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     const MoeItem *__restrict__ items, const uint32_t *__restrict__ n_items, GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.z;
-  if ((uint32_t)item >= *n_items) return;
-  const MoeItem it = items[item];
+  MoeItem it;
+  if (items != nullptr) {
+    if ((uint32_t)item >= *n_items) return;
+    it = items[item];
+  } else {
+    if ((size_t)item >= a.c.ptotal) return;
+    const uint32_t e = sorted[item];
+    if (e >= (uint32_t)a.c.experts) return;
+    it = MoeItem{e, (uint32_t)item, 1u, 0u};
+  }
   const GemvGeo geo = GemvGeo::unpack(g0, g1, g2);
   const WeightSpan ws = gemv_weight_of(blockIdx.x, geo.cg1, 0, 0, geo.cgend);
   const uint32_t *tw = ws.wi == 0 ? tw0 : tw1;
@@ -1854,7 +1865,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
   GemvRow *ri = reinterpret_cast<GemvRow *>(smem);
   if (threadIdx.x < GEMV_ROWS) {
     const int b = min((int)threadIdx.x, (int)it.count - 1);
-    const int slot = (int)sorted[it.start + b];
+    const int slot = items != nullptr ? (int)sorted[it.start + b] : item;
     const int in = geo.in_tiles * 16, out = out_tiles * 16;
     ri[threadIdx.x] = GemvRow{(geo.prepared ? slot : slot / topk) * in, slot * out, slot, 0};
   }

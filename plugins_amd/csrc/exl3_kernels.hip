@@ -1149,8 +1149,13 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
   mgu.nweights = 2;
-  const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, L.max_items);
-  const dim3 grid_d(a.hidden / 128, L.ks_d, L.max_items);
+  // one row: every slot its own work item, read from the routes directly,
+  // no route launch (a row's routes name distinct experts; a repeated one
+  // would only be read twice)
+  const bool direct = a.rows == 1 && a.inds != nullptr;
+  const int nz = direct ? L.slots : L.max_items;
+  const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, nz);
+  const dim3 grid_d(a.hidden / 128, L.ks_d, nz);
   // down: in a launch of few workgroups every workgroup forms the mid step
   // (the SwiGLU of its slots' gate and up rows, the down rotation) for its
   // k-slice in its prepare, which costs less than the mid launch; in larger
@@ -1171,8 +1176,13 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   uint32_t gg[3];
   if (!moe_geo(mgu, grid_gu, &gg[0], &gg[1], &gg[2]) || !moe_geo(md, grid_d, &gg[0], &gg[1], &gg[2]))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
-                     a.experts, sorted, items, n_items, (uint32_t)MOE_ITEM_ROWS);
+  if (!direct)
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MOE_ROUTE_THREADS), 0, s, a.inds, L.slots,
+                       a.experts, sorted, items, n_items, (uint32_t)MOE_ITEM_ROWS);
+  const uint32_t *isorted = direct ? a.inds : sorted;
+  const MoeItem *iitems = direct ? nullptr : items;
+  const uint32_t *in_items = direct ? nullptr : n_items;
+  mgu.a.c.experts = md.a.c.experts = a.experts;
   mgu.tw[0] = reinterpret_cast<const uint32_t *>(gate.trellis);
   mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
   mgu.a.w[0] = moe_weight(gate, g, pgu);
@@ -1187,7 +1197,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     }
   }
   moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu,
-                  sorted, items, n_items, a.topk);
+                  isorted, iitems, in_items, a.topk);
   if (!fused_mid)
     hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
                        a.experts, down.suh, xd, a.inter, a.limit, sh_index,
@@ -1199,8 +1209,8 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     md.a.w[0].sh_suh = shared->down.suh;
     md.a.w[0].sh_svh = shared->down.svh;
   }
-  moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md, sorted,
-                  items, n_items, fused_mid ? 1 : a.topk);
+  moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md,
+                  isorted, iitems, in_items, fused_mid ? 1 : a.topk);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
                      a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();
