@@ -202,6 +202,34 @@ def _graph_ms(torch, fn, reps: int = 20) -> float:
     return _median_ms(torch, g.replay, max(reps, 20))
 
 
+def gemv_cache_resident(torch, X, distinct: int = 2):
+    """The headline pass (36 layers of launches, batch 1, K=4) with the
+    weights of `distinct` layers reused (layer l uses layer l % distinct):
+    at 2 layers 193 MB, inside the 256 MB Infinity Cache, so the pass reads
+    no weights from HBM after the first replay.  Set beside the streamed
+    pass it shows how much of the launch time HBM bandwidth accounts for."""
+    lins_d = build_model(torch, X, distinct, seed=1234)
+    per = len(SHAPES)
+    lins = [lins_d[(l % distinct) * per + j] for l in range(LAYERS) for j in range(per)]
+    nbytes = sum(packed_bytes(i, o) for _, i, o, _ in lins)
+    xs = {i: torch.randn(1, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
+    ys = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+    groups = []
+    for l0 in range(0, len(lins), per):
+        groups += [[l0, l0 + 1, l0 + 2], [l0 + 3], [l0 + 4, l0 + 5], [l0 + 6]]
+
+    def step():
+        for g in groups:
+            i = lins[g[0]][1]
+            X.matmul_shared([lins[j][3].weight for j in g], xs[i], outs=[ys[j] for j in g])
+    ms = _graph_ms(torch, step, 20)
+    return {"gemv_pass_cache_resident": {
+        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "ms_per_step": round(ms, 4),
+        "us_per_launch": round(ms * 1e3 / len(groups), 3),
+        "distinct_mb": round(sum(packed_bytes(i, o) for _, i, o, _ in lins_d) / 1e6, 1),
+        "timing": "median of 20 graph replays"}}
+
+
 def gemv_sweep(torch, X, ks=(2, 3, 4, 5, 6, 8), batches=(1, 2, 4, 8), reps=20):
     """the decode GEMV over the Qwen3-8B-shaped linears at
     each rate K and batch (as many layers as make >= 512 MB of weights at
@@ -539,6 +567,11 @@ def main() -> int:
         except Exception as ex:  # reported, not hidden
             extra["prefill_gemm_error"] = repr(ex)
     extra["gemv_gbs_per_shape"] = shapes
+    try:
+        log("cache-resident pass")
+        extra.update(gemv_cache_resident(torch, X))
+    except Exception as ex:  # reported, not hidden
+        extra["gemv_cache_resident_error"] = repr(ex)
     if not args.no_decode and args.only != "gemv":
         try:
             log("decode step")
@@ -576,15 +609,21 @@ def main() -> int:
         # The VALU ceiling: the GB/s at which the pass's measured VALU
         # instructions (SQ_INSTS_VALU of the counter run, decode and every
         # fixed part included) would keep every SIMD's VALU busy: 1024 SIMDs
-        # at the held shader clock, one wave-instruction per VALU_CYCLES.
+        # at the held shader clock, VALU_CYCLES per wave-instruction, plus
+        # the measured extra cycles of the decode's one v_mul_lo_u32 per
+        # weight (valu_rates.hip; SQ_INSTS_VALU counts it as one).
         vi = prof.get("valu_wave_insts_per_step")
         if vi:
-            rate = 256 * 4 * prof["shader_clock_hz"] / prof["valu_cycles_per_inst"]
-            valu_ceiling = {"gbs": round(step_bytes / (vi / rate) / 1e9, 1),
-                            "frac_of_hbm_peak": round(step_bytes / (vi / rate) / 1e9 / HBM_PEAK_GBS, 3),
+            muls = step_bytes * 8 / K_BITS / 64
+            cycles = vi * prof["valu_cycles_per_inst"] + muls * prof.get("mul_lo_extra_cycles", 0.0)
+            secs = cycles / (256 * 4 * prof["shader_clock_hz"])
+            valu_ceiling = {"gbs": round(step_bytes / secs / 1e9, 1),
+                            "frac_of_hbm_peak": round(step_bytes / secs / 1e9 / HBM_PEAK_GBS, 3),
                             "valu_insts_per_weight": round(vi * 64 / (step_bytes * 8 / K_BITS), 2),
                             "basis": "SQ_INSTS_VALU per step (profiles/gemv_k4_qwen3_8b_decode.md) at "
                                      f"{prof['valu_cycles_per_inst']} cycles per wave-instruction, "
+                                     f"+{prof.get('mul_lo_extra_cycles', 0.0)} cycles per v_mul_lo_u32 "
+                                     "(one per weight; profiles/gemv_valu_rates_cache_resident.md), "
                                      f"{prof['shader_clock_hz'] / 1e9:.2f} GHz, 1024 SIMDs"}
 
     line = {

@@ -2,6 +2,7 @@
 
     python -m plugins_amd.build          # or: python plugins_amd/build.py
     python -m plugins_amd.build --timeline   # the diagnostic GEMV-timeline build
+    python -m plugins_amd.build --valu-rates # the VALU instruction-rate program
 
 Objects go to plugins_amd/_build/, the library to plugins_amd/lib/.  hipcc
 cross-compiles gfx950 code objects without a GPU.  Device code is built with
@@ -98,5 +99,25 @@ def build(verbose: bool = True, timeline: bool = False) -> str:
     return lib_path
 
 
+# The measurement program for the VALU issue cost of the decode's integer
+# multiply (csrc/valu_rates.hip): an executable, not part of the library.
+VALU_RATES = os.path.join(LIBDIR, "valu_rates")
+
+
+def build_valu_rates(verbose: bool = True) -> str:
+    os.makedirs(LIBDIR, exist_ok=True)
+    flags = [f for f in DEVICE_FLAGS if f != "-fPIC"]
+    cmd = [_hipcc(), *flags, os.path.join(CSRC, "valu_rates.hip"), "-o", VALU_RATES]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on valu_rates.hip:\n" + r.stdout + r.stderr)
+    if verbose:
+        print("built", VALU_RATES)
+    return VALU_RATES
+
+
 if __name__ == "__main__":
-    build(timeline="--timeline" in sys.argv[1:])
+    if "--valu-rates" in sys.argv[1:]:
+        build_valu_rates()
+    else:
+        build(timeline="--timeline" in sys.argv[1:])
