@@ -616,6 +616,10 @@ __device__ __forceinline__ void gemv_mfma(const uint32_t (&p)[16], h8_t alo, h8_
 constexpr uint32_t PARTIAL_EMPTY = 0xFFFFFFFFu;
 constexpr int PARTIAL_POLL_MAX = 1 << 20;
 
+// The pause between polls of the split-K hand-off (s_sleep units of 64 cycles).
+#ifndef EXL3_POLL_SLEEP
+#define EXL3_POLL_SLEEP 2
+#endif
 __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, float *partial,
                                                  int nrows, const RowMap &rm, int ks, size_t out,
                                                  int col0) {
@@ -664,7 +668,7 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
       if (e == threadIdx.x && k0 == 0) EXL3_TL(7);
 #endif
       for (int n = 0; pending != 0 && n < a.poll_max; ++n) {
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
 #pragma unroll
         for (int j = 0; j < 16; ++j)
           if (pending & (1u << j)) v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
