@@ -48,10 +48,18 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
  * Calls that share a scratch must be ordered on one stream. */
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax);
 
+/* The key splits exl3d_attn_decode(_rope) uses for these sizes (0 for sizes
+ * it refuses), and the query heads per kv head it serves (4). */
+int exl3d_attn_splits(int B, int nkv, int Tmax);
+int exl3d_attn_heads_per_kv(void);
+
 /* Decode attention, grouped-query (nq = 4 nkv): out [B][nq*D] f16 =
  * softmax(q k^T * scale) v over keys 0 .. pos[b] of row b's cache, split
- * over the keys (for small grids one launch, the last split of each (row,
- * kv head) combining the splits; else a second launch combines them). */
+ * over the keys (one workgroup per split and kv head), then a second launch
+ * combines the splits.  out NULL: no combine; the split slots stay in
+ * scratch as [B][nkv][exl3d_attn_splits()][4][D + 2] f32 (a split's
+ * unnormalised o values, then its running max m and sum l), for a consumer
+ * that combines them (exl3d_attn_o). */
 int exl3d_attn_decode(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                       const int32_t *pos, int B, int nq, int nkv, int Tmax, float scale,
                       uint16_t *out, float *scratch, size_t scratch_bytes, hipStream_t s);
@@ -82,6 +90,20 @@ int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t 
 int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
                   const uint16_t *norm_w, const float *nssq, float eps, const uint16_t *up,
                   float *res, float *res_ssq, uint16_t *const *outs, hipStream_t s);
+
+/* The decode step's attention and o projection: exl3d_attn_decode_rope,
+ * then res [B][out] += f32(att @ o^T) with res_ssq [B][out/128] the new
+ * res's sums of squares per 128 columns (exl3d_linears with res).  Rows
+ * that fit one prepare batch of o's GEMV (B = 1 at Qwen3-8B's shapes) skip
+ * the combine launch: o's prepare combines the split slots itself, with
+ * the combine's arithmetic, so att is not written; other rows combine into
+ * att (f16 [B][nq*D]) first.  Results are equal either way.  Returns 0, a
+ * HIP error, or -1 when the weight or shapes are refused. */
+int exl3d_attn_o(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *qn,
+                 const uint16_t *kn, const int32_t *pos, int B, int nq, int nkv, float eps,
+                 float theta, uint16_t *kcache, uint16_t *vcache, int Tmax, float scale,
+                 const exl3_weight *o, float *res, float *res_ssq, uint16_t *att, float *scratch,
+                 size_t scratch_bytes, hipStream_t s);
 
 /* out = f16(silu(g) * u), n elements. */
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s);

@@ -578,8 +578,11 @@ int attn_launch(bool rope, const uint16_t *q, const RopeArgs &ra, uint16_t *kcac
     go(attn_decode_kernel<true>);
   else
     go(attn_decode_kernel<false>);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s, scratch,
-                     nq, nkv, ns, out);
+  // out NULL: the slots stay for a consumer that combines them itself (the
+  // o projection's attention prologue)
+  if (out != nullptr)
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s,
+                       scratch, nq, nkv, ns, out);
   return hipGetLastError();
 }
 
@@ -615,6 +618,14 @@ int exl3d_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *v, 
                      pos, nq, nkv, eps, theta, qout, kcache, vcache, Tmax);
   return hipGetLastError();
 }
+
+int exl3d_attn_splits(int B, int nkv, int Tmax) {
+  if (B <= 0 || nkv <= 0 || Tmax <= 0) return 0;
+  int ts;
+  return attn_split(Tmax, B, nkv, &ts);
+}
+
+int exl3d_attn_heads_per_kv(void) { return AT_G; }
 
 size_t exl3d_attn_scratch_bytes(int B, int nq, int nkv, int Tmax) {
   int ts;

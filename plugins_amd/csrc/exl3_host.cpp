@@ -1916,3 +1916,48 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
   if (e == hipErrorInvalidValue) return -1;
   return e;
 }
+
+int exl3d_attn_o(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *qn,
+                 const uint16_t *kn, const int32_t *pos, int B, int nq, int nkv, float eps,
+                 float theta, uint16_t *kcache, uint16_t *vcache, int Tmax, float scale,
+                 const exl3_weight *o, float *res, float *res_ssq, uint16_t *att, float *scratch,
+                 size_t scratch_bytes, hipStream_t s) {
+  const WeightPriv *pv = priv_of(o);
+  if (!pv || pv->experts != 0 || !res || !res_ssq || B < 1 || B > exl3::GEMV_ROWS_MAX) return -1;
+  const int G = exl3d_attn_heads_per_kv();
+  const int ns = exl3d_attn_splits(B, nkv, Tmax);
+  if (ns < 1 || nq != G * nkv || pv->in != (int64_t)nq * EXL3D_HEAD_DIM) return -1;
+  const bool fused = exl3::gemv_one_batch((int)pv->in, (int)pv->out, !pv->f.integer_rate(), B);
+  if (!fused && !att) return -1;
+  if (hipSetDevice(pv->device) != hipSuccess) return hipErrorInvalidDevice;
+  int r = exl3d_attn_decode_rope(q, k, v, qn, kn, pos, B, nq, nkv, eps, theta, kcache, vcache,
+                                 Tmax, scale, fused ? nullptr : att, scratch, scratch_bytes, s);
+  if (r != 0) return r;
+  if (!fused) return exl3d_linears(&o, 1, att, B, nullptr, nullptr, 0.0f, nullptr, res, res_ssq,
+                                   nullptr, s);
+  const int in = (int)pv->in;
+  StreamScratch *ss = scratch_for(pv->device, s);
+  std::lock_guard<std::mutex> g(ss->mu);
+  int wout = (int)pv->out;
+  exl3::GemvLinear l;
+  l.trellis = (const uint16_t *)o->w.data;
+  l.suh = (const uint16_t *)o->scales.data;
+  l.svh = (const uint16_t *)o->biases.data;
+  l.y = nullptr;
+  l.zout = nullptr;
+  l.out = wout;
+  exl3::Scratch sc;
+  hipError_t e = gemv_scratch(ss, &wout, 1, in, B, !pv->f.integer_rate(), &sc, s);
+  if (e != hipSuccess) return e;
+  exl3::GemvFuse fz;
+  fz.res = res;
+  fz.res_ssq = res_ssq;
+  fz.attn_part = scratch;
+  fz.attn_nkv = nkv;
+  fz.attn_g = G;
+  fz.attn_nsplit = ns;
+  e = exl3::launch_gemv_fused(&l, 1, pv->f, scratch, exl3::ACT_F16, exl3::ACT_F16, B, in, &sc, fz,
+                              s);
+  if (e == hipErrorInvalidValue) return -1;
+  return e;
+}

@@ -183,11 +183,15 @@ struct GemvCfg {
   float *res_ssq;
   int shared_expert;  // routed launches: the index of the shared expert (-1: none)
   int experts;        // routed launches without an item list: expert indices below this
+  // attention prologue: the decode attention's per-split slots
+  // [rows][attn_nkv][attn_nsplit][attn_g][128 + 2] (o values, then m, l)
+  const float *attn_part;
+  int attn_nkv, attn_g, attn_nsplit;
 };
 
 // Prologue forms of the GEMV prepare (compile time: they decide which loads
 // a workgroup issues at its start).
-constexpr int PRO_PLAIN = 0, PRO_SWIGLU = 1, PRO_RMSNORM = 2;
+constexpr int PRO_PLAIN = 0, PRO_SWIGLU = 1, PRO_RMSNORM = 2, PRO_ATTN = 3;
 
 
 // The SwiGLU of one element pair of gate (g) and up (u), f16 bits: the MoE
@@ -385,6 +389,83 @@ __device__ __forceinline__ void gemv_prep_load_up(const uint16_t *x2, const RowM
     const int row = it / nb, blk = it - row * nb;
     const int k = tk0 * 16 + blk * 128 + 2 * lane;
     r.x1[j] = ld_global_u32(x2 + (size_t)rm.in_off(row) + k);
+  }
+}
+
+// Attention prologue: input element pair (2 lane, 2 lane + 1) of query head
+// hq of batch row b, combined from the decode attention's split slots as
+// its combine step does (decoder_ops.hip attn_combine_kernel): M = the
+// largest m_s, f_s = e^(m_s - M) (0 for an empty split), out =
+// f16(sum_s o_s f_s / sum_s l_s f_s), both sums in split order, the same
+// f32 operations, so the values equal the combine's output bit for bit.
+// Lane i holds m, l of split c0 + i of its 64-split chunk c0; a split's
+// factor and l * f reach every lane by readlane, in split order.
+__device__ __forceinline__ uint32_t attn_combine_pair(const GemvCfg &a, int b, int hq, int lane) {
+  constexpr int D = 128, CH = 32;
+  const int kvh = hq / a.attn_g, g = hq - kvh * a.attn_g, ns = a.attn_nsplit;
+  const size_t sst = (size_t)a.attn_g * (D + 2);
+  const float *base = a.attn_part + ((size_t)b * a.attn_nkv + kvh) * ns * sst + g * (D + 2);
+  typedef float f2v_t __attribute__((ext_vector_type(2)));
+  auto ld_o = [&](int s) {
+    return *(const __attribute__((address_space(1))) f2v_t *)(base + (size_t)s * sst + 2 * lane);
+  };
+  auto ld_ml = [&](int c0, float &m, float &l) {
+    const int s = min(c0 + lane, ns - 1);
+    const f2v_t v = *(const __attribute__((address_space(1))) f2v_t *)(base + (size_t)s * sst + D);
+    m = c0 + lane < ns ? v.x : -INFINITY;
+    l = v.y;
+  };
+  // one round: m, l of the first 64 splits and o of the first CH
+  f2v_t ov[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) ov[j] = ld_o(min(j, ns - 1));
+  float mv, lv;
+  ld_ml(0, mv, lv);
+  float M = mv;
+  for (int c0 = 64; c0 < ns; c0 += 64) {
+    float m2, l2;
+    ld_ml(c0, m2, l2);
+    M = fmaxf(M, m2);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, xor_lanes(M, m));
+  float Ls = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
+  float fv = 0.0f, pv = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += CH) {
+    if ((s0 & 63) == 0) {
+      if (s0 > 0) ld_ml(s0, mv, lv);
+      fv = mv == -INFINITY ? 0.0f : __expf(mv - M);
+      pv = lv * fv;
+    }
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) ov[j] = ld_o(min(s0 + j, ns - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (s0 + j < ns) {
+        const int ln = (s0 + j) & 63;
+        const float f = bits<float>((uint32_t)__builtin_amdgcn_readlane((int)bits<uint32_t>(fv), ln));
+        const float p = bits<float>((uint32_t)__builtin_amdgcn_readlane((int)bits<uint32_t>(pv), ln));
+        Ls += p;
+        acc0 += ov[j].x * f;
+        acc1 += ov[j].y * f;
+      }
+    }
+  }
+  return (uint32_t)f2h(acc0 / Ls) | ((uint32_t)f2h(acc1 / Ls) << 16);
+}
+
+// The attention prologue's input pairs of every item into x0 (f16 bits).
+__device__ __forceinline__ void gemv_prep_attn(const GemvCfg &a, int nitems, int nb, int tk0,
+                                               int base, int wave, int lane, PrepRegs &r) {
+#pragma unroll
+  for (int j = 0; j < PREP_BATCH; ++j) {
+    if (!prep_item_live(j, base, wave, nitems)) break;
+    const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
+    const int row = it / nb, blk = it - row * nb;
+    r.x0[j] = attn_combine_pair(a, row, tk0 / 8 + blk, lane);
+    r.x1[j] = 0u;
   }
 }
 
@@ -820,10 +901,13 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // items in one pass (gemv_rows_*)
   PrepRegs pr;
   RowsRegs<NP> rr;
-  if constexpr (ONEB)
-    gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
-  else
+  static_assert(PRO != PRO_ATTN || ONEB, "the attention prologue is for rows in one prepare batch");
+  if constexpr (ONEB) {
+    if constexpr (PRO != PRO_ATTN)
+      gemv_prep_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, 0, wave, lane, pr);
+  } else {
     gemv_rows_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, rr);
+  }
   if constexpr (K > 0) {
 #pragma unroll
     for (int i = 0; i < K; ++i) bw[0][i] = wp[i];
@@ -881,6 +965,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     resv[r2].x = v.x;
     resv[r2].y = v.y;
   }
+  if constexpr (PRO == PRO_ATTN) gemv_prep_attn(a, nitems, nb, tk0, 0, wave, lane, pr);
   if constexpr (ONEB)
     gemv_prep_store<PRO>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
                          FOLD ? hsum : nullptr, a.limit, in, a.eps);
@@ -2031,7 +2116,8 @@ void gemv_go(const Format &f, int prep, dim3 grid, size_t lds, hipStream_t s,
              const GemvArgs &a) {
   const dim3 blk(GEMV_THREADS);
   // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up); a.c.nssq set: the
-  // RMSNorm prologue (x is the f32 residual; rows in one prepare batch)
+  // RMSNorm prologue (x is the f32 residual; rows in one prepare batch);
+  // a.c.attn_part set: the attention prologue (x unused; one batch)
   auto go2 = [&](auto CBC, auto MC, auto PC) {
     constexpr int CB = decltype(CBC)::value;
     constexpr bool M = decltype(MC)::value;
@@ -2044,6 +2130,11 @@ void gemv_go(const Format &f, int prep, dim3 grid, size_t lds, hipStream_t s,
     if constexpr (O == 0) {
       if (a.c.nssq != nullptr) {
         hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_RMSNORM>), grid, blk, lds, s, tw[0],
+                           tw[1], tw[2], tw[3], x, g0, g1, g2, a);
+        return;
+      }
+      if (a.c.attn_part != nullptr) {
+        hipLaunchKernelGGL((gemv_kernel<K, CB, M, O, PRO_ATTN>), grid, blk, lds, s, tw[0],
                            tw[1], tw[2], tw[3], x, g0, g1, g2, a);
         return;
       }

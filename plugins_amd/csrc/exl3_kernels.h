@@ -141,6 +141,10 @@ struct GemvFuse {
   float eps = 0.0f;
   float *res = nullptr;
   float *res_ssq = nullptr;
+  // the attention prologue: x is the decode attention's split slots
+  // [rows][attn_nkv][attn_nsplit][attn_g][128 + 2], combined in the prepare
+  const float *attn_part = nullptr;
+  int attn_nkv = 0, attn_g = 0, attn_nsplit = 0;
 };
 hipError_t launch_gemv_fused(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, int ydt, int rows, int in, Scratch *sc, const GemvFuse &fz,

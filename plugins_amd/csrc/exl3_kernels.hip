@@ -470,6 +470,10 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   a.c.eps = fz.eps;
   a.c.res = fz.res;
   a.c.res_ssq = fz.res_ssq;
+  a.c.attn_part = fz.attn_part;
+  a.c.attn_nkv = fz.attn_nkv;
+  a.c.attn_g = fz.attn_g;
+  a.c.attn_nsplit = fz.attn_nsplit;
   GemvGeo geo{};
   geo.cg1 = cgs[1];
   geo.cg2 = cgs[2];
@@ -490,6 +494,11 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
       (!oneb || xdt != OUT_F32 || prepared || fz.norm_w == nullptr || in / 128 > NORM_MAXBLK))
     return hipErrorInvalidValue;
   if (fz.res != nullptr && (count != 1 || fz.res_ssq == nullptr)) return hipErrorInvalidValue;
+  if (fz.attn_part != nullptr &&
+      (!oneb || count != 1 || xdt != OUT_F16 || prepared || fz.nssq != nullptr ||
+       fz.up != nullptr || fz.attn_nkv < 1 || fz.attn_g < 1 || fz.attn_nsplit < 1 ||
+       in != fz.attn_nkv * fz.attn_g * 128))
+    return hipErrorInvalidValue;
   rate_dispatch(generic ? 0 : f.n / 16, [&](auto KC) {
     gemv_go<decltype(KC)::value>(f, prep, grid, lds, s, tw, x, g0, g1, g2, a);
   });

@@ -63,6 +63,11 @@ _DEC_SIGS = {
     "exl3d_attn_decode_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_int, c_int, c_int, c_float, c_float, c_void_p, c_void_p,
                                        c_int, c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "exl3d_attn_splits": (c_int, [c_int, c_int, c_int]),
+    "exl3d_attn_heads_per_kv": (c_int, []),
+    "exl3d_attn_o": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                             c_int, c_float, c_float, c_void_p, c_void_p, c_int, c_float, c_void_p,
+                             c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "exl3d_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 _dec = None
@@ -151,6 +156,23 @@ def attn_decode_rope(q, k, v, qn, kn, pos, kcache, vcache, out, scratch, eps, th
                                          1.0 / math.sqrt(HEAD_DIM), _p(out), _p(scratch),
                                          scratch.numel() * scratch.element_size(),
                                          X.stream_handle(stream)), "attn_decode_rope")
+
+
+def attn_o(q, k, v, qn, kn, pos, kcache, vcache, o, res, res_ssq, att, scratch, eps, theta,
+           stream=None):
+    """exl3d_attn_o: attn_decode_rope, then res += att @ o^T (residual finish,
+    res_ssq its sums of squares per 128 columns); at rows that fit one
+    prepare batch o's prepare combines the attention's splits (att is then
+    not written)."""
+    B = q.shape[0]
+    nq, nkv, tmax = q.shape[1] // HEAD_DIM, kcache.shape[1], kcache.shape[2]
+    rc = dec_lib().exl3d_attn_o(_p(q), _p(k), _p(v), _p(qn), _p(kn), _p(pos), B, nq, nkv, eps, theta,
+                                _p(kcache), _p(vcache), tmax, 1.0 / math.sqrt(HEAD_DIM),
+                                ctypes.byref(o), _p(res), _p(res_ssq), _p(att), _p(scratch),
+                                scratch.numel() * scratch.element_size(), X.stream_handle(stream))
+    if rc == -1:
+        raise RuntimeError("attn_o: weight or shapes refused")
+    _ck(rc, "attn_o")
 
 
 def silu_mul(g, u, out, stream=None):
@@ -245,19 +267,21 @@ class Qwen3Decoder:
 
         Five launches a layer: q+k+v with the input RMSNorm of the residual h
         in their prepare; attention with q/k norm, RoPE and the KV append;
-        o, whose finish adds into h (and leaves h's sums of squares per 128
-        columns for the next norm); gate+up with the post-attention RMSNorm
-        in their prepare; down with the SwiGLU in its prepare and its finish
-        adding into h."""
+        o, whose prepare combines the attention's key splits and whose
+        finish adds into h (and leaves h's sums of squares per 128 columns
+        for the next norm); gate+up with the post-attention RMSNorm in their
+        prepare; down with the SwiGLU in its prepare and its finish adding
+        into h.  Rows beyond one prepare batch (batch 16) add the
+        attention's combine launch and norm / SwiGLU launches."""
         c = self.cfg
         embed(self.ids, self.embed_table, self.h, self.ssq, stream)
         for L in self.layers:
             linears([L["q"].weight, L["k"].weight, L["v"].weight], self.h,
                     outs=[self.q, self.k, self.v], norm_w=L["in_norm"], nssq=self.ssq, eps=c.eps,
                     stream=stream)
-            attn_decode_rope(self.q, self.k, self.v, L["q_norm"], L["k_norm"], self.pos, L["kc"],
-                             L["vc"], self.att, self.scratch, c.eps, c.theta, stream)
-            linears([L["o"].weight], self.att, res=self.h, res_ssq=self.ssq, stream=stream)
+            attn_o(self.q, self.k, self.v, L["q_norm"], L["k_norm"], self.pos, L["kc"], L["vc"],
+                   L["o"].weight, self.h, self.ssq, self.att, self.scratch, c.eps, c.theta,
+                   stream)
             linears([L["gate"].weight, L["up"].weight], self.h, outs=[self.g, self.u],
                     norm_w=L["post_norm"], nssq=self.ssq, eps=c.eps, stream=stream)
             linears([L["down"].weight], self.g, up=self.u, res=self.h, res_ssq=self.ssq,

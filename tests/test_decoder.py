@@ -192,6 +192,50 @@ def _ssq(h):
 
 
 @gpu
+@pytest.mark.parametrize("B,T,lens", [(1, 2048, [2047]), (1, 80, [40]), (1, 20000, [19999]),
+                                      (2, 300, [299, 7]), (16, 300, None)])
+def test_attention_o_fused_equals_separate(B, T, lens):
+    # exl3d_attn_o against its two steps (attention with its combine launch,
+    # then the o linear with the residual finish): at rows in one prepare
+    # batch o's prepare combines the key splits itself (with 128 splits at
+    # T = 20000: two chunks of the split loop), above it the steps run as
+    # they are; residual and its sums of squares equal bit for bit
+    from plugins_amd import qwen3 as Q
+    g = torch.Generator().manual_seed(60 + B + T)
+    nq, nkv = 32, 8
+    lo = Q.random_linear(torch, nq * 128, 4096, 4, torch.Generator(device="cuda").manual_seed(7))
+    q = torch.randn(B, nq * 128, generator=g).half().cuda()
+    k = torch.randn(B, nkv * 128, generator=g).half().cuda()
+    v = torch.randn(B, nkv * 128, generator=g).half().cuda()
+    qn = (1 + 0.1 * torch.randn(128, generator=g)).half().cuda()
+    kn = (1 + 0.1 * torch.randn(128, generator=g)).half().cuda()
+    kc = torch.randn(B, nkv, T, 128, generator=g).half().cuda()
+    vc = torch.randn(B, nkv, T, 128, generator=g).half().cuda()
+    pos = torch.tensor(lens if lens else [int(x) for x in torch.randint(0, T, (B,), generator=g)],
+                       dtype=torch.int32).cuda()
+    h = torch.randn(B, 4096, generator=g).cuda()
+    scratch = torch.zeros(Q.attn_scratch_bytes(B, nq, nkv, T) // 4 + 1, device="cuda")
+    # the two steps
+    kc1, vc1, h1 = kc.clone(), vc.clone(), h.clone()
+    att1 = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
+    ssq1 = torch.empty(B, 32, device="cuda")
+    Q.attn_decode_rope(q, k, v, qn, kn, pos, kc1, vc1, att1, scratch, 1e-6, 1e6)
+    Q.linears([lo.weight], att1, res=h1, res_ssq=ssq1)
+    # the fused entry
+    kc2, vc2, h2 = kc.clone(), vc.clone(), h.clone()
+    att2 = torch.empty(B, nq * 128, dtype=torch.float16, device="cuda")
+    ssq2 = torch.empty(B, 32, device="cuda")
+    scratch.zero_()
+    Q.attn_o(q, k, v, qn, kn, pos, kc2, vc2, lo.weight, h2, ssq2, att2, scratch, 1e-6, 1e6)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(h1, h2), float((h1 - h2).abs().max())
+    assert torch.equal(ssq1, ssq2)
+    if B == 16:
+        assert torch.equal(att1, att2)  # beyond one prepare batch: combined into att as before
+
+
+@gpu
 @pytest.mark.parametrize("B", [1, 16])
 @pytest.mark.parametrize("H,I", [(512, 1024), (4096, 12288)])
 def test_linears_fusions(B, H, I):
