@@ -183,8 +183,9 @@ struct GemvCfg {
   float *res_ssq;
   int shared_expert;  // routed launches: the index of the shared expert (-1: none)
   int experts;        // routed launches without an item list: expert indices below this
-  // attention prologue: the decode attention's per-split slots
-  // [rows][attn_nkv][attn_nsplit][attn_g][128 + 2] (o values, then m, l)
+  // attention prologue (set: on; the launch's x is then this pointer): the
+  // decode attention's per-split slots [rows][attn_nkv][attn_nsplit]
+  // [attn_g][128 + 2] (o values, then m, l)
   const float *attn_part;
   int attn_nkv, attn_g, attn_nsplit;
 };
@@ -399,72 +400,95 @@ __device__ __forceinline__ void gemv_prep_load_up(const uint16_t *x2, const RowM
 // f16(sum_s o_s f_s / sum_s l_s f_s), both sums in split order, the same
 // f32 operations, so the values equal the combine's output bit for bit.
 // Lane i holds m, l of split c0 + i of its 64-split chunk c0; a split's
-// factor and l * f reach every lane by readlane, in split order.
-__device__ __forceinline__ uint32_t attn_combine_pair(const GemvCfg &a, int b, int hq, int lane) {
-  constexpr int D = 128, CH = 32;
-  const int kvh = hq / a.attn_g, g = hq - kvh * a.attn_g, ns = a.attn_nsplit;
-  const size_t sst = (size_t)a.attn_g * (D + 2);
-  const float *base = a.attn_part + ((size_t)b * a.attn_nkv + kvh) * ns * sst + g * (D + 2);
-  typedef float f2v_t __attribute__((ext_vector_type(2)));
-  auto ld_o = [&](int s) {
-    return *(const __attribute__((address_space(1))) f2v_t *)(base + (size_t)s * sst + 2 * lane);
-  };
-  auto ld_ml = [&](int c0, float &m, float &l) {
-    const int s = min(c0 + lane, ns - 1);
-    const f2v_t v = *(const __attribute__((address_space(1))) f2v_t *)(base + (size_t)s * sst + D);
-    m = c0 + lane < ns ? v.x : -INFINITY;
-    l = v.y;
-  };
-  // one round: m, l of the first 64 splits and o of the first CH
-  f2v_t ov[CH];
-#pragma unroll
-  for (int j = 0; j < CH; ++j) ov[j] = ld_o(min(j, ns - 1));
+// factor and l * f reach every lane by readlane, in split order.  The first
+// round of loads (o of splits 0..31, m and l of splits 0..63) is issued by
+// attn_load, early in the workgroup; attn_combine does the rest.
+constexpr int ATTN_CH = 32;
+typedef float attn_f2_t __attribute__((ext_vector_type(2)));
+struct AttnLoads {
+  attn_f2_t ov[ATTN_CH];
   float mv, lv;
-  ld_ml(0, mv, lv);
-  float M = mv;
+};
+struct AttnItem {
+  const float *base;  // split 0's slot of this head
+  size_t sst;         // floats between splits
+  int ns;
+};
+__device__ __forceinline__ AttnItem attn_item(const float *part, const GemvCfg &a, int b, int hq) {
+  constexpr int D = 128;
+  const int kvh = hq / a.attn_g, g = hq - kvh * a.attn_g;
+  const size_t sst = (size_t)a.attn_g * (D + 2);
+  return AttnItem{part + ((size_t)b * a.attn_nkv + kvh) * a.attn_nsplit * sst + g * (D + 2), sst,
+                  a.attn_nsplit};
+}
+__device__ __forceinline__ attn_f2_t attn_ld_o(const AttnItem &t, int s, int lane) {
+  return *(const __attribute__((address_space(1))) attn_f2_t *)(t.base + (size_t)s * t.sst +
+                                                                2 * lane);
+}
+__device__ __forceinline__ void attn_ld_ml(const AttnItem &t, int c0, int lane, float &m,
+                                           float &l) {
+  const int s = min(c0 + lane, t.ns - 1);
+  const attn_f2_t v =
+      *(const __attribute__((address_space(1))) attn_f2_t *)(t.base + (size_t)s * t.sst + 128);
+  m = c0 + lane < t.ns ? v.x : -INFINITY;
+  l = v.y;
+}
+__device__ __forceinline__ void attn_load(const AttnItem &t, int lane, AttnLoads &L) {
+#pragma unroll
+  for (int j = 0; j < ATTN_CH; ++j) L.ov[j] = attn_ld_o(t, min(j, t.ns - 1), lane);
+  attn_ld_ml(t, 0, lane, L.mv, L.lv);
+}
+__device__ __forceinline__ uint32_t attn_combine(const AttnItem &t, int lane, AttnLoads &L) {
+  const int ns = t.ns;
+  float M = L.mv;
   for (int c0 = 64; c0 < ns; c0 += 64) {
     float m2, l2;
-    ld_ml(c0, m2, l2);
+    attn_ld_ml(t, c0, lane, m2, l2);
     M = fmaxf(M, m2);
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, xor_lanes(M, m));
   float Ls = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
-  float fv = 0.0f, pv = 0.0f;
-  for (int s0 = 0; s0 < ns; s0 += CH) {
+  float mv = L.mv, lv = L.lv, fv = 0.0f, pv = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += ATTN_CH) {
     if ((s0 & 63) == 0) {
-      if (s0 > 0) ld_ml(s0, mv, lv);
+      if (s0 > 0) attn_ld_ml(t, s0, lane, mv, lv);
       fv = mv == -INFINITY ? 0.0f : __expf(mv - M);
       pv = lv * fv;
     }
     if (s0 > 0) {
 #pragma unroll
-      for (int j = 0; j < CH; ++j) ov[j] = ld_o(min(s0 + j, ns - 1));
+      for (int j = 0; j < ATTN_CH; ++j) L.ov[j] = attn_ld_o(t, min(s0 + j, ns - 1), lane);
     }
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
+    for (int j = 0; j < ATTN_CH; ++j) {
       if (s0 + j < ns) {
         const int ln = (s0 + j) & 63;
         const float f = bits<float>((uint32_t)__builtin_amdgcn_readlane((int)bits<uint32_t>(fv), ln));
         const float p = bits<float>((uint32_t)__builtin_amdgcn_readlane((int)bits<uint32_t>(pv), ln));
         Ls += p;
-        acc0 += ov[j].x * f;
-        acc1 += ov[j].y * f;
+        acc0 += L.ov[j].x * f;
+        acc1 += L.ov[j].y * f;
       }
     }
   }
   return (uint32_t)f2h(acc0 / Ls) | ((uint32_t)f2h(acc1 / Ls) << 16);
 }
 
-// The attention prologue's input pairs of every item into x0 (f16 bits).
-__device__ __forceinline__ void gemv_prep_attn(const GemvCfg &a, int nitems, int nb, int tk0,
-                                               int base, int wave, int lane, PrepRegs &r) {
+// The attention prologue's input pairs of every item into x0 (f16 bits);
+// the wave's first item's first round of loads was issued into L (when the
+// item is live).
+__device__ __forceinline__ void gemv_prep_attn(const float *part, const GemvCfg &a, int nitems,
+                                               int nb, int tk0, int base, int wave, int lane,
+                                               AttnLoads &L, PrepRegs &r) {
 #pragma unroll
   for (int j = 0; j < PREP_BATCH; ++j) {
     if (!prep_item_live(j, base, wave, nitems)) break;
     const int it = min(base + wave + j * (GEMV_THREADS / 64), nitems - 1);
     const int row = it / nb, blk = it - row * nb;
-    r.x0[j] = attn_combine_pair(a, row, tk0 / 8 + blk, lane);
+    const AttnItem t = attn_item(part, a, row, tk0 / 8 + blk);
+    if (j > 0) attn_load(t, lane, L);
+    r.x0[j] = attn_combine(t, lane, L);
     r.x1[j] = 0u;
   }
 }
@@ -912,7 +936,17 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
 #pragma unroll
     for (int i = 0; i < K; ++i) bw[0][i] = wp[i];
   }
-  // The loads above use preloaded arguments only.  W.suh comes from the
+  // attention prologue: the first round of the wave's first item (x is the
+  // attention's split slots)
+  AttnLoads al;
+  if constexpr (PRO == PRO_ATTN) {
+    if (prep_item_live(0, 0, wave, nitems)) {
+      const int row = wave / nb, blk = wave - row * nb;
+      attn_load(attn_item((const float *)x, a, row, tk0 / 8 + blk), lane, al);
+    }
+  }
+  // The loads above use preloaded arguments only (the attention prologue's
+  // also its geometry from the argument segment).  W.suh comes from the
   // argument segment (a scalar load issued at entry); passing it through an
   // empty asm statement that also orders memory keeps the wait for that
   // scalar load after the loads above are issued.
@@ -965,7 +999,8 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     resv[r2].x = v.x;
     resv[r2].y = v.y;
   }
-  if constexpr (PRO == PRO_ATTN) gemv_prep_attn(a, nitems, nb, tk0, 0, wave, lane, pr);
+  if constexpr (PRO == PRO_ATTN)
+    gemv_prep_attn((const float *)x, a, nitems, nb, tk0, 0, wave, lane, al, pr);
   if constexpr (ONEB)
     gemv_prep_store<PRO>(geo.xdt, geo.prepared, nitems, nb, 0, wave, lane, xs, kr, pr,
                          FOLD ? hsum : nullptr, a.limit, in, a.eps);
@@ -2117,7 +2152,8 @@ void gemv_go(const Format &f, int prep, dim3 grid, size_t lds, hipStream_t s,
   const dim3 blk(GEMV_THREADS);
   // a.c.x2 set: the SwiGLU prologue (x is gate, x2 up); a.c.nssq set: the
   // RMSNorm prologue (x is the f32 residual; rows in one prepare batch);
-  // a.c.attn_part set: the attention prologue (x unused; one batch)
+  // a.c.attn_part set: the attention prologue (x is the split slots; one
+  // batch)
   auto go2 = [&](auto CBC, auto MC, auto PC) {
     constexpr int CB = decltype(CBC)::value;
     constexpr bool M = decltype(MC)::value;
