@@ -1240,11 +1240,22 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
       exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &pf);
   e = grow(ss, &ss->moe, &ss->moe_bytes, need, s);
   if (e != hipSuccess) return hip_failed(e);
-  e = exl3::launch_moe_shared_route(
-      (const uint32_t *)inds.data, scores.data, sdt, opts->logits.data, (int)E, (int)k,
-      opts->logit.data, opts->gate_vec.data, x.data, xdt, (int)rows, (int)hidden, r_inds,
-      r_scores, s);
-  if (e != hipSuccess) return e == hipErrorInvalidValue ? kShape : hip_failed(e);
+  // one row with its routes given: the routed launches read the k routes
+  // and take slot k as the shared expert, the combine forms the gate; else
+  // the route launch writes the (k + 1)-wide routes first
+  const bool direct = !opts->logits.data &&
+                      exl3::moe_shared_direct(a, !pg->f.integer_rate(), !pd->f.integer_rate());
+  if (direct) {
+    a.inds = (const uint32_t *)inds.data;
+    a.scores = scores.data;
+    a.sdt = sdt;
+  } else {
+    e = exl3::launch_moe_shared_route(
+        (const uint32_t *)inds.data, scores.data, sdt, opts->logits.data, (int)E, (int)k,
+        opts->logit.data, opts->gate_vec.data, x.data, xdt, (int)rows, (int)hidden, r_inds,
+        r_scores, s);
+    if (e != hipSuccess) return e == hipErrorInvalidValue ? kShape : hip_failed(e);
+  }
   exl3::Scratch slots;
   e = slots_for(ss, pf, s, &slots);
   if (e != hipSuccess) return hip_failed(e);
@@ -1252,7 +1263,12 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
     return exl3::MoeBank{(const uint16_t *)w->w.data, (const uint16_t *)w->scales.data,
                          (const uint16_t *)w->biases.data, p->f, (int)p->in, (int)p->out};
   };
-  const exl3::MoeShared sh{bank(opts->gate, sg), bank(opts->up, su), bank(opts->down, sd)};
+  exl3::MoeShared sh{bank(opts->gate, sg), bank(opts->up, su), bank(opts->down, sd)};
+  if (direct) {
+    sh.routes_k = (int)k;
+    sh.logit = opts->logit.data;
+    sh.gate_vec = opts->gate_vec.data;
+  }
   e = exl3::launch_moe(a, bank(gate, pg), bank(up, pu), bank(down, pd), ss->moe, ss->moe_bytes,
                        slots, s, &sh);
   if (e != hipSuccess) return e == hipErrorInvalidValue ? kShape : hip_failed(e);

@@ -183,6 +183,7 @@ struct GemvCfg {
   float *res_ssq;
   int shared_expert;  // routed launches: the index of the shared expert (-1: none)
   int experts;        // routed launches without an item list: expert indices below this
+  int routes_k;       // ... > 0: sorted holds k routes, slot k is the shared expert
   // attention prologue (set: on; the launch's x is then this pointer): the
   // decode attention's per-split slots [rows][attn_nkv][attn_nsplit]
   // [attn_g][128 + 2] (o values, then m, l)
@@ -1961,7 +1962,8 @@ static_assert(MOE_ITEM_ROWS * (MOE_TPS_MAX / 8) <= PREP_PASSES * PREP_GROUPS,
 // launch's weights (gate and up side by side, or down).  Raw inputs are rows
 // slot / topk of x; prepared inputs are rows slot.  Without an item list
 // (items null: one row's slots) item z is slot z alone, its expert
-// sorted[z] (the routes), skipped when not below a.c.experts.  PRO_SWIGLU (down): x is
+// sorted[z] (the routes; with a.c.routes_k = k > 0 slot k is the shared
+// expert), skipped when not below a.c.experts.  PRO_SWIGLU (down): x is
 // the slots' gate rows and a.c.x2 their up rows (topk 1: row slot), the
 // mid step's SwiGLU and rotation formed in the prepare.
 template <int K, int CB, bool MASKED, int PRO>
@@ -1977,7 +1979,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     it = items[item];
   } else {
     if ((size_t)item >= a.c.ptotal) return;
-    const uint32_t e = sorted[item];
+    // uniform across the workgroup; readfirstlane keeps it in a scalar
+    // register for the address arithmetic that follows
+    const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(
+        a.c.routes_k > 0 && item >= a.c.routes_k ? a.c.shared_expert : (int)sorted[item]);
     if (e >= (uint32_t)a.c.experts) return;
     it = MoeItem{e, (uint32_t)item, 1u, 0u};
   }

@@ -224,7 +224,17 @@ size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
 // path only (moe_uses_gemm false), of the banks' formats and widths.
 struct MoeShared {
   MoeBank gate, up, down;
+  // one row with its k routes given (routes_k = k > 0): a.inds / a.scores
+  // are the caller's k routes (scores in a.sdt) and slot k the shared
+  // expert, whose gate sigmoid(logit or x . gate_vec) (xdt) the combine
+  // forms; no route launch (see moe_shared_direct)
+  int routes_k = 0;
+  const void *logit = nullptr, *gate_vec = nullptr;
 };
+// Whether launch_moe takes a one-row swiglu_shared call with given routes
+// without the route launch (its launches are small enough for the mid step
+// in the down GEMV's prepare).
+bool moe_shared_direct(const MoeArgs &a, bool gu_generic, bool d_generic);
 hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                       const MoeBank &down, void *scratch, size_t scratch_bytes,
                       const Scratch &slots, hipStream_t s, const MoeShared *shared = nullptr);

@@ -848,6 +848,25 @@ __device__ __forceinline__ float round_act(float v, int dt) {
   return v;
 }
 
+// The shared expert's gate of row `row` (one wave; every lane returns it):
+// sigmoid of the given logit, or of f(x . gate_vec) summed lane-strided
+// then across the wave, rounded to the activation dtype xdt.
+__device__ __forceinline__ float shared_gate(size_t row, int lane, const void *logit,
+                                             const void *gate_vec, const void *x, int xdt,
+                                             int hidden) {
+  float lg;
+  if (logit != nullptr) {
+    lg = load_act(logit, row, xdt);
+  } else {
+    float d = 0.0f;
+    for (int i = lane; i < hidden; i += 64)
+      d += load_act(x, row * hidden + i, xdt) * load_act(gate_vec, i, xdt);
+    for (int m = 32; m >= 1; m >>= 1) d += __shfl_xor(d, m, 64);
+    lg = round_act(d, xdt);
+  }
+  return round_act(1.0f / (1.0f + expf(-lg)), xdt);
+}
+
 __global__ __launch_bounds__(64) void moe_shared_route_kernel(
     const uint32_t *__restrict__ inds, const void *__restrict__ scores, int sdt,
     const void *__restrict__ logits, int E, int k, const void *__restrict__ logit,
@@ -909,20 +928,48 @@ __global__ __launch_bounds__(64) void moe_shared_route_kernel(
     inds_out[row * kk + lane] = inds[row * k + lane];
     scores_out[row * kk + lane] = load_act(scores, row * k + lane, sdt);
   }
-  float lg;
-  if (logit != nullptr) {
-    lg = load_act(logit, row, xdt);
-  } else {
-    float d = 0.0f;
-    for (int i = lane; i < hidden; i += 64)
-      d += load_act(x, row * hidden + i, xdt) * load_act(gate_vec, i, xdt);
-    for (int m = 32; m >= 1; m >>= 1) d += __shfl_xor(d, m, 64);
-    lg = round_act(d, xdt);
-  }
+  const float gate = shared_gate(row, lane, logit, gate_vec, x, xdt, hidden);
   if (lane == 0) {
     inds_out[row * kk + k] = (uint32_t)E;
-    scores_out[row * kk + k] = round_act(1.0f / (1.0f + expf(-lg)), xdt);
+    scores_out[row * kk + k] = gate;
   }
+}
+
+// The combine of a one-row swiglu_shared call whose k routes are given
+// (no route launch): y[row] = sum over the routed slots j < k (expert below
+// experts) of score_j * d[slot j], then + gate * d[slot k], gate the shared
+// expert's sigmoid formed here by one wave as moe_shared_route_kernel forms
+// it; the same f32 operations in the same order as moe_combine_kernel over
+// that kernel's (k + 1)-wide routes, so results are equal bit for bit.
+__global__ __launch_bounds__(256) void moe_combine_shared_kernel(
+    const uint16_t *__restrict__ d, const uint32_t *__restrict__ inds,
+    const void *__restrict__ scores, int sdt, int k, int experts,
+    const void *__restrict__ logit, const void *__restrict__ gate_vec,
+    const void *__restrict__ x, int xdt, int hidden, void *__restrict__ y, int ydt) {
+  __shared__ float gsh;
+  const size_t row = blockIdx.y;
+  if (threadIdx.x < 64) {
+    const float gate = shared_gate(row, (int)threadIdx.x, logit, gate_vec, x, xdt, hidden);
+    if (threadIdx.x == 0) gsh = gate;
+  }
+  __syncthreads();
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= hidden) return;
+  const size_t kk = (size_t)k + 1;
+  float acc = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t e = inds[row * k + j];
+    if (e >= (uint32_t)experts) continue;
+    const float w = load_act(scores, row * k + j, sdt);
+    acc = acc + f32_value(w * h2f(d[(row * kk + j) * hidden + i]));
+  }
+  acc = acc + f32_value(gsh * h2f(d[(row * kk + k) * hidden + i]));
+  if (ydt == OUT_F16)
+    ((uint16_t *)y)[row * hidden + i] = f2h(acc);
+  else if (ydt == OUT_BF16)
+    ((uint16_t *)y)[row * hidden + i] = f2bf(acc);
+  else
+    ((float *)y)[row * hidden + i] = acc;
 }
 
 hipError_t launch_moe_shared_route(const uint32_t *inds, const void *scores, int sdt,
@@ -1080,6 +1127,13 @@ MoeGemv moe_gemv(const void *x, int xdt, bool prepared, size_t slots, int in, in
 
 }  // namespace
 
+bool moe_shared_direct(const MoeArgs &a, bool gu_generic, bool d_generic) {
+  if (a.rows != 1 || a.topk <= 0 || a.experts <= 0 || a.hidden % 128 != 0) return false;
+  const MoeLayout L = moe_layout(a, gu_generic, d_generic);
+  return !L.gemm &&
+         (size_t)(a.hidden / 128) * L.ks_d * L.slots <= MOE_FUSED_MID_MAX_WG;
+}
+
 size_t moe_scratch_bytes(const MoeArgs &a, bool gu_generic, bool d_generic,
                          size_t *partial_floats) {
   if (a.rows <= 0 || a.topk <= 0) {
@@ -1114,6 +1168,11 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
       return hipErrorInvalidValue;
   }
   const int sh_index = shared ? a.experts - 1 : -1;
+  // one row, k routes given: slot k is the shared expert, no route launch
+  const int routes_k = shared ? shared->routes_k : 0;
+  if (routes_k > 0 && (a.rows != 1 || a.inds == nullptr || a.topk != routes_k + 1 ||
+                       (shared->logit == nullptr && shared->gate_vec == nullptr)))
+    return hipErrorInvalidValue;
   if (scratch_bytes < L.total || slots.status == nullptr || slots.partial == nullptr ||
       slots.partial_floats < L.partial_floats || L.slots > 65535 ||
       L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
@@ -1170,6 +1229,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   // k-slice in its prepare, which costs less than the mid launch; in larger
   // launches the repeats across column groups cost more than the launch
   const bool fused_mid = (size_t)grid_d.x * grid_d.y * grid_d.z <= MOE_FUSED_MID_MAX_WG;
+  if (routes_k > 0 && !fused_mid) return hipErrorInvalidValue;
   MoeGemv md = fused_mid ? moe_gemv(g, OUT_F16, false, L.slots, a.inter, a.hidden, down.f, L.ks_d,
                                     L.tps_d)
                          : moe_gemv(xd, OUT_F16, true, L.slots, a.inter, a.hidden, down.f, L.ks_d,
@@ -1192,6 +1252,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   const MoeItem *iitems = direct ? nullptr : items;
   const uint32_t *in_items = direct ? nullptr : n_items;
   mgu.a.c.experts = md.a.c.experts = a.experts;
+  mgu.a.c.routes_k = md.a.c.routes_k = routes_k;
   mgu.tw[0] = reinterpret_cast<const uint32_t *>(gate.trellis);
   mgu.tw[1] = reinterpret_cast<const uint32_t *>(up.trellis);
   mgu.a.w[0] = moe_weight(gate, g, pgu);
@@ -1220,8 +1281,13 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   }
   moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md,
                   isorted, iitems, in_items, fused_mid ? 1 : a.topk);
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s, d,
-                     a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
+  if (routes_k > 0)
+    hipLaunchKernelGGL(moe_combine_shared_kernel, dim3((a.hidden + 255) / 256, 1), dim3(256), 0,
+                       s, d, a.inds, a.scores, a.sdt, routes_k, a.experts, shared->logit,
+                       shared->gate_vec, a.x, a.xdt, a.hidden, a.y, a.ydt);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((a.hidden + 255) / 256, a.rows), dim3(256), 0, s,
+                       d, a.inds, a.scores, a.sdt, a.topk, a.experts, a.hidden, a.y, a.ydt);
   return hipGetLastError();
 }
 

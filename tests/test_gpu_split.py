@@ -186,6 +186,32 @@ def test_swiglu_shared_against_oracle(rows, mode):
     assert (S.row_rel(got, want) < 3e-3).all()
 
 
+@pytest.mark.parametrize("gate", ["logit", "gate_vec"])
+def test_swiglu_shared_one_row_equals_batched_row(gate):
+    # one row with given routes runs without the route launch (the routed
+    # launches read the k routes, the combine forms the shared gate); the
+    # same row inside a 2-row call runs through the route launch: equal bit
+    # for bit, gate from the logit or from x . gate_vec
+    rng = np.random.default_rng(950 + len(gate))
+    E, hidden, inter, k, n = 8, 512, 256, 3, 64
+    parts, banks, keep = _banks(rng, E, hidden, inter, n)
+    sparts = [S.linear(rng, hidden, inter, n), S.linear(rng, hidden, inter, n),
+              S.linear(rng, inter, hidden, n)]
+    shared = [X.Linear(dev_u16(t), dev_f16(u), dev_f16(v)) for t, u, v in sparts]
+    x = S.activations(rng, 2, hidden)
+    logits = rng.standard_normal((2, E)).astype(np.float32)
+    inds, scores = O.route_topk(logits, k)
+    kw = ({"logit": dev_f16(rng.standard_normal(2).astype(np.float16))} if gate == "logit" else
+          {"gate_vec": dev_f16((rng.standard_normal(hidden) * 0.05).astype(np.float16))})
+    ti, ts = torch.from_numpy(inds).to(DEV), torch.from_numpy(scores).to(DEV)
+    y2 = X.swiglu_shared(*banks, dev_f16(x), [s.weight for s in shared], inds=ti, scores=ts, **kw)
+    kw1 = {key: v[:1] for key, v in kw.items()} if gate == "logit" else kw
+    y1 = X.swiglu_shared(*banks, dev_f16(x[:1]), [s.weight for s in shared], inds=ti[:1].contiguous(),
+                         scores=ts[:1].contiguous(), **kw1)
+    torch.cuda.synchronize()
+    assert torch.equal(y1[0], y2[0])
+
+
 def test_swiglu_shared_refusals():
     rng = np.random.default_rng(901)
     E, hidden, inter, k, n = 8, 512, 256, 2, 64
