@@ -351,7 +351,8 @@ def test_load_from_safetensors_pack(tmp_path):
 
 def _bank(rng, E, in_f, out_f, n):
     t, u, v = S.linear(rng, in_f, out_f, n, experts=E)
-    return (t, u, v), X.wrap(dev_u16(t), dev_f16(u), dev_f16(v)), (dev_u16(t), dev_f16(u), dev_f16(v))
+    w = X.wrap(dev_u16(t), dev_f16(u), dev_f16(v))
+    return (t, u, v), w, w._keep  # the wrapped tensors themselves (the Weight holds them too)
 
 
 @pytest.mark.parametrize("rows,limit", [(1, 0), (3, 0), (16, 0), (5, 10), (64, 0)])
