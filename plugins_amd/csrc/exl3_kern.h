@@ -726,6 +726,86 @@ constexpr int PARTIAL_POLL_MAX = 1 << 20;
 #ifndef EXL3_POLL_SLEEP
 #define EXL3_POLL_SLEEP 2
 #endif
+
+// The last split's sum of the other splits' slots for this thread's
+// elements e = e0 + tid + GEMV_THREADS j (j < EM, e < E): rounds of KC splits,
+// every element's slots of a round read at once; a slot still empty is read
+// again in the same round (at most poll_max times), and each slot read is
+// set back to the empty mark.  zf[e] = f16(sum_k v_k + zf[e]), the sum in
+// split order.  Returns whether a wait gave up.
+template <int EM, int KC>
+__device__ __forceinline__ bool splitk_sum(float *zf, __amdgpu_buffer_rsrc_t pr, uint32_t sstride,
+                                           float *partial, size_t stride, int E, int e0, int ks,
+                                           const RowMap &rm, size_t out, int col0, int poll_max) {
+  static_assert(EM * KC <= 32, "one pending bit per read");
+  const float empty = bits<float>(PARTIAL_EMPTY);
+  uint32_t po[EM];
+  float s[EM];
+  bool live[EM];
+#pragma unroll
+  for (int i = 0; i < EM; ++i) {
+    const int e = e0 + threadIdx.x + GEMV_THREADS * i;
+    live[i] = e < E;
+    const int ec = live[i] ? e : 0;  // (a dead element's place is never read)
+    po[i] = (uint32_t)(((size_t)rm.prow(ec >> 7) * out + col0 + (ec & 127)) * 4);
+    s[i] = 0.0f;
+  }
+  bool gave_up = false;
+  for (int k0 = 0; k0 < ks; k0 += KC) {
+    const int nk = min(KC, ks - k0);
+    float v[EM][KC];
+    uint32_t pending = 0;
+#pragma unroll
+    for (int i = 0; i < EM; ++i)
+#pragma unroll
+      for (int j = 0; j < KC; ++j)
+        if (live[i] && j < nk) v[i][j] = ld_agent_at(pr, po[i], (uint32_t)(k0 + j) * sstride);
+#pragma unroll
+    for (int i = 0; i < EM; ++i)
+#pragma unroll
+      for (int j = 0; j < KC; ++j)
+        if (live[i] && j < nk && bits<uint32_t>(v[i][j]) == PARTIAL_EMPTY)
+          pending |= 1u << (i * KC + j);
+#ifdef EXL3_TIMELINE
+    if (k0 == 0) EXL3_TL(7);
+#endif
+    for (int n = 0; pending != 0 && n < poll_max; ++n) {
+      __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
+#pragma unroll
+      for (int i = 0; i < EM; ++i)
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+          if (pending & (1u << (i * KC + j)))
+            v[i][j] = ld_agent_at(pr, po[i], (uint32_t)(k0 + j) * sstride);
+#pragma unroll
+      for (int i = 0; i < EM; ++i)
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+          if ((pending & (1u << (i * KC + j))) && bits<uint32_t>(v[i][j]) != PARTIAL_EMPTY)
+            pending &= ~(1u << (i * KC + j));
+    }
+    gave_up |= pending != 0;
+#pragma unroll
+    for (int i = 0; i < EM; ++i) {
+      if (!live[i]) continue;
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        if (j >= nk) break;
+        if (!(pending & (1u << (i * KC + j))))
+          st_agent(partial + (po[i] >> 2) + (size_t)(k0 + j) * stride, empty);
+        s[i] = s[i] + v[i][j];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < EM; ++i) {
+    const int e = e0 + threadIdx.x + GEMV_THREADS * i;
+    if (live[i]) zf[e] = h2f(f2h(s[i] + zf[e]));
+  }
+  return gave_up;
+}
+
+template <bool MULTI>
 __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, float *partial,
                                                  int nrows, const RowMap &rm, int ks, size_t out,
                                                  int col0) {
@@ -749,49 +829,25 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
 #endif
     return false;
   }
-  const float empty = bits<float>(PARTIAL_EMPTY);
   const __amdgpu_buffer_rsrc_t pr = buffer_of(partial);
   const uint32_t sstride = (uint32_t)(stride * 4);  // bytes between splits' planes
+  // a thread's elements e = tid + 512 j.  MULTI (the rows-form launches,
+  // many rows): the elements share each round of slot reads (2 elements x 8
+  // splits, or 4 x 4), so the rows beyond 4 cost few extra round trips;
+  // else (launches of few rows, whose registers set their occupancy) one
+  // element at a time, 16 splits a round
   bool gave_up = false;
-  for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
-    const int b = e >> 7, col = e & 127;
-    const uint32_t po = (uint32_t)(((size_t)rm.prow(b) * out + col0 + col) * 4);
-    float s = 0.0f;
-    for (int k0 = 0; k0 < ks; k0 += 16) {
-      const int nk = min(16, ks - k0);
-      float v[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (j < nk)
-          v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
-      // every slot still empty is read again in the same round, so the wait
-      // is one round trip after the last store lands (not one per slot)
-      uint32_t pending = 0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (j < nk && bits<uint32_t>(v[j]) == PARTIAL_EMPTY) pending |= 1u << j;
-#ifdef EXL3_TIMELINE
-      if (e == threadIdx.x && k0 == 0) EXL3_TL(7);
-#endif
-      for (int n = 0; pending != 0 && n < a.poll_max; ++n) {
-        __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (pending & (1u << j)) v[j] = ld_agent_at(pr, po, (uint32_t)(k0 + j) * sstride);
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if ((pending & (1u << j)) && bits<uint32_t>(v[j]) != PARTIAL_EMPTY) pending &= ~(1u << j);
-      }
-      gave_up |= pending != 0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (j >= nk) break;
-        if (!(pending & (1u << j)))
-          st_agent(partial + (po >> 2) + (size_t)(k0 + j) * stride, empty);
-        s = s + v[j];
-      }
-    }
-    zf[e] = h2f(f2h(s + zf[e]));
+  if constexpr (MULTI) {
+    if (E <= 2 * GEMV_THREADS)
+      gave_up = splitk_sum<2, 8>(zf, pr, sstride, partial, stride, E, 0, ks, rm, out, col0,
+                                 a.poll_max);
+    else
+      gave_up = splitk_sum<4, 4>(zf, pr, sstride, partial, stride, E, 0, ks, rm, out, col0,
+                                 a.poll_max);
+  } else {
+    for (int e0 = 0; e0 < E; e0 += GEMV_THREADS)
+      gave_up |= splitk_sum<1, 16>(zf, pr, sstride, partial, stride, E, e0, ks, rm, out, col0,
+                                   a.poll_max);
   }
   if (gave_up) atomicOr(a.status, 1u);
   lds_barrier();
@@ -1114,7 +1170,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   lds_barrier();
   EXL3_TL(3);
-  if (!gemv_splitk_last(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) {
+  if (!gemv_splitk_last<!ONEB>(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) {
     EXL3_TL(4);
     return;
   }

@@ -14,10 +14,11 @@ p90, max; microseconds from the launch's first wave) of:
 and for gate+up the medians per dispatch round (workgroup id // 256: the
 first, second and third workgroup each CU holds).
 
-    python -m plugins_amd.timeline [--lib PATH]
+    python -m plugins_amd.timeline [--lib PATH] [--batch N]
 
 --lib: another timeline build of the library (the default is the one
-`python -m plugins_amd.build --timeline` writes).
+`python -m plugins_amd.build --timeline` writes); --batch: rows of the
+activations (default 1; 16 is config 4's batch).
 """
 from __future__ import annotations
 
@@ -49,9 +50,10 @@ def main() -> int:
     L.exl3_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     L.exl3_timeline_clear.argtypes = []
     import bench
+    rows = int(sys.argv[sys.argv.index("--batch") + 1]) if "--batch" in sys.argv else 1
     lins = bench.build_model(torch, X, 36, seed=1234, k_bits=4)
-    xs = {i: torch.randn(1, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
-    ys = [torch.empty(1, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
+    xs = {i: torch.randn(rows, i, device="cuda").to(torch.float16) for i in (4096, 12288)}
+    ys = [torch.empty(rows, o, dtype=torch.float16, device="cuda") for _, _, o, _ in lins]
     kinds = {"q+k+v": [0, 1, 2], "o": [3], "gate+up": [4, 5], "down": [6]}
 
     def launch(g):
