@@ -15,6 +15,8 @@
 #include <type_traits>
 
 #include "../../include/exl3_decoder.h"
+#include "exl3_device.h"
+#include "exl3_kernels.h"
 
 namespace {
 
@@ -67,11 +69,20 @@ __global__ __launch_bounds__(64) void embed_ssq_kernel(const int32_t *__restrict
 constexpr int RN_THREADS = 512;
 constexpr int RN_PER = 2;  // 8-element pieces per thread: rows up to 8192
 
+// Consumers of the normalized rows (PREP): each gets the rows prepared with
+// its suh, set c of xp at c * rows * H.
+struct PrepTo {
+  const uint16_t *suh[4];
+  uint16_t *xp;
+  int count;
+};
+
+template <bool PREP>
 __global__ __launch_bounds__(RN_THREADS) void add_rmsnorm_kernel(float *__restrict__ h,
                                                                  const uint16_t *__restrict__ add,
                                                                  const uint16_t *__restrict__ w,
                                                                  uint16_t *__restrict__ out, int H,
-                                                                 float eps) {
+                                                                 float eps, PrepTo pt) {
   __shared__ float part[RN_THREADS / 64];
   float *hr = h + (size_t)blockIdx.x * H;
   const uint16_t *ar = add ? add + (size_t)blockIdx.x * H : nullptr;
@@ -120,7 +131,17 @@ __global__ __launch_bounds__(RN_THREADS) void add_rmsnorm_kernel(float *__restri
       for (int e = 0; e < 4; ++e)
         o4[e] = (uint32_t)f2h(v[j][2 * e] * r * h2f((uint16_t)(ww[e] & 0xFFFFu))) |
                 ((uint32_t)f2h(v[j][2 * e + 1] * r * h2f((uint16_t)(ww[e] >> 16))) << 16);
-      *reinterpret_cast<uint4 *>(orow + i) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+      if constexpr (PREP) {
+        // H a multiple of 512: a wave's 64 lanes are all in range here, and
+        // 16 consecutive lanes hold one 128-block
+        for (int c = 0; c < pt.count; ++c) {
+          const uint4 su = *reinterpret_cast<const uint4 *>(pt.suh[c] + i);
+          const uint4 pv = exl3::prep_block8(o4, su, (int)(threadIdx.x & 15));
+          *reinterpret_cast<uint4 *>(pt.xp + ((size_t)c * gridDim.x + blockIdx.x) * H + i) = pv;
+        }
+      } else {
+        *reinterpret_cast<uint4 *>(orow + i) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+      }
     }
   }
 }
@@ -605,7 +626,8 @@ int exl3d_embed(const int32_t *ids, int B, const uint16_t *table, int H, float *
 int exl3d_add_rmsnorm(float *h, const uint16_t *add, const uint16_t *w, uint16_t *out, int B,
                       int H, float eps, hipStream_t s) {
   if (B <= 0 || H <= 0 || H % 8 != 0 || H > RN_THREADS * RN_PER * 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(B), dim3(RN_THREADS), 0, s, h, add, w, out, H, eps);
+  hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3(B), dim3(RN_THREADS), 0, s, h, add, w, out, H,
+                     eps, PrepTo{});
   return hipGetLastError();
 }
 
@@ -673,3 +695,25 @@ int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n
 }
 
 }  // extern "C"
+
+namespace exl3 {
+
+hipError_t launch_rmsnorm_prepare(const float *h, const uint16_t *w, int B, int H, float eps,
+                                  const uint16_t *const *suh, int count, uint16_t *xp,
+                                  hipStream_t s) {
+  if (B <= 0 || B > 65535 || H <= 0 || H % 512 != 0 || H > RN_THREADS * RN_PER * 8 ||
+      count < 1 || count > 4 || xp == nullptr)
+    return hipErrorInvalidValue;
+  PrepTo pt{};
+  for (int c = 0; c < count; ++c) {
+    if (suh[c] == nullptr) return hipErrorInvalidValue;
+    pt.suh[c] = suh[c];
+  }
+  pt.xp = xp;
+  pt.count = count;
+  hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3(B), dim3(RN_THREADS), 0, s,
+                     const_cast<float *>(h), nullptr, w, nullptr, H, eps, pt);
+  return hipGetLastError();
+}
+
+}  // namespace exl3

@@ -329,4 +329,41 @@ __device__ __forceinline__ void had128_lds(float *v, int rows, int tid, int nthr
   }
 }
 
+// The prepare of the 128-block that 16 consecutive lanes hold, 8 elements
+// each (lane j of the group: elements 8j .. 8j + 7, given as f16 pairs xo):
+// f16(x) * suh in f32, Hadamard-128 with stages on index bits 0-2 in
+// register and 3-6 across the 16 lanes, each (lo + hi, lo - hi) as
+// had128_pair forms them, * 1/sqrt(128), f16 pairs.  The GEMV prologue's
+// rows form and prepare8_kernel run the same operations in the same order.
+// All 64 lanes of the wave take part (xor_lanes).
+__device__ __forceinline__ uint4 prep_block8(const uint32_t (&xo)[4], uint4 su, int j) {
+  const uint32_t ss[4] = {su.x, su.y, su.z, su.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f((uint16_t)(xo[i] & 0xFFFFu)) * h2f((uint16_t)(ss[i] & 0xFFFFu));
+    v[2 * i + 1] = h2f((uint16_t)(xo[i] >> 16)) * h2f((uint16_t)(ss[i] >> 16));
+  }
+#pragma unroll
+  for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if ((i & b) == 0) {
+        const float lo = v[i], hi = v[i + b];
+        v[i] = lo + hi;
+        v[i + b] = lo - hi;
+      }
+#pragma unroll
+  for (int bit = 1; bit <= 8; bit <<= 1) {
+    const float sg = (j & bit) == 0 ? 1.0f : -1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = butterfly(sg, v[i], xor_lanes(v[i], bit));
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = (uint32_t)f2h(v[2 * i] * HAD_SCALE) | ((uint32_t)f2h(v[2 * i + 1] * HAD_SCALE) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 }  // namespace exl3

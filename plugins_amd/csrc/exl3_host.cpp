@@ -1909,9 +1909,33 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
   const bool pre_norm = norm_w && (!exl3::gemv_one_batch(in, total, !pvs[0]->f.integer_rate(), B) ||
                                    in / 128 > exl3::NORM_MAXBLK);
   const bool pre_swiglu = up && B > exl3::SWIGLU_PROLOGUE_ROWS;
-  if (pre_norm || pre_swiglu) {
-    // rows the prologue does not take: the RMSNorm (of h as it stands) or
-    // the SwiGLU first, into scratch, then a plain GEMV
+  // rows the prologue does not take: the RMSNorm (of h as it stands) or the
+  // SwiGLU first, with each weight's prepare in the same pass where the
+  // shapes allow (every column group of the GEMV would otherwise redo the
+  // prepare of its k-slice for all rows), into scratch as stacked prepared
+  // rows; else the plain rows, then a GEMV that prepares them
+  const bool prep_norm = pre_norm && in % 512 == 0 && in <= 8192;
+  const bool prep_swiglu = pre_swiglu && count == 1 && in % 128 == 0;
+  if (prep_norm || prep_swiglu) {
+    const int sets = prep_norm ? count : 1;
+    e = grow(ss, &ss->xp, &ss->xp_bytes, (size_t)sets * B * in * sizeof(uint16_t), s);
+    if (e != hipSuccess) return e;
+    uint16_t *xs = (uint16_t *)ss->xp;
+    if (prep_norm) {
+      const uint16_t *suhs[4];
+      for (int i = 0; i < count; ++i) suhs[i] = ls[i].suh;
+      e = exl3::launch_rmsnorm_prepare((const float *)x, norm_w, B, in, eps, suhs, count, xs, s);
+      fz.nssq = nullptr;
+      fz.norm_w = nullptr;
+    } else {
+      e = exl3::launch_swiglu_prepare((const uint16_t *)x, up, ls[0].suh, xs, B, in, 0.0f, s);
+      fz.up = nullptr;
+    }
+    if (e != hipSuccess) return e;
+    fz.stacked = true;
+    x = xs;
+    xdt = exl3::ACT_F16;
+  } else if (pre_norm || pre_swiglu) {
     e = grow(ss, &ss->xp, &ss->xp_bytes, (size_t)B * in * sizeof(uint16_t), s);
     if (e != hipSuccess) return e;
     uint16_t *xs = (uint16_t *)ss->xp;

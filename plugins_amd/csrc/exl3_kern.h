@@ -225,9 +225,10 @@ struct GemvArgs {
 // costs a load; gridDim itself is a load from the implicit arguments):
 //   g0 = cg1 | cg2 << 16     first column groups of weights 1, 2 (0: absent)
 //   g1 = cg3 | cgend << 16   ... of weight 3, and the end of the last weight
-//   g2 = in_tiles | tps << 16 | rows << 23 | xdt << 28 | prepared << 30
+//   g2 = in_tiles | tps << 16 | rows << 23 | xdt << 28 | prepared << 30 |
+//        stacked << 31 (prepared rows: one [rows][in] set per weight, stacked)
 struct GemvGeo {
-  int cg1, cg2, cg3, cgend, in_tiles, tps, rows, xdt, prepared;
+  int cg1, cg2, cg3, cgend, in_tiles, tps, rows, xdt, prepared, stacked;
   __host__ __device__ static GemvGeo unpack(uint32_t g0, uint32_t g1, uint32_t g2) {
     GemvGeo g;
     g.cg1 = (int)(g0 & 0xFFFFu);
@@ -239,11 +240,12 @@ struct GemvGeo {
     g.rows = (int)((g2 >> 23) & 0x1Fu);
     g.xdt = (int)((g2 >> 28) & 3u);
     g.prepared = (int)((g2 >> 30) & 1u);
+    g.stacked = (int)(g2 >> 31);
     return g;
   }
 };
 // Fields: cg1, cg2, cg3, cgend, in_tiles 16 bits each; tps / 8 in 7 bits
-// (tps a multiple of 8, at most 1016); rows 5, xdt 2, prepared 1.  False
+// (tps a multiple of 8, at most 1016); rows 5, xdt 2, prepared 1, stacked 1.  False
 // when a value does not fit its field (the launchers refuse the launch).
 inline bool gemv_geo_pack(const GemvGeo &g, uint32_t *g0, uint32_t *g1, uint32_t *g2) {
   if (g.cg1 < 0 || g.cg1 > 0xFFFF || g.cg2 < 0 || g.cg2 > 0xFFFF || g.cg3 < 0 ||
@@ -254,7 +256,8 @@ inline bool gemv_geo_pack(const GemvGeo &g, uint32_t *g0, uint32_t *g1, uint32_t
   *g0 = (uint32_t)g.cg1 | ((uint32_t)g.cg2 << 16);
   *g1 = (uint32_t)g.cg3 | ((uint32_t)g.cgend << 16);
   *g2 = (uint32_t)g.in_tiles | ((uint32_t)(g.tps / 8) << 16) | ((uint32_t)g.rows << 23) |
-        ((uint32_t)g.xdt << 28) | ((uint32_t)(g.prepared & 1) << 30);
+        ((uint32_t)g.xdt << 28) | ((uint32_t)(g.prepared & 1) << 30) |
+        ((uint32_t)(g.stacked & 1) << 31);
   return true;
 }
 
@@ -627,48 +630,55 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
   for (int p = 0; p < NP; ++p) {
     const int G = min((int)(threadIdx.x >> 4) + PREP_GROUPS * p, nblk - 1);
     const int row = G / nb, blk = G - row * nb;
-    float v[8];
+    uint32_t y[4];
+    if (prepared) {
+      // prepared rows (a producer formed the rotation): taken as they are,
+      // the rotation's VALU work skipped (a uniform branch)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float a, b;
-      if constexpr (PRO == PRO_SWIGLU) {
-        swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
-      } else {
-        prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
-        const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
-        const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
-        if (!prepared && xdt == OUT_F32) {
-          a = fa;
-          b = fb;
+      for (int e = 0; e < 4; ++e) y[e] = r.x[p][0][e];
+    } else {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a, b;
+        if constexpr (PRO == PRO_SWIGLU) {
+          swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
+        } else {
+          prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
+          const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
+          const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
+          if (xdt == OUT_F32) {
+            a = fa;
+            b = fb;
+          }
+        }
+        const uint32_t su = r.su[p][e];
+        v[2 * e] = h2f(f2h(a)) * h2f((uint16_t)(su & 0xFFFFu));
+        v[2 * e + 1] = h2f(f2h(b)) * h2f((uint16_t)(su >> 16));
+      }
+      // stages on bits 0, 1, 2 (in-register), then 3-6 (lanes xor 1, 2, 4, 8)
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (e & m) continue;
+          const float lo = v[e], hi = v[e + m];
+          v[e] = lo + hi;
+          v[e + m] = lo - hi;
         }
       }
-      const uint32_t su = r.su[p][e];
-      v[2 * e] = h2f(f2h(a)) * h2f((uint16_t)(su & 0xFFFFu));
-      v[2 * e + 1] = h2f(f2h(b)) * h2f((uint16_t)(su >> 16));
-    }
-    // stages on bits 0, 1, 2 (in-register), then 3-6 (lanes xor 1, 2, 4, 8)
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
+      for (int m = 1; m < 16; m <<= 1) {
+        const float sg = (li & m) == 0 ? 1.0f : -1.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (e & m) continue;
-        const float lo = v[e], hi = v[e + m];
-        v[e] = lo + hi;
-        v[e + m] = lo - hi;
+        for (int e = 0; e < 8; ++e) v[e] = butterfly(sg, v[e], xor_lanes(v[e], m));
       }
-    }
 #pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      const float sg = (li & m) == 0 ? 1.0f : -1.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = butterfly(sg, v[e], xor_lanes(v[e], m));
-    }
-    uint32_t y[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t rot =
-          (uint32_t)f2h(v[2 * e] * HAD_SCALE) | ((uint32_t)f2h(v[2 * e + 1] * HAD_SCALE) << 16);
-      y[e] = prepared ? r.x[p][0][e] : rot;
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t rot =
+            (uint32_t)f2h(v[2 * e] * HAD_SCALE) | ((uint32_t)f2h(v[2 * e + 1] * HAD_SCALE) << 16);
+        y[e] = rot;
+      }
     }
     const u4_t yv = {y[0], y[1], y[2], y[3]};
     *reinterpret_cast<u4_t *>(xs + row * kr + blk * 128 + 8 * li) = yv;
@@ -1206,7 +1216,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
   const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
   const int out_tiles = 8 * (ws.c1 - ws.c0);
   const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
-  gemv_wg<K, CB, MASKED, PREP, PRO>(tw, out_tiles, x, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
+  // stacked prepared rows: weight wi's set follows the sets of weights < wi
+  const void *xw = geo.stacked ? (const void *)((const uint16_t *)x + (size_t)ws.wi * geo.rows *
+                                                                          geo.in_tiles * 16)
+                               : x;
+  gemv_wg<K, CB, MASKED, PREP, PRO>(tw, out_tiles, xw, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
                                blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
 }
 

@@ -145,6 +145,9 @@ struct GemvFuse {
   // [rows][attn_nkv][attn_nsplit][attn_g][128 + 2], combined in the prepare
   const float *attn_part = nullptr;
   int attn_nkv = 0, attn_g = 0, attn_nsplit = 0;
+  // x holds prepared rows, one [rows][in] set per weight, stacked in the
+  // weights' order (a producer formed each weight's prepare)
+  bool stacked = false;
 };
 hipError_t launch_gemv_fused(const GemvLinear *ls, int count, const Format &f, const void *x,
                              int xdt, int ydt, int rows, int in, Scratch *sc, const GemvFuse &fz,
@@ -154,6 +157,17 @@ constexpr int NORM_MAXBLK = 64;
 // Whether a GEMV launch's rows fit one prepare batch (what the RMSNorm
 // prologue needs).
 bool gemv_one_batch(int in, int total_out, bool generic, int rows);
+// xp = the prepare (with suh, the consumer linear's) of h = f16(silu(g) *
+// u) over [rows][in], in one launch: the prepared rows a GEMV with
+// GemvFuse.stacked reads (in a multiple of 128).
+hipError_t launch_swiglu_prepare(const uint16_t *g, const uint16_t *u, const uint16_t *suh,
+                                 uint16_t *xp, int rows, int in, float limit, hipStream_t s);
+// The RMSNorm of an f32 residual h [B][H] (exl3d_add_rmsnorm's arithmetic)
+// prepared for `count` (<= 4) consumer linears: xp holds count stacked
+// [B][H] sets, set c prepared with suh[c] (H a multiple of 512, <= 8192).
+hipError_t launch_rmsnorm_prepare(const float *h, const uint16_t *w, int B, int H, float eps,
+                                  const uint16_t *const *suh, int count, uint16_t *xp,
+                                  hipStream_t s);
 // h = f16(silu(g) * u) elementwise, the SwiGLU prologue's arithmetic.
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, uint16_t *h, size_t n, float limit,
                          hipStream_t s);

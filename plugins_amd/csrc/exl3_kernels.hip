@@ -481,7 +481,8 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   geo.cgend = totcg;
   geo.rows = rows;
   geo.xdt = xdt;
-  geo.prepared = prepared ? 1 : 0;
+  geo.prepared = prepared || fz.stacked ? 1 : 0;
+  geo.stacked = fz.stacked ? 1 : 0;
   geo.in_tiles = in / 16;
   geo.tps = tps;
   uint32_t g0, g1, g2;
@@ -494,6 +495,9 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
       (!oneb || xdt != OUT_F32 || prepared || fz.norm_w == nullptr || in / 128 > NORM_MAXBLK))
     return hipErrorInvalidValue;
   if (fz.res != nullptr && (count != 1 || fz.res_ssq == nullptr)) return hipErrorInvalidValue;
+  if (fz.stacked && (xdt != OUT_F16 || fz.nssq != nullptr || fz.up != nullptr ||
+                     fz.attn_part != nullptr))
+    return hipErrorInvalidValue;
   if (fz.attn_part != nullptr &&
       (!oneb || count != 1 || xdt != OUT_F16 || prepared || fz.nssq != nullptr ||
        fz.up != nullptr || fz.attn_nkv < 1 || fz.attn_g < 1 || fz.attn_nsplit < 1 ||
@@ -520,6 +524,35 @@ hipError_t launch_gemv_fused(const GemvLinear *ls, int count, const Format &f, c
 
 namespace {
 // h = f16(silu(g) * u) elementwise (the prologue's arithmetic, swiglu1).
+// h = f16(silu(g) * u) and its prepare with suh (the consumer's), in one
+// pass: a 16-lane group per 128-block of the flattened [rows][in] (in a
+// multiple of 128), 8 elements a lane; the prepared rows equal what the
+// GEMV prologue forms from h (prep_block8).  Groups past the last block
+// redo the last one (whole waves), storing nothing.
+__global__ __launch_bounds__(256) void swiglu_prepare_kernel(const uint16_t *__restrict__ g,
+                                                             const uint16_t *__restrict__ u,
+                                                             const uint16_t *__restrict__ suh,
+                                                             uint16_t *__restrict__ xp, int nblk,
+                                                             uint32_t nblocks, float limit) {
+  const int j = threadIdx.x & 15;
+  const uint32_t gb0 = blockIdx.x * 16u + (threadIdx.x >> 4);
+  const bool valid = gb0 < nblocks;
+  const uint32_t gb = valid ? gb0 : nblocks - 1;
+  const size_t off = (size_t)gb * 128 + 8 * j;
+  const int k = (int)(gb % (uint32_t)nblk) * 128 + 8 * j;
+  const uint4 gv = *reinterpret_cast<const uint4 *>(g + off);
+  const uint4 uv = *reinterpret_cast<const uint4 *>(u + off);
+  const uint4 su = *reinterpret_cast<const uint4 *>(suh + k);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    h[i] = (uint32_t)f2h(swiglu1((uint16_t)(gw[i] & 0xFFFFu), (uint16_t)(uw[i] & 0xFFFFu), limit)) |
+           ((uint32_t)f2h(swiglu1((uint16_t)(gw[i] >> 16), (uint16_t)(uw[i] >> 16), limit)) << 16);
+  const uint4 o = prep_block8(h, su, j);
+  if (valid) *reinterpret_cast<uint4 *>(xp + off) = o;
+}
+
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ g,
                                                      const uint16_t *__restrict__ u,
                                                      uint16_t *__restrict__ h, size_t n,
@@ -539,12 +572,14 @@ hipError_t launch_gemv_swiglu(const GemvLinear &l, const Format &f, const uint16
     fz.limit = limit;
     return gemv_multi(&l, 1, f, g, OUT_F16, false, ydt, rows, in, &sc, fz, s);
   }
-  // more rows: every column group would redo the rows' SwiGLU, so it runs
-  // once here
+  // more rows: every column group would redo the rows' SwiGLU and prepare,
+  // so both run once here, into prepared rows
   if (h == nullptr) return hipErrorInvalidValue;
-  hipError_t e = launch_swiglu(g, u, h, (size_t)rows * in, limit, s);
+  hipError_t e = launch_swiglu_prepare(g, u, l.suh, h, rows, in, limit, s);
   if (e != hipSuccess) return e;
-  return gemv_multi(&l, 1, f, h, OUT_F16, false, ydt, rows, in, &sc, GemvFuse{}, s);
+  GemvFuse fz{};
+  fz.stacked = true;
+  return gemv_multi(&l, 1, f, h, OUT_F16, false, ydt, rows, in, &sc, fz, s);
 }
 
 hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, uint16_t *h, size_t n, float limit,
@@ -552,6 +587,17 @@ hipError_t launch_swiglu(const uint16_t *g, const uint16_t *u, uint16_t *h, size
   if (n == 0 || !(limit >= 0.0f)) return hipErrorInvalidValue;
   const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, u, h, n, limit);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_prepare(const uint16_t *g, const uint16_t *u, const uint16_t *suh,
+                                 uint16_t *xp, int rows, int in, float limit, hipStream_t s) {
+  if (rows <= 0 || in <= 0 || in % 128 != 0 || !(limit >= 0.0f) || suh == nullptr)
+    return hipErrorInvalidValue;
+  const int nblk = in / 128;
+  const uint32_t nblocks = (uint32_t)rows * (uint32_t)nblk;
+  hipLaunchKernelGGL(swiglu_prepare_kernel, dim3((nblocks + 15) / 16), dim3(256), 0, s, g, u, suh,
+                     xp, nblk, nblocks, limit);
   return hipGetLastError();
 }
 

@@ -279,6 +279,32 @@ def test_linears_fusions(B, H, I):
 
 
 @gpu
+@pytest.mark.parametrize("count", [1, 2, 3])
+def test_linears_norm_prepare_equals_separate_norm(count):
+    # beyond one prepare batch, exl3d_linears forms the RMSNorm and every
+    # weight's prepare in one pass (stacked prepared rows); against the norm
+    # as its own launch followed by the linears on its output: equal bit for
+    # bit (the same norm, the same prepare arithmetic, the same GEMV plan)
+    from plugins_amd import qwen3 as Q
+    B, H = 16, 4096
+    g = torch.Generator().manual_seed(70 + count)
+    lins = [Q.random_linear(torch, H, o, 4, torch.Generator(device="cuda").manual_seed(10 + i))
+            for i, o in enumerate([4096, 1024, 1024][:count])]
+    h = torch.randn(B, H, generator=g).cuda()
+    w = (1 + 0.1 * torch.randn(H, generator=g)).half().cuda()
+    ssq = _ssq(h.cpu()).cuda()
+    outs1 = [torch.empty(B, l.out_features, dtype=torch.float16, device="cuda") for l in lins]
+    Q.linears([l.weight for l in lins], h, outs=outs1, norm_w=w, nssq=ssq, eps=1e-6)
+    xn = torch.empty(B, H, dtype=torch.float16, device="cuda")
+    Q.add_rmsnorm(h.clone(), None, w, xn, 1e-6)
+    outs2 = [torch.empty(B, l.out_features, dtype=torch.float16, device="cuda") for l in lins]
+    Q.linears([l.weight for l in lins], xn, outs=outs2)
+    torch.cuda.synchronize()
+    for a, b in zip(outs1, outs2):
+        assert torch.equal(a, b), float((a.float() - b.float()).abs().max())
+
+
+@gpu
 def test_silu_mul():
     from plugins_amd import qwen3 as Q
     g = torch.Generator().manual_seed(4)
