@@ -97,7 +97,9 @@ int exl3d_linears(const exl3_weight *const *ws, int count, const void *x, int B,
  * that fit one prepare batch of o's GEMV (B = 1 at Qwen3-8B's shapes) skip
  * the combine launch: o's prepare combines the split slots itself, with
  * the combine's arithmetic, so att is not written; other rows combine into
- * att (f16 [B][nq*D]) first.  Results are equal either way.  Returns 0, a
+ * att (f16 [B][nq*D]) first, written as o's prepared rows (the attention
+ * output rotated with o's suh, which o's GEMV then takes as they are).
+ * Results are equal either way.  Returns 0, a
  * HIP error, or -1 when the weight or shapes are refused. */
 int exl3d_attn_o(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *qn,
                  const uint16_t *kn, const int32_t *pos, int B, int nq, int nkv, float eps,

@@ -484,8 +484,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 // / sum_s l_s e^(m_s - M), f16.  One workgroup per (row, kv head): the
 // splits' m and l go through LDS, each thread's o values of 32 splits at a
 // time are in flight together, and every sum runs in split order.
+// suh set: out gets the combined rows prepared for the consumer linear
+// (its suh over the nq * D inputs; the GEMV reads them as prepared rows):
+// each head is one 128-block, prepared by wave 0 (16 lanes a head).
 __global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
-    const float *__restrict__ part, int nq, int nkv, int nsplit, uint16_t *__restrict__ out) {
+    const float *__restrict__ part, int nq, int nkv, int nsplit, uint16_t *__restrict__ out,
+    const uint16_t *__restrict__ suh) {
   constexpr int D = EXL3D_HEAD_DIM;
   constexpr int CH = 32;  // splits whose o values a thread has in flight at once
   __shared__ float msh[AT_G][AC_MAXS], lsh[AT_G][AC_MAXS];
@@ -525,7 +529,23 @@ __global__ __launch_bounds__(AT_G * EXL3D_HEAD_DIM) void attn_combine_kernel(
       }
     }
   }
-  out[((size_t)b * nq + kvh * AT_G + h) * D + d] = f2h(acc / Ls);
+  const uint16_t y = f2h(acc / Ls);
+  if (suh == nullptr) {
+    out[((size_t)b * nq + kvh * AT_G + h) * D + d] = y;
+    return;
+  }
+  static_assert(AT_G * 16 == 64, "one wave prepares the workgroup's heads");
+  __shared__ __attribute__((aligned(16))) uint16_t ob[AT_G][D];
+  ob[h][d] = y;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int hh = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const uint4 xv = *reinterpret_cast<const uint4 *>(&ob[hh][8 * j]);
+    const uint32_t xo[4] = {xv.x, xv.y, xv.z, xv.w};
+    const size_t col = (size_t)(kvh * AT_G + hh) * D + 8 * j;
+    const uint4 su = *reinterpret_cast<const uint4 *>(suh + col);
+    *reinterpret_cast<uint4 *>(out + (size_t)b * nq * D + col) = exl3::prep_block8(xo, su, j);
+  }
 }
 
 
@@ -603,7 +623,7 @@ int attn_launch(bool rope, const uint16_t *q, const RopeArgs &ra, uint16_t *kcac
   // o projection's attention prologue)
   if (out != nullptr)
     hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s,
-                       scratch, nq, nkv, ns, out);
+                       scratch, nq, nkv, ns, out, (const uint16_t *)nullptr);
   return hipGetLastError();
 }
 
@@ -697,6 +717,17 @@ int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n
 }  // extern "C"
 
 namespace exl3 {
+
+hipError_t launch_attn_combine_prepare(const float *part, int B, int nq, int nkv, int Tmax,
+                                       const uint16_t *suh, uint16_t *xp, hipStream_t s) {
+  if (B <= 0 || B > 65535 || nkv <= 0 || nq != AT_G * nkv || suh == nullptr || xp == nullptr)
+    return hipErrorInvalidValue;
+  int ts;
+  const int ns = attn_split(Tmax, B, nkv, &ts);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv, B), dim3(AT_G * EXL3D_HEAD_DIM), 0, s, part,
+                     nq, nkv, ns, xp, suh);
+  return hipGetLastError();
+}
 
 hipError_t launch_rmsnorm_prepare(const float *h, const uint16_t *w, int B, int H, float eps,
                                   const uint16_t *const *suh, int count, uint16_t *xp,

@@ -1971,11 +1971,37 @@ int exl3d_attn_o(const uint16_t *q, const uint16_t *k, const uint16_t *v, const 
   if (!fused && !att) return -1;
   if (hipSetDevice(pv->device) != hipSuccess) return hipErrorInvalidDevice;
   int r = exl3d_attn_decode_rope(q, k, v, qn, kn, pos, B, nq, nkv, eps, theta, kcache, vcache,
-                                 Tmax, scale, fused ? nullptr : att, scratch, scratch_bytes, s);
+                                 Tmax, scale, nullptr, scratch, scratch_bytes, s);
   if (r != 0) return r;
-  if (!fused) return exl3d_linears(&o, 1, att, B, nullptr, nullptr, 0.0f, nullptr, res, res_ssq,
-                                   nullptr, s);
   const int in = (int)pv->in;
+  if (!fused) {
+    // the combine writes att as o's prepared rows, so o's column groups do
+    // not each redo the prepare of their k-slice for all rows
+    hipError_t e = exl3::launch_attn_combine_prepare(scratch, B, nq, nkv, Tmax,
+                                                     (const uint16_t *)o->scales.data, att, s);
+    if (e != hipSuccess) return e;
+    StreamScratch *ss = scratch_for(pv->device, s);
+    std::lock_guard<std::mutex> g(ss->mu);
+    int wout = (int)pv->out;
+    exl3::GemvLinear l;
+    l.trellis = (const uint16_t *)o->w.data;
+    l.suh = (const uint16_t *)o->scales.data;
+    l.svh = (const uint16_t *)o->biases.data;
+    l.y = nullptr;
+    l.zout = nullptr;
+    l.out = wout;
+    exl3::Scratch sc;
+    e = gemv_scratch(ss, &wout, 1, in, B, !pv->f.integer_rate(), &sc, s);
+    if (e != hipSuccess) return e;
+    exl3::GemvFuse fz;
+    fz.res = res;
+    fz.res_ssq = res_ssq;
+    fz.stacked = true;
+    e = exl3::launch_gemv_fused(&l, 1, pv->f, att, exl3::ACT_F16, exl3::ACT_F16, B, in, &sc, fz,
+                                s);
+    if (e == hipErrorInvalidValue) return -1;
+    return e;
+  }
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
   int wout = (int)pv->out;

@@ -162,6 +162,11 @@ bool gemv_one_batch(int in, int total_out, bool generic, int rows);
 // GemvFuse.stacked reads (in a multiple of 128).
 hipError_t launch_swiglu_prepare(const uint16_t *g, const uint16_t *u, const uint16_t *suh,
                                  uint16_t *xp, int rows, int in, float limit, hipStream_t s);
+// The decode attention's combine (its split slots in part, as
+// exl3d_attn_decode_rope with out NULL leaves them) into prepared rows xp
+// [B][nq * 128] for the consumer linear with suh.
+hipError_t launch_attn_combine_prepare(const float *part, int B, int nq, int nkv, int Tmax,
+                                       const uint16_t *suh, uint16_t *xp, hipStream_t s);
 // The RMSNorm of an f32 residual h [B][H] (exl3d_add_rmsnorm's arithmetic)
 // prepared for `count` (<= 4) consumer linears: xp holds count stacked
 // [B][H] sets, set c prepared with suh[c] (H a multiple of 512, <= 8192).

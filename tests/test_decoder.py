@@ -231,8 +231,7 @@ def test_attention_o_fused_equals_separate(B, T, lens):
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert torch.equal(h1, h2), float((h1 - h2).abs().max())
     assert torch.equal(ssq1, ssq2)
-    if B == 16:
-        assert torch.equal(att1, att2)  # beyond one prepare batch: combined into att as before
+    # (beyond one prepare batch att holds o's prepared rows, not the output)
 
 
 @gpu
