@@ -638,24 +638,38 @@ __device__ __forceinline__ void gemv_rows_store(int xdt, int prepared, int nblk,
       for (int e = 0; e < 4; ++e) y[e] = r.x[p][0][e];
     } else {
       float v[8];
+      // f16(x) * suh: inputs that are f16 values already (f16 rows, the
+      // SwiGLU's f16 results) skip the rounding, an identity for them (a
+      // uniform branch on the dtype)
+      auto unpack = [&](auto IS16) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float a, b;
-        if constexpr (PRO == PRO_SWIGLU) {
-          swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
-        } else {
-          prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // f16 / bf16 pair e
-          const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
-          const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
-          if (xdt == OUT_F32) {
-            a = fa;
-            b = fb;
+        for (int e = 0; e < 4; ++e) {
+          float a, b;
+          if constexpr (PRO == PRO_SWIGLU) {
+            swiglu_unpack(r.x[p][0][e], r.x[p][1][e], limit, a, b);  // gate, up pieces
+          } else if constexpr (decltype(IS16)::value) {
+            a = h2f((uint16_t)(r.x[p][0][e] & 0xFFFFu));
+            b = h2f((uint16_t)(r.x[p][0][e] >> 16));
+          } else {
+            prep_unpack(r.x[p][0][e], 0u, xdt, a, b);  // bf16 pair e
+            const float fa = bits<float>(r.x[p][e >> 1][2 * (e & 1)]);
+            const float fb = bits<float>(r.x[p][e >> 1][2 * (e & 1) + 1]);
+            if (xdt == OUT_F32) {
+              a = fa;
+              b = fb;
+            }
+            a = h2f(f2h(a));
+            b = h2f(f2h(b));
           }
+          const uint32_t su = r.su[p][e];
+          v[2 * e] = a * h2f((uint16_t)(su & 0xFFFFu));
+          v[2 * e + 1] = b * h2f((uint16_t)(su >> 16));
         }
-        const uint32_t su = r.su[p][e];
-        v[2 * e] = h2f(f2h(a)) * h2f((uint16_t)(su & 0xFFFFu));
-        v[2 * e + 1] = h2f(f2h(b)) * h2f((uint16_t)(su >> 16));
-      }
+      };
+      if (PRO == PRO_SWIGLU || xdt == OUT_F16)
+        unpack(std::true_type{});
+      else
+        unpack(std::false_type{});
       // stages on bits 0, 1, 2 (in-register), then 3-6 (lanes xor 1, 2, 4, 8)
 #pragma unroll
       for (int m = 1; m < 8; m <<= 1) {
