@@ -611,7 +611,8 @@ def main() -> int:
         # fixed part included) would keep every SIMD's VALU busy: 1024 SIMDs
         # at the held shader clock, VALU_CYCLES per wave-instruction, plus
         # the measured extra cycles of the decode's one v_mul_lo_u32 per
-        # weight (valu_rates.hip; SQ_INSTS_VALU counts it as one).
+        # weight (timed against v_xor_b32 in the same dependent-chain loop by
+        # a standalone probe; SQ_INSTS_VALU counts it as one).
         vi = prof.get("valu_wave_insts_per_step")
         if vi:
             muls = step_bytes * 8 / K_BITS / 64
@@ -623,7 +624,7 @@ def main() -> int:
                             "basis": "SQ_INSTS_VALU per step (profiles/gemv_k4_qwen3_8b_decode.md) at "
                                      f"{prof['valu_cycles_per_inst']} cycles per wave-instruction, "
                                      f"+{prof.get('mul_lo_extra_cycles', 0.0)} cycles per v_mul_lo_u32 "
-                                     "(one per weight; profiles/gemv_valu_rates_cache_resident.md), "
+                                     "(one per weight, timed by a standalone instruction-rate probe), "
                                      f"{prof['shader_clock_hz'] / 1e9:.2f} GHz, 1024 SIMDs"}
 
     line = {

@@ -156,7 +156,10 @@ typedef struct exl3_load_ctx {
 
 /* kit `Swiglu` options (`.limit`, `.verify_rows`:
  * turboexl3_qwen38/src/direct/moe.zig:65, turboexl3_ds41/plugin.zig:272-280).
- * limit > 0 clamps gate to min(g, limit) and up to [-limit, limit]. */
+ * limit > 0 clamps gate to min(g, limit) and up to [-limit, limit] (a NaN
+ * passes through).  verify_rows: routed calls take the decode chain (the
+ * grouped GEMV items) at any row count, as the reference sends verify rows
+ * down its decode chain (sushi_ds41/src/sushi/exl3/root.zig:149). */
 typedef struct exl3_swiglu_opts {
   uint32_t size;
   int32_t limit;
@@ -235,9 +238,17 @@ typedef struct exl3_indexer exl3_indexer;
  */
 
 /* QuantTable.claims (quant.zig:29; turboexl3_ds41/config.zig:43-47):
- * claims an EXL3 quantization block (`quant_method: "exl3"` or
- * `format: "exl3"`) by marker, anything else `no`. */
+ * exllamav3's block (`quant_method: "exl3"`) on a DeepSeek-V4.1 pack
+ * (config `model_type` "deepseek_v41") by marker, anything else `no`; the
+ * claim of exl3_quant_table_get(). */
 exl3_claim exl3_claims(exl3_str block_json, exl3_str config_json);
+
+/* turboexl3_qwen38's claim rule (turboexl3_qwen38/config.zig:18-32) as a
+ * quant table's claim: a Qwen3.8 pack (config `model_type` "qwen4_exp" or
+ * "qwen4_exp_text") whose config names a non-null `trunk_quant` block, by
+ * marker; anything else `no` (exl3_validate refuses the blocks it does not
+ * decode by name).  The claim of exl3_quant_table_qwen38_get(). */
+exl3_claim exl3_claims_qwen38(exl3_str block_json, exl3_str config_json);
 
 /* QuantTable.validate (quant.zig:31; turboexl3_ds41/config.zig:49-54, and
  * turboexl3's block rules as turboexl3_qwen38/config.zig:86-105 restates
@@ -254,7 +265,10 @@ uint64_t exl3_bill(exl3_str block_json, exl3_str model_dir, uint64_t stored);
 
 /* QuantTable.open / close (quant.zig:34-35; turboexl3_ds41/plugin.zig:52-82):
  * parses the block (codebook, window) into ctx->state and initialises the
- * device; close frees ctx->state (loaded weights outlive it). */
+ * device, after the load-time self-check (exl3_self_check, for the block's
+ * codebook on ctx->device, on ctx->stream) has passed: a failed check
+ * refuses the open with its name; close frees ctx->state (loaded weights
+ * outlive it). */
 exl3_verdict exl3_open(exl3_load_ctx *ctx);
 void exl3_close(exl3_load_ctx *ctx);
 
@@ -294,7 +308,12 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3
 /* exl3_matmul without any allocation: no counterpart in the reference; for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Same kernels and the
- * same results as exl3_matmul, bit for bit.  `out` must be the caller's
+ * same results as exl3_matmul, bit for bit, with one exception: a weight
+ * admitted by exl3_resident takes the dense GEMM over its held matrix in
+ * exl3_matmul above 16 rows, while this entry always runs the trellis
+ * kernels (within the matmul bar of each other, not bit for bit).  A
+ * split-K wait that gives up here sets the array's status word, which
+ * exl3_stream_status reports.  `out` must be the caller's
  * buffer (x's dtype, the result's shape).  Scratch comes from one array per
  * GPU, 64 MiB, held by the library from its load onto that GPU until the
  * process ends: 8 MiB of split-K slots (GEMV, up to 16 rows) and 56 MiB of
@@ -484,12 +503,27 @@ typedef struct exl3_quant_table {
 } exl3_quant_table;
 
 /* The exported table (the reference exports it as `exportName(name,
- * version)`, quant.zig:22; plugin name turboexl3_ds41/plugin.zig:22). */
+ * version)`, quant.zig:22; plugin name turboexl3_ds41/plugin.zig:22):
+ * "turboexl3_mi355x", claiming as turboexl3_ds41 does (exl3_claims). */
 const exl3_quant_table *exl3_quant_table_get(void);
+
+/* The same entries under the name "turboexl3_mi355x_qwen38", claiming as
+ * turboexl3_qwen38 does (exl3_claims_qwen38): the table a host serving
+ * Qwen3.8 packs loads. */
+const exl3_quant_table *exl3_quant_table_qwen38_get(void);
 
 /* ------------------------------------------------------- support entries */
 
-/* Frees an array this library allocated (owned != 0); no-op otherwise. */
+/* Frees an array this library allocated (owned != 0); no-op otherwise.  The
+ * entries that hand back a new array (out->data NULL, the reference's
+ * convention, quant.zig:41-50) take it from a pool per (device, stream), and
+ * this returns its memory to the pool of the stream it was made for, so a
+ * steady serving loop of new arrays and frees calls no hipMalloc or hipFree
+ * after its first step.  The next call on that stream may reuse the memory
+ * at once (work on a stream is ordered); a caller that read the array on
+ * another stream synchronizes that stream before freeing it.  A pool keeps
+ * at most 1 GiB (the oldest blocks beyond it go back to the driver);
+ * exl3_scratch_release empties it. */
 void exl3_array_free(exl3_array *a);
 
 /* A weight over device arrays the caller already holds (borrowed, not freed
@@ -554,8 +588,10 @@ void exl3_pack_dir_close(exl3_pack_dir *dir);
  * captured earlier on the stream may still read it), so growth never
  * invalidates a captured graph; call this once no graph captured on the
  * stream will be replayed again (e.g. before destroying the stream).  The
- * next call on the stream makes its scratch anew.  Refused while the stream
- * is being captured.  No counterpart in the reference (MLX owns its
+ * next call on the stream makes its scratch anew.  It also returns to the
+ * driver the memory of output arrays freed with exl3_array_free that the
+ * stream's pool keeps (see exl3_array_free).  Refused while the stream is
+ * being captured.  No counterpart in the reference (MLX owns its
  * temporaries there). */
 exl3_verdict exl3_scratch_release(int32_t device, exl3_stream s);
 
@@ -565,8 +601,11 @@ exl3_verdict exl3_scratch_release(int32_t device, exl3_stream s);
  * and one that gives up (a partial sum that never arrived) leaves NaN in its
  * outputs and sets a status word instead of blocking.  This synchronizes the
  * stream, returns FAILED (with the reason) if any wait gave up, and then
- * resets the slots so later calls are sound; ok otherwise.  No counterpart
- * in the reference (MLX's kernels do not hand off across workgroups). */
+ * resets the slots so later calls are sound; ok otherwise.  It also reads
+ * the device's exl3_matmul_noalloc array (shared by every stream on the
+ * device: the caller synchronizes the streams that use it first) and resets
+ * it the same way.  No counterpart in the reference (MLX's kernels do not
+ * hand off across workgroups). */
 exl3_verdict exl3_stream_status(int32_t device, exl3_stream s);
 
 /* Diagnostic: the split-K wait's bound in polls for launches issued from now
@@ -575,18 +614,50 @@ exl3_verdict exl3_stream_status(int32_t device, exl3_stream s);
  * tests of exl3_stream_status use; every kernel still exits normally. */
 void exl3_set_splitk_poll_bound(int32_t polls);
 
+/* Diagnostic for failure-handling tests: while set (nonzero), launches have
+ * the splits other than the last skip their partial-sum stores, so the last
+ * split's bounded wait gives up (at the bound above) and the status word is
+ * set; every kernel still exits normally.  Off by default. */
+void exl3_set_splitk_test_drop(int32_t on);
+
+/* The load-time self-check that exl3_open runs before it accepts a pack
+ * (turboexl3_ds41/src/exl3/quant.zig:469-503 `accept` -> selfcheck.zig:
+ * 861-930).  Host part: SHA-256 against its standard's example, and the
+ * manifest's golden planes (turboexl3_ds41/src/exl3/kernels/exl3/
+ * manifest.json: splitmix64-seeded mul1 code at K = 2 and 3, 5120 x 2304)
+ * against their code digests.  Device part, on `device`: every state of the
+ * mul1 codebook through the kernels' decode against the manifest's table
+ * digest (exl3_open checks the block's codebook: mul1 or mcg); each plane's
+ * W_hat from exl3_decode_matrix against its digest; one-hot rows through
+ * exl3_inner -- the prefill GEMM, all rows in one call, and the decode GEMV,
+ * 16 rows a call -- equal to W_hat bit for bit.  A failure is refused
+ * (EXL3_FAILED) with "Exl3SelfCheckFailed" and the check's name; a device
+ * part that passed is not run again in the process.  device < 0: the host
+ * part only (needs no GPU).  Not a QuantTable entry. */
+exl3_verdict exl3_self_check(int32_t device);
+
+/* Diagnostic for tests of the refusal path: the named check of the
+ * self-check ("sha256", "code", "states", "decode", "gemm", "gemv") is made
+ * to fail (its expected digest replaced, or one element of its output
+ * flipped), and the self-check runs in full on every call while a fault is
+ * set; NULL or "" clears it. */
+void exl3_set_self_check_fault(const char *check);
+
 /* Library version string and the kernel variant a matmul of `rows` rows
- * takes ("gemv", "gemm"): diagnostics for tests and benchmarks. */
+ * takes ("gemv", "gemm"; a grouped linear, `rows` rows per group:
+ * "gemm-groups", one prepare and one grouped GEMM launch for every group,
+ * or "per-group"): diagnostics for tests and benchmarks. */
 const char *exl3_version(void);
 const char *exl3_matmul_path(const exl3_weight *w, int64_t rows);
 
-/* The kernel path a swiglu of `rows` rows takes (topk 0: no routes):
- * "dense-gemv", "dense-gemm", "dense-items", "routed-gemv" (grouped GEMV
- * items of up to 8 slots of one expert) or "routed-gemm" (grouped GEMM over
- * items of up to 256 slots, for prefill-sized expert batches): a diagnostic
- * for tests and benchmarks. */
+/* The kernel path a swiglu of `rows` rows takes (topk 0: no routes;
+ * verify_rows as exl3_swiglu_opts): "dense-gemv", "dense-gemm",
+ * "dense-items", "routed-gemv" (grouped GEMV items of up to 8 slots of one
+ * expert) or "routed-gemm" (grouped GEMM over items of up to 256 slots, for
+ * prefill-sized expert batches): a diagnostic for tests and benchmarks. */
 const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
-                             const exl3_weight *down, int64_t rows, int32_t topk);
+                             const exl3_weight *down, int64_t rows, int32_t topk,
+                             bool verify_rows);
 
 #ifdef __cplusplus
 }

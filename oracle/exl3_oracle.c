@@ -515,7 +515,8 @@ void exl3o_route_topk(const float *logits, size_t rows, size_t experts, size_t k
 
 /* sx/expert_exl3_kernels.zig:3151-3206: for each routed slot, gate and up
  * projections of x, h = silu(g) * u in f32, the down projection of h, and
- * y += score * down.  limit > 0 clamps as mtl/q3_exl3_prep_gu_epi.metal:47-56. */
+ * y += score * down.  limit > 0 clamps as mtl/q3_exl3_prep_gu_epi.metal:47-56
+ * (gate <= limit, up in [-limit, limit], NaN kept). */
 void exl3o_moe_swiglu(const float *x, size_t rows, const uint16_t *gate_t, const uint16_t *gate_suh,
                       const uint16_t *gate_svh, const uint16_t *up_t, const uint16_t *up_suh,
                       const uint16_t *up_svh, const uint16_t *down_t, const uint16_t *down_suh,
@@ -538,10 +539,10 @@ void exl3o_moe_swiglu(const float *x, size_t rows, const uint16_t *gate_t, const
                     1, hidden, inter, n, codebook, window, 0, uy);
       for (size_t i = 0; i < inter; ++i) {
         float g = exl3o_h2f(gy[i]), u = exl3o_h2f(uy[i]);
-        if (limit > 0.0f) {
-          g = g < limit ? g : limit;
-          u = u > -limit ? u : -limit;
-          u = u < limit ? u : limit;
+        if (limit > 0.0f) { /* mtl/q3_exl3_prep_gu_epi.metal:47-52: a NaN passes through */
+          g = (isnan(g) || g < limit) ? g : limit;
+          u = (isnan(u) || u > -limit) ? u : -limit;
+          u = (isnan(u) || u < limit) ? u : limit;
         }
         h[i] = (g / (1.0f + expf(-g))) * u;
       }

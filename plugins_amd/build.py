@@ -1,8 +1,6 @@
 """Builds libexl3_mi355x.so (HIP kernels for gfx950 + the C ABI) in-tree.
 
     python -m plugins_amd.build          # or: python plugins_amd/build.py
-    python -m plugins_amd.build --timeline   # the diagnostic GEMV-timeline build
-    python -m plugins_amd.build --valu-rates # the VALU instruction-rate program
 
 Objects go to plugins_amd/_build/, the library to plugins_amd/lib/.  hipcc
 cross-compiles gfx950 code objects without a GPU.  Device code is built with
@@ -45,6 +43,7 @@ SOURCES = [
     ("exl3_codebooks.cpp", "exl3_codebooks", HOST_FLAGS),
     ("exl3_dense.cpp", "exl3_dense", HOST_FLAGS),
     ("exl3_pack.cpp", "exl3_pack", HOST_FLAGS),
+    ("exl3_selfcheck.cpp", "exl3_selfcheck", HOST_FLAGS),
 ]
 
 
@@ -68,22 +67,12 @@ def _compile(src: str, name: str, flags: list[str]) -> str:
     return obj
 
 
-# The diagnostic build with the GEMV phase timeline compiled in
-# (EXL3_TIMELINE; plugins_amd/timeline.py reads it): a library of its own.
-TIMELINE_LIB = os.path.join(LIBDIR, "libexl3_mi355x_timeline.so")
-
-
-def build(verbose: bool = True, timeline: bool = False) -> str:
-    """Compiles every source and links the shared library; returns its path.
-    timeline: the diagnostic build (objects with a _tl suffix, TIMELINE_LIB)."""
+def build(verbose: bool = True) -> str:
+    """Compiles every source and links the shared library; returns its path."""
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = SOURCES
     lib_path = LIB
-    if timeline:
-        device = lambda f: any(x.startswith("--offload-arch") for x in f)  # noqa: E731
-        srcs = [(s, n + "_tl", f + ["-DEXL3_TIMELINE"] if device(f) else f) for s, n, f in SOURCES]
-        lib_path = TIMELINE_LIB
     jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda sf: _compile(*sf), srcs))
@@ -99,25 +88,5 @@ def build(verbose: bool = True, timeline: bool = False) -> str:
     return lib_path
 
 
-# The measurement program for the VALU issue cost of the decode's integer
-# multiply (csrc/valu_rates.hip): an executable, not part of the library.
-VALU_RATES = os.path.join(LIBDIR, "valu_rates")
-
-
-def build_valu_rates(verbose: bool = True) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    flags = [f for f in DEVICE_FLAGS if f != "-fPIC"]
-    cmd = [_hipcc(), *flags, os.path.join(CSRC, "valu_rates.hip"), "-o", VALU_RATES]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("hipcc failed on valu_rates.hip:\n" + r.stdout + r.stderr)
-    if verbose:
-        print("built", VALU_RATES)
-    return VALU_RATES
-
-
 if __name__ == "__main__":
-    if "--valu-rates" in sys.argv[1:]:
-        build_valu_rates()
-    else:
-        build(timeline="--timeline" in sys.argv[1:])
+    build()

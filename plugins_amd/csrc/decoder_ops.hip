@@ -184,27 +184,6 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   dst[lane + HALF] = f2h(y1);
 }
 
-// The attention's phase timeline of a diagnostic build (EXL3_TIMELINE): lane
-// 0 of each wave stores the 100 MHz real-time counter at each phase,
-// [workgroup][wave][event], for the first ATL_WGS workgroups of a launch.
-// Events: 0 entry, 1 q ready (after the q/k prologue), 2 key loop done, 3
-// states merged, 4 the split's slot stored.  A product build compiles them
-// out.
-#ifdef EXL3_TIMELINE
-constexpr int ATL_WGS = 1024;
-__device__ unsigned long long g_attn_tl[ATL_WGS * 4 * 8];
-#define ATL(k)                                                                            \
-  do {                                                                                    \
-    const size_t wg_ = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z); \
-    if ((threadIdx.x & 63) == 0 && wg_ < ATL_WGS)                                         \
-      g_attn_tl[(wg_ * 4 + (threadIdx.x >> 6)) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
-  } while (0)
-#else
-#define ATL(k) \
-  do {         \
-  } while (0)
-#endif
-
 // The q/k norm + RoPE of one head's dims 8 li .. 8 li + 7 held by the 16
 // lanes of a key group (lane li): RMSNorm with weight nw (sum of squares over
 // the 16 lanes), f16, then rotate-half RoPE with the pair partner in lane
@@ -302,7 +281,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int L = p + 1;
   const int t0 = s * TS, t1 = min(t0 + TS, L);
   const int nsplit = gridDim.x;
-  ATL(0);
   float qr[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h)
@@ -380,7 +358,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   for (int h = 0; h < AT_G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qr[h][e] *= scale;
-  ATL(1);
   float m[AT_G], l[AT_G], o[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h) {
@@ -441,7 +418,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       }
     }
   }
-  ATL(2);
   // merge the 16 states (4 waves x 4 key groups) per head
   const int st = wave * 4 + g;
 #pragma unroll
@@ -467,7 +443,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       a1 += sm[i][h][d + 1] * f;
     }
   }
-  ATL(3);
   const size_t sstride = (size_t)AT_G * (D + 2);
   float *slots = part + ((size_t)b * nkv + kvh) * nsplit * sstride;
   float *dst = slots + s * sstride + h * (D + 2);
@@ -477,7 +452,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     dst[D] = M;
     dst[D + 1] = Ls;
   }
-  ATL(4);
 }
 
 // The split combine, its own launch: out[b][head][d] = sum_s o_s e^(m_s - M)
@@ -693,18 +667,6 @@ int exl3d_attn_decode_rope(const uint16_t *q, const uint16_t *k, const uint16_t 
   return attn_launch(true, q, ra, kcache, vcache, pos, B, nq, nkv, Tmax, scale, out, scratch,
                      scratch_bytes, s);
 }
-
-#ifdef EXL3_TIMELINE
-// The attention timeline (diagnostic build only): copy out, clear.
-int exl3d_attn_timeline_read(void *dst, size_t bytes) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_attn_tl), bytes);
-}
-int exl3d_attn_timeline_clear(void) {
-  void *p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_attn_tl));
-  return e != hipSuccess ? (int)e : (int)hipMemset(p, 0, sizeof(g_attn_tl));
-}
-#endif
 
 int exl3d_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t n, hipStream_t s) {
   if (n == 0) return hipErrorInvalidValue;

@@ -35,6 +35,15 @@ typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
 // 1/sqrt(128) as the reference's kernels write it (expert_exl3_kernels.zig:930).
 constexpr float HAD_SCALE = 0.08838834764831845f;
+
+// The SwiGLU clamp (turboexl3_ds41/src/exl3/kernels/exl3/
+// q3_exl3_prep_gu_epi.metal:47-52): gate to <= limit, up to [-limit, limit];
+// a NaN passes through unchanged (a plain min would turn it into a bound).
+__device__ __forceinline__ void swiglu_clamp(float &g, float &u, float limit) {
+  g = (g != g || g < limit) ? g : limit;
+  u = (u != u || u > -limit) ? u : -limit;
+  u = (u != u || u < limit) ? u : limit;
+}
 // mul1: x = cw * 0x83DCD12D; w = f16((1024 + bytesum(x)) * f16(0x1EEE) + f16(0xC931))
 // (expert_exl3.zig:275-284; turboexl3_ds41/src/exl3/kernels.zig:966-975).
 constexpr uint32_t MUL1_MULT = 0x83DCD12Du;

@@ -27,6 +27,7 @@
 #include "exl3_dense.h"
 #include "exl3_json.h"
 #include "exl3_kernels.h"
+#include "exl3_selfcheck.h"
 
 using exl3::CodebookTable;
 using exl3::Format;
@@ -41,6 +42,7 @@ using exl3::codebook_row;
 namespace {
 
 const char *const kName = "turboexl3_mi355x";
+const char *const kNameQwen38 = "turboexl3_mi355x_qwen38";
 
 exl3_verdict ok() { return exl3_verdict{EXL3_OK, ""}; }
 exl3_verdict refuse(int32_t code, const char *why) { return exl3_verdict{code, why}; }
@@ -328,11 +330,30 @@ struct OpenState {
 
 extern "C" {
 
+// turboexl3_ds41/config.zig:43-47: exllamav3's block (`quant_method`
+// exl3) on a DeepSeek-V4.1 pack (config `model_type` deepseek_v41).
 exl3_claim exl3_claims(exl3_str block_json, exl3_str config_json) {
-  (void)config_json;
   const Json b = parse(block_json);
   if (!b.is_object()) return EXL3_CLAIM_NO;
-  return parse_block(b).exl3 ? EXL3_CLAIM_BY_MARKER : EXL3_CLAIM_NO;
+  const Json *qm = b.get("quant_method");
+  if (!qm || !qm->is_string("exl3")) return EXL3_CLAIM_NO;
+  const Json c = parse(config_json);
+  const Json *mt = c.is_object() ? c.get("model_type") : nullptr;
+  return mt && mt->is_string("deepseek_v41") ? EXL3_CLAIM_BY_MARKER : EXL3_CLAIM_NO;
+}
+
+// turboexl3_qwen38/config.zig:18-32 as a quant table's claim: a Qwen3.8 pack
+// (config `model_type` qwen4_exp or qwen4_exp_text, src/direct/config.zig:12)
+// whose config names a non-null `trunk_quant` block; the block itself is
+// validate's to refuse by name.
+exl3_claim exl3_claims_qwen38(exl3_str block_json, exl3_str config_json) {
+  (void)block_json;
+  const Json c = parse(config_json);
+  if (!c.is_object()) return EXL3_CLAIM_NO;
+  const Json *mt = c.get("model_type");
+  if (!mt || !(mt->is_string("qwen4_exp") || mt->is_string("qwen4_exp_text"))) return EXL3_CLAIM_NO;
+  const Json *t = c.get("trunk_quant");
+  return t && t->kind != Json::NUL ? EXL3_CLAIM_BY_MARKER : EXL3_CLAIM_NO;
 }
 
 exl3_verdict exl3_validate(exl3_str block_json, exl3_str config_json, const exl3_pack_dir *dir) {
@@ -368,12 +389,22 @@ exl3_verdict exl3_open(exl3_load_ctx *ctx) {
   const Block blk = parse_block(parse(ctx->block_json));
   if (!blk.exl3 || blk.codebook < 0 || blk.codebook > PACK_MCG || blk.window < 0)
     return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: not an exllamav3 mul1 or mcg block");
+  // the self-check's host part first (it needs no device)
+  exl3_verdict v = exl3::self_check(-1, 0, nullptr);
+  if (v.code != EXL3_OK) return v;
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
     return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: no HIP device");
   if (ctx->device < 0 || ctx->device >= count)
     return refuse(EXL3_UNSUPPORTED, "turboexl3_mi355x: no such device");
   if (hipSetDevice(ctx->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
+  // the kernels must decode the golden planes and the codebook's states
+  // exactly on this device before a pack is accepted (turboexl3_ds41/src/
+  // exl3/quant.zig:469-503)
+  v = exl3::self_check(ctx->device,
+                       blk.codebook == PACK_MCG ? exl3::CB_FORM_MCG : exl3::CB_FORM_MUL1,
+                       (hipStream_t)ctx->stream);
+  if (v.code != EXL3_OK) return v;
   OpenState *st = new OpenState{blk.codebook, blk.window};
   ctx->state = st;
   return ok();
@@ -626,9 +657,11 @@ void exl3_release(exl3_weight *w) {
   std::memset(w, 0, sizeof(*w));
 }
 
+static bool out_release(void *p);  // the output pool (below)
+
 void exl3_array_free(exl3_array *a) {
   if (a && a->owned && a->data) {
-    (void)hipFree(a->data);
+    if (!out_release(a->data)) (void)hipFree(a->data);
     a->data = nullptr;
     a->owned = 0;
   }
@@ -689,12 +722,102 @@ exl3_verdict exl3_weight_wrap(exl3_array trellis, exl3_array suh, exl3_array svh
 }
 
 // Allocates the output array when the caller passed none; checks it otherwise.
+// ------------------------------------------------------- output arrays
+//
+// The reference's entries hand back a new array the caller owns
+// (quant.zig:41-50); here exl3_array_free gives its memory to a pool of the
+// (device, stream) the array was made for, and the next call on that
+// stream that makes an array of a size the pool holds (up to twice the
+// request) takes it without hipMalloc.  Work on the stream is ordered, so a
+// reused block's earlier readers on it have run; a caller that read the
+// array on another stream synchronizes before freeing it (as with a
+// stream-ordered allocator).  Each stream's pool holds at most
+// OUT_POOL_BYTES (beyond it the oldest blocks go back to the driver);
+// exl3_scratch_release empties the stream's pool.
+struct OutBlock {
+  void *p;
+  size_t bytes;
+};
+struct OutPool {
+  std::vector<OutBlock> free;  // oldest first
+  size_t held = 0;
+};
+constexpr size_t OUT_POOL_BYTES = (size_t)1 << 30;
+std::mutex g_out_mu;
+std::map<std::pair<int, hipStream_t>, OutPool> g_out_pools;
+struct OutLive {
+  int device;
+  hipStream_t s;
+  size_t bytes;
+};
+std::map<void *, OutLive> g_out_live;  // arrays handed out, not freed yet
+
+static void *out_alloc(int device, hipStream_t s, size_t bytes) {
+  bytes = (std::max<size_t>(bytes, 256) + 255) & ~(size_t)255;
+  {
+    std::lock_guard<std::mutex> g(g_out_mu);
+    OutPool &pool = g_out_pools[{device, s}];
+    size_t best = pool.free.size();
+    for (size_t i = 0; i < pool.free.size(); ++i) {
+      const size_t b = pool.free[i].bytes;
+      if (b >= bytes && b <= 2 * bytes && (best == pool.free.size() || b < pool.free[best].bytes))
+        best = i;
+    }
+    if (best < pool.free.size()) {
+      const OutBlock blk = pool.free[best];
+      pool.free.erase(pool.free.begin() + (std::ptrdiff_t)best);
+      pool.held -= blk.bytes;
+      g_out_live[blk.p] = OutLive{device, s, blk.bytes};
+      return blk.p;
+    }
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> g(g_out_mu);
+  g_out_live[p] = OutLive{device, s, bytes};
+  return p;
+}
+
+// Returns p to its stream's pool; false if p is not an array of the pool's.
+static bool out_release(void *p) {
+  std::vector<void *> drop;
+  {
+    std::lock_guard<std::mutex> g(g_out_mu);
+    auto it = g_out_live.find(p);
+    if (it == g_out_live.end()) return false;
+    const OutLive l = it->second;
+    g_out_live.erase(it);
+    OutPool &pool = g_out_pools[{l.device, l.s}];
+    pool.free.push_back(OutBlock{p, l.bytes});
+    pool.held += l.bytes;
+    while (pool.held > OUT_POOL_BYTES && !pool.free.empty()) {
+      drop.push_back(pool.free.front().p);
+      pool.held -= pool.free.front().bytes;
+      pool.free.erase(pool.free.begin());
+    }
+  }
+  for (void *q : drop) (void)hipFree(q);
+  return true;
+}
+
+// Empties (device, stream)'s pool (the caller has synchronized the stream).
+static void out_pool_drop(int device, hipStream_t s) {
+  std::vector<OutBlock> blocks;
+  {
+    std::lock_guard<std::mutex> g(g_out_mu);
+    auto it = g_out_pools.find({device, s});
+    if (it == g_out_pools.end()) return;
+    blocks.swap(it->second.free);
+    g_out_pools.erase(it);
+  }
+  for (const OutBlock &b : blocks) (void)hipFree(b.p);
+}
+
 static exl3_verdict output_for(exl3_array *out, const exl3_array &x, int64_t last,
-                               int64_t rows) {
+                               int64_t rows, int device, hipStream_t s) {
   if (out->data == nullptr) {
-    void *p = nullptr;
-    if (hipMalloc(&p, std::max<size_t>((size_t)(rows * last) * dt_size(x.dtype), 256)) != hipSuccess)
-      return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
+    void *p = out_alloc(device, s, (size_t)(rows * last) * dt_size(x.dtype));
+    if (p == nullptr) return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
     exl3_array a = x;
     a.data = p;
     a.shape[a.ndim - 1] = last;
@@ -819,10 +942,14 @@ static hipError_t run_linear(const exl3_weight *w, const WeightPriv *pv, const v
 
 // A grouped linear (G linears stored as a G-bank): x [..., G, in] ->
 // y [..., G, out], x[..., g, :] through linear g (turboexl3_ds41/plugin.zig:
-// 252-261; sushi_ds41/src/sushi/exl3/linear.zig:24-36).  Per group: its rows
-// gathered into scratch by a strided 2-D copy, the linear's kernels (GEMV or
-// GEMM by the row count, as exl3_matmul), the result copied into y's group
-// columns.
+// 252-261; sushi_ds41/src/sushi/exl3/linear.zig:24-36).  Prompt rows (above
+// 16, integer rates): x read in place, one prepare launch for every group
+// (row r g of the flattened [rows G, in] takes group g's suh), one grouped
+// GEMM launch over every group's 256-row tiles with the finish fused, y
+// written in place (turboexl3_ds41/src/woa_join.zig:1-5: one prepare and
+// one finish launch for all groups).  Otherwise per group: its rows gathered
+// into scratch by a strided 2-D copy, the linear's kernels (GEMV or GEMM by
+// the row count, as exl3_matmul), the result copied into y's group columns.
 static exl3_verdict grouped_matmul(const exl3_weight *w, const WeightPriv *pv, exl3_array x,
                                    hipStream_t s, exl3_array *out) {
   const int xdt = act_of(x.dtype);
@@ -832,12 +959,27 @@ static exl3_verdict grouped_matmul(const exl3_weight *w, const WeightPriv *pv, e
   const int64_t rows = numel(x) / (G * in);
   if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = output_for(out, x, outf, rows * G);
+  exl3_verdict v = output_for(out, x, outf, rows * G, pv->device, s);
   if (v.code != EXL3_OK) return v;
   const size_t esz = dt_size(x.dtype);
-  const size_t xg_bytes = ((size_t)rows * in * esz + 255) & ~(size_t)255;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> lk(ss->mu);
+  const int64_t slots = rows * G;
+  if (rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate() &&
+      (uint64_t)slots * in * 2 <= 0xFFFFFFFFull && G * ((rows + 255) / 256) <= 65535) {
+    hipError_t e = grow(ss, &ss->xp, &ss->xp_bytes, (size_t)slots * in * 2, s);
+    const int64_t chunk = 65535 - 65535 % G;  // prepare windows of whole rows
+    for (int64_t r0 = 0; r0 < slots && e == hipSuccess; r0 += chunk)
+      e = exl3::launch_prepare((const char *)x.data + (size_t)r0 * in * esz, xdt,
+                               (const uint16_t *)w->scales.data, (uint16_t *)ss->xp + (size_t)r0 * in,
+                               (int)std::min<int64_t>(chunk, slots - r0), (int)in, s, (int)G);
+    if (e == hipSuccess)
+      e = exl3::launch_gemm_groups((const uint16_t *)w->w.data, pv->f, (const uint16_t *)ss->xp,
+                                   (const uint16_t *)w->biases.data, out->data, xdt, (int)rows,
+                                   (int)G, (int)in, (int)outf, s);
+    return e == hipSuccess ? ok() : hip_failed(e);
+  }
+  const size_t xg_bytes = ((size_t)rows * in * esz + 255) & ~(size_t)255;
   hipError_t e = grow(ss, &ss->aux, &ss->aux_bytes, xg_bytes + (size_t)rows * outf * esz, s);
   if (e != hipSuccess) return hip_failed(e);
   char *xg = (char *)ss->aux, *yg = xg + xg_bytes;
@@ -875,7 +1017,7 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream stream,
   if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = output_for(out, x, pv->out, rows);
+  exl3_verdict v = output_for(out, x, pv->out, rows, pv->device, s);
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
@@ -982,7 +1124,7 @@ exl3_verdict exl3_matmul_shared(const exl3_weight *const *ws, uint32_t count, ex
   if (hipSetDevice(pvs[0]->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   void *ys[4];
   for (uint32_t i = 0; i < count; ++i) {
-    exl3_verdict v = output_for(&outs[i], x, pvs[i]->out, rows);
+    exl3_verdict v = output_for(&outs[i], x, pvs[i]->out, rows, pvs[0]->device, s);
     if (v.code != EXL3_OK) return v;
     ys[i] = outs[i].data;
   }
@@ -1032,6 +1174,7 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
   a.hidden = (int)hidden;
   a.inter = (int)pg->out;
   a.limit = (float)opts->limit;
+  a.verify_rows = opts->verify_rows;
   a.experts = (int)std::max<int64_t>(pg->experts, 1);
   if (inds.data == nullptr) {
     // No routes: the dense SwiGLU MLP of single-linear weights
@@ -1056,7 +1199,7 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
     a.topk = (int)topk;
   }
   if (pg->f.n != pu->f.n) return kRate;
-  exl3_verdict v = output_for(out, x, hidden, rows);
+  exl3_verdict v = output_for(out, x, hidden, rows, pg->device, s);
   if (v.code != EXL3_OK) return v;
   if (inds.data == nullptr && rows <= exl3::GEMV_ROWS_MAX && pg->f.same_decode(pu->f)) {
     // Dense MLP at decode sizes: gate and up in one GEMV launch (f16), then
@@ -1124,15 +1267,33 @@ exl3_verdict exl3_swiglu(const exl3_weight *gate, const exl3_weight *up, const e
                    (const uint16_t *)down->biases.data, pd->f, (int)pd->in, (int)pd->out};
   StreamScratch *ss = scratch_for(pg->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
+  // A launch orders at most MOE_SLOTS_MAX slots (rows x topk): a larger call
+  // (a long prompt's prefill) runs as windows of whole rows, one launch
+  // sequence each, in row order on the stream over the same scratch.  Rows
+  // are independent, so the windows' results are the rows' results.
+  const int64_t wrows = std::max<int64_t>(1, exl3::MOE_SLOTS_MAX / a.topk);
+  exl3::MoeArgs wa = a;
+  wa.rows = (int)std::min<int64_t>(rows, wrows);
   size_t pf = 0;
   const size_t need =
-      exl3::moe_scratch_bytes(a, !pg->f.integer_rate(), !pd->f.integer_rate(), &pf);
+      exl3::moe_scratch_bytes(wa, !pg->f.integer_rate(), !pd->f.integer_rate(), &pf);
   hipError_t e = grow(ss, &ss->moe, &ss->moe_bytes, need, s);
   if (e != hipSuccess) return hip_failed(e);
   exl3::Scratch slots;
   e = slots_for(ss, pf, s, &slots);
   if (e != hipSuccess) return hip_failed(e);
-  e = exl3::launch_moe(a, bg, bu, bd, ss->moe, ss->moe_bytes, slots, s);
+  const size_t xsz = xdt == exl3::ACT_F32 ? 4 : 2;
+  const size_t ssz = a.inds ? (a.sdt == exl3::ACT_F32 ? 4 : 2) : 0;
+  for (int64_t r0 = 0; r0 < rows && e == hipSuccess; r0 += wrows) {
+    wa.rows = (int)std::min<int64_t>(rows - r0, wrows);
+    wa.x = (const char *)a.x + (size_t)r0 * hidden * xsz;
+    wa.y = (char *)a.y + (size_t)r0 * hidden * xsz;
+    if (a.inds) {
+      wa.inds = a.inds + (size_t)r0 * a.topk;
+      wa.scores = (const char *)a.scores + (size_t)r0 * a.topk * ssz;
+    }
+    e = exl3::launch_moe(wa, bg, bu, bd, ss->moe, ss->moe_bytes, slots, s);
+  }
   if (e != hipSuccess) {
     if (e == hipErrorInvalidValue) return kShape;
     return hip_failed(e);
@@ -1231,7 +1392,7 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
     return refuse(EXL3_UNSUPPORTED,
                   "turboexl3_mi355x: the shared expert rides the routed GEMV launches; at "
                   "prefill-sized batches the host runs swiglu and its shared expert's chain");
-  exl3_verdict v = output_for(out, x, hidden, rows);
+  exl3_verdict v = output_for(out, x, hidden, rows, pg->device, s);
   if (v.code != EXL3_OK) return v;
   a.y = out->data;
   a.ydt = xdt;
@@ -1355,11 +1516,10 @@ exl3_verdict exl3_inner(const exl3_weight *w, exl3_array xp, exl3_array z, exl3_
 // A new device array of `dt` with x's leading dims and last dimension `last`
 // (2-D [rows, last] when lead is null), `extra` bytes beyond the data.
 static exl3_verdict new_array(exl3_array *out, const exl3_array *lead, int64_t rows, int64_t last,
-                              int dt, size_t extra) {
+                              int dt, size_t extra, int device, hipStream_t s) {
   const size_t bytes = ((size_t)(rows * last) * dt_size(dt) + 255) & ~(size_t)255;
-  void *p = nullptr;
-  if (hipMalloc(&p, std::max<size_t>(bytes + extra, 256)) != hipSuccess)
-    return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
+  void *p = out_alloc(device, s, bytes + extra);
+  if (p == nullptr) return refuse(EXL3_TOO_LARGE, "turboexl3_mi355x: out of device memory");
   exl3_array a{};
   if (lead) {
     a = *lead;
@@ -1400,7 +1560,7 @@ exl3_verdict exl3_linear_split(const exl3_weight *w, exl3_array x, const exl3_li
   const int odt = opts->inner ? (int)EXL3_DT_F16 : (int)x.dtype;
   // with a side stream the prepared rows ride behind the result in its allocation
   const size_t xp_bytes = side != s ? (size_t)rows * pv->in * 2 : 0;
-  exl3_verdict v = new_array(out, &x, rows, pv->out, odt, xp_bytes);
+  exl3_verdict v = new_array(out, &x, rows, pv->out, odt, xp_bytes, pv->device, s);
   if (v.code != EXL3_OK) return v;
   void *y = opts->inner ? nullptr : out->data;
   uint16_t *z = opts->inner ? (uint16_t *)out->data : nullptr;
@@ -1454,7 +1614,7 @@ exl3_verdict exl3_linear_finish(const exl3_weight *w, const exl3_linear_parts *o
   if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = new_array(out, nullptr, rows, pv->out, opts->dtype, 0);
+  exl3_verdict v = new_array(out, nullptr, rows, pv->out, opts->dtype, 0, pv->device, s);
   if (v.code != EXL3_OK) return v;
   const size_t ysz = dt_size(opts->dtype);
   hipError_t e = hipSuccess;
@@ -1491,7 +1651,7 @@ exl3_verdict exl3_linear_prepared(const exl3_weight *w, exl3_array xp,
   if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = new_array(out, &xp, rows, pv->out, opts->dtype, 0);
+  exl3_verdict v = new_array(out, &xp, rows, pv->out, opts->dtype, 0, pv->device, s);
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
@@ -1546,7 +1706,7 @@ exl3_verdict exl3_linear_piece(const exl3_weight *w, exl3_array x, const exl3_li
   if (rows <= 0 || rows > (int64_t)1 << 24) return kShape;
   hipStream_t s = (hipStream_t)stream;
   if (hipSetDevice(pv->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = new_array(out, &x, rows, pv->out, EXL3_DT_F16, 0);
+  exl3_verdict v = new_array(out, &x, rows, pv->out, EXL3_DT_F16, 0, pv->device, s);
   if (v.code != EXL3_OK) return v;
   StreamScratch *ss = scratch_for(pv->device, s);
   std::lock_guard<std::mutex> g(ss->mu);
@@ -1565,15 +1725,17 @@ exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
   {
     std::lock_guard<std::mutex> g(g_scratch_mu);
     auto it = g_scratch.find({device, s});
-    if (it == g_scratch.end()) return ok();
-    ss = &it->second;
+    if (it != g_scratch.end()) ss = &it->second;
   }
-  std::lock_guard<std::mutex> g(ss->mu);
   if (hipSetDevice(device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   if (capturing(s))
     return refuse(EXL3_FAILED, "turboexl3_mi355x: scratch released while its stream is being captured");
+  std::unique_lock<std::mutex> g;
+  if (ss) g = std::unique_lock<std::mutex>(ss->mu);
   hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_failed(e);
+  out_pool_drop(device, s);  // the freed output arrays the stream's calls kept
+  if (!ss) return ok();
   for (void **p : {&ss->xp, &ss->kpart, &ss->slots, &ss->moe, &ss->aux}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
@@ -1588,24 +1750,32 @@ exl3_verdict exl3_scratch_release(int32_t device, exl3_stream stream) {
 
 void exl3_set_splitk_poll_bound(int32_t polls) { exl3::set_splitk_poll_max(polls); }
 
+void exl3_set_splitk_test_drop(int32_t on) { exl3::set_splitk_drop(on); }
+
 exl3_verdict exl3_stream_status(int32_t device, exl3_stream stream) {
   hipStream_t s = (hipStream_t)stream;
   StreamScratch *ss = nullptr;
   {
     std::lock_guard<std::mutex> g(g_scratch_mu);
     auto it = g_scratch.find({device, s});
-    if (it == g_scratch.end()) return ok();
-    ss = &it->second;
+    if (it != g_scratch.end()) ss = &it->second;
   }
-  std::lock_guard<std::mutex> g(ss->mu);
   if (hipSetDevice(device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
   if (capturing(s))
     return refuse(EXL3_FAILED, "turboexl3_mi355x: status read while its stream is being captured");
+  std::unique_lock<std::mutex> g;
+  if (ss) g = std::unique_lock<std::mutex>(ss->mu);
   hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_failed(e);
-  std::vector<std::pair<void *, size_t>> bufs = ss->retired_slots;
-  if (ss->slots) bufs.push_back({ss->slots, ss->slot_bytes});
+  // the device's no-alloc array (exl3_matmul_noalloc) has a status word too
   bool failed = false;
+  e = exl3::noalloc_status(device, &failed);
+  if (e != hipSuccess) return hip_failed(e);
+  std::vector<std::pair<void *, size_t>> bufs;
+  if (ss) {
+    bufs = ss->retired_slots;
+    if (ss->slots) bufs.push_back({ss->slots, ss->slot_bytes});
+  }
   for (auto &b : bufs) {
     uint32_t st = 0;
     e = hipMemcpy(&st, b.first, 4, hipMemcpyDeviceToHost);
@@ -1631,12 +1801,15 @@ const char *exl3_version(void) { return "exl3_mi355x 0.2.0 (gfx950)"; }
 const char *exl3_matmul_path(const exl3_weight *w, int64_t rows) {
   const WeightPriv *pv = priv_of(w);
   if (!pv) return "none";
+  if (pv->groups != 0)  // rows: rows of each group
+    return rows > exl3::GEMV_ROWS_MAX && pv->f.integer_rate() ? "gemm-groups" : "per-group";
   if (rows <= exl3::GEMV_ROWS_MAX) return "gemv";
   return pv->f.gemm_rate() ? "gemm" : "gemv";
 }
 
 const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
-                             const exl3_weight *down, int64_t rows, int32_t topk) {
+                             const exl3_weight *down, int64_t rows, int32_t topk,
+                             bool verify_rows) {
   const WeightPriv *pg = priv_of(gate), *pu = priv_of(up), *pd = priv_of(down);
   if (!pg || !pu || !pd || rows <= 0) return "none";
   if (topk <= 0) {
@@ -1649,6 +1822,7 @@ const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,
   a.topk = (int)topk;
   a.experts = (int)std::max<int64_t>(pg->experts, 1);
   a.inds = reinterpret_cast<const uint32_t *>(&a);  // routed: any non-null
+  a.verify_rows = verify_rows;
   return exl3::moe_uses_gemm(a, !pg->f.integer_rate(), !pd->f.integer_rate()) ? "routed-gemm"
                                                                               : "routed-gemv";
 }
@@ -1810,7 +1984,7 @@ exl3_verdict exl3_linear_joined(exl3_weight_span ws, exl3_array x, exl3_stream s
     return refuse(EXL3_UNSUPPORTED,
                   "turboexl3_mi355x: linear_joined at decode widths (the EXL3 GEMV serves them)");
   if (hipSetDevice(j->device) != hipSuccess) return hip_failed(hipErrorInvalidDevice);
-  exl3_verdict v = output_for(out, x, j->cols, rows);
+  exl3_verdict v = output_for(out, x, j->cols, rows, j->device, (hipStream_t)stream);
   if (v.code != EXL3_OK) return v;
   const hipError_t e = exl3::dense_gemm(x.data, xdt, j->data, j->cols, out->data, xdt, rows, j->in,
                                         j->cols, (hipStream_t)stream);
@@ -1822,42 +1996,28 @@ static exl3_verdict register_kernels(const void *host) {
   return ok();
 }
 
+#define EXL3_TABLE_ENTRIES                                                       \
+  &exl3_validate, &exl3_bill, &exl3_open, &exl3_close, &exl3_load_tensor, &exl3_load_bank, \
+      &exl3_release, &exl3_matmul, &exl3_moe, &register_kernels, &exl3_swiglu,           \
+      &exl3_linear_split, &exl3_linear_finish, &exl3_linear_prepared, &exl3_linear_pieces, \
+      &exl3_linear_piece, nullptr /* attn_in: the host's chain */, nullptr /* attn_prep */, \
+      nullptr /* linear_prepared_idx */, nullptr /* gated_out */,                        \
+      nullptr /* merged_gated_out */, nullptr /* q_planes */, nullptr /* indexer */,       \
+      &exl3_swiglu_shared, &exl3_resident, &exl3_resident_pending, &exl3_unrotate,        \
+      &exl3_linear_joined
+
+// The two tables differ only in their claim: ds41's rule (kTable) and
+// qwen38's (kTableQwen38, under its own name).
 static const exl3_quant_table kTable = {
-    (uint32_t)sizeof(exl3_quant_table),
-    EXL3_ABI_VERSION,
-    {kName, 16},
-    &exl3_claims,
-    &exl3_validate,
-    &exl3_bill,
-    &exl3_open,
-    &exl3_close,
-    &exl3_load_tensor,
-    &exl3_load_bank,
-    &exl3_release,
-    &exl3_matmul,
-    &exl3_moe,
-    &register_kernels,
-    &exl3_swiglu,
-    &exl3_linear_split,
-    &exl3_linear_finish,
-    &exl3_linear_prepared,
-    &exl3_linear_pieces,
-    &exl3_linear_piece,
-    nullptr,  // attn_in: the host's chain
-    nullptr,  // attn_prep
-    nullptr,  // linear_prepared_idx
-    nullptr,  // gated_out
-    nullptr,  // merged_gated_out
-    nullptr,  // q_planes
-    nullptr,  // indexer
-    &exl3_swiglu_shared,
-    &exl3_resident,
-    &exl3_resident_pending,
-    &exl3_unrotate,
-    &exl3_linear_joined,
-};
+    (uint32_t)sizeof(exl3_quant_table), EXL3_ABI_VERSION, {kName, 16}, &exl3_claims,
+    EXL3_TABLE_ENTRIES};
+static const exl3_quant_table kTableQwen38 = {
+    (uint32_t)sizeof(exl3_quant_table), EXL3_ABI_VERSION, {kNameQwen38, 23}, &exl3_claims_qwen38,
+    EXL3_TABLE_ENTRIES};
+#undef EXL3_TABLE_ENTRIES
 
 const exl3_quant_table *exl3_quant_table_get(void) { return &kTable; }
+const exl3_quant_table *exl3_quant_table_qwen38_get(void) { return &kTableQwen38; }
 
 }  // extern "C"
 

@@ -16,38 +16,6 @@
 
 namespace exl3 {
 
-// The GEMV phase timeline of a diagnostic build (EXL3_TIMELINE defined:
-// `python -m plugins_amd.build --timeline`, read by plugins_amd/timeline.py):
-// lane 0 of each wave stores the 100 MHz real-time counter at each phase of
-// its workgroup, [workgroup][wave][event], for the first 4096 workgroups of
-// a launch.  Events: 0 entry, 1 rows prepared (after the barrier), 2 loop
-// done, 3 reduced (before the split-K hand-off), 4 partial stored (the
-// other splits), 5 hand-off done and 6 finish done (the last split), 7 the
-// partial's stores acknowledged (the other splits) or the first read of the
-// slots returned (the last split).  A product build compiles the stores
-// out.
-#ifdef EXL3_TIMELINE
-constexpr int TIMELINE_WGS = 4096;
-static __device__ unsigned long long g_timeline[TIMELINE_WGS * 8 * 8];
-// The entry stamp also carries the XCD the workgroup runs on (HW_REG_XCC_ID)
-// in bits 56-59 (the counter's values stay far below 2^56).
-__device__ __forceinline__ unsigned long long timeline_xcc() {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
-  return (unsigned long long)(v & 15u) << 56;
-}
-#define EXL3_TL(k)                                                                           \
-  do {                                                                                       \
-    const size_t wg_ = (size_t)blockIdx.x + (size_t)gridDim.x * blockIdx.y;                  \
-    if ((threadIdx.x & 63) == 0 && wg_ < TIMELINE_WGS)                                       \
-      g_timeline[(wg_ * 8 + (threadIdx.x >> 6)) * 8 + (k)] =                                 \
-          __builtin_amdgcn_s_memrealtime() | ((k) == 0 ? timeline_xcc() : 0ull);             \
-  } while (0)
-#else
-#define EXL3_TL(k) \
-  do {             \
-  } while (0)
-#endif
 
 template <int... Is, typename F>
 __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F &&f) {
@@ -165,6 +133,10 @@ struct GemvCfg {
   // the word a split-K wait that gives up sets, and the wait's bound
   uint32_t *status;
   int poll_max;
+  // failure-handling tests only (the host sets it on request): the splits
+  // other than the last skip their partial-sum stores, so the last split's
+  // wait gives up at its bound
+  int drop_partials;
   int ydt;
   int ksplit;
   CbRow dec;            // window mask and table row
@@ -197,17 +169,11 @@ constexpr int PRO_PLAIN = 0, PRO_SWIGLU = 1, PRO_RMSNORM = 2, PRO_ATTN = 3;
 
 
 // The SwiGLU of one element pair of gate (g) and up (u), f16 bits: the MoE
-// mid step's arithmetic (turboexl3_ds41/src/exl3/kernels/exl3/
-// q3_exl3_prep_gu_epi.metal:47-56 for the clamp): h = f16(silu(g) * u),
-// silu(g) = g / (1 + e^-g) in f32, with gate clamped to <= limit and up to
-// [-limit, limit] when limit > 0.
+// mid step's arithmetic: h = f16(silu(g) * u), silu(g) = g / (1 + e^-g) in
+// f32, clamped first when limit > 0 (swiglu_clamp).
 __device__ __forceinline__ float swiglu1(uint16_t gb, uint16_t ub, float limit) {
   float gv = h2f(gb), uv = h2f(ub);
-  if (limit > 0.0f) {
-    gv = gv < limit ? gv : limit;
-    uv = uv > -limit ? uv : -limit;
-    uv = uv < limit ? uv : limit;
-  }
+  if (limit > 0.0f) swiglu_clamp(gv, uv, limit);
   return h2f(f2h(f32_value(gv / (1.0f + expf(-gv))) * uv));
 }
 __device__ __forceinline__ void swiglu_unpack(uint32_t g2, uint32_t u2, float limit, float &a,
@@ -790,9 +756,6 @@ __device__ __forceinline__ bool splitk_sum(float *zf, __amdgpu_buffer_rsrc_t pr,
       for (int j = 0; j < KC; ++j)
         if (live[i] && j < nk && bits<uint32_t>(v[i][j]) == PARTIAL_EMPTY)
           pending |= 1u << (i * KC + j);
-#ifdef EXL3_TIMELINE
-    if (k0 == 0) EXL3_TL(7);
-#endif
     for (int n = 0; pending != 0 && n < poll_max; ++n) {
       __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
 #pragma unroll
@@ -841,16 +804,13 @@ __device__ __forceinline__ bool gemv_splitk_last(float *zf, const GemvCfg &a, fl
   }
   const size_t stride = a.ptotal * out;
   if (ks != a.ksplit - 1) {
+    if (a.drop_partials) return false;
     for (int e = threadIdx.x; e < E; e += GEMV_THREADS) {
       const int b = e >> 7, col = e & 127;
       float v = zf[e];
       if (v != v) v = bits<float>(0x7FC00000u);  // never PARTIAL_EMPTY
       st_agent(partial + ks * stride + (size_t)rm.prow(b) * out + col0 + col, v);
     }
-#ifdef EXL3_TIMELINE
-    wait_stores();
-    EXL3_TL(7);
-#endif
     return false;
   }
   const __amdgpu_buffer_rsrc_t pr = buffer_of(partial);
@@ -963,7 +923,6 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // else the rows form in PREP passes
   constexpr bool ONEB = PREP == 0;
   constexpr int NP = ONEB ? 1 : PREP;
-  EXL3_TL(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = wave & 3, kp = wave >> 2;
@@ -1089,7 +1048,6 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     gemv_rows_store<PRO, NP>(geo.xdt, geo.prepared, nitems, nb, xs, kr, rr,
                              FOLD ? hsum : nullptr, a.limit);
   lds_barrier();
-  EXL3_TL(1);
 
   const int arow = min(lane & 15, nrows - 1);
   const uint16_t *xa = xs + arow * kr + (kp * part + g) * 16;
@@ -1167,7 +1125,6 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
     }
   }
 
-  EXL3_TL(2);
   // C of a 16x16 MFMA: lane l holds rows 4(l/16)+i, column l%16.
   const int col = (2 * q + t) * 16 + c;
   float *zk = zp + kp * zrows * 128;
@@ -1193,17 +1150,13 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   float *zf = zp;
   for (int e = tid; e < nrows * 128; e += GEMV_THREADS) zf[e] = zp[e] + zp[zrows * 128 + e];
   lds_barrier();
-  EXL3_TL(3);
   if (!gemv_splitk_last<!ONEB>(zf, a, W.partial, nrows, rm, ks, out, cg * 128)) {
-    EXL3_TL(4);
     return;
   }
-  EXL3_TL(5);
   if (a.res != nullptr)
     gemv_finish_res(zf, a.res, a.res_ssq, out, nrows, rm, sv, cg, resv);
   else
     gemv_finish(zf, a.ydt, W.y, W.zout, nrows, rm, sv, cg * 128);
-  EXL3_TL(6);
 }
 
 // The weight of grid column group `gx` (weights' groups side by side) and
@@ -2121,6 +2074,11 @@ struct GemmGroup {
   const MoeItem *items;
   const uint32_t *n_items;
   size_t expert_words;  // trellis dwords per expert
+  // groups > 0: a grouped linear's items, formed from blockIdx.y without an
+  // item list: group g = y / T, tile t = y % T (T = ceil(rows / 256)), rows
+  // t 256 .. of the group, whose slots are row * groups + g
+  int groups;
+  int rows;
 };
 
 template <int K, int CB, bool MASKED>
@@ -2130,8 +2088,15 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_grouped_kernel(
     CbRow mask, GemmGroup gg) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[GW_LDS_BYTES / 2];
   __shared__ uint32_t rows[GM_BM];
-  if (blockIdx.y >= *gg.n_items) return;  // the whole workgroup, before any barrier
-  const MoeItem item = gg.items[blockIdx.y];
+  MoeItem item;
+  if (gg.groups > 0) {
+    const int tpg = (gg.rows + GM_BM - 1) / GM_BM;
+    const int g = (int)blockIdx.y / tpg, t = (int)blockIdx.y - g * tpg;
+    item = MoeItem{(uint32_t)g, (uint32_t)(t * GM_BM), (uint32_t)min(GM_BM, gg.rows - t * GM_BM), 0u};
+  } else {
+    if (blockIdx.y >= *gg.n_items) return;  // the whole workgroup, before any barrier
+    item = gg.items[blockIdx.y];
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool mw = wave < 8;
@@ -2142,7 +2107,9 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_grouped_kernel(
   const size_t out = (size_t)out_tiles * 16;
   constexpr int NW = 8 * K;
   const int NS = in_tiles / 4;
-  if (tid < GM_BM) rows[tid] = gg.sorted[item.start + min(tid, M - 1)];
+  if (tid < GM_BM)
+    rows[tid] = gg.groups > 0 ? (item.start + min(tid, M - 1)) * (uint32_t)gg.groups + item.expert
+                              : gg.sorted[item.start + min(tid, M - 1)];
   lds_barrier();
 
   f16v_t acc[2][2];

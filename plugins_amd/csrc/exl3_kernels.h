@@ -76,21 +76,43 @@ constexpr size_t NOALLOC_SLOT_BYTES = (size_t)8 << 20;
 // The array's address on `device` (current), set up on the first call per
 // device (refused with hipErrorStreamCaptureUnsupported while s is capturing).
 hipError_t noalloc_scratch(int device, hipStream_t s, void **base);
+// The array's status word on `device` (the caller has synchronized the
+// calls' stream): *gave_up set when a split-K wait gave up, after which the
+// slots hold the empty mark again and the word is zero.  Nothing to read on a
+// device where no call has set the array up.
+hipError_t noalloc_status(int device, bool *gave_up);
 // The split-K wait's bound in polls (PARTIAL_POLL_MAX unless lowered by
 // set_splitk_poll_max; a negative value restores it).
 int splitk_poll_max();
 void set_splitk_poll_max(int polls);
+// Failure-handling tests: launches issued while set have the splits other
+// than the last skip their partial-sum stores (the last split's wait then
+// gives up at its bound; every kernel exits normally).
+int splitk_drop();
+void set_splitk_drop(int on);
 
 // Output / activation element types understood by the kernels.
 enum ActType { ACT_F16 = 0, ACT_BF16 = 1, ACT_F32 = 2 };
 
-// prepare: x [rows, in] (ACT_*) -> xp f16 [rows, in]; suh f16 [in].
+// prepare: x [rows, in] (ACT_*) -> xp f16 [rows, in]; suh f16 [in], or with
+// groups > 1 suh [groups, in] and row r taking suh row r % groups (a grouped
+// linear's x [rows / groups, groups, in] read in place).
 hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t *xp, int rows,
-                          int in, hipStream_t s);
+                          int in, hipStream_t s, int groups = 1);
+// The prefill GEMM over a grouped linear (G linears stored as a G-bank,
+// trellis [G][in/16][out/16][n], svh [G][out]): xp f16 [rows, G, in]
+// (prepared, slot r G + g = row r of group g) -> y [rows, G, out] in ydt,
+// one launch over every group's 256-row tiles (integer rates).
+hipError_t launch_gemm_groups(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                              const uint16_t *svh, void *y, int ydt, int rows, int groups,
+                              int in, int out, hipStream_t s);
 // finish: z f16 [rows, out] -> y [rows, out] (ACT_*); svh f16 [out].
 hipError_t launch_finish(const uint16_t *z, const uint16_t *svh, void *y, int ydt, int rows,
                          int out, hipStream_t s);
 // decode: trellis [in/16][out/16][n] -> W_inner f16 [in, out].
+// Every state of f's codebook into w (65536 f16; pair1: 131072, a weight
+// pair per codeword), through the kernels' device decode.
+hipError_t launch_decode_states(const Format &f, uint16_t *w, hipStream_t s);
 hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in, int out,
                                 uint16_t *w, hipStream_t s);
 
@@ -218,6 +240,9 @@ struct MoeBank {
 // contribute nothing), scores [rows, topk] (ACT_*); inds == nullptr: the
 // dense SwiGLU of expert 0 (topk 1, score 1).  limit > 0 clamps gate and up.
 // y [rows, hidden] in ydt.
+// The most slots (rows x topk) one launch_moe call orders; the host runs
+// larger calls as windows of whole rows.
+constexpr int MOE_SLOTS_MAX = 65535;
 struct MoeArgs {
   const void *x;
   int xdt;
@@ -228,10 +253,13 @@ struct MoeArgs {
   float limit;
   void *y;
   int ydt;
+  // the decode chain (grouped GEMV items) at any row count
+  // (exl3_swiglu_opts.verify_rows)
+  bool verify_rows;
 };
 // Whether a routed call takes the grouped GEMM (prefill-sized expert
-// batches: at least 32 slots per expert on average, integer rates) rather
-// than the grouped GEMV's items of up to 8 slots.
+// batches: at least 32 slots per expert on average, integer rates, and not
+// verify_rows) rather than the grouped GEMV's items of up to 8 slots.
 bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic);
 // Staging bytes for a call, and (in *partial_floats) the partial-sum slots
 // of its Scratch.

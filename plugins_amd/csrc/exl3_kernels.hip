@@ -33,10 +33,12 @@ namespace exl3 {
 // of the block lives in lane i/2, register i%2 (had128_pair: the stage on
 // index bit 0 in-register, bits 1..6 across lanes; each stage (lo + hi,
 // lo - hi) in bit order, as the reference computes it).
+// Row r takes suh row r % groups (groups 1: one suh for every row; a grouped
+// linear's [rows, G, in] input: group g's suh for its rows).
 __global__ __launch_bounds__(256) void prepare_kernel(const void *__restrict__ x, int xdt,
                                                       const uint16_t *__restrict__ suh,
                                                       uint16_t *__restrict__ xp, int in,
-                                                      int nblk) {
+                                                      int nblk, int groups) {
   const int lane = threadIdx.x & 63;
   const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (blk >= nblk) return;  // whole waves
@@ -44,7 +46,8 @@ __global__ __launch_bounds__(256) void prepare_kernel(const void *__restrict__ x
   const int k = blk * 128 + 2 * lane;
   // f16(x) * suh in f32 (expert_exl3.zig:490-493; the kernel's
   // float(x) * float(suh), expert_exl3_kernels.zig:908-912).
-  const uint32_t su = *reinterpret_cast<const uint32_t *>(suh + k);
+  const uint32_t su =
+      *reinterpret_cast<const uint32_t *>(suh + (size_t)(blockIdx.y % (unsigned)groups) * in + k);
   float v0 = h2f(f2h(load_act(x, base + k, xdt))) * h2f((uint16_t)(su & 0xFFFFu));
   float v1 = h2f(f2h(load_act(x, base + k + 1, xdt))) * h2f((uint16_t)(su >> 16));
   had128_pair(v0, v1, lane);
@@ -88,13 +91,14 @@ __global__ __launch_bounds__(64) void finish_kernel(const uint16_t *__restrict__
 __global__ __launch_bounds__(256) void prepare8_kernel(const void *__restrict__ x, int xdt,
                                                        const uint16_t *__restrict__ suh,
                                                        uint16_t *__restrict__ xp, int nblk,
-                                                       uint32_t nblocks) {
+                                                       uint32_t nblocks, int groups) {
   const int j = threadIdx.x & 15;
   const uint32_t gb0 = blockIdx.x * 16u + (threadIdx.x >> 4);
   const bool valid = gb0 < nblocks;  // a 16-lane group is valid or not as a whole
   const uint32_t gb = valid ? gb0 : nblocks - 1;
   const size_t off = (size_t)gb * 128 + 8 * j;
   const int k = (int)(gb % (uint32_t)nblk) * 128 + 8 * j;
+  const size_t ks = (size_t)((gb / (uint32_t)nblk) % (uint32_t)groups) * nblk * 128 + k;
   float v[8];
   if (xdt == OUT_F32) {
     const float4 a = *reinterpret_cast<const float4 *>((const float *)x + off);
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(256) void prepare8_kernel(const void *__restrict__ 
       v[2 * i + 1] = xdt == OUT_F16 ? h2f(hi) : bf2f(hi);
     }
   }
-  const uint4 su = *reinterpret_cast<const uint4 *>(suh + k);
+  const uint4 su = *reinterpret_cast<const uint4 *>(suh + ks);
   const uint32_t ss[4] = {su.x, su.y, su.z, su.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -142,19 +146,19 @@ __global__ __launch_bounds__(256) void prepare8_kernel(const void *__restrict__ 
 }
 
 hipError_t launch_prepare(const void *x, int xdt, const uint16_t *suh, uint16_t *xp, int rows,
-                          int in, hipStream_t s) {
-  if (rows <= 0 || in <= 0 || in % 128 != 0) return hipErrorInvalidValue;
+                          int in, hipStream_t s, int groups) {
+  if (rows <= 0 || in <= 0 || in % 128 != 0 || groups <= 0) return hipErrorInvalidValue;
   if (rows > 65535) return hipErrorInvalidValue;
   const int nblk = in / 128;
   const size_t nblocks = (size_t)rows * nblk;
   const bool aligned = (((uintptr_t)x | (uintptr_t)suh | (uintptr_t)xp) & 15) == 0;
   if (aligned && nblocks * 16 < ((size_t)1 << 31)) {
     hipLaunchKernelGGL(prepare8_kernel, dim3((unsigned)((nblocks + 15) / 16)), dim3(256), 0, s, x,
-                       xdt, suh, xp, nblk, (uint32_t)nblocks);
+                       xdt, suh, xp, nblk, (uint32_t)nblocks, groups);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(prepare_kernel, dim3((nblk + 3) / 4, rows), dim3(256), 0, s, x, xdt, suh, xp,
-                     in, nblk);
+                     in, nblk, groups);
   return hipGetLastError();
 }
 
@@ -271,6 +275,33 @@ hipError_t launch_decode_matrix(const uint16_t *trellis, const Format &f, int in
   }
 }
 
+// Every state of a codebook, the table the load-time self-check hashes:
+// w[s] = the weight codeword s decodes to (mul1, mcg, the hash-mask tables;
+// 65536 f16), through the same device decode the GEMV and GEMM use (pairs of
+// codewords, the window's mask applied first).  pair1 decodes a pair of
+// weights from one codeword: w[2c], w[2c + 1] for codeword c (131072 f16).
+template <int CB>
+__global__ __launch_bounds__(256) void decode_states_kernel(uint16_t *__restrict__ w, CbRow d) {
+  const uint32_t p = blockIdx.x * 256u + threadIdx.x;  // pair index
+  uint32_t v;
+  if constexpr (CB == CB_PAIR1)
+    v = decode_pair<CB>(0u, p, d);
+  else
+    v = decode_pair<CB>(2u * p, 2u * p + 1u, d);
+  reinterpret_cast<uint32_t *>(w)[p] = v;
+}
+
+hipError_t launch_decode_states(const Format &f, uint16_t *w, hipStream_t s) {
+  const CbRow d = f.dec();
+  switch (f.codebook) {
+    case CB_MCG: hipLaunchKernelGGL(decode_states_kernel<CB_MCG>, dim3(128), dim3(256), 0, s, w, d); break;
+    case CB_HASH: hipLaunchKernelGGL(decode_states_kernel<CB_HASH>, dim3(128), dim3(256), 0, s, w, d); break;
+    case CB_PAIR1: hipLaunchKernelGGL(decode_states_kernel<CB_PAIR1>, dim3(256), dim3(256), 0, s, w, d); break;
+    default: hipLaunchKernelGGL(decode_states_kernel<CB_MUL1>, dim3(128), dim3(256), 0, s, w, d);
+  }
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------ un-rotation
 
 // W_public = diag(suh) H W_inner H diag(svh) / 128 per 128 x 128 block, in
@@ -374,6 +405,9 @@ int splitk_poll_max() {
   return v >= 0 ? v : PARTIAL_POLL_MAX;
 }
 void set_splitk_poll_max(int polls) { g_poll_bound.store(polls, std::memory_order_relaxed); }
+static std::atomic<int> g_splitk_drop{0};
+int splitk_drop() { return g_splitk_drop.load(std::memory_order_relaxed); }
+void set_splitk_drop(int on) { g_splitk_drop.store(on != 0, std::memory_order_relaxed); }
 
 void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int tps_max) {
   const int nb = in / 128;
@@ -458,6 +492,7 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
   if (ksplit > 1 && sc[0].status == nullptr) return hipErrorInvalidValue;
   a.c.status = sc[0].status;
   a.c.poll_max = splitk_poll_max();
+  a.c.drop_partials = splitk_drop();
   a.c.ydt = ydt;
   a.c.ptotal = (size_t)rows;
   a.c.ksplit = ksplit;
@@ -699,6 +734,29 @@ hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t 
   return hipGetLastError();
 }
 
+// A grouped linear's prefill: the grouped GEMM over every group's row tiles
+// in one launch, items formed from the grid (GemmGroup.groups), each
+// group's trellis and svh at its index in the G-bank, the finish fused.
+hipError_t launch_gemm_groups(const uint16_t *trellis, const Format &f, const uint16_t *xp,
+                              const uint16_t *svh, void *y, int ydt, int rows, int groups,
+                              int in, int out, hipStream_t s) {
+  if (rows < 1 || groups < 1 || in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0)
+    return hipErrorInvalidValue;
+  if (!f.integer_rate() || y == nullptr) return hipErrorInvalidValue;
+  // activation offsets (bytes from xp) are 32-bit in the kernel
+  if ((size_t)rows * groups * in * 2 > 0xFFFFFFFFu) return hipErrorInvalidValue;
+  const size_t tiles_y = (size_t)groups * ((rows + GM_BM - 1) / GM_BM);
+  if (tiles_y > 65535) return hipErrorInvalidValue;
+  GemmGroup gg{nullptr, nullptr, nullptr, (size_t)(in / 16) * (out / 16) * (f.n / 2), groups, rows};
+  const dim3 grid(out / GM_BN, (unsigned)tiles_y);
+  const uint32_t *tw = reinterpret_cast<const uint32_t *>(trellis);
+  rate_dispatch(f.n / 16, [&](auto KC) {
+    constexpr int K = decltype(KC)::value;
+    if constexpr (K > 0) gemm_grouped_go<K>(f, grid, s, tw, xp, svh, y, ydt, in / 16, out / 16, gg);
+  });
+  return hipGetLastError();
+}
+
 // ====================================================================== MoE
 //
 // Routed SwiGLU experts (sushi_ds41/src/sushi/exl3/expert_exl3_kernels.zig:
@@ -836,11 +894,7 @@ __global__ __launch_bounds__(64) void moe_mid_kernel(const uint16_t *__restrict_
   for (int j = 0; j < 2; ++j) {
     const int i = i0 + 64 * j;
     float gv = h2f(g[slot * inter + i]), uv = h2f(u[slot * inter + i]);
-    if (limit > 0.0f) {
-      gv = gv < limit ? gv : limit;
-      uv = uv > -limit ? uv : -limit;
-      uv = uv < limit ? uv : limit;
-    }
+    if (limit > 0.0f) swiglu_clamp(gv, uv, limit);
     const float h = f32_value(gv / (1.0f + expf(-gv))) * uv;
     v[j] = h2f(f2h(h)) * h2f(sud[i]);
   }
@@ -1056,7 +1110,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic) {
   const long slots = (long)a.rows * a.topk;
-  return !gu_generic && !d_generic && a.inds != nullptr &&
+  return !gu_generic && !d_generic && a.inds != nullptr && !a.verify_rows &&
          slots >= (long)MOE_GEMM_SLOTS_PER_EXPERT * a.experts;
 }
 
@@ -1220,7 +1274,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
                        (shared->logit == nullptr && shared->gate_vec == nullptr)))
     return hipErrorInvalidValue;
   if (scratch_bytes < L.total || slots.status == nullptr || slots.partial == nullptr ||
-      slots.partial_floats < L.partial_floats || L.slots > 65535 ||
+      slots.partial_floats < L.partial_floats || L.slots > MOE_SLOTS_MAX ||
       L.max_items > 65535 || (int64_t)L.slots * std::max(a.hidden, a.inter) >= (int64_t)1 << 31)
     return hipErrorInvalidValue;
   float *partial = slots.partial;
@@ -1288,6 +1342,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   }
   mgu.a.c.status = md.a.c.status = slots.status;
   mgu.a.c.poll_max = md.a.c.poll_max = splitk_poll_max();
+  mgu.a.c.drop_partials = md.a.c.drop_partials = splitk_drop();
   uint32_t gg[3];
   if (!moe_geo(mgu, grid_gu, &gg[0], &gg[1], &gg[2]) || !moe_geo(md, grid_d, &gg[0], &gg[1], &gg[2]))
     return hipErrorInvalidValue;

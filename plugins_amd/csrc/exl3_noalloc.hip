@@ -15,9 +15,10 @@
 //   [NOALLOC_SLOT_BYTES, NOALLOC_BYTES) staging: the GEMM's prepared rows,
 //                                      then its split-K planes
 // Every call leaves the slots empty and the status word as it found it (zero
-// unless a split-K wait gave up), and overwrites the staging it uses, so the
-// array needs no clearing between calls; calls that overlap on one GPU (two
-// streams at once) race on it.
+// unless a split-K wait gave up: exl3_stream_status reads the word, and after
+// a give-up refills the slots and clears it), and overwrites the staging it
+// uses, so the array needs no clearing between calls; calls that overlap on
+// one GPU (two streams at once) race on it.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -59,6 +60,22 @@ hipError_t noalloc_scratch(int device, hipStream_t s, void **base) {
   }
   *base = g_ptr[device];
   return hipSuccess;
+}
+
+hipError_t noalloc_status(int device, bool *gave_up) {
+  if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(g_mu);
+  if (g_ptr[device] == nullptr) return hipSuccess;  // never set up: no call ran
+  uint32_t st = 0;
+  hipError_t e = hipMemcpy(&st, g_ptr[device], 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess || st == 0) return e;
+  *gave_up = true;
+  // the caller has synchronized the stream of the calls: every late store
+  // has landed, so the slots can take the empty mark again
+  e = hipMemset((char *)g_ptr[device] + SLOT_HEADER_BYTES, 0xFF,
+                NOALLOC_SLOT_BYTES - SLOT_HEADER_BYTES);
+  if (e == hipSuccess) e = hipMemset(g_ptr[device], 0, 4);
+  return e;
 }
 
 }  // namespace exl3

@@ -24,14 +24,3 @@ template EXL3_GEMM_FRAC_GO(5);
 
 }  // namespace exl3
 
-#if defined(EXL3_TIMELINE) && EXL3_INST_K == 4
-// The K=4 kernels' phase timeline (a diagnostic build only): copy out, clear.
-extern "C" int exl3_timeline_read(void *dst, size_t bytes) {
-  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(exl3::g_timeline), bytes);
-}
-extern "C" int exl3_timeline_clear(void) {
-  void *p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(exl3::g_timeline));
-  return e != hipSuccess ? (int)e : (int)hipMemset(p, 0, sizeof(exl3::g_timeline));
-}
-#endif

@@ -142,6 +142,7 @@ class QuantTable(Structure):
 # Every symbol include/exl3_mi355x.h declares, with its ctypes signature.
 SIGNATURES = {
     "exl3_claims": (c_int32, [Str, Str]),
+    "exl3_claims_qwen38": (c_int32, [Str, Str]),
     "exl3_validate": (Verdict, [Str, Str, POINTER(PackDir)]),
     "exl3_bill": (c_uint64, [Str, Str, c_uint64]),
     "exl3_open": (Verdict, [POINTER(LoadCtx)]),
@@ -155,6 +156,7 @@ SIGNATURES = {
     "exl3_swiglu": (Verdict, [POINTER(Weight), POINTER(Weight), POINTER(Weight), Array, Array, Array,
                               POINTER(SwigluOpts), c_void_p, POINTER(Array)]),
     "exl3_quant_table_get": (POINTER(QuantTable), []),
+    "exl3_quant_table_qwen38_get": (POINTER(QuantTable), []),
     "exl3_array_free": (None, [POINTER(Array)]),
     "exl3_weight_wrap": (Verdict, [Array, Array, Array, Str, c_int32, POINTER(Weight)]),
     "exl3_decode_matrix": (Verdict, [POINTER(Weight), c_int32, Array, c_void_p]),
@@ -167,10 +169,14 @@ SIGNATURES = {
     "exl3_pack_dir_open": (c_void_p, [c_char_p]),
     "exl3_pack_dir_close": (None, [c_void_p]),
     "exl3_matmul_path": (c_char_p, [POINTER(Weight), c_int64]),
-    "exl3_swiglu_path": (c_char_p, [POINTER(Weight), POINTER(Weight), POINTER(Weight), c_int64, c_int32]),
+    "exl3_swiglu_path": (c_char_p, [POINTER(Weight), POINTER(Weight), POINTER(Weight), c_int64, c_int32,
+                                    c_bool]),
     "exl3_scratch_release": (Verdict, [c_int32, c_void_p]),
     "exl3_stream_status": (Verdict, [c_int32, c_void_p]),
     "exl3_set_splitk_poll_bound": (None, [c_int32]),
+    "exl3_set_splitk_test_drop": (None, [c_int32]),
+    "exl3_self_check": (Verdict, [c_int32]),
+    "exl3_set_self_check_fault": (None, [c_char_p]),
     "exl3_matmul_noalloc": (Verdict, [POINTER(Weight), Array, c_void_p, Array]),
     "exl3_linear_split": (Verdict, [POINTER(Weight), Array, POINTER(LinearParts), c_void_p,
                                     POINTER(Array)]),
@@ -265,7 +271,13 @@ def stream_handle(stream=None) -> int:
 # --------------------------------------------------------- table entries
 
 def claims(block_json: str, config_json: str = "{}") -> int:
+    """turboexl3_ds41's claim rule (the default table's)."""
     return int(lib().exl3_claims(Str.of(block_json), Str.of(config_json)))
+
+
+def claims_qwen38(block_json: str, config_json: str = "{}") -> int:
+    """turboexl3_qwen38's claim rule (the qwen38 table's)."""
+    return int(lib().exl3_claims_qwen38(Str.of(block_json), Str.of(config_json)))
 
 
 def validate(block_json: str, config_json: str = "{}", dir: PackDir | None = None) -> Verdict:
@@ -277,8 +289,11 @@ def bill(block_json: str, model_dir: str, stored: int) -> int:
     return int(lib().exl3_bill(Str.of(block_json), Str.of(model_dir), stored))
 
 
-def quant_table() -> QuantTable:
-    return lib().exl3_quant_table_get().contents
+def quant_table(qwen38: bool = False) -> QuantTable:
+    """The exported table: ds41's claim rule, or with qwen38 the table under
+    its own name that claims as turboexl3_qwen38 does."""
+    get = lib().exl3_quant_table_qwen38_get if qwen38 else lib().exl3_quant_table_get
+    return get().contents
 
 
 def version() -> str:
@@ -675,10 +690,11 @@ def matmul_path(w: Weight, rows: int) -> str:
     return lib().exl3_matmul_path(ctypes.byref(w), rows).decode()
 
 
-def swiglu_path(gate: Weight, up: Weight, down: Weight, rows: int, topk: int = 0) -> str:
-    """The kernel path a swiglu call takes (topk 0: dense, no routes)."""
+def swiglu_path(gate: Weight, up: Weight, down: Weight, rows: int, topk: int = 0,
+                verify_rows: bool = False) -> str:
+    """The kernel path a swiglu of `rows` rows takes (exl3_swiglu_path)."""
     return lib().exl3_swiglu_path(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), rows,
-                                  topk).decode()
+                                  topk, bool(verify_rows)).decode()
 
 
 class Linear:

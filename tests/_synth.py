@@ -7,6 +7,10 @@ from __future__ import annotations
 import numpy as np
 
 
+# 1/sqrt(128) as the kernels and the oracle hold it (f32)
+HAD_SCALE = float(np.float32(0.08838834764831845))
+
+
 def linear(rng: np.random.Generator, in_f: int, out_f: int, n: int, experts: int | None = None):
     lead = () if experts is None else (experts,)
     trellis = rng.integers(0, 65536, lead + (in_f // 16, out_f // 16, n), dtype=np.uint16)

@@ -96,12 +96,49 @@ def _ds41_config():
                        "text_config": {"num_experts_per_tok": c["num_experts_per_tok"]}})
 
 
-def test_claims_exl3_blocks_by_marker():
-    # ds41's fixture block (quant_method exl3) and the qwen38 packs' blocks (format exl3)
+def _q38_config(k):
+    c = CONFIGS[k]
+    return json.dumps({"model_type": c["model_type"], "trunk_quant": c["trunk_quant"],
+                       "expert_quant": c["expert_quant"],
+                       "text_config": {"num_experts_per_tok": c["num_experts_per_tok"]}})
+
+
+def test_claims_follow_ds41():
+    # turboexl3_ds41/config.zig:43-47,68-74: exllamav3's block on a
+    # DeepSeek-V4.1 pack only
     assert X.claims(_ds41_block(), _ds41_config()) == X.CLAIM_BY_MARKER
+    assert X.claims(_ds41_block(), '{"model_type":"qwen4_exp"}') == X.CLAIM_NO
+    assert X.claims(_ds41_block(), "{}") == X.CLAIM_NO
+    assert X.claims('{"quant_method":"fp8"}', _ds41_config()) == X.CLAIM_NO
+    assert X.claims("{", _ds41_config()) == X.CLAIM_NO
+    for k in ("k2", "k3", "k4", "k5"):  # qwen38's packs are the other table's
+        assert X.claims(json.dumps(CONFIGS[k]["trunk_quant"]), _q38_config(k)) == X.CLAIM_NO
+
+
+def test_claims_qwen38_rule():
+    # turboexl3_qwen38/config.zig:18-32: a qwen4_exp pack naming a trunk block
     for k in ("k2", "k3", "k4", "k5"):
-        assert X.claims(json.dumps(CONFIGS[k]["trunk_quant"])) == X.CLAIM_BY_MARKER
-        assert X.claims(json.dumps(CONFIGS[k]["expert_quant"])) == X.CLAIM_BY_MARKER
+        for part in ("trunk_quant", "expert_quant"):
+            assert X.claims_qwen38(json.dumps(CONFIGS[k][part]), _q38_config(k)) == X.CLAIM_BY_MARKER
+    c = json.loads(_q38_config("k3"))
+    for mt, tq, want in (("qwen4_exp_text", c["trunk_quant"], X.CLAIM_BY_MARKER),
+                         ("qwen4_exp", None, X.CLAIM_NO), ("deepseek_v41", c["trunk_quant"], X.CLAIM_NO)):
+        cfg = json.dumps({"model_type": mt, "trunk_quant": tq})
+        assert X.claims_qwen38("{}", cfg) == want, (mt, tq)
+    assert X.claims_qwen38("{}", json.dumps({"model_type": "qwen4_exp"})) == X.CLAIM_NO
+    assert X.claims_qwen38(_ds41_block(), _ds41_config()) == X.CLAIM_NO
+    assert X.claims_qwen38("{}", "[") == X.CLAIM_NO
+
+
+def test_two_tables_differ_only_in_their_claim():
+    a, b = X.quant_table(), X.quant_table(qwen38=True)
+    assert ctypes.string_at(b.name.ptr, b.name.len) == b"turboexl3_mi355x_qwen38"
+    assert a.claims == ctypes.cast(X.lib().exl3_claims, ctypes.c_void_p).value
+    assert b.claims == ctypes.cast(X.lib().exl3_claims_qwen38, ctypes.c_void_p).value
+    assert (a.size, a.version) == (b.size, b.version)
+    for f in X.TABLE_ENTRIES:
+        if f != "claims":
+            assert getattr(a, f) == getattr(b, f), f
 
 
 def test_claims_nothing_else():
@@ -248,8 +285,10 @@ def test_matmul_refuses_without_a_weight():
 
 def test_json_reader_edge_cases():
     # escapes, nesting and trailing garbage go through the C++ reader
-    assert X.claims('{"quant_method":"ex\\u006c3"}') == X.CLAIM_BY_MARKER
-    assert X.claims('{"a":[1,2,{"b":null}],"format":"exl3"}') == X.CLAIM_BY_MARKER
-    assert X.claims('{"format":"exl3"} x') == X.CLAIM_NO
-    assert X.claims('{"format":"exl3",}') == X.CLAIM_NO
-    assert X.claims('[' * 300 + ']' * 300) == X.CLAIM_NO
+    cfg = _ds41_config()
+    assert X.claims('{"quant_method":"ex\\u006c3"}', cfg) == X.CLAIM_BY_MARKER
+    assert X.claims('{"a":[1,2,{"b":null}],"quant_method":"exl3"}', cfg) == X.CLAIM_BY_MARKER
+    assert X.claims('{"quant_method":"exl3"} x', cfg) == X.CLAIM_NO
+    assert X.claims('{"quant_method":"exl3",}', cfg) == X.CLAIM_NO
+    assert X.claims('[' * 300 + ']' * 300, cfg) == X.CLAIM_NO
+    assert X.claims('{"quant_method":"exl3"}', '{"model_type":"deepseek_v41"} x') == X.CLAIM_NO

@@ -75,8 +75,8 @@ def test_table_codebook_decode_narrowed_windows(form, n, window):
 @pytest.mark.parametrize("form,n", [("spec1-w15", 16), ("spec1-w15", 40), ("spec1-w15", 128), ("std1", 48),
                                     ("pair1", 32), ("pair1", 40), ("pair1", 64), ("spec1-w16", 24)])
 def test_table_codebook_matmul_against_oracle(form, n, rows):
-    # GEMV at <= 16 rows, the GEMM above at the integer rates, 16-row GEMV
-    # passes at the fractional ones
+    # GEMV at <= 16 rows, the GEMM above (integer rates and the half-integer
+    # rates n = 24 and 40 alike)
     rng = np.random.default_rng(4000 + n + rows)
     in_f, out_f = 512, 384
     lin, trellis, suh, svh = make(rng, form, in_f, out_f, n)

@@ -372,11 +372,49 @@ def test_swiglu_routed_against_oracle(rows, limit):
     assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
 
 
+@pytest.mark.parametrize("which", ["gate", "up"])
+@pytest.mark.parametrize("rows", [1, 16, 200])
+def test_swiglu_clamp_keeps_nan(rows, which):
+    """The clamp passes a NaN through (turboexl3_ds41/src/exl3/kernels/exl3/
+    q3_exl3_prep_gu_epi.metal:47-52): a NaN in expert 1's gate (or up) svh
+    makes one column of its output NaN, and every row routed to expert 1
+    must come out NaN (down's Hadamard spreads it), in the grouped GEMV
+    (1, 16 rows) and the grouped GEMM (200 rows); the other rows within the
+    bar of the oracle.  The dense MLP with the NaN weight: every row NaN."""
+    rng = np.random.default_rng(4400 + rows)
+    E, hidden, inter, topk, n, limit = 4, 256, 128, 2, 48, 10
+    g_np = S.linear(rng, hidden, inter, n, experts=E)
+    u_np = S.linear(rng, hidden, inter, n, experts=E)
+    d_np = S.linear(rng, inter, hidden, n, experts=E)
+    (g_np if which == "gate" else u_np)[2][1, 5] = 0x7E00
+    banks = [X.wrap(dev_u16(t), dev_f16(su), dev_f16(sv)) for t, su, sv in (g_np, u_np, d_np)]
+    x = S.activations(rng, rows, hidden)
+    inds, scores = O.route_topk(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    inds[0, 0] = 1 if inds[0, 1] != 1 else inds[0, 0]  # row 0 routed to expert 1
+    y = X.swiglu(*banks, dev_f16(x).reshape(rows, 1, hidden),
+                 torch.from_numpy(inds).to(DEV).reshape(rows, 1, topk),
+                 torch.from_numpy(scores).to(DEV).reshape(rows, 1, topk), limit=limit)
+    got = y.float().cpu().numpy().reshape(rows, hidden)
+    want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n,
+                        limit=float(limit))
+    hit = (inds == 1).any(axis=1)
+    assert hit[0] and np.isnan(want[hit]).all() and np.isfinite(want[~hit]).all()
+    assert np.isnan(got[hit]).all()
+    assert np.isfinite(got[~hit]).all()
+    if (~hit).any():
+        assert S.rel_fro(got[~hit], want[~hit]) < 1e-3
+    # the dense MLP over expert 1's linears (GEMV prologue at <= 16 rows, the
+    # GEMM and the elementwise SwiGLU above)
+    lins = [X.Linear(dev_u16(t[1]), dev_f16(su[1]), dev_f16(sv[1])) for t, su, sv in (g_np, u_np, d_np)]
+    yd = X.swiglu(*(l.weight for l in lins), dev_f16(x), limit=limit).float().cpu().numpy()
+    assert np.isnan(yd).all()
+
+
 @pytest.mark.parametrize("E,topk,rows,limit", [(4, 2, 128, 0), (2, 1, 600, 0), (3, 2, 200, 7)])
 def test_swiglu_routed_prefill_sizes(E, topk, rows, limit):
     # prefill-sized expert batches (32+ slots per expert on average, an
-    # expert past 256 slots): the routed GEMV items (the grouped-GEMM form
-    # for these batches is switched off), against the oracle's composition
+    # expert past 256 slots): the grouped GEMM over routed items of <= 256
+    # slots, against the oracle's composition
     rng = np.random.default_rng(E * 1000 + rows + limit)
     hidden, inter, n = 512, 256, 48
     g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
@@ -390,6 +428,36 @@ def test_swiglu_routed_prefill_sizes(E, topk, rows, limit):
     want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n,
                         limit=float(limit))
     assert S.rel_fro(y.float().cpu().numpy().reshape(rows, hidden), want) < 1e-3
+
+
+def test_swiglu_verify_rows_takes_the_decode_chain():
+    """verify_rows (the reference sends verify rows down its decode chain at
+    any batch, sushi_ds41/src/sushi/exl3/root.zig:149): at 64 slots per
+    expert, where a call takes the grouped GEMM, it takes the grouped GEMV
+    items instead -- the same values, bit for bit, as the rows split into
+    calls small enough for the GEMV items -- within the bar of the oracle."""
+    rng = np.random.default_rng(77)
+    E, hidden, inter, topk, n, rows = 4, 256, 128, 2, 48, 128
+    g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
+    u_np, u, u_keep = _bank(rng, E, hidden, inter, n)
+    d_np, d, d_keep = _bank(rng, E, inter, hidden, n)
+    x = S.activations(rng, rows, hidden)
+    inds, scores = O.route_topk(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    assert X.swiglu_path(g, u, d, rows, topk) == "routed-gemm"
+    assert X.swiglu_path(g, u, d, rows, topk, verify_rows=True) == "routed-gemv"
+    xd, ids, scs = dev_f16(x), torch.from_numpy(inds).to(DEV), torch.from_numpy(scores).to(DEV)
+
+    def call(a, b, verify):
+        return X.swiglu(g, u, d, xd[a:b].reshape(b - a, 1, hidden), ids[a:b].reshape(b - a, 1, topk),
+                        scs[a:b].reshape(b - a, 1, topk), verify_rows=verify).reshape(b - a, hidden)
+
+    yv = call(0, rows, True)
+    part = rows // 4  # 64 slots: below 32 per expert, the GEMV items without the flag
+    assert X.swiglu_path(g, u, d, part, topk) == "routed-gemv"
+    assert torch.equal(yv, torch.cat([call(a, a + part, False) for a in range(0, rows, part)]))
+    want = O.moe_swiglu(x.astype(np.float32), g_np, u_np, d_np, inds, scores, hidden, inter, n)
+    assert S.rel_fro(yv.float().cpu().numpy(), want) < 1e-3
+    assert S.rel_fro(call(0, rows, False).float().cpu().numpy(), want) < 1e-3
 
 
 def test_swiglu_routed_long_splits():
@@ -545,11 +613,12 @@ def test_scratch_growth_keeps_captured_graphs_valid():
 
 
 def test_splitk_give_up_is_reported_and_recovered():
-    """A split-K wait that gives up (forced from the host: a bound of 0 polls,
-    so the last split stops at the first slot that has not landed) leaves NaN
-    in its output and sets the stream's status; exl3_stream_status reports it
-    and resets the slots, after which calls at the default bound are exact
-    again.  Every kernel exits normally throughout."""
+    """A split-K wait that gives up leaves NaN in its output and sets the
+    stream's status; exl3_stream_status reports it and resets the slots,
+    after which calls are exact again.  The give-up is forced from the host:
+    the splits other than the last skip their partial-sum stores (the test
+    hook exl3_set_splitk_test_drop) and the wait's bound is 8 polls, so the
+    last split's wait gives up every time and every kernel exits normally."""
     rng = np.random.default_rng(901)
     lin, *_ = make(rng, 4096, 4096, 64)  # 16 splits at batch 1
     x = dev_f16(S.activations(rng, 1, 4096))
@@ -558,23 +627,18 @@ def test_splitk_give_up_is_reported_and_recovered():
         want = lin(x, stream=s)
     torch.cuda.synchronize()
     assert X.stream_status(0, s).is_ok()
-    gave_up = None
     try:
-        X.lib().exl3_set_splitk_poll_bound(0)
-        for _ in range(40):
-            with torch.cuda.stream(s):
-                y = lin(x, stream=s)
-            v = X.stream_status(0, s)
-            if not v.is_ok():
-                gave_up = (v, y)
-                break
+        X.lib().exl3_set_splitk_poll_bound(8)
+        X.lib().exl3_set_splitk_test_drop(1)
+        with torch.cuda.stream(s):
+            y = lin(x, stream=s)
+        v = X.stream_status(0, s)
     finally:
+        X.lib().exl3_set_splitk_test_drop(0)
         X.lib().exl3_set_splitk_poll_bound(-1)
-    if gave_up is None:
-        pytest.skip("no split-K wait gave up at a bound of 0 polls in 40 calls")
-    v, y = gave_up
     assert v.code == X.FAILED and "did not arrive" in v.reason
-    assert torch.isnan(y.float()).any()
+    assert torch.isnan(y.float()).all()  # every column group's wait gave up
+    assert X.stream_status(0, s).is_ok()  # reported once, then reset
     for _ in range(3):
         with torch.cuda.stream(s):
             again = lin(x, stream=s)

@@ -395,3 +395,27 @@ def test_moe_swiglu_against_composed_projections(limit):
             d = O.h2f(O.project(h.astype(np.float32), down[0][e], down[1][e], down[2][e], inter, hidden, 48))
             want[r] += scores[r, j] * d[0]
     np.testing.assert_allclose(y, want, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("which", ["gate", "up"])
+def test_moe_clamp_keeps_nan(which):
+    """The clamp of mtl/q3_exl3_prep_gu_epi.metal:47-52 passes a NaN through
+    (isnan(g) ? g : min(g, limit), the same for up's two bounds): one NaN
+    column of expert 1's gate (or up) output, forced by a NaN in its svh,
+    makes every row routed to expert 1 NaN through down's Hadamard, under a
+    clamp; a clamp that turned NaN into a bound would leave them finite.
+    Rows not routed to expert 1 stay finite."""
+    rng = np.random.default_rng(33)
+    E, hidden, inter, k, rows = 4, 256, 128, 2, 6
+    gate = [np.stack(z) for z in zip(*[_rand_linear(rng, hidden, inter, 3)[:3] for _ in range(E)])]
+    up = [np.stack(z) for z in zip(*[_rand_linear(rng, hidden, inter, 3)[:3] for _ in range(E)])]
+    down = [np.stack(z) for z in zip(*[_rand_linear(rng, inter, hidden, 3)[:3] for _ in range(E)])]
+    bank = gate if which == "gate" else up
+    bank[2][1, 5] = 0x7E00  # f16 NaN in expert 1's svh, column 5
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)
+    inds = np.array([[1, 0], [2, 3], [3, 1], [0, 2], [1, 2], [3, 0]], np.int32)
+    scores = np.full((rows, k), 0.5, np.float32)
+    y = O.moe_swiglu(x, gate, up, down, inds, scores, hidden, inter, 48, limit=10.0)
+    hit = (inds == 1).any(axis=1)
+    assert np.isnan(y[hit]).all()
+    assert np.isfinite(y[~hit]).all()

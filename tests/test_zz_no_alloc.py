@@ -2,8 +2,11 @@
 exl3_matmul: the same kernels, so the outputs agree bit for bit, on two calls
 in a row with the second smaller, at GEMV sizes (split-K slots) and GEMM sizes
 (prepared rows and split-K planes); a call beyond the array's 64 MiB is
-refused before any launch; and captured into a HIP graph (the callers it is
-for) its replays equal the eager result."""
+refused before any launch; captured into a HIP graph (the callers it is
+for) its replays equal the eager result; a split-K wait that gives up inside
+it is reported by exl3_stream_status, which resets the array; and for a
+weight admitted by exl3_resident it keeps the trellis kernels (exl3_matmul
+takes the dense GEMM over the held matrix above 16 rows)."""
 import ctypes
 
 import numpy as np
@@ -93,3 +96,53 @@ def test_noalloc_in_a_graph():
         # eager work between replays on the same array
         g2, w2 = both(lin, x)
         assert torch.equal(g2, w2)
+
+
+def test_noalloc_give_up_is_reported_and_reset():
+    """The array's status word: a split-K wait that gives up in a no-alloc
+    call (forced from the host: the splits other than the last skip their
+    stores, the wait's bound is 8 polls) is reported by exl3_stream_status,
+    which refills the array's slots; later calls equal exl3_matmul again."""
+    rng = np.random.default_rng(17)
+    lin = linear(rng, 4096, 4096)  # 16 splits at batch 1
+    x = torch.from_numpy(S.activations(rng, 1, 4096)).to(DEV)
+    got, want = both(lin, x)
+    assert torch.equal(got, want)
+    assert X.stream_status(0).is_ok()
+    out = torch.empty_like(want)
+    try:
+        X.lib().exl3_set_splitk_poll_bound(8)
+        X.lib().exl3_set_splitk_test_drop(1)
+        X.check(noalloc(lin, x, out), "matmul_noalloc")
+        v = X.stream_status(0)
+    finally:
+        X.lib().exl3_set_splitk_test_drop(0)
+        X.lib().exl3_set_splitk_poll_bound(-1)
+    assert v.code == X.FAILED and "did not arrive" in v.reason
+    assert torch.isnan(out.float()).all()
+    assert X.stream_status(0).is_ok()
+    for rows in (1, 3):
+        xr = torch.from_numpy(S.activations(rng, rows, 4096)).to(DEV)
+        g2, w2 = both(lin, xr)
+        assert torch.equal(g2, w2)
+    assert X.stream_status(0).is_ok()
+
+
+def test_noalloc_keeps_trellis_kernels_for_resident_weights():
+    """A weight admitted by exl3_resident: exl3_matmul above 16 rows takes the
+    dense GEMM over the held matrix; the no-alloc entry keeps the trellis
+    GEMM, equal bit for bit to exl3_matmul of the same weight before it was
+    admitted, and within the matmul bar of the resident result."""
+    rng = np.random.default_rng(23)
+    lin = linear(rng, 1024, 512)
+    x = torch.from_numpy(S.activations(rng, 64, 1024)).to(DEV)
+    got0, want0 = both(lin, x)
+    assert torch.equal(got0, want0)
+    X.resident([lin.weight])
+    try:
+        got, want_res = both(lin, x)
+        assert torch.equal(got, want0)  # trellis kernels, as before admission
+        g64, w64 = got.double(), want_res.double()
+        assert float(torch.linalg.norm(g64 - w64) / torch.linalg.norm(w64)) < 1e-3
+    finally:
+        X.resident([])
