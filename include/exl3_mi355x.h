@@ -309,9 +309,10 @@ exl3_verdict exl3_matmul(const exl3_weight *w, exl3_array x, exl3_stream s, exl3
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Same kernels and the
  * same results as exl3_matmul, bit for bit, with one exception: a weight
- * admitted by exl3_resident takes the dense GEMM over its held matrix in
- * exl3_matmul above 16 rows, while this entry always runs the trellis
- * kernels (within the matmul bar of each other, not bit for bit).  A
+ * that holds a matrix through exl3_resident (a rate without the prefill
+ * GEMM) or exl3_unrotate takes a dense GEMM in exl3_matmul above 16 rows,
+ * while this entry always runs the trellis kernels (within the matmul bar
+ * of each other, not bit for bit).  A
  * split-K wait that gives up here sets the array's status word, which
  * exl3_stream_status reports.  `out` must be the caller's
  * buffer (x's dtype, the result's shape).  Scratch comes from one array per
@@ -406,13 +407,18 @@ exl3_verdict exl3_swiglu_shared(const exl3_weight *gate, const exl3_weight *up,
                                 exl3_array scores, const exl3_shared_swiglu *opts,
                                 exl3_stream s, exl3_array *out);
 
-/* QuantTable.resident (quant.zig:96-99): memory for speed.  Admits ws'
- * single linears: each one's decoded matrix (W_inner f16 [in, out], in * out
- * * 2 bytes) is held from its first matmul at prefill widths (over 16 rows)
- * on, and that matmul becomes the prepare, a dense f16 GEMM (hipBLASLt) over
- * the held matrix and the finish; decode widths keep the EXL3 GEMV.
- * *bytes = what ws' matrices take.  Refused EXL3_TOO_LARGE past room (0:
- * no bound), admitting none; an empty ws drops every kept matrix. */
+/* QuantTable.resident (quant.zig:96-99): memory for speed, spent only where
+ * it buys speed.  Admits ws' single linears.  At a rate without the prefill
+ * GEMM (any n but the integer rates and n = 24, 40: those run 16-row GEMV
+ * passes above 16 rows), the decoded matrix (W_inner f16 [in, out], in *
+ * out * 2 bytes) is held from its first matmul at prefill widths (over 16
+ * rows) on, and that matmul becomes the prepare, a dense f16 GEMM
+ * (hipBLASLt) over the held matrix and the finish.  At the GEMM's rates the
+ * fused decode GEMM outruns that path, so the matmul keeps the GEMM and
+ * nothing is held: the admission reserves the bytes (resident_pending) for
+ * exl3_unrotate, whose public matrices do outrun it.  Decode widths keep the
+ * EXL3 GEMV.  *bytes = what ws' matrices take.  Refused EXL3_TOO_LARGE past
+ * room (0: no bound), admitting none; an empty ws drops every kept matrix. */
 exl3_verdict exl3_resident(exl3_weight_span ws, uint64_t room, exl3_stream s, uint64_t *bytes);
 
 /* QuantTable.resident_pending (quant.zig:100-101): the bytes admitted and

@@ -550,12 +550,20 @@ exl3_verdict exl3_load_bank(const exl3_load_ctx *ctx, exl3_str name, uint32_t in
 
 // The weights exl3_resident admitted (quant.zig:96-107: `resident`,
 // `resident_pending`, `unrotate`, `linear_joined`).  Memory for speed at
-// prefill widths: a held W_inner f16 makes the matmul a prepare, a dense f16
-// GEMM (hipBLASLt) and the finish; an un-rotated group's public matrix makes
-// it one dense GEMM in the activation dtype.  Decode widths keep the EXL3
-// GEMV, which reads 2 to 8 times fewer bytes.
+// prefill widths, where it buys speed: a held W_inner f16 makes the matmul a
+// prepare, a dense f16 GEMM (hipBLASLt) and the finish -- held only at the
+// rates without the prefill GEMM (those run 16-row GEMV passes otherwise);
+// at the GEMM's rates the fused decode GEMM is faster than the held path
+// (prepare, dense GEMM, z round trip, finish), so the admission reserves the
+// bytes (pending) and holds nothing until `unrotate`.  An un-rotated group's
+// public matrix makes the matmul one dense GEMM in the activation dtype, at
+// every rate.  Decode widths keep the EXL3 GEMV, which reads 2 to 8 times
+// fewer bytes.
 static std::mutex g_res_mu;
 static std::set<WeightPriv *> g_resident;
+
+// Whether an admitted weight holds its W_inner for prefill matmuls.
+static bool holds_inner(const WeightPriv *pv) { return !pv->f.gemm_rate(); }
 
 static uint64_t resident_bytes(const WeightPriv *pv) { return (uint64_t)pv->in * pv->out * 2; }
 
@@ -618,6 +626,7 @@ static hipError_t resident_matmul(const exl3_weight *w, WeightPriv *pv, const ex
     const char *wj = (const char *)r.joined->data + (size_t)r.col * dt_size(x.dtype);
     return exl3::dense_gemm(x.data, xdt, wj, r.joined->cols, y, xdt, rows, pv->in, pv->out, s);
   }
+  if (!holds_inner(pv)) return hipSuccess;  // the prefill GEMM is the faster path
   hipError_t e = resident_hold(w, pv, s);
   if (e == hipErrorStreamCaptureUnsupported) return hipSuccess;
   if (e != hipSuccess) return e;
@@ -895,9 +904,9 @@ static hipError_t run_linears(const exl3_weight *const *ws, const WeightPriv *co
         }
         xp = (const uint16_t *)ss->xp;
       }
-      const exl3::GemmSplit sp = exl3::gemm_split((int)rows, in, (int)pvs[i]->out);
-      if (sp.splits > 1) {
-        hipError_t e = grow(ss, &ss->kpart, &ss->kpart_bytes, sp.part_floats * 4, s);
+      const size_t kpf = exl3::gemm_kpart_floats(rows, in, (int)pvs[i]->out);
+      if (kpf > 0) {
+        hipError_t e = grow(ss, &ss->kpart, &ss->kpart_bytes, kpf * 4, s);
         if (e != hipSuccess) return e;
       }
       hipError_t e = exl3::launch_gemm(
@@ -1062,8 +1071,7 @@ exl3_verdict exl3_matmul_noalloc(const exl3_weight *w, exl3_array x, exl3_stream
   size_t slot_floats = 0, xp_bytes = 0, kpart_bytes = 0;
   if (gemm) {
     xp_bytes = ((size_t)rows * pv->in * 2 + 255) & ~(size_t)255;
-    const exl3::GemmSplit sp = exl3::gemm_split((int)rows, (int)pv->in, (int)pv->out);
-    if (sp.splits > 1) kpart_bytes = sp.part_floats * 4;
+    kpart_bytes = exl3::gemm_kpart_floats(rows, (int)pv->in, (int)pv->out) * 4;
   } else {
     const int outs[1] = {(int)pv->out};
     slot_floats = gemv_slot_need(outs, 1, (int)pv->in,

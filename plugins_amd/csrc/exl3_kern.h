@@ -1194,49 +1194,24 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
 // ===================================================================== GEMM
 //
 // Workgroup tile 256 rows x 128 columns (one Hadamard block of the output),
-// 8 waves, two per SIMD (on gfx950 one wave issues at most one VALU
-// instruction every 8 cycles, so the weight decode needs more than one wave
-// per SIMD to keep pace with the MFMAs).  Wave w owns rows 64 (w / 2) .. + 63
-// and columns 64 (w % 2) .. + 63 as 2 x 2 v_mfma_f32_32x32x16_f16 tiles (64
-// f32 accumulators per lane).  The k loop runs in stages of 64 (four k-tile
-// rows), double-buffered in LDS.  Per stage:
-//  * the next stage's 256 chunks (4 k-tile rows x 8 output tiles x 8 chunks)
-//    are decoded into MFMA B fragments and stored as B^T [n][k]: waves 0-3
-//    decode rows 0-7 of each chunk's two columns, waves 4-7 rows 8-15
-//    (uniform code per wave);
-//  * the activations (prepared rows, f16) are loaded coalesced (8 lanes per
-//    128-byte row piece: an MFMA-layout load that puts 32 rows in one
-//    instruction runs at a quarter of the rate) three stages ahead and
-//    stored into LDS as A [m][k] the stage before they are used;
-//  * both operands are read from LDS in MFMA layout (rows padded to 72
-//    halfs, so the 16-byte reads of 16 consecutive rows hit distinct banks);
-//    within a stage, MFMA step kk contracts k = 32 h + 8 kk + e over lane
-//    half h and element e, the same order for both operands;
-//  * the 16 MFMAs of a wave are issued one per slot, and each slot also
-//    issues a share of the decode, the LDS traffic and the global loads, in
-//    an order fixed at compile time (scheduling barriers between slots);
-//  * one barrier, after the stores into the next buffer and the last reads
-//    of the current one; the next stage's first fragments are read right
-//    after it, under the stage's last MFMAs.
-// The MFMAs take the weights as their first operand, so the accumulators
-// hold z^T: a lane holds one row of z and 16 of its columns.  That is the
-// operand layout of a second MFMA, which applies the finish's Hadamard
-// stages on column bits 0-4 (H_32, +-1 entries: exact products, f32 sums) to
-// f16(z); the 128-column block spans two waves, so stages 5 and 6 go through
-// LDS, then * 1/sqrt(128) * svh.  Each decoded weight serves 256 rows.  Tiles
-// of 128 columns keep the grid a multiple of the 256 CUs at the Qwen3-8B
-// shapes (M = 2048: 256 tiles for 4096 outputs, 768 for 12288).
+// stages of 64 k (four k-tile rows).  The operands meet in LDS in MFMA
+// layout; within a stage, MFMA step kk contracts k = 32 h + 8 kk + e over
+// lane half h and element e, the same order for both operands.  The MFMAs
+// take the weights as their first operand, so the accumulators hold z^T: a
+// lane holds one row of z and 16 of its columns.  That is the operand layout
+// of a second MFMA, which applies the finish's Hadamard stages on column
+// bits 0-4 (H_32, +-1 entries: exact products, f32 sums) to f16(z); the
+// 128-column block spans two waves, so stages 5 and 6 go through LDS, then
+// * 1/sqrt(128) * svh.  Each decoded weight serves 256 rows.  Tiles of 128
+// columns keep the grid a multiple of the 256 CUs at the Qwen3-8B shapes
+// (M = 2048: 256 tiles for 4096 outputs, 768 for 12288).
 
-constexpr int GM_BM = 256, GM_BN = 128, GM_BK = 64, GM_THREADS = 512;
+constexpr int GM_BM = 256, GM_BN = 128, GM_BK = 64;
 constexpr int GM_LD = GM_BK + 8;         // halfs per LDS row of A / column of B^T
-constexpr int GM_ATILE = GM_BM * GM_LD;  // halfs of A per stage buffer
 constexpr int GM_BTILE = GM_BN * GM_LD;  // halfs of B^T per stage buffer
-constexpr int GM_STAGE = GM_ATILE + GM_BTILE;
-constexpr int GM_LDS_BYTES = 2 * GM_STAGE * 2;  // two stage buffers (108 KiB)
 // finish exchange: 64 rows of the 128 columns after the H_32 step (f32),
-// rows padded to 132 floats (33 KiB: within the two stage buffers)
+// rows padded to 132 floats (33 KiB)
 constexpr int GM_FLD = 132;
-static_assert(64 * GM_FLD * 4 <= GM_LDS_BYTES, "finish exchange exceeds the stage buffers");
 
 // Pair place in fragment order: fragment f (0: column a, rows 0-7; 1: column
 // a+8, rows 0-7; 2: column a, rows 8-15; 3: column a+8, rows 8-15) holds
@@ -1245,185 +1220,12 @@ __host__ __device__ constexpr int gm_pair(int f, int J) {
   return ((f == 0) ? 0 : (f == 1) ? 2 : (f == 2) ? 1 : 3) + 4 * J;
 }
 
-// The main loop of one wave; HALF = 0: the wave decodes fragments 0 and 1 of
-// its chunk, 1: fragments 2 and 3.  aoff: element offsets of this thread's
-// four activation pieces (rows 64 u apart) in xp; ast: the first piece's
-// place in an A buffer; ard / brd: the wave's A / B fragment reads.
-//
-// Everything a stage waits for was issued stages earlier: the packed words
-// of stage x are loaded GM_WL stages ahead (a few registers each, so deep:
-// the history exchange of stage x, two stages before its use, then never
-// waits on HBM latency), the activations of stage x three stages ahead
-// (stored into LDS during stage x - 1).
+// Word sets of the decode waves' packed-word ring: the words of stage x are
+// loaded gm_wl stages ahead (a few registers each, so deep: the history
+// exchange of stage x, two stages before its use, then never waits on HBM
+// latency).
 template <int K>
 constexpr int gm_wl() { return K <= 4 ? 6 : 3; }  // word sets (divides the 6-stage trip)
-
-template <int K, int CB, bool MASKED, int HALF>
-__device__ __forceinline__ void gemm_main(f16v_t (&acc)[2][2], uint16_t *lds,
-                                          const uint32_t *twc, size_t wstage, int src, int bst,
-                                          const uint16_t *xp, const int (&aoff)[4], int ast,
-                                          int ard, int brd, int NS, CbRow mask) {
-  constexpr int WL = gm_wl<K>();
-  u4_t ra[3][4];       // activation pieces of stage x in set x % 3
-  uint32_t wn[WL][K];  // packed words of stage x in set x % WL
-  uint32_t hist[2];    // history dword of the chunk of stage x in hist[x % 2]
-  h8_t af[2][2];       // A fragments of a step (step % 2) [row block]
-  h8_t bf[2][2];       // B fragments of a step (step % 2) [column block]
-
-  auto load_a = [&](auto R, int st) {
-    constexpr int r = decltype(R)::value;
-    st = min(st, NS - 1);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      ra[r][u] = *reinterpret_cast<const u4_t *>(xp + aoff[u] + st * GM_BK);
-  };
-  auto store_a = [&](auto R, int buf, int u) {
-    constexpr int r = decltype(R)::value;
-    *reinterpret_cast<u4_t *>(lds + buf * GM_STAGE + ast + 64 * u * GM_LD) = ra[r][u];
-  };
-  auto load_w = [&](auto S, int st) {
-    constexpr int q = decltype(S)::value;
-    const uint32_t *p = twc + (size_t)min(st, NS - 1) * wstage;
-#pragma unroll
-    for (int j = 0; j < K; ++j) wn[q][j] = p[j];
-  };
-  auto read_af = [&](auto Q, int buf, int kk, int i) {
-    constexpr int q = decltype(Q)::value;
-    af[q][i] = *reinterpret_cast<const h8_t *>(lds + buf * GM_STAGE + ard + i * 32 * GM_LD + 8 * kk);
-  };
-  auto read_bf = [&](auto Q, int buf, int kk, int j) {
-    constexpr int q = decltype(Q)::value;
-    bf[q][j] = *reinterpret_cast<const h8_t *>(lds + buf * GM_STAGE + GM_ATILE + brd +
-                                               j * 32 * GM_LD + 8 * kk);
-  };
-  auto bperm = [&](auto S, auto HS) {
-    constexpr int q = decltype(S)::value, hq = decltype(HS)::value;
-    hist[hq] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)wn[q][K - 1]);
-  };
-  // pair P of the chunk held in word set S (history hist[HS])
-  auto pair = [&](auto S, auto HS, auto P) -> uint32_t {
-    constexpr int q = decltype(S)::value, hq = decltype(HS)::value, p = decltype(P)::value;
-    uint32_t wd[K + 1];
-    wd[0] = hist[hq];
-#pragma unroll
-    for (int j = 0; j < K; ++j) wd[j + 1] = wn[q][j];
-    return chunk_pair_cw<K, CB, MASKED, p>(wd, mask);
-  };
-  auto store_frag = [&](int buf, int f, const uint32_t (&v4)[4]) {
-    const u4_t v = {v4[0], v4[1], v4[2], v4[3]};
-    *reinterpret_cast<u4_t *>(lds + buf * GM_STAGE + GM_ATILE + bst + 8 * (f & 1) * GM_LD +
-                              8 * (f >> 1)) = v;
-  };
-  using IC0 = std::integral_constant<int, 0>;
-  using IC1 = std::integral_constant<int, 1>;
-
-  // Stage st (PH = st % 6; buffer st % 2): stores the activations of stage
-  // st + 1 and decodes its words into the other buffer, loads the words of
-  // stage st + WL and the activations of stage st + 3 (into the sets of
-  // stage st, consumed), reads the next stage's first fragments after the
-  // barrier, and forms the history of stage st + 2.
-  auto stage = [&](auto PH, int st) {
-    constexpr int ph = decltype(PH)::value;
-    using A1 = std::integral_constant<int, (ph + 1) % 3>;   // activations of st + 1
-    using A0 = std::integral_constant<int, ph % 3>;         // ... of st, then st + 3
-    using W0 = std::integral_constant<int, ph % WL>;        // words of st, then st + WL
-    using W1 = std::integral_constant<int, (ph + 1) % WL>;  // words of st + 1
-    using W2 = std::integral_constant<int, (ph + 2) % WL>;  // words of st + 2
-    using H1 = std::integral_constant<int, (ph + 1) & 1>;
-    using H2 = std::integral_constant<int, ph & 1>;
-    const int cur = st & 1, nxt = cur ^ 1;
-    uint32_t fr[4];
-    static_for<16>([&](auto SL) {
-      constexpr int s = decltype(SL)::value;
-      constexpr int kk = s >> 2, i = (s >> 1) & 1, j = s & 1;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk & 1][j], af[kk & 1][i], acc[i][j],
-                                                          0, 0, 0);
-      // the next step's fragments, under this step's MFMAs (the last step's
-      // two per slot, so that they are in before the barrier)
-      if constexpr (kk < 2) {
-        using QN = std::integral_constant<int, (kk + 1) & 1>;
-        if constexpr ((s & 3) < 2) read_af(QN{}, cur, kk + 1, s & 1);
-        if constexpr ((s & 3) >= 2) read_bf(QN{}, cur, kk + 1, s & 1);
-      }
-      if constexpr (s == 8) {
-        read_af(IC1{}, cur, 3, 0);
-        read_af(IC1{}, cur, 3, 1);
-      }
-      if constexpr (s == 9) {
-        read_bf(IC1{}, cur, 3, 0);
-        read_bf(IC1{}, cur, 3, 1);
-      }
-      // the next stage's activations into the other buffer
-      if constexpr (s < 4) store_a(A1{}, nxt, s);
-      // decode of the next stage: one pair per slot, a fragment store after
-      // every fourth
-      if constexpr (s >= 1 && s <= 8) {
-        constexpr int fl = (s - 1) >> 2, J = (s - 1) & 3;
-        constexpr int f = 2 * HALF + fl;
-        fr[J] = pair(W1{}, H1{}, std::integral_constant<int, gm_pair(f, J)>{});
-        if constexpr (J == 3) store_frag(nxt, f, fr);
-      }
-      if constexpr (s == 9) {
-        load_w(W0{}, st + WL);
-        load_a(A0{}, st + 3);
-      }
-      // the next buffer is complete and this one is read (the last step's
-      // fragments are in registers): one barrier, then the next stage's
-      // first fragments
-      if constexpr (s == 10) lds_barrier();
-      if constexpr (s == 12) {
-        read_af(IC0{}, nxt, 0, 0);
-        read_af(IC0{}, nxt, 0, 1);
-      }
-      if constexpr (s == 13) {
-        read_bf(IC0{}, nxt, 0, 0);
-        read_bf(IC0{}, nxt, 0, 1);
-      }
-      if constexpr (s == 15) bperm(W2{}, H2{});
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-
-  // prologue: words of stages 0 .. WL-1, activations of stages 0-2 in
-  // flight; stage 0 decoded and stored into buffer 0, the first fragments
-  // read, the history of stage 1 formed
-  static_for<WL>([&](auto W) { load_w(W, decltype(W)::value); });
-  load_a(IC0{}, 0);
-  load_a(IC1{}, 1);
-  load_a(std::integral_constant<int, 2>{}, 2);
-  bperm(IC0{}, IC0{});
-  static_for<2>([&](auto FL) {
-    constexpr int f = 2 * HALF + decltype(FL)::value;
-    uint32_t v4[4];
-    static_for<4>([&](auto J) {
-      v4[J] = pair(IC0{}, IC0{}, std::integral_constant<int, gm_pair(f, decltype(J)::value)>{});
-    });
-    store_frag(0, f, v4);
-  });
-#pragma unroll
-  for (int u = 0; u < 4; ++u) store_a(IC0{}, 0, u);
-  bperm(IC1{}, IC1{});
-  lds_barrier();
-  read_af(IC0{}, 0, 0, 0);
-  read_af(IC0{}, 0, 0, 1);
-  read_bf(IC0{}, 0, 0, 0);
-  read_bf(IC0{}, 0, 0, 1);
-
-  // six stages per trip (word sets cycle by WL, activations by 3, the rest by 2)
-  int st = 0;
-  for (; st + 6 <= NS; st += 6) {
-    static_for<6>([&](auto PH) { stage(PH, st + decltype(PH)::value); });
-  }
-  // NS is even: 0, 2 or 4 stages left
-  if (st < NS) {
-    stage(std::integral_constant<int, 0>{}, st);
-    stage(std::integral_constant<int, 1>{}, st + 1);
-    if (st + 2 < NS) {
-      stage(std::integral_constant<int, 2>{}, st + 2);
-      stage(std::integral_constant<int, 3>{}, st + 3);
-    }
-  }
-}
 
 // The end of a GEMM tile, by all THREADS threads of the workgroup (mw: this
 // wave holds accumulators, wave tile (wm, wc); the others take part in the
@@ -1541,85 +1343,18 @@ __device__ __forceinline__ void gemm_tile_end(f16v_t (&acc)[2][2], uint16_t *lds
   });
 }
 
-template <int K, int CB, bool MASKED>
-__global__ __launch_bounds__(GM_THREADS, 1) void gemm_kernel(
-    const uint32_t *__restrict__ tw, const uint16_t *__restrict__ xp,
-    const uint16_t *__restrict__ svh, void *__restrict__ y, int ydt, uint16_t *__restrict__ zout,
-    int M, int in_tiles, int out_tiles, CbRow mask, float *__restrict__ kpart) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[GM_LDS_BYTES / 2];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wc = wave & 1;
-  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking the
-  // row block as n % (row blocks) gives each XCD a few row blocks of the
-  // activations to keep in its L2.  (Only the speed depends on this.)
-  const int mblocks = gridDim.y;
-  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
-  const int cg = lin / mblocks;  // output columns 128 cg ..
-  const int m0 = (lin % mblocks) * GM_BM;
-  const int in = in_tiles * 16;
-  const size_t out = (size_t)out_tiles * 16;
-  constexpr int NW = 8 * K;     // trellis dwords per tile
-  const int NS = in_tiles / 4;  // stages (even, >= 2: in is a multiple of 128)
-
-  // decoder role: chunk c of output tile tnl of k-tile row tkl of a stage
-  // (threads t and t + 256 take the same chunk); the 8 chunks of a tile sit
-  // in 8 consecutive lanes
-  const int dt = tid & 255;
-  const int tkl = dt >> 6, tnl = (dt >> 3) & 7, c = dt & 7;
-  const uint32_t *twc = tw + ((size_t)tkl * out_tiles + cg * 8 + tnl) * NW + c * K;
-  const size_t wstage = (size_t)4 * out_tiles * NW;  // dwords per stage
-  const int src = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of chunk c-1
-  const int bst = (tnl * 16 + c) * GM_LD + tkl * 16;     // fragment 0's LDS place
-
-  // activation loads: 16-byte piece (tid & 7) of rows (tid >> 3) + 64 u of
-  // the tile; rows past M read row M - 1 (not stored: rows of an MFMA are
-  // independent)
-  int aoff[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) aoff[u] = min(m0 + (tid >> 3) + 64 * u, M - 1) * in + (tid & 7) * 8;
-  const int ast = (tid >> 3) * GM_LD + (tid & 7) * 8;
-  // fragment reads: row 64 wm + 32 i + (lane & 31) / column
-  // 64 wc + 32 j + (lane & 31), k 32 h + 8 kk with h = lane / 32
-  const int h = lane >> 5;
-  const int ard = (64 * wm + (lane & 31)) * GM_LD + 32 * h;
-  const int brd = (64 * wc + (lane & 31)) * GM_LD + 32 * h;
-
-  f16v_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  // split-K (small grids): split ks of S takes an even run of the stages
-  const int S = gridDim.z, ks = blockIdx.z;
-  const int P = NS / 2;
-  const int st0 = 2 * (P * ks / S), st1 = 2 * (P * (ks + 1) / S);
-  if (wave < 4)
-    gemm_main<K, CB, MASKED, 0>(acc, lds, twc + (size_t)st0 * wstage, wstage, src, bst,
-                                xp + st0 * GM_BK, aoff, ast, ard, brd, st1 - st0, mask);
-  else
-    gemm_main<K, CB, MASKED, 1>(acc, lds, twc + (size_t)st0 * wstage, wstage, src, bst,
-                                xp + st0 * GM_BK, aoff, ast, ard, brd, st1 - st0, mask);
-
-  gemm_tile_end<GM_THREADS>(acc, lds, true, wm, wc, m0, cg, M, out, S, ks, svh, y, ydt, zout,
-                            kpart);
-}
-
 // ================================================ GEMM, specialised waves
 //
-// gemm_ws_kernel: gemm_kernel's tile (256 rows x 128 columns, 64-k stages),
-// arithmetic and result, with the work split by wave.  Waves 0-7 (the MFMA
+// gemm_ws_kernel: the tile above (256 rows x 128 columns, 64-k stages), with
+// the work split by wave.  Waves 0-7 (the MFMA
 // waves, wave tile 64 x 64) issue the MFMAs and bring the activations into
 // LDS with direct global-to-LDS loads (no registers; three A buffers, the
 // loads of stage x issued during stage x - 2).  Waves 8-15 (the decode
 // waves) decode the next stage's packed words into the other B buffer: the
 // 256 chunks of a stage, half a chunk per thread (waves 8-11 rows 0-7 of
 // each chunk's columns, waves 12-15 rows 8-15).  Four waves per SIMD: the
-// decode's VALU work issues beside the other waves' MFMAs.  One barrier per stage, as in
-// gemm_kernel.
+// decode's VALU work issues beside the other waves' MFMAs.  One barrier per
+// stage.
 //
 // A buffer (unpadded, 128 bytes a row): 16-byte piece q of row R sits at
 // piece place q ^ ((R / 2) % 8), so a fragment read (rows R0 .. R0 + 15 of
@@ -1898,7 +1633,10 @@ __global__ __launch_bounds__(GW_THREADS, 1) void gemm_ws_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool mw = wave < 8;
   const int wm = (wave & 7) >> 1, wc = wave & 1;
-  const int mblocks = gridDim.y;  // row block n % (row blocks) per XCD, as gemm_kernel
+  // Workgroup n runs on XCD n % 8 (the dispatcher's round robin); taking the
+  // row block as n % (row blocks) gives each XCD a few row blocks of the
+  // activations to keep in its L2.  (Only the speed depends on this.)
+  const int mblocks = gridDim.y;
   const int lin = blockIdx.x + gridDim.x * blockIdx.y;
   const int cg = lin / mblocks;
   const int m0 = (lin % mblocks) * GM_BM;
@@ -2272,35 +2010,17 @@ void moe_gemv_go(const Format &f, int pro, dim3 grid, size_t lds, hipStream_t s,
   });
 }
 
-#ifndef EXL3_GEMM_WS
-#define EXL3_GEMM_WS 1
-#endif
-constexpr bool GEMM_WAVE_SPECIALISED = EXL3_GEMM_WS != 0;
 
 template <int K>
 void gemm_go(const Format &f, dim3 grid, hipStream_t s, const uint32_t *tw, const uint16_t *xp,
              const uint16_t *svh, void *y, int ydt, uint16_t *zout, int M, int in_tiles,
              int out_tiles, float *kpart) {
   static_assert(K > 0, "the GEMM serves integer rates");
-  const dim3 blk(GM_THREADS);
   const CbRow m = f.dec();
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, blk, 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles,
-                       m, kpart);
-  };
-  // the specialised kernel addresses the activations with 32-bit offsets
-  if (GEMM_WAVE_SPECIALISED && (size_t)M * in_tiles * 32 <= 0xFFFFFFFFu) {
-    auto gow = [&](auto kern) {
-      hipLaunchKernelGGL(kern, grid, dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, zout, M,
-                         in_tiles, out_tiles, m, kpart);
-    };
-    cb_dispatch<K>(f, [&](auto CBC, auto MC) {
-      gow(gemm_ws_kernel<K, decltype(CBC)::value, decltype(MC)::value>);
-    });
-    return;
-  }
   cb_dispatch<K>(f, [&](auto CBC, auto MC) {
-    go(gemm_kernel<K, decltype(CBC)::value, decltype(MC)::value>);
+    hipLaunchKernelGGL((gemm_ws_kernel<K, decltype(CBC)::value, decltype(MC)::value>), grid,
+                       dim3(GW_THREADS), 0, s, tw, xp, svh, y, ydt, zout, M, in_tiles, out_tiles, m,
+                       kpart);
   });
 }
 

@@ -218,6 +218,9 @@ struct GemmSplit {
   size_t part_floats = 0;
 };
 GemmSplit gemm_split(int rows, int in, int out);
+// The split-K plane floats a launch_gemm call of `rows` rows needs (its row
+// windows' largest; 0: no split).
+size_t gemm_kpart_floats(int64_t rows, int in, int out);
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
                        int out, float *kpart, size_t kpart_floats, hipStream_t s);

@@ -701,15 +701,39 @@ GemmSplit gemm_split(int rows, int in, int out) {
   return g;
 }
 
+// The most rows one GEMM launch takes: the kernel addresses a launch's
+// activations with 32-bit byte offsets, so a call past that runs as windows
+// of whole row tiles, each its own launch (rows are independent: the same
+// results).
+static int64_t gemm_window_rows(int in) {
+  return std::max<int64_t>(GM_BM, (int64_t)(0xFFFFFFFFull / ((uint64_t)in * 2)) / GM_BM * GM_BM);
+}
+
+size_t gemm_kpart_floats(int64_t rows, int in, int out) {
+  const int64_t wmax = gemm_window_rows(in);
+  const int64_t last = rows > wmax ? (rows - 1) % wmax + 1 : rows;
+  size_t need = gemm_split((int)std::min(rows, wmax), in, out).part_floats;
+  return std::max(need, gemm_split((int)last, in, out).part_floats);
+}
+
 hipError_t launch_gemm(const uint16_t *trellis, const Format &f, const uint16_t *xp,
                        const uint16_t *svh, void *y, int ydt, uint16_t *zout, int rows, int in,
                        int out, float *kpart, size_t kpart_floats, hipStream_t s) {
   if (rows < 1 || in <= 0 || out <= 0 || in % 128 != 0 || out % 128 != 0) return hipErrorInvalidValue;
   if (!f.gemm_rate()) return hipErrorInvalidValue;
-  // the half-integer rates run the specialised-wave kernel only, whose
-  // activation offsets are 32-bit
-  if (!f.integer_rate() && (size_t)rows * (in / 16) * 32 > 0xFFFFFFFFu) return hipErrorInvalidValue;
   if (y == nullptr && zout == nullptr) return hipErrorInvalidValue;
+  const int64_t wmax = gemm_window_rows(in);
+  if (rows > wmax) {
+    const size_t ysz = ydt == OUT_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < rows; r0 += wmax) {
+      const int r = (int)std::min<int64_t>(wmax, rows - r0);
+      const hipError_t e = launch_gemm(
+          trellis, f, xp + (size_t)r0 * in, svh, y ? (char *)y + (size_t)r0 * out * ysz : nullptr,
+          ydt, zout ? zout + (size_t)r0 * out : nullptr, r, in, out, kpart, kpart_floats, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   const int mblocks = (rows + GM_BM - 1) / GM_BM;
   if (mblocks > 65535) return hipErrorInvalidValue;
   const GemmSplit sp = gemm_split(rows, in, out);

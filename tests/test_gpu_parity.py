@@ -264,6 +264,30 @@ def test_gemm_full_size_sampled_rows():
     assert S.rel_fro(y[pick], yo) < 1e-3
 
 
+def test_gemm_beyond_32bit_activation_offsets():
+    """Prefill activations past 4 GiB (270,000 rows x 8192 f16 = 4.4 GB): the
+    GEMM kernel addresses a launch's activations with 32-bit offsets, so such
+    calls run as windows of whole row tiles (261,888 rows of 16 KiB here; the
+    last window of 8,112 rows splits k).  Rows on both sides of the window
+    edge and of the 4 GiB offset against the oracle's projection, within the
+    bar."""
+    rng = np.random.default_rng(8192)
+    in_f, out_f, n, rows = 8192, 256, 64, 270000
+    assert rows * in_f * 2 > 1 << 32
+    lin, trellis, suh, svh = make(rng, in_f, out_f, n)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(rows, in_f, generator=g, device=DEV, dtype=torch.float32).to(torch.float16)
+    y = lin(x)
+    torch.cuda.synchronize()
+    sample = np.array([0, 1, 131071, 261887, 261888, 262143, 262144, 269999])
+    xs = x[torch.from_numpy(sample).to(DEV)].cpu().numpy()
+    got = y[torch.from_numpy(sample).to(DEV)].float().cpu().numpy()
+    del x, y
+    want = S.h2f(O.project(xs.astype(np.float32), trellis, suh, svh, in_f, out_f, n))
+    assert S.rel_fro(got, want) < 1e-3
+    assert S.row_rel(got, want).max() < 2e-3
+
+
 @pytest.mark.parametrize("rows,in_f,out_f,n", [(17, 4096, 1024, 64), (128, 4096, 4096, 64),
                                                (300, 2048, 512, 48), (513, 1024, 256, 80)])
 def test_gemm_split_k(rows, in_f, out_f, n):

@@ -2,9 +2,11 @@
 unrotate, linear_joined) through the C ABI: the un-rotated public matrix bit
 for bit against the oracle's reconstructPublic (sushi_ds41/src/sushi/exl3/
 expert_exl3.zig:440-488, the same f32 operation order) and against the
-float64 formula; prefill matmuls over held and joined matrices within the
-1e-3 relative Frobenius bar of the oracle's projection (bf16: 2^-8); decode widths
-unchanged (the EXL3 GEMV, bit for bit); the accounting and the refusals.
+float64 formula; prefill matmuls over held matrices (rates without the
+prefill GEMM; at the GEMM's rates nothing is held and the GEMM stays, bit for
+bit) and joined matrices within the 1e-3 relative Frobenius bar of the
+oracle's projection (bf16: 2^-8); decode widths unchanged (the EXL3 GEMV, bit
+for bit); the accounting and the refusals.
 Paths relative to /root/reference/plugins/."""
 import numpy as np
 import pytest
@@ -99,9 +101,28 @@ def test_joined_group_against_the_oracle(act):
 
 
 @pytest.mark.parametrize("rows", [17, 64, 300])
-def test_resident_prefill_matmul(rows):
+def test_resident_holds_nothing_at_gemm_rates(rows):
+    """At the prefill GEMM's rates the fused GEMM outruns the held-matrix
+    path: resident admits the weight and reserves its bytes (pending, for
+    unrotate) but holds nothing, and prefill matmuls stay the EXL3 GEMM, bit
+    for bit."""
     in_f, out_f = 512, 384
-    rng, lin, (t, u, v) = _lin(31 + rows, in_f, out_f)
+    rng, lin, _ = _lin(61 + rows, in_f, out_f, n=64)
+    x = dev_f16(S.activations(rng, rows, in_f))
+    plain = lin(x)
+    assert X.resident([lin.weight]) == in_f * out_f * 2
+    assert X.resident_pending() == in_f * out_f * 2
+    assert (bits(lin(x)) == bits(plain)).all()
+    assert X.resident_pending() == in_f * out_f * 2
+
+
+@pytest.mark.parametrize("rows", [17, 64, 300])
+def test_resident_prefill_matmul(rows):
+    """A rate without the prefill GEMM (n = 50: 16-row GEMV passes above 16
+    rows): the held W_inner path, within the bar."""
+    in_f, out_f, n = 512, 384, 50
+    rng, lin, (t, u, v) = _lin(31 + rows, in_f, out_f, n=n)
+    assert X.matmul_path(lin.weight, rows) == "gemv"
     x = dev_f16(S.activations(rng, rows, in_f))
     plain = lin(x)
     one = dev_f16(S.activations(rng, 1, in_f))
@@ -113,7 +134,7 @@ def test_resident_prefill_matmul(rows):
     assert X.resident_pending() == in_f * out_f * 2
     y = lin(x)  # the first prefill call holds the decoded matrix
     assert X.resident_pending() == 0
-    yo = S.h2f(O.project(x.float().cpu().numpy(), t, u, v, in_f, out_f, 64))
+    yo = S.h2f(O.project(x.float().cpu().numpy(), t, u, v, in_f, out_f, n))
     assert S.rel_fro(y.float().cpu().numpy(), yo) < 1e-3
     assert S.rel_fro(y.float().cpu().numpy(), plain.float().cpu().numpy()) < 1e-3
     # twice in a row: the same bytes
@@ -125,7 +146,7 @@ def test_resident_prefill_matmul(rows):
 
 def test_resident_refusals():
     in_f, out_f = 256, 256
-    rng, lin, _ = _lin(41, in_f, out_f)
+    rng, lin, _ = _lin(41, in_f, out_f, n=50)
     with pytest.raises(X.Exl3Error) as e:
         X.resident([lin.weight], room=in_f * out_f * 2 - 1)
     assert e.value.code == X.TOO_LARGE
@@ -150,8 +171,8 @@ def test_resident_refusals():
 
 def test_release_of_a_resident_weight():
     in_f, out_f = 256, 256
-    rng, lin, _ = _lin(51, in_f, out_f)
-    _, keep, _ = _lin(52, in_f, out_f)
+    rng, lin, _ = _lin(51, in_f, out_f, n=50)
+    _, keep, _ = _lin(52, in_f, out_f, n=50)
     X.resident([lin.weight, keep.weight])
     x = dev_f16(S.activations(rng, 32, in_f))
     lin(x)

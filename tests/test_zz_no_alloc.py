@@ -129,20 +129,25 @@ def test_noalloc_give_up_is_reported_and_reset():
 
 
 def test_noalloc_keeps_trellis_kernels_for_resident_weights():
-    """A weight admitted by exl3_resident: exl3_matmul above 16 rows takes the
-    dense GEMM over the held matrix; the no-alloc entry keeps the trellis
-    GEMM, equal bit for bit to exl3_matmul of the same weight before it was
-    admitted, and within the matmul bar of the resident result."""
+    """A weight that holds a matrix through exl3_resident (n = 50, a rate
+    without the prefill GEMM): exl3_matmul above 16 rows takes the dense GEMM
+    over it; the no-alloc entry keeps the trellis kernels, equal bit for bit
+    to exl3_matmul of the weight before it was admitted, and within the
+    matmul bar of the resident result.  At a GEMM rate (n = 64) nothing is
+    held and the two entries stay equal bit for bit."""
     rng = np.random.default_rng(23)
-    lin = linear(rng, 1024, 512)
+    lin = linear(rng, 1024, 512, n=50)
+    lin64 = linear(rng, 1024, 512, n=64)
     x = torch.from_numpy(S.activations(rng, 64, 1024)).to(DEV)
     got0, want0 = both(lin, x)
     assert torch.equal(got0, want0)
-    X.resident([lin.weight])
+    X.resident([lin.weight, lin64.weight])
     try:
         got, want_res = both(lin, x)
         assert torch.equal(got, want0)  # trellis kernels, as before admission
         g64, w64 = got.double(), want_res.double()
         assert float(torch.linalg.norm(g64 - w64) / torch.linalg.norm(w64)) < 1e-3
+        a, b = both(lin64, x)
+        assert torch.equal(a, b)
     finally:
         X.resident([])
