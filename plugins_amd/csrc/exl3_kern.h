@@ -918,7 +918,7 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
                                         const GemvGeo &geo, const GemvCfg &a,
                                         const GemvWeight &W, int expert, int nrows,
                                         const RowMap &rm, int cg, int ks, char *smem,
-                                        int rows_alloc) {
+                                        int rows_alloc, const uint16_t *psuh = nullptr) {
   // PREP 0: the rows' items fit one prepare batch (one item per wave);
   // else the rows form in PREP passes
   constexpr bool ONEB = PREP == 0;
@@ -972,6 +972,16 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   } else {
     gemv_rows_load_x(x, geo.xdt, geo.prepared, rm, nitems, nb, tk0, rr);
   }
+  // psuh (a preloaded argument, plain prologue): suh's loads go out right
+  // after x's, and no load waits for the argument segment
+  const bool early = PRO == PRO_PLAIN && psuh != nullptr;
+  if (early) {
+    if constexpr (ONEB)
+      gemv_prep_load_su(x, geo.prepared, psuh + (size_t)expert * in, nitems, nb, tk0, 0, wave,
+                        lane, pr);
+    else
+      gemv_rows_load_su(x, geo.prepared, psuh + (size_t)expert * in, nitems, nb, tk0, rr);
+  }
   if constexpr (K > 0) {
 #pragma unroll
     for (int i = 0; i < K; ++i) bw[0][i] = wp[i];
@@ -990,13 +1000,15 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   // argument segment (a scalar load issued at entry); passing it through an
   // empty asm statement that also orders memory keeps the wait for that
   // scalar load after the loads above are issued.
-  const uint16_t *suh0 = W.suh;
-  asm volatile("" : "+s"(suh0)::"memory");
-  const uint16_t *suh = suh0 + (size_t)expert * in;
-  if constexpr (ONEB)
-    gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
-  else
-    gemv_rows_load_su(x, geo.prepared, suh, nitems, nb, tk0, rr);
+  if (!early) {
+    const uint16_t *suh0 = W.suh;
+    asm volatile("" : "+s"(suh0)::"memory");
+    const uint16_t *suh = suh0 + (size_t)expert * in;
+    if constexpr (ONEB)
+      gemv_prep_load_su(x, geo.prepared, suh, nitems, nb, tk0, 0, wave, lane, pr);
+    else
+      gemv_rows_load_su(x, geo.prepared, suh, nitems, nb, tk0, rr);
+  }
   if constexpr (PRO == PRO_SWIGLU) {
     // SwiGLU prologue: x is gate; up from the argument segment, like suh
     const uint16_t *up = a.x2;
@@ -1020,7 +1032,8 @@ __device__ __forceinline__ void gemv_wg(const uint32_t *twe, int out_tiles, cons
   }
   // svh of this lane's two columns (read whether or not the finish runs: a
   // load without a branch around it)
-  const uint16_t *svp = W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : suh;
+  const uint16_t *svp =
+      W.svh != nullptr ? W.svh + (size_t)expert * out + cg * 128 : W.suh + (size_t)expert * in;
   const uint32_t sv = ld_global_u32(svp + 2 * lane);
   // residual finish: the column group's residual pairs of the rows this wave
   // finishes (rows wave, wave + 8), loaded now so the finish does not wait
@@ -1183,12 +1196,21 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(
   const uint32_t *tw = ws.wi == 0 ? tw0 : ws.wi == 1 ? tw1 : ws.wi == 2 ? tw2 : tw3;
   const int out_tiles = 8 * (ws.c1 - ws.c0);
   const RowMap rm{nullptr, geo.in_tiles * 16, out_tiles * 16};
+  // launches of fewer than four weights carry suh pointers in the unused
+  // trellis arguments (gemv_multi puts them there): one weight tw1; two tw2,
+  // tw3; three tw3 for weight 0
+  const int nwt = 1 + (geo.cg1 > 0) + (geo.cg2 > 0) + (geo.cg3 > 0);
+  const uint16_t *psuh =
+      nwt == 1   ? (const uint16_t *)tw1
+      : nwt == 2 ? (const uint16_t *)(ws.wi == 0 ? tw2 : tw3)
+      : nwt == 3 && ws.wi == 0 ? (const uint16_t *)tw3
+                               : nullptr;
   // stacked prepared rows: weight wi's set follows the sets of weights < wi
   const void *xw = geo.stacked ? (const void *)((const uint16_t *)x + (size_t)ws.wi * geo.rows *
                                                                           geo.in_tiles * 16)
                                : x;
   gemv_wg<K, CB, MASKED, PREP, PRO>(tw, out_tiles, xw, geo, a.c, a.w[ws.wi], 0, geo.rows, rm,
-                               blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows);
+                               blockIdx.x - ws.c0, blockIdx.y, smem + 256, geo.rows, psuh);
 }
 
 // ===================================================================== GEMM

@@ -490,6 +490,16 @@ static hipError_t gemv_multi(const GemvLinear *ls, int count, const Format &f, c
     w.partial = sc[i].partial;
   }
   if (ksplit > 1 && sc[0].status == nullptr) return hipErrorInvalidValue;
+  // the unused trellis arguments carry suh pointers, which gemv_kernel's
+  // workgroups read without waiting for the argument segment
+  if (count == 1) {
+    tw[1] = reinterpret_cast<const uint32_t *>(ls[0].suh);
+  } else if (count == 2) {
+    tw[2] = reinterpret_cast<const uint32_t *>(ls[0].suh);
+    tw[3] = reinterpret_cast<const uint32_t *>(ls[1].suh);
+  } else if (count == 3) {
+    tw[3] = reinterpret_cast<const uint32_t *>(ls[0].suh);
+  }
   a.c.status = sc[0].status;
   a.c.poll_max = splitk_poll_max();
   a.c.drop_partials = splitk_drop();
