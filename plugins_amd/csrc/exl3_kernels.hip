@@ -1150,6 +1150,22 @@ bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic) {
 
 namespace {
 
+// A grouped GEMV launch's k-splits: as many as keep the launch within one
+// round of co-resident workgroups (three per CU on 256 CUs: a second,
+// partial round and the split-K hand-off cost more than the longer splits;
+// DeepSeek-V3's down at one row: 448 workgroups unsplit, 3 % faster a call
+// than 896 in two splits), splits of at most MOE_TPS_MAX k-tiles.
+constexpr int MOE_RESIDENT_WG = 3 * 256;
+void moe_plan(int in, int out, int groups, int *ksplit, int *tps) {
+  const int nb = in / 128;
+  const int cgs = std::max(1, out / 128) * std::max(1, groups);
+  const int ks = std::min(nb, std::max(1, MOE_RESIDENT_WG / cgs));
+  int bps = std::min(MOE_TPS_MAX / 8, (nb + ks - 1) / ks);
+  bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
+  *tps = 8 * bps;
+  *ksplit = (nb + bps - 1) / bps;
+}
+
 MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   MoeLayout L{};
   const int slots = a.rows * a.topk;
@@ -1158,8 +1174,8 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   const int item_rows = L.gemm ? GM_BM : MOE_ITEM_ROWS;
   L.max_items = std::min(a.experts, slots) + (slots + item_rows - 1) / item_rows;
   const int groups = std::max(1, std::min(a.experts, slots));
-  gemv_plan(a.hidden, a.inter, 2 * groups, 1, &L.ks_gu, &L.tps_gu, MOE_TPS_MAX);
-  gemv_plan(a.inter, a.hidden, groups, 1, &L.ks_d, &L.tps_d, MOE_TPS_MAX);
+  moe_plan(a.hidden, a.inter, 2 * groups, &L.ks_gu, &L.tps_gu);
+  moe_plan(a.inter, a.hidden, groups, &L.ks_d, &L.tps_d);
   if (generic_gu && L.tps_gu > 32) {
     L.tps_gu = 32;
     L.ks_gu = (a.hidden / 16 + 31) / 32;
