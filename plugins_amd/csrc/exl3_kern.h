@@ -1754,6 +1754,10 @@ constexpr int MOE_ITEM_ROWS = 8;
 constexpr int MOE_TPS_MAX = 128;
 static_assert(MOE_ITEM_ROWS * (MOE_TPS_MAX / 8) <= PREP_PASSES * PREP_GROUPS,
               "a work item's prepare exceeds the rows form");
+// One-row items (no item list) take splits of up to 160 k-tiles: their rows
+// form is one pass, and one row of LDS keeps three workgroups a CU.
+constexpr int MOE_DIRECT_TPS_MAX = 160;
+static_assert(MOE_DIRECT_TPS_MAX / 8 <= PREP_GROUPS, "a one-row item's prepare exceeds one pass");
 
 // Grouped GEMV: blockIdx.z = work item, blockIdx.x = column group over the
 // launch's weights (gate and up side by side, or down).  Raw inputs are rows
@@ -1811,7 +1815,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void moe_gemv_kernel(
     gemv_wg<K, CB, MASKED, decltype(P)::value, PRO>(twe, out_tiles, x, geo, a.c, Wx,
                                                sh ? 0 : (int)it.expert, (int)it.count, rm,
                                                blockIdx.x - ws.c0, blockIdx.y, smem + 256,
-                                               MOE_ITEM_ROWS);
+                                               items != nullptr ? MOE_ITEM_ROWS : 1);
   };
   const int items_n = (int)it.count * (geo.tps / 8);
   if (items_n <= PREP_ITEMS)

@@ -1127,6 +1127,7 @@ struct MoeLayout {
   size_t partial_floats;  // slots in the separate slot buffer: gate, up, down
   int slots, max_items, ks_gu, ks_d, tps_gu, tps_d;
   bool gemm;  // prefill-sized expert batches: grouped GEMMs over 256-slot items
+  bool direct;  // one row, routes given: every slot its own one-row item
 };
 
 // Down GEMV launches of at most this many workgroups take the mid step in
@@ -1154,13 +1155,16 @@ namespace {
 // round of co-resident workgroups (three per CU on 256 CUs: a second,
 // partial round and the split-K hand-off cost more than the longer splits;
 // DeepSeek-V3's down at one row: 448 workgroups unsplit, 3 % faster a call
-// than 896 in two splits), splits of at most MOE_TPS_MAX k-tiles.
+// than 896 in two splits), splits of at most MOE_TPS_MAX k-tiles, or
+// MOE_DIRECT_TPS_MAX for one-row items (direct: DeepSeek-V3's gate+up at one
+// row in 3 splits of 19 blocks, 768 workgroups, ~4 % faster a call than 4
+// splits of up to 16 blocks, 1024 workgroups).
 constexpr int MOE_RESIDENT_WG = 3 * 256;
-void moe_plan(int in, int out, int groups, int *ksplit, int *tps) {
+void moe_plan(int in, int out, int groups, bool direct, int *ksplit, int *tps) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
   const int ks = std::min(nb, std::max(1, MOE_RESIDENT_WG / cgs));
-  int bps = std::min(MOE_TPS_MAX / 8, (nb + ks - 1) / ks);
+  int bps = std::min((direct ? MOE_DIRECT_TPS_MAX : MOE_TPS_MAX) / 8, (nb + ks - 1) / ks);
   bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
   *tps = 8 * bps;
   *ksplit = (nb + bps - 1) / bps;
@@ -1171,11 +1175,15 @@ MoeLayout moe_layout(const MoeArgs &a, bool generic_gu, bool generic_d) {
   const int slots = a.rows * a.topk;
   L.slots = slots;
   L.gemm = moe_uses_gemm(a, generic_gu, generic_d);
+  // one row with its routes given: every slot its own work item, read from
+  // the routes directly (no route launch; a row's routes name distinct
+  // experts, and a repeated one would only be read twice)
+  L.direct = !L.gemm && a.rows == 1 && a.inds != nullptr;
   const int item_rows = L.gemm ? GM_BM : MOE_ITEM_ROWS;
   L.max_items = std::min(a.experts, slots) + (slots + item_rows - 1) / item_rows;
   const int groups = std::max(1, std::min(a.experts, slots));
-  moe_plan(a.hidden, a.inter, 2 * groups, &L.ks_gu, &L.tps_gu);
-  moe_plan(a.inter, a.hidden, groups, &L.ks_d, &L.tps_d);
+  moe_plan(a.hidden, a.inter, 2 * groups, L.direct, &L.ks_gu, &L.tps_gu);
+  moe_plan(a.inter, a.hidden, groups, L.direct, &L.ks_d, &L.tps_d);
   if (generic_gu && L.tps_gu > 32) {
     L.tps_gu = 32;
     L.ks_gu = (a.hidden / 16 + 31) / 32;
@@ -1367,10 +1375,8 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
   const size_t gu_part = (size_t)L.ks_gu * L.slots * a.inter;
   MoeGemv mgu = moe_gemv(a.x, a.xdt, false, L.slots, a.hidden, a.inter, gate.f, L.ks_gu, L.tps_gu);
   mgu.nweights = 2;
-  // one row: every slot its own work item, read from the routes directly,
-  // no route launch (a row's routes name distinct experts; a repeated one
-  // would only be read twice)
-  const bool direct = a.rows == 1 && a.inds != nullptr;
+  // one-row items (direct) allocate one row of LDS
+  const bool direct = L.direct;
   const int nz = direct ? L.slots : L.max_items;
   const dim3 grid_gu(2 * (a.inter / 128), L.ks_gu, nz);
   const dim3 grid_d(a.hidden / 128, L.ks_d, nz);
@@ -1417,7 +1423,8 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
       mgu.a.w[i].sh_svh = sb[i]->svh;
     }
   }
-  moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_gu, gu_generic), s, mgu,
+  const int lds_rows = direct ? 1 : MOE_ITEM_ROWS;
+  moe_gemv_launch(gate.f, grid_gu, gemv_lds_bytes(lds_rows, L.tps_gu, gu_generic), s, mgu,
                   isorted, iitems, in_items, a.topk);
   if (!fused_mid)
     hipLaunchKernelGGL(moe_mid_kernel, dim3(a.inter / 128, L.slots), dim3(64), 0, s, g, u, a.inds,
@@ -1430,7 +1437,7 @@ hipError_t launch_moe(const MoeArgs &a, const MoeBank &gate, const MoeBank &up,
     md.a.w[0].sh_suh = shared->down.suh;
     md.a.w[0].sh_svh = shared->down.svh;
   }
-  moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(MOE_ITEM_ROWS, L.tps_d, d_generic), s, md,
+  moe_gemv_launch(down.f, grid_d, gemv_lds_bytes(lds_rows, L.tps_d, d_generic), s, md,
                   isorted, iitems, in_items, fused_mid ? 1 : a.topk);
   if (routes_k > 0)
     hipLaunchKernelGGL(moe_combine_shared_kernel, dim3((a.hidden + 255) / 256, 1), dim3(256), 0,
