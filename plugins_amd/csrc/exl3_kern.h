@@ -99,6 +99,10 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr int GEMV_THREADS = 512;
 constexpr int GEMV_ROWS = 16;
 constexpr int GEMV_TPS_MAX = 64;
+// k-tile rows a GEMV workgroup takes at one or two rows (their prepare items
+// fit the rows form's first pass)
+constexpr int GEMV_TPS_ONE_ROW_MAX = 128;
+static_assert(2 * (GEMV_TPS_ONE_ROW_MAX / 8) <= GEMV_THREADS / 16, "two rows in one pass");
 constexpr int GEMV_KSPLIT_MAX = 64;
 constexpr int GEMV_MAXW = 4;
 // Prepare items (one row's 128-block) per wave per batch, and per batch of
