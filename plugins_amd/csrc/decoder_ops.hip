@@ -547,11 +547,14 @@ int device_cus() {
 }
 
 int attn_split(int Tmax, int B, int nkv, int *TS) {
-  // keys per split: a power of two >= 64 (four iterations of the
-  // workgroup's 16 keys), at most ~2048 workgroups overall (each is bound
-  // by its own memory round trips, so many in flight), at most AC_MAXS
-  // splits
-  int ts = 64;
+  // keys per split: a power of two >= 128 (each key group's 4 keys in
+  // flight twice), at most ~2048 workgroups overall (each is bound by its
+  // own memory round trips, so many in flight), at most AC_MAXS splits.
+  // Fewer splits leave fewer slots for the o projection's prologue to
+  // combine (each of its column groups reads its heads' slots): at batch 1,
+  // context 2048, 16 splits of 128 keys took 2.27 ms a step against 2.31
+  // with 32 of 64 and 2.35 with 8 of 256.
+  int ts = 128;
   while (((long)((Tmax + ts - 1) / ts) * B * nkv > 2048 || (Tmax + ts - 1) / ts > AC_MAXS))
     ts *= 2;
   // then whole rounds of the compute units: a second workgroup on a CU gets
