@@ -723,16 +723,19 @@ __global__ __launch_bounds__(512) void gemm_splitk_finish_kernel(
 }  // namespace
 
 // Split-K of a GEMM whose tiles fill at most half the GPU: S splits (an
-// even run of stages each) so that tiles x S reaches ~256 workgroups; their
-// f32 sums take S planes of rows x out floats.  Above 128 tiles the planes'
-// traffic costs more than the idle CUs (gate+up at 512 rows: 192 tiles,
-// 547 TFLOP/s split in two against 629 whole).
+// even run of stages each), the most that keep tiles x S within one round
+// of the 256 CUs (one workgroup a CU: its LDS); their f32 sums take S planes
+// of rows x out floats.  A partial second round costs a whole split's time
+// (gate+up at 128 rows: 96 tiles, 45.7 us a call in 2 splits against 57.3 in
+// 3, 288 workgroups).  Above 128 tiles the planes' traffic costs more than
+// the idle CUs (gate+up at 512 rows: 192 tiles, 547 TFLOP/s split in two
+// against 629 whole).
 GemmSplit gemm_split(int rows, int in, int out) {
   GemmSplit g;
   const int mblocks = (rows + GM_BM - 1) / GM_BM;
   const int tiles = ((out + GM_BN - 1) / GM_BN) * mblocks;
   const int pairs = in / 16 / 4 / 2;  // stage pairs
-  int S = tiles > GM_SPLIT_TILES ? 1 : (256 + tiles - 1) / tiles;
+  int S = tiles > GM_SPLIT_TILES ? 1 : 256 / tiles;
   S = std::max(1, std::min(S, std::min(pairs, GM_SPLIT_MAX)));
   g.splits = S;
   g.tiles = tiles;

@@ -644,7 +644,7 @@ def test_splitk_give_up_is_reported_and_recovered():
     hook exl3_set_splitk_test_drop) and the wait's bound is 8 polls, so the
     last split's wait gives up every time and every kernel exits normally."""
     rng = np.random.default_rng(901)
-    lin, *_ = make(rng, 4096, 4096, 64)  # 16 splits at batch 1
+    lin, *_ = make(rng, 4096, 4096, 64)  # 8 splits at batch 1
     x = dev_f16(S.activations(rng, 1, 4096))
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):

@@ -104,7 +104,7 @@ def test_noalloc_give_up_is_reported_and_reset():
     stores, the wait's bound is 8 polls) is reported by exl3_stream_status,
     which refills the array's slots; later calls equal exl3_matmul again."""
     rng = np.random.default_rng(17)
-    lin = linear(rng, 4096, 4096)  # 16 splits at batch 1
+    lin = linear(rng, 4096, 4096)  # 8 splits at batch 1
     x = torch.from_numpy(S.activations(rng, 1, 4096)).to(DEV)
     got, want = both(lin, x)
     assert torch.equal(got, want)
