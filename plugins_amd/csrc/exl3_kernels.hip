@@ -415,9 +415,10 @@ void set_splitk_drop(int on) { g_splitk_drop.store(on != 0, std::memory_order_re
 //   (768 workgroups, against 11 of 3: 528, 16 CUs holding a third), o 8 of 4
 //   (256), down 8 of 12 (256), gate+up 4 of 8 (768); the pass 1.7 % faster
 //   than with ~512 workgroups a launch.
-// * Else ~512 workgroups over `groups` column groups; ~256 for more than 4
-//   rows, whose split-K partial sums (rows x 128 floats per workgroup) would
-//   otherwise add half the weight bytes again at 16 rows.
+// * Else ~512 workgroups over `groups` column groups; above 4 rows at most
+//   256 (one round: q+k+v 5 splits, 240 workgroups, against 6 and 288, 0.3 %
+//   faster a decode step at 16 rows), whose split-K partial sums (rows x 128
+//   floats per workgroup) would otherwise add half the weight bytes again.
 void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int tps_max) {
   const int nb = in / 128;
   const int cgs = std::max(1, out / 128) * std::max(1, groups);
@@ -442,7 +443,7 @@ void gemv_plan(int in, int out, int groups, int rows, int *ksplit, int *tps, int
     }
   }
   const int target = rows > 4 ? 256 : 512;
-  int ks = std::min(nb, std::max(1, (target + cgs - 1) / cgs));
+  int ks = std::min(nb, std::max(1, rows > 4 ? target / cgs : (target + cgs - 1) / cgs));
   int bps = std::min(tps_max / 8, (nb + ks - 1) / ks);  // blocks per split
   bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
   *tps = 8 * bps;
