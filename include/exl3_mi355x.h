@@ -658,7 +658,7 @@ const char *exl3_matmul_path(const exl3_weight *w, int64_t rows);
 
 /* The kernel path a swiglu of `rows` rows takes (topk 0: no routes;
  * verify_rows as exl3_swiglu_opts): "dense-gemv", "dense-gemm",
- * "dense-items", "routed-gemv" (grouped GEMV items of up to 8 slots of one
+ * "dense-items", "routed-gemv" (grouped GEMV items of up to 4 slots of one
  * expert) or "routed-gemm" (grouped GEMM over items of up to 256 slots, for
  * prefill-sized expert batches): a diagnostic for tests and benchmarks. */
 const char *exl3_swiglu_path(const exl3_weight *gate, const exl3_weight *up,

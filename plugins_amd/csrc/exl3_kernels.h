@@ -262,7 +262,7 @@ struct MoeArgs {
 };
 // Whether a routed call takes the grouped GEMM (prefill-sized expert
 // batches: at least 32 slots per expert on average, integer rates, and not
-// verify_rows) rather than the grouped GEMV's items of up to 8 slots.
+// verify_rows) rather than the grouped GEMV's items of up to 4 slots.
 bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic);
 // Staging bytes for a call, and (in *partial_floats) the partial-sum slots
 // of its Scratch.

@@ -1199,6 +1199,11 @@ void moe_plan(int in, int out, int groups, bool direct, int *ksplit, int *tps) {
   const int ks = std::min(nb, std::max(1, MOE_RESIDENT_WG / cgs));
   int bps = std::min((direct ? MOE_DIRECT_TPS_MAX : MOE_TPS_MAX) / 8, (nb + ks - 1) / ks);
   bps = std::max(bps, (nb + GEMV_KSPLIT_MAX - 1) / GEMV_KSPLIT_MAX);
+  // splits of even length: the fewest splits of at most bps blocks, then
+  // the blocks spread over them (56 blocks at most 32 a split: 28 + 28, not
+  // 32 + 24)
+  const int nsplit = (nb + bps - 1) / bps;
+  bps = (nb + nsplit - 1) / nsplit;
   *tps = 8 * bps;
   *ksplit = (nb + bps - 1) / bps;
 }

@@ -486,10 +486,10 @@ def test_swiglu_verify_rows_takes_the_decode_chain():
 
 def test_swiglu_routed_long_splits():
     # enough experts and columns that the planner gives the gate+up launch
-    # 128-tile splits (the most a work item takes: 16 blocks of its rows),
-    # items of up to 8 slots; against the oracle's composition
+    # 256-tile splits (the most a work item takes: 32 blocks of its rows),
+    # items of up to 4 slots; against the oracle's composition
     rng = np.random.default_rng(77)
-    E, hidden, inter, topk, n, rows = 40, 2048, 1024, 8, 48, 8
+    E, hidden, inter, topk, n, rows = 40, 4096, 1024, 8, 48, 8
     g_np, g, g_keep = _bank(rng, E, hidden, inter, n)
     u_np, u, u_keep = _bank(rng, E, hidden, inter, n)
     d_np, d, d_keep = _bank(rng, E, inter, hidden, n)

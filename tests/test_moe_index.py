@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 E, HIDDEN, INTER, TOPK, K = 256, 7168, 2048, 8, 3
-GM_BM, MOE_ITEM_ROWS = 256, 8
+GM_BM, MOE_ITEM_ROWS = 256, 4
 
 
 def route(inds: np.ndarray, experts: int, item_rows: int):
@@ -122,7 +122,7 @@ def test_grouped_gemm_indices_deepseek_v3(tokens):
 
 @pytest.mark.parametrize("tokens", [1, 16, 64, 2048])
 def test_routed_gemv_items_deepseek_v3(tokens):
-    """moe_gemv_kernel's items of up to 8 slots: rows, outputs and the
+    """moe_gemv_kernel's items of up to 4 slots: rows, outputs and the
     partial-sum rows stay inside slots x width."""
     rng = np.random.default_rng(1 + tokens)
     slots = tokens * TOPK
