@@ -1184,9 +1184,10 @@ bool moe_uses_gemm(const MoeArgs &a, bool gu_generic, bool d_generic) {
 
 namespace {
 
-// A grouped GEMV launch's k-splits: as many as keep the launch within one
-// round of co-resident workgroups (three per CU on 256 CUs: a second,
-// partial round and the split-K hand-off cost more than the longer splits;
+// A grouped GEMV launch's k-splits: as many as keep the launch within 768
+// workgroups (three a CU; the grouped kernel's registers hold two a CU
+// resident, and the third starts as the first two end: a further partial
+// round and the split-K hand-off cost more than the longer splits;
 // DeepSeek-V3's down at one row: 448 workgroups unsplit, 3 % faster a call
 // than 896 in two splits), splits of at most MOE_TPS_MAX k-tiles, or
 // MOE_DIRECT_TPS_MAX for one-row items (direct: DeepSeek-V3's gate+up at one
