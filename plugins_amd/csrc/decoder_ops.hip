@@ -354,10 +354,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       __syncthreads();
     }
   }
+  // q is f16-exact here (the raw f16 rows, or norm_rope8's f16 rounding):
+  // packed in pairs for v_dot2_f32_f16 against the keys' packed halves; the
+  // scale multiplies the summed score
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  h2_t qh[AT_G][4];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qr[h][e] *= scale;
+    for (int i = 0; i < 4; ++i)
+      qh[h][i] = __builtin_bit_cast(h2_t, (uint32_t)f2h(qr[h][2 * i]) |
+                                              ((uint32_t)f2h(qr[h][2 * i + 1]) << 16));
   float m[AT_G], l[AT_G], o[AT_G][8];
 #pragma unroll
   for (int h = 0; h < AT_G; ++h) {
@@ -371,26 +378,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     // independent (formed side by side), then one online-softmax update per
     // head takes all of them (keys past the split's end score -inf and weigh
     // 0; the first key of a block is always in range, so the new maximum is
-    // finite)
+    // finite).  Products of f16 halves summed in f32 (v_dot2_f32_f16); the
+    // weights rounded to f16 for the value sums (pairs of keys per dot2),
+    // and the same rounded weights summed into l.
+    static_assert(AT_KD % 2 == 0, "value sums take keys in pairs");
     for (int tb = tg; tb < t1; tb += 16 * AT_KD) {
-      float sc[AT_KD][AT_G], vf[AT_KD][8];
+      float sc[AT_KD][AT_G];
+      h2_t vp[AT_KD / 2][8];
 #pragma unroll
       for (int j = 0; j < AT_KD; ++j) {
         const int t = tb + 16 * j;
-        float kf[8];
-        unpack8(kr[j], kf);
-        unpack8(vr[j], vf[j]);
+        const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+        if (j & 1) {
+          // dims 2i / 2i + 1 of keys j - 1 and j in one pair each
+          const uint32_t a[4] = {vr[j - 1].x, vr[j - 1].y, vr[j - 1].z, vr[j - 1].w};
+          const uint32_t b[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vp[j >> 1][2 * i] =
+                __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(b[i], a[i], 0x05040100u));
+            vp[j >> 1][2 * i + 1] =
+                __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(b[i], a[i], 0x07060302u));
+          }
+        }
         const int tn = min(t + 16 * AT_KD, t1 - 1);
         kr[j] = ld(kcache, tn);
-        vr[j] = ld(vcache, tn);
+        if (j & 1) {
+          vr[j - 1] = ld(vcache, min(t - 16 + 16 * AT_KD, t1 - 1));
+          vr[j] = ld(vcache, tn);
+        }
 #pragma unroll
         for (int h = 0; h < AT_G; ++h) {
-          // fused multiply-adds (this op's own arithmetic, not the
-          // reference's rounding points)
           float d = 0.0f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], kf[e], d);
-          sc[j][h] = row16_sum(d);
+          for (int i = 0; i < 4; ++i)
+            d = __builtin_amdgcn_fdot2(qh[h][i], __builtin_bit_cast(h2_t, kw[i]), d, false);
+          sc[j][h] = row16_sum(d) * scale;
           if (t >= t1) sc[j][h] = -INFINITY;
         }
       }
@@ -400,18 +423,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
         for (int j = 0; j < AT_KD; ++j) mn = fmaxf(mn, sc[j][h]);
         const float c = __expf(m[h] - mn);
-        float pr[AT_KD], ps = 0.0f;
+        uint32_t pb[AT_KD];
+        float ps = 0.0f;
 #pragma unroll
         for (int j = 0; j < AT_KD; ++j) {
-          pr[j] = __expf(sc[j][h] - mn);
-          ps += pr[j];
+          pb[j] = f2h(__expf(sc[j][h] - mn));
+          ps += h2f((uint16_t)pb[j]);
         }
         l[h] = fmaf(l[h], c, ps);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float a = o[h][e] * c;
 #pragma unroll
-          for (int j = 0; j < AT_KD; ++j) a = fmaf(pr[j], vf[j][e], a);
+          for (int jp = 0; jp < AT_KD / 2; ++jp)
+            a = __builtin_amdgcn_fdot2(
+                __builtin_bit_cast(h2_t, pb[2 * jp] | (pb[2 * jp + 1] << 16)), vp[jp][e], a, false);
           o[h][e] = a;
         }
         m[h] = mn;
