@@ -572,6 +572,23 @@ int device_cus() {
   return cached[dev];
 }
 
+// Workgroups of the attention kernel resident at once on the device (its
+// registers allow 3 a CU on gfx950), read once per device.
+int attn_resident_wgs() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return device_cus();
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void *>(&attn_decode_kernel<true>), 256, 0) != hipSuccess ||
+        n <= 0)
+      n = 1;
+    cached[dev] = n * device_cus();
+  }
+  return cached[dev];
+}
+
 int attn_split(int Tmax, int B, int nkv, int *TS) {
   // keys per split: a power of two >= 128 (each key group's 4 keys in
   // flight twice), at most ~2048 workgroups overall (each is bound by its
@@ -583,13 +600,14 @@ int attn_split(int Tmax, int B, int nkv, int *TS) {
   int ts = 128;
   while (((long)((Tmax + ts - 1) / ts) * B * nkv > 2048 || (Tmax + ts - 1) / ts > AC_MAXS))
     ts *= 2;
-  // then whole rounds of the compute units: a second workgroup on a CU gets
-  // its data after the first's, so the few workgroups past a multiple of the
-  // CU count would finish last (at batch 1, context 2048: 33 x 8 = 264
+  // then whole rounds of resident workgroups: the few workgroups past a
+  // round would finish last (at batch 1, context 2048: 33 x 8 = 264
   // workgroups ran ~4 us behind on 8 CUs); the splits grow so the grid is
-  // the round count below it times the CUs
+  // the round count below it times the resident workgroups (at batch 16,
+  // context 2048: 6 splits, 768 workgroups, 4.08 ms a step against 4.16
+  // with 8 splits, 1024 workgroups, counted in rounds of the 256 CUs)
   const long per = (long)B * nkv;
-  const int cus = device_cus();
+  const int cus = attn_resident_wgs();
   const long wgs = (long)((Tmax + ts - 1) / ts) * per;
   const long rounds = wgs / cus;
   if (rounds >= 1) {

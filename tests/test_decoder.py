@@ -197,7 +197,7 @@ def _ssq(h):
 def test_attention_o_fused_equals_separate(B, T, lens):
     # exl3d_attn_o against its two steps (attention with its combine launch,
     # then the o linear with the residual finish): at rows in one prepare
-    # batch o's prepare combines the key splits itself (with 128 splits at
+    # batch o's prepare combines the key splits itself (with 96 splits at
     # T = 20000: two chunks of the split loop), above it the steps run as
     # they are; residual and its sums of squares equal bit for bit
     from plugins_amd import qwen3 as Q
